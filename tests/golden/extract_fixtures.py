@@ -1,0 +1,126 @@
+"""Extract the reference's frozen attention fixtures into compact test vectors.
+
+Run once in a container that has the reference tree mounted:
+
+    python tests/golden/extract_fixtures.py [/root/reference]
+
+It reads only data files (headerless little-endian arrays, JSON manifests)
+from ``tests/fixtures/`` of the reference, checks each array's SHA-256 against
+the manifest that ships with it, and writes ``<name>.npz`` (arrays) plus
+``<name>.json`` (case metadata) next to this script.  Nothing here imports or
+runs reference code.  The test suite reads only the outputs, so the GPU box
+never needs the reference tree.
+
+Fixture sets taken (all used by the reference's own attention tests):
+  tiny-v1                    tests/cpu_attention.rs:16-79, tests/cached_attention.rs:5-56
+  fp16-v1                    half-storage reconstruction of tiny-v1 (manifest gate_policy)
+  gemma-local-attention-v1   src/cpu/window_attention/tests.rs:31-131
+  gemma-kv-v1                src/cpu/span_attention/tests.rs:212, src/model/window_cache/tests.rs:77
+  gemma-softcap-v1           src/cpu/softcap/tests.rs:19
+  qwen3-attention-inputs-v1  src/metal/compensated_attention.rs:465-561 (inputs only)
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+DTYPES = {"f32le": "<f4", "f16le": "<f2", "u32le": "<u4"}
+
+
+def sha(data: bytes) -> str:
+    return hashlib.sha256(data).hexdigest()
+
+
+def read_array(root: str, meta: dict) -> np.ndarray:
+    path = os.path.join(root, meta["file"])
+    data = open(path, "rb").read()
+    assert len(data) == meta["bytes"], path
+    if "sha256" in meta:
+        assert sha(data) == meta["sha256"], f"hash mismatch for {path}"
+    dtype = meta.get("dtype") or meta["file"].rsplit(".", 1)[1]
+    return np.frombuffer(data, dtype=DTYPES[dtype]).reshape(meta["shape"]).copy()
+
+
+def tiny_like(ref: str, name: str, out: str, keys: list[str]):
+    root = os.path.join(ref, "tests", "fixtures", name)
+    manifest = json.load(open(os.path.join(root, "manifest.json")))
+    arrays, meta = {}, {"cases": manifest["cases"], "model": manifest["model"], "gates": {}}
+    for case in manifest["cases"]:
+        tokens_key = f"cases.{case}.tokens"
+        if tokens_key in manifest["arrays"]:
+            arrays[tokens_key] = read_array(root, manifest["arrays"][tokens_key])
+        for layer in range(manifest["model"]["num_layers"]):
+            for key in keys:
+                full = f"cases.{case}.layers.{layer}.{key}"
+                if full not in manifest["arrays"]:
+                    continue
+                m = manifest["arrays"][full]
+                arrays[full] = read_array(root, m)
+                if m.get("gate_against_source_fp32"):
+                    meta["gates"][full] = m["gate_against_source_fp32"]
+    np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
+
+
+def json_arrays(obj, prefix, arrays):
+    """Replace {dtype, shape, values} leaves by a name into `arrays`."""
+    if isinstance(obj, dict):
+        if set(obj) >= {"dtype", "shape", "values"}:
+            dtype = np.dtype(obj["dtype"])
+            values = obj["values"]
+            if dtype == np.bool_:
+                a = np.array(values, dtype=np.bool_)
+            else:
+                a = np.array([np.nan if v is None else v for v in values], dtype=dtype)
+            arrays[prefix] = a.reshape(obj["shape"])
+            return {"array": prefix}
+        return {k: json_arrays(v, f"{prefix}.{k}", arrays) for k, v in obj.items()}
+    if isinstance(obj, list):
+        return [json_arrays(v, f"{prefix}.{i}", arrays) for i, v in enumerate(obj)]
+    return obj
+
+
+def math_json(ref: str, name: str, out: str):
+    path = os.path.join(ref, "tests", "fixtures", name, "math.json")
+    raw = open(path, "rb").read()
+    data = json.loads(raw)
+    arrays = {}
+    cases = json_arrays(data["cases"], "cases", arrays)
+    meta = {"source_sha256": sha(raw), "format": data.get("format"), "cases": cases}
+    np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
+
+
+def qwen3_inputs(ref: str, out: str):
+    root = os.path.join(ref, "tests", "fixtures", "qwen3-attention-inputs-v1")
+    manifest = json.load(open(os.path.join(root, "manifest.json")))
+    raw = open(os.path.join(root, "inputs.f16le"), "rb").read()
+    assert len(raw) == manifest["bytes"] and sha(raw) == manifest["sha256"]
+    arrays = {}
+    for a in manifest["arrays"]:
+        chunk = raw[a["offset"]:a["offset"] + a["bytes"]]
+        arrays[a["name"]] = np.frombuffer(chunk, dtype="<f2").reshape(a["shape"]).copy()
+    meta = {k: manifest[k] for k in ("positions", "query_heads", "kv_heads", "head_dim", "layer")}
+    np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
+
+
+def main(ref: str):
+    attn = ["q_projection", "k_projection", "q_rotary", "k_rotary", "v_projection",
+            "attention_scores", "attention_probabilities", "attention_context"]
+    tiny_like(ref, "tiny-v1", "tiny_v1", attn)
+    tiny_like(ref, "fp16-v1", "fp16_v1", attn + ["cache_k", "cache_v"])
+    math_json(ref, "gemma-local-attention-v1", "gemma_local_attention_v1")
+    math_json(ref, "gemma-kv-v1", "gemma_kv_v1")
+    math_json(ref, "gemma-softcap-v1", "gemma_softcap_v1")
+    qwen3_inputs(ref, "qwen3_attention_inputs_v1")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -1,0 +1,483 @@
+"""Pin the CPU oracle against the reference's frozen vectors and closed forms.
+
+Each oracle function is checked by at least one of: a reference fixture, a
+known-answer case from the reference's tests, a closed form, or brute force.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from goldens import TINY_CASES, Golden, close, head_major_to_token_major
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    return Golden("tiny_v1")
+
+
+def _tiny_layer(tiny, case, layer):
+    p = f"cases.{case}.layers.{layer}"
+    return {k: tiny.arrays[f"{p}.{k}"] for k in (
+        "q_projection", "k_projection", "q_rotary", "k_rotary", "v_projection",
+        "attention_scores", "attention_probabilities", "attention_context")}
+
+
+# ---- tiny-v1: rotary + full-prefix attention (tests/cpu_attention.rs:16-79) ----
+
+def test_rotary_and_attention_match_tiny_fixture(orc, tiny):
+    for case in TINY_CASES:
+        tokens = len(tiny.arrays[f"cases.{case}.tokens"])
+        offset = tiny.meta["cases"][case]["position_offset"]
+        for layer in range(2):
+            a = _tiny_layer(tiny, case, layer)
+            q = orc.rotary(a["q_projection"], tokens, 4, 8, offset, 1e6)
+            k = orc.rotary(a["k_projection"], tokens, 2, 8, offset, 1e6)
+            close(q, a["q_rotary"])
+            close(k, a["k_rotary"])
+            ctx, sc, pr = orc.attention(q, k, a["v_projection"], tokens, 4, 2, 8)
+            close(sc, a["attention_scores"])
+            close(pr, a["attention_probabilities"])
+            close(ctx, a["attention_context"])
+
+
+def test_rotary_known_answer_and_chunk_offsets(orc, tiny):
+    """src: tests/cpu_attention.rs:81-128."""
+    x = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    assert np.array_equal(orc.rotary(x, 1, 1, 4, 0, 1.0), x)
+    out = orc.rotary(x, 1, 1, 4, 1, 1.0)
+    s, c = np.float32(math.sin(1.0)), np.float32(math.cos(1.0))
+    close(out, [c - 3 * s, 2 * c - 4 * s, s + 3 * c, 2 * s + 4 * c])
+    inp = tiny.arrays["cases.capacity.layers.0.q_projection"].reshape(-1)
+    whole = orc.rotary(inp, 32, 4, 8, 5, 1e6)
+    for t in range(32):
+        one = orc.rotary(inp[t * 32:(t + 1) * 32], 1, 4, 8, 5 + t, 1e6)
+        assert np.array_equal(one, whole[t * 32:(t + 1) * 32])
+        for h in range(4):
+            a = inp[t * 32 + h * 8:t * 32 + h * 8 + 8].astype(np.float64)
+            b = whole[t * 32 + h * 8:t * 32 + h * 8 + 8].astype(np.float64)
+            assert abs((a ** 2).sum() - (b ** 2).sum()) <= 1e-6 * max((a ** 2).sum(), 1.0)
+
+
+# ---- tiny-v1 over a head-major cache with NaN stale tails (tests/cached_attention.rs:5-56) ----
+
+def test_cached_attention_with_stale_tails_at_all_offsets(orc, tiny):
+    for case in TINY_CASES:
+        for layer in range(2):
+            a = _tiny_layer(tiny, case, layer)
+            q = a["q_rotary"].reshape(-1)
+            tokens = q.size // 32
+            cap = tokens + 3
+            kc = np.full(2 * cap * 8, np.nan, np.float32)
+            vc = kc.copy()
+            k = a["k_rotary"].reshape(tokens, 2, 8)
+            v = a["v_projection"].reshape(tokens, 2, 8)
+            for h in range(2):
+                kc[h * cap * 8:(h * cap + tokens) * 8] = k[:, h].reshape(-1)
+                vc[h * cap * 8:(h * cap + tokens) * 8] = v[:, h].reshape(-1)
+            expected = a["attention_context"].reshape(-1)
+            for offset in range(tokens):
+                n = tokens - offset
+                ctx, _, _ = orc.attention_cached(q[offset * 32:], kc, vc, n, 4, 2, 8, cap, offset)
+                close(ctx, expected[offset * 32:])
+
+
+def test_cached_equals_full_prefix_bitwise(orc, tiny):
+    """The cached path keeps the full-prefix FP32 dot/context order (src/cpu/attention.rs:194-195)."""
+    a = _tiny_layer(tiny, "capacity", 1)
+    tokens = 32
+    full, _, _ = orc.attention(a["q_rotary"], a["k_rotary"], a["v_projection"], tokens, 4, 2, 8)
+    cap = 40
+    kc = np.zeros(2 * cap * 8, np.float32)
+    vc = kc.copy()
+    k = a["k_rotary"].reshape(tokens, 2, 8)
+    v = a["v_projection"].reshape(tokens, 2, 8)
+    for h in range(2):
+        kc[h * cap * 8:(h * cap + tokens) * 8] = k[:, h].reshape(-1)
+        vc[h * cap * 8:(h * cap + tokens) * 8] = v[:, h].reshape(-1)
+    q = a["q_rotary"].reshape(-1)
+    out = np.zeros_like(full)
+    start = 0
+    for chunk in (7, 1, 13, 11):
+        ctx, _, _ = orc.attention_cached(q[start * 32:(start + chunk) * 32], kc, vc, chunk, 4, 2, 8,
+                                         cap, start)
+        out[start * 32:(start + chunk) * 32] = ctx
+        start += chunk
+    assert np.array_equal(out.view(np.uint32), full.view(np.uint32))
+
+
+# ---- known answers from tests/cpu_attention.rs:130-313 ----
+
+def test_grouped_heads_read_shared_value_head(orc):
+    ctx, sc, pr = orc.attention(np.zeros(8), np.zeros(4), [1.0, 2.0, 3.0, 4.0], 1, 4, 2, 2)
+    assert ctx.tolist() == [1, 2, 1, 2, 3, 4, 3, 4]
+    assert sc.tolist() == [0.0] * 4 and pr.tolist() == [1.0] * 4
+
+
+def test_future_changes_preserve_earlier_context_and_zero_masked(orc, tiny):
+    q = tiny.arrays["cases.prompt.layers.0.q_rotary"].reshape(-1).copy()
+    k = tiny.arrays["cases.prompt.layers.0.k_rotary"].reshape(-1).copy()
+    v = tiny.arrays["cases.prompt.layers.0.v_projection"].reshape(-1).copy()
+    before, _, _ = orc.attention(q, k, v, 4, 4, 2, 8)
+    q[96:] = 7.0
+    k[48:] = -5.0
+    v[48:] = 100.0
+    after, _, pr = orc.attention(q, k, v, 4, 4, 2, 8)
+    assert np.array_equal(before[:96], after[:96])
+    assert not np.array_equal(before[96:], after[96:])
+    pr = pr.reshape(4, 4, 4)
+    for h in range(4):
+        for t in range(4):
+            assert np.all(pr[h, t, t + 1:].view(np.uint32) == 0)
+
+
+def test_invalid_inputs_fail_before_mutation(orc):
+    out = np.full(4, 123.0, np.float32)
+    for theta in (0.0, -1.0, float("nan"), float("inf")):
+        with pytest.raises(orc.OracleError) as e:
+            orc.rotary(np.ones(4), 1, 1, 4, 0, theta)
+        assert e.value.code == orc.INVALID_PARAMETER
+    with pytest.raises(orc.OracleError) as e:
+        orc.rotary(np.ones(3), 1, 1, 3, 0, 1e6)
+    assert e.value.code == orc.INVALID_PARAMETER
+    with pytest.raises(orc.OracleError) as e:
+        orc.rotary(np.ones(4), 2, 1, 2, 2 ** 64 - 1, 1e6)
+    assert e.value.code == orc.SIZE_OVERFLOW
+    with pytest.raises(orc.OracleError) as e:
+        orc.rotary(np.ones(4) * np.nan, 1, 1, 4, 0, 1e6)
+    assert e.value.code == orc.NON_FINITE
+    sc, pr = np.full(2, 456.0, np.float32), np.full(2, 789.0, np.float32)
+    with pytest.raises(orc.OracleError) as e:
+        orc.attention(np.ones(4), np.ones(6), np.ones(6), 1, 2, 3, 2, out=(out, sc, pr))
+    assert e.value.code == orc.INVALID_PARAMETER
+    with pytest.raises(orc.OracleError) as e:
+        orc.attention(np.ones(4), np.ones(2), np.full(2, np.nan), 1, 2, 1, 2, out=(out, sc, pr))
+    assert (e.value.code, e.value.tensor) == (orc.NON_FINITE, "v")
+    with pytest.raises(orc.OracleError) as e:
+        orc.attention(np.ones(4), np.ones(1), np.ones(2), 1, 2, 1, 2, out=(out, sc, pr))
+    assert (e.value.code, e.value.tensor) == (orc.LENGTH, "k")
+    assert out.tolist() == [123.0] * 4 and sc.tolist() == [456.0] * 2 and pr.tolist() == [789.0] * 2
+
+
+def test_cached_rejects_invalid_shapes_before_writes(orc):
+    """tests/cached_attention.rs:58-99."""
+    for variant in range(7):
+        shape = dict(tokens=1, query_heads=2, kv_heads=1, head_dim=2, capacity=3, offset=1)
+        k, v, q = np.zeros(6, np.float32), np.zeros(6, np.float32), np.zeros(4, np.float32)
+        if variant == 0:
+            shape["offset"] = 2 ** 64 - 1
+        elif variant == 1:
+            shape["offset"] = 3
+        elif variant == 2:
+            shape["kv_heads"] = 3
+        elif variant == 3:
+            shape["tokens"] = 0
+        elif variant == 4:
+            shape["head_dim"] = 2 ** 64 - 1
+        elif variant == 5:
+            k[0] = np.nan
+        else:
+            v[2] = np.inf
+        ctx = np.full(4, 123.0, np.float32)
+        sc, pr = np.full(3, 456.0, np.float32), np.full(3, 789.0, np.float32)
+        with pytest.raises(orc.OracleError):
+            orc.attention_cached(q, k, v, shape["tokens"], shape["query_heads"], shape["kv_heads"],
+                                 shape["head_dim"], shape["capacity"], shape["offset"],
+                                 out=(ctx, sc, pr))
+        assert ctx.tolist() == [123.0] * 4 and sc.tolist() == [456.0] * 3
+        assert pr.tolist() == [789.0] * 3
+
+
+def test_arithmetic_overflow_is_non_finite(orc):
+    with pytest.raises(orc.OracleError) as e:
+        orc.rotary(np.full(2, np.finfo(np.float32).max), 1, 1, 2, 1, 1.0)
+    assert (e.value.code, e.value.tensor) == (orc.NON_FINITE, "rotary output")
+    with pytest.raises(orc.OracleError) as e:
+        orc.attention([np.finfo(np.float32).max], [2.0], [0.0], 1, 1, 1, 1)
+    assert (e.value.code, e.value.tensor) == (orc.NON_FINITE, "attention scores")
+
+
+# ---- closed forms that a dropped term / wrong index would break ----
+
+def test_zero_query_gives_uniform_probabilities_and_mean_of_values(orc):
+    """Zero Q -> probabilities 1/L; dyadic V -> exact mean (src/metal/native_profile.rs:96-197)."""
+    rng = np.random.default_rng(3)
+    L, D, hq, hkv = 16, 8, 4, 2
+    cap = 20
+    k = rng.standard_normal(hkv * cap * D).astype(np.float32)
+    v = np.zeros((hkv, cap, D), np.float32)
+    v[:, :L] = rng.integers(-8, 8, size=(hkv, L, D)) / 4.0
+    q = np.zeros(hq * D, np.float32)
+    ctx, sc, pr = orc.attention_cached(q, k, v.reshape(-1), 1, hq, hkv, D, cap, L - 1)
+    assert np.all(pr[:L] == np.float32(1.0 / L))
+    expected = v[:, :L].mean(axis=1)
+    for h in range(hq):
+        assert np.array_equal(ctx[h * D:(h + 1) * D], expected[h // 2])
+
+
+def test_softmax_known_values_and_mask(orc):
+    out = orc.softmax([0.0, math.log(3.0)], 1, 2)
+    close(out, [0.25, 0.75], atol=1e-7, rtol=0)
+    out = orc.softmax([1.0, 2.0, 3.0, 4.0], 2, 2, mask=[1, 0, 0, 1])
+    assert out.tolist() == [1.0, 0.0, 0.0, 1.0]
+    with pytest.raises(orc.OracleError) as e:
+        orc.softmax([1.0, 2.0], 1, 2, mask=[0, 0])
+    assert e.value.code == orc.FULLY_MASKED
+
+
+def test_window_one_attends_to_self_only(orc):
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal(3 * 2 * 4).astype(np.float32)
+    k = rng.standard_normal(1 * 6 * 4).astype(np.float32)
+    v = rng.standard_normal(1 * 6 * 4).astype(np.float32)
+    ctx, _, pr = orc.window_attention(q, k, v, 3, 6, 6, 2, 1, 4, 3, 0, 1, 1.0)
+    for t in range(3):
+        for h in range(2):
+            row = pr.reshape(2, 3, 6)[h, t]
+            assert row[3 + t] == 1.0 and row.sum() == 1.0
+            assert np.array_equal(ctx.reshape(3, 2, 4)[t, h], v.reshape(6, 4)[3 + t])
+
+
+def test_window_equals_cached_composition_in_fp64(orc):
+    """Independent FP64 brute force for a wide-window GQA case with absolute origins."""
+    rng = np.random.default_rng(11)
+    Q, K, hq, hkv, D, W, cap = 5, 12, 6, 3, 7, 4, 15
+    q = rng.standard_normal(Q * hq * D).astype(np.float32)
+    k = rng.standard_normal(hkv * cap * D).astype(np.float32)
+    v = rng.standard_normal(hkv * cap * D).astype(np.float32)
+    scale = 0.37
+    ctx, sc, pr = orc.window_attention(q, k, v, Q, K, cap, hq, hkv, D, 107, 100, W, scale)
+    qq = q.reshape(Q, hq, D).astype(np.float64)
+    kk = k.reshape(hkv, cap, D).astype(np.float64)
+    vv = v.reshape(hkv, cap, D).astype(np.float64)
+    for h in range(hq):
+        g = h // (hq // hkv)
+        for t in range(Q):
+            pos = 107 + t
+            s = (kk[g, :K] @ qq[t, h]) * scale
+            vis = [j for j in range(K) if 100 + j <= pos and pos - (100 + j) < W]
+            p = np.exp(s[vis] - s[vis].max())
+            p /= p.sum()
+            close(pr.reshape(hq, Q, K)[h, t, vis], p, atol=1e-7, rtol=1e-6)
+            close(ctx.reshape(Q, hq, D)[t, h], p @ vv[g, vis], atol=1e-6, rtol=1e-5)
+
+
+# ---- gemma-local-attention-v1 (src/cpu/window_attention/tests.rs:31-131) ----
+
+def test_window_attention_matches_gemma_local_fixture(orc):
+    g = Golden("gemma_local_attention_v1")
+    for case in g.meta["cases"]:
+        if case["queries"] == 0:
+            continue
+        Q, K, hq, hkv, D = case["queries"], case["keys"], case["q_heads"], case["kv_heads"], case["dims"]
+        cap = K + 2
+        arr = {n: g[case["arrays"][n]] for n in case["arrays"]}
+        q = head_major_to_token_major(arr["q"], hq, Q, D)
+        k = np.full((hkv, cap, D), np.nan, np.float32)
+        v = k.copy()
+        k[:, :K] = arr["k"]
+        v[:, :K] = arr["v"]
+        ctx, sc, pr = orc.window_attention(
+            q, k.reshape(-1), v.reshape(-1), Q, K, cap, hq, hkv, D,
+            case["origin"] + K - Q, case["origin"], case["window"], case["scale"])
+        close(ctx, head_major_to_token_major(arr["output"], hq, Q, D))
+        close(sc, arr["scores"])
+        close(pr, arr["probabilities"])
+        mask = arr["mask"].reshape(-1)
+        for h in range(hq):
+            row = pr.reshape(hq, Q * K)[h]
+            assert np.all(row[~mask].view(np.uint32) == 0)
+
+
+# ---- gemma-kv-v1 ring views (src/cpu/span_attention/tests.rs:212) ----
+
+def test_span_attention_over_ring_matches_gemma_kv_fixture(orc):
+    g = Golden("gemma_kv_v1")
+    checked = 0
+    for case in g.meta["cases"]:
+        hkv, hq, D, cap, W = case["kv_heads"], case["query_heads"], case["dims"], case["capacity"], case["window"]
+        for step in case["steps"]:
+            arr = {n: g[step["arrays"][n]] for n in step["arrays"]}
+            tokens, offset = step["count"], step["before"]
+            ring_k = arr["ring_before_k"].reshape(hkv, cap, D)
+            ring_v = arr["ring_before_v"].reshape(hkv, cap, D)
+            spans = orc.old_spans(cap, offset, W)
+            frozen = step["old_spans"]
+            live = [s for s in spans if s[2] > 0]
+            assert [[s[1], s[2]] for s in live] == frozen
+            segments = []
+            for position, slot, rows in spans:
+                if rows == 0:
+                    segments.append(orc.Segment(np.zeros(0), np.zeros(0), 0, 0, offset))
+                    continue
+                stride = cap * D
+                begin = slot * D
+                end = (hkv - 1) * stride + begin + rows * D
+                segments.append(orc.Segment(ring_k.reshape(-1)[begin:end], ring_v.reshape(-1)[begin:end],
+                                            rows, stride, position))
+            segments.append(orc.Segment(arr["new_k"].reshape(-1), arr["new_v"].reshape(-1), tokens,
+                                        tokens * D, offset))
+            start = orc.view_start(offset, W)
+            keys = offset + tokens - start
+            q = head_major_to_token_major(arr["q"], hq, tokens, D)
+            ctx, _, _ = orc.span_attention(q, segments, tokens, keys, hq, hkv, D, offset, start, W, 1.0)
+            close(ctx, head_major_to_token_major(arr["context"], hq, tokens, D))
+            # committed ring after copy_runs equals the frozen state
+            after_k, after_v = ring_k.copy(), ring_v.copy()
+            new_k = arr["new_k"].reshape(hkv, tokens, D)
+            new_v = arr["new_v"].reshape(hkv, tokens, D)
+            for src, slot, rows in orc.copy_runs(cap, offset, tokens, W is not None):
+                after_k[:, slot:slot + rows] = new_k[:, src:src + rows]
+                after_v[:, slot:slot + rows] = new_v[:, src:src + rows]
+            assert np.array_equal(after_k.reshape(-1), arr["ring_after_k"].reshape(-1))
+            assert np.array_equal(after_v.reshape(-1), arr["ring_after_v"].reshape(-1))
+            checked += 1
+    assert checked >= 20
+
+
+# ---- ring geometry brute force (src/model/window_rows.rs:95-190) ----
+
+def test_old_spans_match_absolute_rows(orc):
+    for cap in range(1, 13):
+        for sliding in (False, True):
+            window = cap if sliding else None
+            for offset in range(49):
+                if not sliding and offset > cap:
+                    continue
+                spans = orc.old_spans(cap, offset, window)
+                actual = [(p + i, s + i) for p, s, r in spans for i in range(r)]
+                expected = [(p, p % cap if sliding else p) for p in range(offset)
+                            if not sliding or offset - p < cap]
+                assert actual == expected
+                assert orc.view_start(offset, window) == (expected[0][0] if expected else offset)
+
+
+def test_copy_runs_match_tokenwise_oracle(orc):
+    for cap in range(1, 13):
+        for sliding in (False, True):
+            for offset in range(49):
+                for tokens in range(1, 17):
+                    if offset + tokens > 64 or (not sliding and offset + tokens > cap):
+                        continue
+                    slot_of = (lambda p: p % cap) if sliding else (lambda p: p)
+                    actual = [None] * cap
+                    for p in range(offset):
+                        actual[slot_of(p)] = p
+                    expected = list(actual)
+                    before = list(actual)
+                    for p in range(offset, offset + tokens):
+                        expected[slot_of(p)] = p
+                    copied = [False] * cap
+                    for src, slot, rows in orc.copy_runs(cap, offset, tokens, sliding):
+                        for i in range(rows):
+                            assert not copied[slot + i]
+                            copied[slot + i] = True
+                            actual[slot + i] = offset + src + i
+                    assert actual == expected
+                    assert sum(copied) == min(tokens, cap)
+                    assert all(actual[s] == before[s] for s in range(cap) if not copied[s])
+
+
+def test_ring_geometry_near_size_boundary(orc):
+    offset = 2 ** 64 - 2
+    spans = orc.old_spans(512, offset, 512)
+    assert spans[0][2] + spans[1][2] == 511
+    assert spans[0][0] == offset - 511
+    assert spans[1][0] + spans[1][2] == offset
+    runs = orc.copy_runs(512, offset, 1, True)
+    assert runs[0] == (0, offset % 512, 1) and runs[1][2] == 0
+    single = orc.old_spans(1, offset, 1)
+    assert single[0][2] + single[1][2] == 0
+    assert orc.view_start(offset, 1) == offset
+
+
+# ---- gemma-softcap-v1 (src/cpu/softcap/tests.rs:19) + score-softcap extension ----
+
+def test_logit_softcap_matches_fixture(orc):
+    g = Golden("gemma_softcap_v1")
+    checked = 0
+    for case in g.meta["cases"]:
+        if case["width"] == 0:
+            with pytest.raises(orc.OracleError):
+                orc.logit_softcap(np.zeros(0), case["cap"])
+            continue
+        out = orc.logit_softcap(g[case["input"]], case["cap"])
+        close(out, g[case["math"]])
+        close(out, g[case["staged_fp32"]])
+        checked += 1
+    assert checked == 5
+    for cap in (0.0, -1.0, float("nan"), float("inf")):
+        with pytest.raises(orc.OracleError):
+            orc.logit_softcap(np.ones(3), cap)
+
+
+def test_score_softcap_equals_softcapped_scores_then_softmax(orc):
+    """The score-softcap extension composes logit_softcap with the window softmax."""
+    rng = np.random.default_rng(9)
+    Q, K, hq, D, cap = 3, 9, 2, 16, 50.0
+    q = (rng.standard_normal(Q * hq * D) * 8).astype(np.float32)
+    k = (rng.standard_normal(K * D) * 8).astype(np.float32)
+    v = rng.standard_normal(K * D).astype(np.float32)
+    _, raw, _ = orc.window_attention(q, k, v, Q, K, K, hq, 1, D, K - Q, 0, None, 0.25)
+    ctx, sc, pr = orc.window_attention(q, k, v, Q, K, K, hq, 1, D, K - Q, 0, None, 0.25, softcap=cap)
+    assert np.array_equal(sc, orc.logit_softcap(raw, cap))
+    assert np.abs(sc).max() <= cap and np.abs(raw).max() > cap
+    s = sc.reshape(hq, Q, K).astype(np.float64)
+    for h in range(hq):
+        for t in range(Q):
+            vis = K - Q + t + 1
+            p = np.exp(s[h, t, :vis] - s[h, t, :vis].max())
+            p /= p.sum()
+            close(pr.reshape(hq, Q, K)[h, t, :vis], p, atol=1e-7, rtol=1e-6)
+
+
+# ---- fp16-v1: half-storage values widened to FP32 (manifest gate_policy) ----
+
+def test_attention_on_half_storage_matches_fp16_fixture(orc):
+    g = Golden("fp16_v1")
+    for case in TINY_CASES:
+        for layer in range(2):
+            p = f"cases.{case}.layers.{layer}"
+            q = g.arrays[f"{p}.q_rotary"].astype(np.float32).reshape(-1)
+            tokens = q.size // 32
+            ck = g.arrays[f"{p}.cache_k"].astype(np.float32)
+            cv = g.arrays[f"{p}.cache_v"].astype(np.float32)
+            assert np.all(ck[:, tokens:] == 0) and np.all(cv[:, tokens:] == 0)
+            k = ck[:, :tokens].transpose(1, 0, 2).reshape(-1)
+            v = cv[:, :tokens].transpose(1, 0, 2).reshape(-1)
+            ctx, sc, pr = orc.attention(q, k, v, tokens, 4, 2, 8)
+            for name, got in (("attention_scores", sc), ("attention_probabilities", pr),
+                              ("attention_context", ctx)):
+                gate = g.meta["gates"][f"{p}.{name}"]
+                close(got, g.arrays[f"{p}.{name}"].astype(np.float32), atol=gate["atol"], rtol=gate["rtol"])
+            # the cached operator over the frozen half cache gives the same context
+            cctx, _, _ = orc.attention_cached(q, ck.reshape(-1), cv.reshape(-1), tokens, 4, 2, 8, 32, 0)
+            assert np.array_equal(cctx, ctx)
+
+
+def test_greedy_lowest_index_on_ties(orc):
+    assert orc.greedy([1.0, 3.0, 3.0, 2.0]) == 1
+    assert orc.greedy([-1.0]) == 0
+    with pytest.raises(orc.OracleError):
+        orc.greedy([1.0, float("nan")])
+
+
+def test_rmsnorm_closed_form(orc):
+    x = np.array([3.0, 4.0], np.float32)
+    out = orc.rmsnorm(x, [1.0, 2.0], 1, 2, 1e-6)
+    rms = math.sqrt((9 + 16) / 2 + 1e-6)
+    close(out, [3 / rms, 8 / rms], atol=1e-7, rtol=1e-7)
+
+
+def test_proportional_rotary_reduces_to_rotary(orc):
+    """Full rotated dims and factor 1 make proportional rotary the split-half rotary."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(3 * 2 * 8).astype(np.float32)
+    a = orc.rotary(x, 3, 2, 8, 4, 10000.0)
+    b = orc.proportional_rotary(x, 3, 2, 8, 8, 4, 10000.0, 1.0)
+    assert np.array_equal(a, b)
+    c = orc.proportional_rotary(x, 3, 2, 8, 4, 4, 10000.0, 1.0)
+    xr = x.reshape(3, 2, 8)
+    cr = c.reshape(3, 2, 8)
+    assert np.array_equal(cr[:, :, 2:4], xr[:, :, 2:4]) and np.array_equal(cr[:, :, 6:], xr[:, :, 6:])
