@@ -1,0 +1,381 @@
+"""Benchmark of the session attention path on one MI355X.
+
+Default workload (Qwen3-shaped single session):
+16 query heads, 8 KV heads, head_dim 128, bf16 KV (and Q stored as bf16),
+per-head RMSNorm (weights N(1, 0.02)) and RoPE (theta 1e6) on seeded N(0,1)
+Q/K, causal prefill of 2048 tokens in 128-token chunks, then 256 decode
+steps at context 2049..2304.  One step = that whole job for one layer:
+16 x (KV append + chunk attention) + 256 x (KV append + decode attention),
+every call through the C ABI.  Inputs are resident in HBM before timing.
+
+Reported (one JSON line): decode attention GB/s over the decode phase as
+`value` (algorithmic bytes: visible keys x 2*Hkv*D*2 + Q/O bytes), prefill
+attention TFLOPS (4*Hq*D per visible (query, key) pair), the roofline of the
+decode attention kernel from HIP events on its stream, the north-star
+configurations (configs[2] batched decode, configs[4] batched prefill), and
+the CPU oracle timed on this host as the baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-north-star", action="store_true", help="skip configs[2]/[4]")
+    ap.add_argument("--only", choices=["c2", "c3", "c5", "d8k"], default=None,
+                    help="run a single workload (for profiling)")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------- inputs
+
+def qk_producer(torch, x, weight, positions, theta):
+    """Per-head RMSNorm (FP32, eps 1e-6) then split-half RoPE; x: [T, H, D] fp32."""
+    d = x.shape[-1]
+    rms = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+    x = x * rms * weight
+    half = d // 2
+    freq = theta ** (-(2.0 * torch.arange(half, device=x.device, dtype=torch.float64)) / d)
+    ang = positions.to(torch.float64)[:, None] * freq[None, :]
+    sin = torch.sin(ang).float()[:, None, :]
+    cos = torch.cos(ang).float()[:, None, :]
+    a, b = x[..., :half], x[..., half:]
+    return torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1)
+
+
+class C2:
+    """Qwen3-shaped single session."""
+    hq, hkv, d = 16, 8, 128
+    prefill, chunk, decode = 2048, 128, 256
+
+    def __init__(self, torch, ops, kvmod, ctx, seed=1234):
+        self.torch, self.ops, self.ctx = torch, ops, ctx
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        total = self.prefill + self.decode
+        self.total = total
+        pos = torch.arange(total, device="cuda")
+        wq = 1.0 + 0.02 * torch.randn(self.d, generator=g, device="cuda")
+        wk = 1.0 + 0.02 * torch.randn(self.d, generator=g, device="cuda")
+        q = torch.randn(total, self.hq, self.d, generator=g, device="cuda")
+        k = torch.randn(total, self.hkv, self.d, generator=g, device="cuda")
+        v = torch.randn(total, self.hkv, self.d, generator=g, device="cuda")
+        self.q = qk_producer(torch, q, wq, pos, 1e6).to(torch.bfloat16).contiguous()
+        self.k = qk_producer(torch, k, wk, pos, 1e6).to(torch.bfloat16).contiguous()
+        self.v = v.to(torch.bfloat16).contiguous()
+        self.layer = kvmod.LayerKv(ctx, self.hkv, self.d, total, torch.bfloat16)
+        self.out = torch.zeros(total, self.hq * self.d, dtype=torch.float32, device="cuda")
+        self.shape = ops.CachedAttentionShape
+
+    def run_prefill(self):
+        ops, layer = self.ops, self.layer
+        kbuf, vbuf = layer.committed()
+        for start in range(0, self.prefill, self.chunk):
+            n = self.chunk
+            layer.append(self.k[start:start + n], self.v[start:start + n], start)
+            ops.attention_cached(self.ctx, self.q[start:start + n], kbuf, vbuf,
+                                 self.out[start:start + n], None, None,
+                                 self.shape(n, self.hq, self.hkv, self.d, self.total, start))
+
+    def run_decode(self):
+        ops, layer = self.ops, self.layer
+        kbuf, vbuf = layer.committed()
+        for start in range(self.prefill, self.total):
+            layer.append(self.k[start:start + 1], self.v[start:start + 1], start)
+            ops.attention_cached(self.ctx, self.q[start:start + 1], kbuf, vbuf,
+                                 self.out[start:start + 1], None, None,
+                                 self.shape(1, self.hq, self.hkv, self.d, self.total, start))
+
+    def prefill_flops(self):
+        pairs = sum(sum(start + t + 1 for t in range(self.chunk))
+                    for start in range(0, self.prefill, self.chunk))
+        return 4.0 * self.hq * self.d * pairs
+
+    def decode_bytes_per_step(self, keys):
+        return keys * 2 * self.hkv * self.d * 2 + self.hq * self.d * 2 + self.hq * self.d * 4
+
+    def decode_bytes(self):
+        return sum(self.decode_bytes_per_step(p + 1) for p in range(self.prefill, self.total))
+
+
+def time_region(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / 1e3, wall
+
+
+def bench_c2(torch, ops, kvmod, ctx, steps, warmup):
+    w = C2(torch, ops, kvmod, ctx)
+    log("c2: qwen3 16/8/128 bf16, prefill 2048 in 128-token chunks + 256 decode steps")
+    # whole-job step timing
+    def step():
+        w.run_prefill()
+        w.run_decode()
+    job_s, job_wall = time_region(torch, step, steps, warmup)
+    ctx.synchronize()
+    # phase timing (same calls), with the kernel profile of each phase
+    ctx.profile(True)
+    pre_s, _ = time_region(torch, w.run_prefill, steps, 0)
+    pre_prof = ctx.profile_read()
+    ctx.profile(True)
+    dec_s, _ = time_region(torch, w.run_decode, steps, 0)
+    dec_prof = ctx.profile_read()
+    ctx.profile(False)
+    ctx.synchronize()
+    flops = w.prefill_flops()
+    dbytes = w.decode_bytes()
+    res = {
+        "job_ms_per_step": job_s / steps * 1e3,
+        "tokens_per_s": (w.total * steps) / job_s,
+        "prefill_ms": pre_s / steps * 1e3,
+        "prefill_tflops": flops * steps / pre_s / 1e12,
+        "prefill_kernel_tflops": flops * steps / (pre_prof["attention_ms"] / 1e3) / 1e12,
+        "decode_ms": dec_s / steps * 1e3,
+        "decode_gbs": dbytes * steps / dec_s / 1e9,
+        "decode_kernel_us": dec_prof["attention_ms"] / dec_prof["launches"] * 1e3,
+        "decode_combine_us": dec_prof["combine_ms"] / dec_prof["launches"] * 1e3,
+        "decode_kernel_gbs": dbytes * steps / (dec_prof["attention_ms"] / 1e3) / 1e9,
+        "decode_launches": dec_prof["launches"],
+        "decode_bytes_per_step_avg": dbytes / w.decode,
+    }
+    return res, w
+
+
+def bench_decode_batch(torch, ops, ctx, steps, warmup, *, batch, lmin, lmax, dtype, seed=7):
+    """batched decode, per-session L ~ U[lmin, lmax], one new token per step."""
+    hq, hkv, d = 16, 8, 128
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(lmin, lmax + 1, (batch,), generator=g).tolist()
+    caps = [l + steps + warmup + 8 for l in lengths]
+    offsets, acc = [], 0
+    for c in caps:
+        offsets.append(acc)
+        acc += hkv * c * d
+    gd = torch.Generator(device="cuda").manual_seed(seed)
+    scales = torch.empty(batch, device="cuda").uniform_(0.5, 2.0, generator=gd)
+    kpool = torch.empty(acc, dtype=dtype, device="cuda")
+    vpool = torch.empty(acc, dtype=dtype, device="cuda")
+    for b in range(batch):
+        n = hkv * caps[b] * d
+        kpool[offsets[b]:offsets[b] + n] = (torch.randn(n, generator=gd, device="cuda") * scales[b]).to(dtype)
+        vpool[offsets[b]:offsets[b] + n] = (torch.randn(n, generator=gd, device="cuda") * scales[b]).to(dtype)
+    q = (torch.randn(batch, hq, d, generator=gd, device="cuda") * scales[:, None, None]).to(dtype)
+    out = torch.zeros(batch * hq * d, dtype=torch.float32, device="cuda")
+    head_strides = [c * d for c in caps]
+    scale = 1.0 / math.sqrt(d)
+    cur = list(lengths)
+
+    def step():
+        for b in range(batch):
+            cur[b] += 1
+        ops.decode_batch(ctx, q, kpool, vpool, offsets, head_strides, cur, out, query_heads=hq,
+                         kv_heads=hkv, head_dim=d, scale=scale)
+
+    bytes_of = lambda ls: sum(l * 2 * hkv * d * kpool.element_size() for l in ls) + \
+        batch * hq * d * (kpool.element_size() + 4)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ctx.profile(True)
+    start_lengths = list(cur)
+    s, _ = time_region(torch, step, steps, 0)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    ctx.synchronize()
+    total_bytes = sum(bytes_of([l + i + 1 for l in start_lengths]) for i in range(steps))
+    return {
+        "batch": batch, "sum_keys": sum(start_lengths), "dtype": str(dtype).replace("torch.", ""),
+        "ms_per_step": s / steps * 1e3,
+        "gbs": total_bytes / s / 1e9,
+        "kernel_us": prof["attention_ms"] / max(1, prof["launches"]) * 1e3,
+        "combine_us": prof["combine_ms"] / max(1, prof["launches"]) * 1e3,
+        "kernel_gbs": total_bytes / (prof["attention_ms"] / 1e3) / 1e9,
+        "kernel_frac_hbm": total_bytes / (prof["attention_ms"] / 1e3) / 1e9 / PEAK_HBM_GBS,
+    }
+
+
+def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096, tokens=128,
+                        seed=11):
+    """32 sessions x (4096 cached + 128 new causal), Llama-3-8B heads, bf16."""
+    hq, hkv, d = 32, 8, 128
+    gd = torch.Generator(device="cuda").manual_seed(seed)
+    cap = cached + tokens
+    per = hkv * cap * d
+    k = torch.randn(batch, hkv, cap, d, generator=gd, device="cuda")
+    mask = torch.rand(batch, hkv, cap, 1, generator=gd, device="cuda") < 0.05
+    k = torch.where(mask, k * 8.0, k).to(torch.bfloat16).reshape(-1)
+    v = torch.randn(batch * per, generator=gd, device="cuda").to(torch.bfloat16)
+    q = torch.randn(batch, tokens, hq, d, generator=gd, device="cuda").to(torch.bfloat16)
+    out = torch.zeros(batch * tokens * hq * d, dtype=torch.float32, device="cuda")
+    offsets = [b * per for b in range(batch)]
+    strides = [cap * d] * batch
+    positions = [cached] * batch
+
+    def step():
+        ops.prefill_batch(ctx, q, k, v, offsets, strides, positions, out, tokens=tokens,
+                          query_heads=hq, kv_heads=hkv, head_dim=d, scale=1.0 / math.sqrt(d))
+
+    pairs = batch * sum(cached + t + 1 for t in range(tokens))
+    flops = 4.0 * hq * d * pairs
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ctx.profile(True)
+    s, _ = time_region(torch, step, steps, 0)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    ctx.synchronize()
+    kernel_s = prof["attention_ms"] / 1e3
+    return {
+        "sessions": batch, "cached": cached, "new": tokens,
+        "ms_per_step": s / steps * 1e3,
+        "tflops": flops * steps / s / 1e12,
+        "kernel_us": prof["attention_ms"] / max(1, prof["launches"]) * 1e3,
+        "kernel_tflops": flops * steps / kernel_s / 1e12,
+        "kernel_frac_mfma": flops * steps / kernel_s / 1e12 / PEAK_BF16_TFLOPS,
+        "gflop_per_step": flops / 1e9,
+    }
+
+
+def cpu_baseline(w, torch):
+    """The oracle (single thread, FP64 softmax) on the C2 decode phase: 32 of 256 steps."""
+    import numpy as np
+
+    import oracle
+
+    oracle.lib()
+    hq, hkv, d, cap = w.hq, w.hkv, w.d, w.total
+    k = w.layer.committed()[0].float().cpu().numpy()
+    v = w.layer.committed()[1].float().cpu().numpy()
+    q = w.q.float().cpu().numpy().reshape(w.total, -1)
+    steps = 32
+    positions = list(range(w.prefill, w.prefill + steps))
+    t0 = time.perf_counter()
+    for p in positions:
+        oracle.attention_cached(q[p], k, v, 1, hq, hkv, d, cap, p)
+    dt = time.perf_counter() - t0
+    nbytes = sum(w.decode_bytes_per_step(p + 1) for p in positions)
+    return {
+        "value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"C2 decode, 1 layer, {steps} of 256 steps (context {positions[0] + 1}..{positions[-1] + 1}), "
+                  f"oracle attention_cached (FP32 dot, FP64 softmax), {dt:.2f} s",
+        "seconds": dt,
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    from toklet_amd import kv as kvmod
+    from toklet_amd import ops
+
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    ctx = ops.Context(0, synchronous=False)
+    result = {}
+    w = None
+    if args.only in (None, "c2"):
+        c2, w = bench_c2(torch, ops, kvmod, ctx, args.steps, args.warmup)
+        log(json.dumps(c2))
+        result["c2"] = c2
+    if not args.no_north_star and args.only in (None, "d8k"):
+        d8k = bench_decode_batch(torch, ops, ctx, 50, 5, batch=1, lmin=8192, lmax=8192,
+                                 dtype=torch.bfloat16)
+        log("single-session decode at 8192: " + json.dumps(d8k))
+        result["decode_8k"] = d8k
+    if not args.no_north_star and args.only in (None, "c3"):
+        c3 = bench_decode_batch(torch, ops, ctx, 20, 3, batch=64, lmin=512, lmax=8192,
+                                dtype=torch.float16)
+        log("c3: " + json.dumps(c3))
+        result["c3"] = c3
+    if not args.no_north_star and args.only in (None, "c5"):
+        c5 = bench_prefill_batch(torch, ops, ctx, 10, 2)
+        log("c5: " + json.dumps(c5))
+        result["c5"] = c5
+    if args.only is not None and args.only != "c2":
+        print(json.dumps(result))
+        return
+
+    c2 = result["c2"]
+    line = {
+        "metric": "decode attn GB/s (% HBM peak); prefill attn TFLOPS (% MFMA peak)",
+        "value": round(c2["decode_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["job_ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, per-head RMSNorm N(1,0.02) weights, RoPE 1e6)",
+        "config": {"workload": "configs[1] Qwen3 16q/8kv/d128 bf16 KV, prefill 2048 in 128-token "
+                               "chunks + 256 decode steps, 1 layer per step",
+                   "query_heads": 16, "kv_heads": 8, "head_dim": 128, "prefill": 2048, "chunk": 128,
+                   "decode_steps": 256},
+        "prefill_tflops": round(c2["prefill_tflops"], 3),
+        "prefill_frac_mfma": round(c2["prefill_tflops"] / PEAK_BF16_TFLOPS, 5),
+        "decode_frac_hbm": round(c2["decode_gbs"] / PEAK_HBM_GBS, 5),
+        "tokens_per_s": round(c2["tokens_per_s"], 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attn_mfma (decode launches of configs[1])",
+            "achieved": round(c2["decode_kernel_gbs"], 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(c2["decode_kernel_gbs"] / PEAK_HBM_GBS, 5),
+            "traffic": None,
+            "avg_kernel_us": round(c2["decode_kernel_us"], 3),
+            "algorithmic_bytes_per_launch": round(c2["decode_bytes_per_step_avg"]),
+        },
+        "prefill_roofline": {
+            "bound": "mfma", "achieved": round(c2["prefill_kernel_tflops"], 3),
+            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(c2["prefill_kernel_tflops"] / PEAK_BF16_TFLOPS, 5),
+        },
+        "north_star": {k: result[k] for k in ("decode_8k", "c3", "c5") if k in result},
+        "detail": c2,
+    }
+    if not args.no_cpu and w is not None:
+        log("cpu baseline: oracle on the host cores")
+        line["cpu_baseline"] = cpu_baseline(w, torch)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,274 @@
+/*
+ * tokhip.h - C ABI of the MI355X (gfx950) session attention library.
+ *
+ * Drop-in device replacement for toklet's session attention path: the
+ * scalar operators in src/cpu/{attention,window_attention,span_attention,
+ * softcap}.rs and the KV owners in src/model/{cache,window_cache}.rs.
+ * Plain pointers and sizes only; no C++ or torch types cross this boundary.
+ *
+ * Conventions
+ *  - Every entry point returns a tkh_status code and, when `err` is not NULL,
+ *    fills it with the same code plus the payload of the matching toklet
+ *    error (tensor name, index, expected/actual length, message).
+ *  - Codes 1..7 mirror toklet::cpu::Error (src/cpu/mod.rs:47-68) in order;
+ *    the remaining codes mirror model::Error::Capacity/InvalidConfig and the
+ *    device runtime.  The message rule follows toklet's C ABI
+ *    (apple/include/toklet.h:9-35): a NULL `err` suppresses the payload.
+ *  - Element lengths (`*_len`) are checked on the host against the shape
+ *    before any launch, as the reference checks slice lengths before writes.
+ *  - Finiteness of Q/K/V is checked inside the kernels through a device
+ *    status word.  A synchronous context reports TKH_NON_FINITE after the
+ *    call, and operator outputs are written only when the status word is
+ *    clean, so an invalid input leaves `context` untouched.
+ *  - Tensors passed to operators are device pointers (HBM).  Q/context use
+ *    [tokens, query_heads, head_dim]; K/V use the reference's head-major
+ *    [kv_heads, capacity, head_dim] layout (strides [capacity*D, D, 1]).
+ *  - Q is stored in the same dtype as K/V (the Metal precedent in
+ *    src/metal/kernels.metal:104-107 and :136-139 also consumes half Q and
+ *    half K/V); context is always FP32.
+ *  - A tkh_context owns one HIP stream, a device workspace and the status
+ *    word.  It is not thread-safe; separate contexts are independent.
+ *  - No operator allocates.  Device memory is allocated only by
+ *    tkh_context_create and tkh_kv_create.
+ */
+#ifndef TOKHIP_H
+#define TOKHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TKH_ABI_VERSION 1u
+
+typedef enum tkh_status {
+    TKH_OK = 0,
+    TKH_ZERO_DIMENSION = 1,    /* cpu::Error::ZeroDimension */
+    TKH_SIZE_OVERFLOW = 2,     /* cpu::Error::SizeOverflow */
+    TKH_LENGTH = 3,            /* cpu::Error::Length */
+    TKH_TOKEN = 4,             /* cpu::Error::Token */
+    TKH_NON_FINITE = 5,        /* cpu::Error::NonFinite */
+    TKH_INVALID_PARAMETER = 6, /* cpu::Error::InvalidParameter */
+    TKH_FULLY_MASKED = 7,      /* cpu::Error::FullyMasked */
+    TKH_CAPACITY = 8,          /* model::Error::Capacity (src/model/window_cache.rs:214-228) */
+    TKH_INVALID_CONFIG = 9,    /* model::Error::InvalidConfig (stale/foreign KV frame, geometry) */
+    TKH_DEVICE = 10,           /* HIP runtime failure */
+    TKH_UNSUPPORTED = 11,      /* a shape/dtype this build does not run */
+} tkh_status;
+
+typedef struct tkh_error {
+    uint32_t code;
+    uint64_t index;    /* NonFinite index / FullyMasked row */
+    uint64_t expected; /* Length */
+    uint64_t actual;   /* Length */
+    char tensor[64];
+    char message[256];
+} tkh_error;
+
+typedef enum tkh_dtype { TKH_F32 = 0, TKH_F16 = 1, TKH_BF16 = 2 } tkh_dtype;
+
+typedef struct tkh_context tkh_context;
+typedef struct tkh_kv tkh_kv;
+
+/* ---------------- library / context ---------------- */
+
+uint32_t tkh_abi_version(void);
+
+/* Create a context on `device`.  `stream` is the hipStream_t every call of
+ * this context is queued on (NULL: the null stream).  `workspace_bytes` bounds the
+ * split-K partial buffers (0: 256 MiB).  `synchronous` != 0 makes every
+ * operator wait for completion and report the device status; otherwise
+ * status accumulates until tkh_context_synchronize. */
+uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, int synchronous,
+                            tkh_context **out, tkh_error *err);
+void tkh_context_destroy(tkh_context *ctx);
+/* Wait for queued work, report and clear the accumulated device status. */
+uint32_t tkh_context_synchronize(tkh_context *ctx, tkh_error *err);
+void *tkh_context_stream(tkh_context *ctx);
+
+/* Kernel timing with HIP events on the context's stream (the role of the
+ * reference's Metal encoder timestamps, src/metal/profile.rs:1-3).  Enabling
+ * resets the totals; reading waits for the stream.  Times are milliseconds
+ * summed over launches: `attention` is the attention kernel alone, `combine`
+ * the split-K combine/publish kernel. */
+typedef struct tkh_profile {
+    uint64_t launches;
+    double attention_ms;
+    double combine_ms;
+} tkh_profile;
+uint32_t tkh_context_profile(tkh_context *ctx, int enable, tkh_error *err);
+uint32_t tkh_context_profile_read(tkh_context *ctx, tkh_profile *out, tkh_error *err);
+
+/* ---------------- operators ---------------- */
+
+/* Shape of toklet::cpu::CachedAttentionShape (src/cpu/attention.rs:180-189). */
+typedef struct tkh_cached_shape {
+    uint64_t tokens, query_heads, kv_heads, head_dim, capacity, offset;
+} tkh_cached_shape;
+
+/* Replaces cpu::attention_cached (src/cpu/attention.rs:201-296).
+ * q/context: [tokens, Hq, D]; k/v: [Hkv, capacity, D] in `dtype`.
+ * scores/probabilities: optional (NULL) [capacity] FP32 rows; when given they
+ * receive the row the reference leaves behind (last query head, last query). */
+uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, tkh_dtype dtype,
+                              const void *q, uint64_t q_len, const void *k, uint64_t k_len,
+                              const void *v, uint64_t v_len, float *context,
+                              uint64_t context_len, float *scores, uint64_t scores_len,
+                              float *probabilities, uint64_t probabilities_len, tkh_error *err);
+
+/* Shape of toklet::cpu::AttentionShape (src/cpu/attention.rs:67-72). */
+typedef struct tkh_attention_shape {
+    uint64_t tokens, query_heads, kv_heads, head_dim;
+} tkh_attention_shape;
+
+/* Replaces cpu::attention (src/cpu/attention.rs:85-178): full-prefix causal
+ * GQA with token-major K/V [tokens, Hkv, D].  scores/probabilities: optional
+ * [Hq, tokens, tokens] FP32 with masked probabilities exactly +0. */
+uint32_t tkh_attention(tkh_context *ctx, const tkh_attention_shape *shape, tkh_dtype dtype,
+                       const void *q, uint64_t q_len, const void *k, uint64_t k_len,
+                       const void *v, uint64_t v_len, float *context, uint64_t context_len,
+                       float *scores, uint64_t scores_len, float *probabilities,
+                       uint64_t probabilities_len, tkh_error *err);
+
+/* Shape of toklet::cpu::WindowAttentionShape (src/cpu/window_attention.rs:6-17)
+ * with Option<usize> window as (has_window, window).  `softcap` (> 0) applies
+ * cap*tanh(score/cap) to every score after scaling (0: disabled). */
+typedef struct tkh_window_shape {
+    uint64_t queries, keys, capacity, query_heads, kv_heads, head_dim;
+    uint64_t query_start, key_start;
+    uint32_t has_window;
+    uint64_t window;
+    float scale;
+    float softcap;
+} tkh_window_shape;
+
+/* Replaces cpu::window_attention (src/cpu/window_attention.rs:36-168).
+ * scores/probabilities: optional [Hq, queries, keys]. */
+uint32_t tkh_window_attention(tkh_context *ctx, const tkh_window_shape *shape, tkh_dtype dtype,
+                              const void *q, uint64_t q_len, const void *k, uint64_t k_len,
+                              const void *v, uint64_t v_len, float *context,
+                              uint64_t context_len, float *scores, uint64_t scores_len,
+                              float *probabilities, uint64_t probabilities_len, tkh_error *err);
+
+/* toklet::cpu::AttentionKvSegment (src/cpu/span_attention.rs:9-16): rows of
+ * KV head h start at h*head_stride elements; an empty segment has keys = 0. */
+typedef struct tkh_segment {
+    const void *k;
+    uint64_t k_len;
+    const void *v;
+    uint64_t v_len;
+    uint64_t keys, head_stride, key_start;
+} tkh_segment;
+
+/* toklet::cpu::SpanAttentionShape (src/cpu/span_attention.rs:18-28) + softcap. */
+typedef struct tkh_span_shape {
+    uint64_t queries, keys, query_heads, kv_heads, head_dim;
+    uint64_t query_start, key_start;
+    uint32_t has_window;
+    uint64_t window;
+    float scale;
+    float softcap;
+} tkh_span_shape;
+
+/* Replaces cpu::span_attention (src/cpu/span_attention.rs:42-220): attention
+ * over <=2 old ring spans plus the staged chunk, without linearising the ring. */
+uint32_t tkh_span_attention(tkh_context *ctx, const tkh_span_shape *shape, tkh_dtype dtype,
+                            const void *q, uint64_t q_len, const tkh_segment segments[3],
+                            float *context, uint64_t context_len, float *scores,
+                            uint64_t scores_len, float *probabilities, uint64_t probabilities_len,
+                            tkh_error *err);
+
+/* Replaces cpu::logit_softcap (src/cpu/softcap.rs:16-29) on a device buffer. */
+uint32_t tkh_logit_softcap(tkh_context *ctx, float *logits, uint64_t len, float cap,
+                           tkh_error *err);
+
+/* Batched single-token decode over independent sessions (no reference
+ * counterpart; the batched form of attention_cached with tokens = 1 that a
+ * multi-session host loop would otherwise issue per session).
+ * q: [batch, Hq, D] in `dtype`; context: [batch, Hq, D] FP32.
+ * Session b reads K/V rows [0, lengths[b]) of head-major caches whose first
+ * element is k_base/v_base + offsets[b] (elements) with per-head stride
+ * head_strides[b].  lengths/offsets/head_strides are host arrays. */
+uint32_t tkh_decode_batch(tkh_context *ctx, uint64_t batch, uint64_t query_heads,
+                          uint64_t kv_heads, uint64_t head_dim, tkh_dtype dtype, const void *q,
+                          const void *k_base, const void *v_base, const uint64_t *offsets,
+                          const uint64_t *head_strides, const uint64_t *lengths, float scale,
+                          float *context, tkh_error *err);
+
+/* Batched chunk prefill: `batch` sessions, each with `tokens` new queries at
+ * cache offset offsets_pos[b] (keys [0, offsets_pos[b] + tokens) visible
+ * causally), K/V addressed as in tkh_decode_batch.  q: [batch, tokens, Hq, D]. */
+uint32_t tkh_prefill_batch(tkh_context *ctx, uint64_t batch, uint64_t tokens,
+                           uint64_t query_heads, uint64_t kv_heads, uint64_t head_dim,
+                           tkh_dtype dtype, const void *q, const void *k_base,
+                           const void *v_base, const uint64_t *offsets,
+                           const uint64_t *head_strides, const uint64_t *positions, float scale,
+                           float *context, tkh_error *err);
+
+/* ---------------- KV owners ---------------- */
+
+/* Byte accounting of capacity::KvOwner::at_capacity (src/capacity.rs:49-80)
+ * for one K/V pair with `storage` element size (bf16 is this build's
+ * addition to KvStorage).  has_window selects Retention::Sliding. */
+uint32_t tkh_kv_planned_bytes(uint64_t heads, uint64_t head_dim, uint64_t capacity,
+                              uint32_t has_window, uint64_t window, tkh_dtype storage,
+                              uint64_t copies, uint64_t *total_bytes, tkh_error *err);
+
+/* Device-resident owner of separate head-major K/V [heads, capacity, dims].
+ * Full retention mirrors model::KvCache's LayerKv (src/model/cache.rs:1-97);
+ * sliding retention mirrors WindowKvCache (src/model/window_cache.rs:21-464)
+ * with slot = position mod capacity and capacity == window. */
+uint32_t tkh_kv_create(tkh_context *ctx, uint64_t heads, uint64_t dims, uint64_t capacity,
+                       uint64_t max_positions, uint32_t has_window, uint64_t window,
+                       tkh_dtype storage, tkh_kv **out, tkh_error *err);
+void tkh_kv_destroy(tkh_kv *kv);
+
+typedef struct tkh_kv_info {
+    uint64_t heads, dims, capacity, max_positions, window, offset, generation, owner;
+    uint32_t has_window;
+    tkh_dtype storage;
+    void *k; /* device base of K [heads, capacity, dims] */
+    void *v;
+    uint64_t allocated_bytes;
+} tkh_kv_info;
+uint32_t tkh_kv_info_get(const tkh_kv *kv, tkh_kv_info *info);
+
+/* LayerKv::append (src/model/cache.rs:64-85): convert token-major new rows
+ * [tokens, heads, dims] (device, `src_dtype`) into head-major rows
+ * [offset, offset+tokens) of a full-retention cache, rounding to the storage
+ * dtype.  Non-finite inputs set the device status (TKH_NON_FINITE). */
+uint32_t tkh_kv_append(tkh_kv *kv, uint64_t offset, uint64_t tokens, tkh_dtype src_dtype,
+                       const void *k, const void *v, tkh_error *err);
+
+/* WindowKvCache::prepare (src/model/window_cache.rs:193-212).  k/v are the
+ * caller's staged new rows [heads, tokens, dims] in the storage dtype on the
+ * device; they must stay unchanged until the frame is committed or dropped. */
+typedef struct tkh_kv_frame {
+    const void *k;
+    const void *v;
+    uint64_t owner, generation, offset, tokens;
+} tkh_kv_frame;
+uint32_t tkh_kv_prepare(const tkh_kv *kv, const void *k, uint64_t k_len, const void *v,
+                        uint64_t v_len, uint64_t tokens, tkh_kv_frame *frame, tkh_error *err);
+
+/* WindowKvCache::view + KvView::segments/attention_shape
+ * (src/model/window_cache.rs:256-267, 355-406): the three segments (<=2 old
+ * spans in the ring, then the staged chunk) and the matching span shape. */
+uint32_t tkh_kv_view(const tkh_kv *kv, const tkh_kv_frame *frame, uint64_t query_heads,
+                     float scale, tkh_segment segments[3], tkh_span_shape *shape,
+                     tkh_error *err);
+
+/* commit_batch (src/model/window_cache.rs:328-337): validate every frame,
+ * then copy only window_rows::copy_runs rows of each into its ring. */
+uint32_t tkh_kv_commit_batch(tkh_kv *const *kvs, const tkh_kv_frame *frames, uint64_t count,
+                             tkh_error *err);
+
+/* reset_batch (src/model/window_cache.rs:342-350): offset 0, new generation. */
+uint32_t tkh_kv_reset_batch(tkh_kv *const *kvs, uint64_t count, tkh_error *err);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

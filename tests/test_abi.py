@@ -1,0 +1,156 @@
+"""The C-ABI library loads, exports every declared symbol, and validates on the host.
+
+These tests run without a GPU: every call below fails host-side validation (or
+has a NULL context) before anything touches the device.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tokhip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tkh_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from toklet_amd import _lib
+
+    return _lib.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_bindings_cover_the_header():
+    from toklet_amd import _lib
+
+    assert set(declared_functions()) == set(_lib.SIGNATURES)
+
+
+def test_abi_version(lib):
+    assert lib.tkh_abi_version() == 1
+
+
+def _cached(lib, shape, q_len, kv_len, ctx_len, scores_len=0):
+    from toklet_amd import _lib
+
+    err = _lib.Error()
+    s = _lib.CachedShape(*shape)
+    rc = lib.tkh_attention_cached(None, ctypes.byref(s), _lib.BF16, None, q_len, None, kv_len,
+                                  None, kv_len, None, ctx_len, None, scores_len, None, 0,
+                                  ctypes.byref(err))
+    return rc, err
+
+
+def test_cached_validation_order_mirrors_reference(lib):
+    """Codes follow src/cpu/attention.rs:218-245 (tests/cached_attention.rs:58-99)."""
+    from toklet_amd import _lib
+
+    base = (1, 2, 1, 2, 3, 1)  # tokens, Hq, Hkv, D, capacity, offset
+    rc, _ = _cached(lib, base, 4, 6, 4)
+    assert rc == _lib.INVALID_PARAMETER  # valid shape: only the NULL context remains
+    rc, err = _cached(lib, (1, 2, 1, 2, 3, 2 ** 64 - 1), 4, 6, 4)
+    assert rc == _lib.SIZE_OVERFLOW
+    rc, err = _cached(lib, (1, 2, 1, 2, 3, 3), 4, 6, 4)
+    assert rc == _lib.INVALID_PARAMETER and b"capacity" in err.tensor
+    rc, err = _cached(lib, (1, 2, 3, 2, 3, 1), 4, 6, 4)
+    assert rc == _lib.INVALID_PARAMETER and b"divisible" in err.tensor
+    rc, err = _cached(lib, (0, 2, 1, 2, 3, 1), 4, 6, 4)
+    assert rc == _lib.ZERO_DIMENSION and err.tensor == b"tokens"
+    rc, err = _cached(lib, (1, 2, 1, 2 ** 64 - 1, 3, 1), 4, 6, 4)
+    assert rc == _lib.SIZE_OVERFLOW
+    rc, err = _cached(lib, base, 4, 5, 4)
+    assert rc == _lib.LENGTH and err.tensor == b"k cache" and err.expected == 6 and err.actual == 5
+    rc, err = _cached(lib, base, 3, 6, 4)
+    assert rc == _lib.LENGTH and err.tensor == b"q"
+
+
+def test_window_validation_and_fully_masked(lib):
+    from toklet_amd import _lib
+
+    def call(**kw):
+        d = dict(queries=2, keys=4, capacity=4, query_heads=2, kv_heads=1, head_dim=2,
+                 query_start=2, key_start=0, has_window=1, window=2, scale=1.0, softcap=0.0)
+        d.update(kw)
+        s = _lib.WindowShape(**d)
+        err = _lib.Error()
+        q = d["queries"] * d["query_heads"] * d["head_dim"]
+        kv = d["kv_heads"] * d["capacity"] * d["head_dim"]
+        rc = lib.tkh_window_attention(None, ctypes.byref(s), _lib.F32, None, q, None, kv, None,
+                                      kv, None, q, None, 0, None, 0, ctypes.byref(err))
+        return rc, err
+
+    assert call()[0] == _lib.INVALID_PARAMETER  # NULL context after a valid shape
+    assert call(window=0)[0] == _lib.INVALID_PARAMETER
+    assert call(scale=0.0)[0] == _lib.INVALID_PARAMETER
+    assert call(keys=5)[0] == _lib.INVALID_PARAMETER
+    assert call(softcap=-1.0)[0] == _lib.INVALID_PARAMETER
+    assert call(queries=0)[0] == _lib.ZERO_DIMENSION
+    # queries at positions 7, 8 with keys at [0, 4) and window 2: nothing visible
+    rc, err = call(query_start=7)
+    assert rc == _lib.FULLY_MASKED and err.index == 0
+
+
+def test_span_segment_validation(lib):
+    from toklet_amd import _lib
+
+    s = _lib.SpanShape(1, 3, 2, 1, 2, 2, 0, 0, 0, 1.0, 0.0)
+    segs = (_lib.Segment * 3)()
+    segs[0] = _lib.Segment(None, 4, None, 4, 2, 4, 0)
+    segs[1] = _lib.Segment(None, 0, None, 0, 0, 0, 2)
+    segs[2] = _lib.Segment(None, 2, None, 2, 1, 2, 2)
+    err = _lib.Error()
+    rc = lib.tkh_span_attention(None, ctypes.byref(s), _lib.F32, None, 4, segs, None, 4, None, 0,
+                                None, 0, ctypes.byref(err))
+    assert rc == _lib.INVALID_PARAMETER and err.tensor == b"context"
+    segs[2] = _lib.Segment(None, 2, None, 2, 1, 2, 3)  # wrong logical origin
+    rc = lib.tkh_span_attention(None, ctypes.byref(s), _lib.F32, None, 4, segs, None, 4, None, 0,
+                                None, 0, ctypes.byref(err))
+    assert rc == _lib.INVALID_PARAMETER and b"origin" in err.tensor
+    segs[2] = _lib.Segment(None, 2, None, 2, 1, 2, 2)
+    segs[0] = _lib.Segment(None, 4, None, 4, 2, 3, 0)  # heads overlap
+    rc = lib.tkh_span_attention(None, ctypes.byref(s), _lib.F32, None, 4, segs, None, 4, None, 0,
+                                None, 0, ctypes.byref(err))
+    assert rc == _lib.INVALID_PARAMETER and b"overlap" in err.tensor
+
+
+def test_softcap_validation(lib):
+    from toklet_amd import _lib
+
+    err = _lib.Error()
+    assert lib.tkh_logit_softcap(None, None, 0, 30.0, ctypes.byref(err)) == _lib.ZERO_DIMENSION
+    for cap in (0.0, -1.0, float("nan"), float("inf")):
+        assert lib.tkh_logit_softcap(None, None, 4, cap, ctypes.byref(err)) == _lib.INVALID_PARAMETER
+
+
+def test_kv_planned_bytes_mirror_kv_owner(lib):
+    """capacity::KvOwner::at_capacity (src/capacity.rs:49-80) with a bf16 storage kind."""
+    from toklet_amd import _lib
+
+    out = ctypes.c_uint64()
+    err = _lib.Error()
+    assert lib.tkh_kv_planned_bytes(8, 128, 2048, 0, 0, _lib.BF16, 36, ctypes.byref(out),
+                                    ctypes.byref(err)) == 0
+    assert out.value == 2 * 36 * 8 * 2048 * 128 * 2
+    assert lib.tkh_kv_planned_bytes(4, 256, 4096, 1, 1024, _lib.F32, 1, ctypes.byref(out),
+                                    ctypes.byref(err)) == 0
+    assert out.value == 2 * 4 * 1024 * 256 * 4
+    assert lib.tkh_kv_planned_bytes(0, 1, 1, 0, 0, _lib.F32, 1, ctypes.byref(out),
+                                    ctypes.byref(err)) == _lib.ZERO_DIMENSION
+    assert lib.tkh_kv_planned_bytes(1, 1, 1, 1, 0, _lib.F32, 1, ctypes.byref(out),
+                                    ctypes.byref(err)) == _lib.ZERO_DIMENSION
+    assert lib.tkh_kv_planned_bytes(2 ** 40, 2 ** 20, 2 ** 10, 0, 0, _lib.F32, 1,
+                                    ctypes.byref(out), ctypes.byref(err)) == _lib.SIZE_OVERFLOW

@@ -1,0 +1,1124 @@
+// api.cpp - host side of the tokhip C ABI (include/tokhip.h).
+//
+// Validation mirrors the reference operators' check order (dimensions,
+// divisibility, size arithmetic, lengths) so error codes agree with
+// toklet::cpu::Error before anything is launched.  A call then becomes a
+// list of device "problems" (device.hpp), a flat tile space split along the
+// key axis when the grid would otherwise be too small for 256 CUs, one
+// attention launch and one combine launch that publishes the context.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "../../include/tokhip.h"
+#include "device.hpp"
+
+extern "C" hipError_t tkh_launch_mfma(const tkh::Params *p, int dtype, int head_dim, int nrb,
+                                      hipStream_t stream);
+extern "C" hipError_t tkh_launch_generic(const tkh::Params *p, int dtype, hipStream_t stream);
+extern "C" hipError_t tkh_launch_combine(const tkh::Params *p, int64_t total_rows,
+                                         hipStream_t stream);
+extern "C" hipError_t tkh_launch_kv_append(int src, int dst, const void *k, const void *v,
+                                           void *kc, void *vc, int64_t tokens, int heads,
+                                           int dims, int64_t capacity, int64_t offset,
+                                           uint32_t *status, hipStream_t stream);
+extern "C" hipError_t tkh_launch_copy_runs(const void *src_k, const void *src_v, void *dst_k,
+                                           void *dst_v, int64_t tokens, int heads,
+                                           int64_t row_bytes, int64_t capacity,
+                                           const int64_t runs[6], hipStream_t stream);
+extern "C" hipError_t tkh_launch_check_finite(int dtype, const void *a, const void *b, int64_t n,
+                                              uint32_t *status, hipStream_t stream);
+extern "C" hipError_t tkh_launch_softcap(float *x, int64_t n, float cap, uint32_t *status,
+                                         hipStream_t stream);
+extern "C" hipError_t tkh_launch_fill_u32(uint32_t *p, uint32_t v, hipStream_t stream);
+
+namespace {
+
+constexpr int kSlots = 16;
+constexpr int kSlotProblems = 1024;
+
+// ---------------------------------------------------------------- errors
+
+uint32_t fail(tkh_error *err, uint32_t code, const char *tensor, uint64_t index,
+              uint64_t expected, uint64_t actual, const char *fmt, ...) {
+    if (err) {
+        err->code = code;
+        err->index = index;
+        err->expected = expected;
+        err->actual = actual;
+        std::snprintf(err->tensor, sizeof err->tensor, "%s", tensor ? tensor : "");
+        va_list ap;
+        va_start(ap, fmt);
+        std::vsnprintf(err->message, sizeof err->message, fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+uint32_t ok(tkh_error *err) {
+    if (err) {
+        std::memset(err, 0, sizeof *err);
+    }
+    return TKH_OK;
+}
+
+#define TRY(expr)                          \
+    do {                                   \
+        uint32_t _rc = (expr);             \
+        if (_rc != TKH_OK) return _rc;     \
+    } while (0)
+
+// src/cpu/mod.rs:84-114 restated for the C ABI.
+uint32_t nonzero(uint64_t value, const char *name, tkh_error *err) {
+    if (value == 0) return fail(err, TKH_ZERO_DIMENSION, name, 0, 0, 0, "%s must be nonzero", name);
+    return TKH_OK;
+}
+uint32_t product(uint64_t a, uint64_t b, uint64_t *out, tkh_error *err) {
+    if (__builtin_mul_overflow(a, b, out))
+        return fail(err, TKH_SIZE_OVERFLOW, nullptr, 0, 0, 0, "tensor size arithmetic overflow");
+    return TKH_OK;
+}
+uint32_t add(uint64_t a, uint64_t b, uint64_t *out, tkh_error *err) {
+    if (__builtin_add_overflow(a, b, out))
+        return fail(err, TKH_SIZE_OVERFLOW, nullptr, 0, 0, 0, "tensor size arithmetic overflow");
+    return TKH_OK;
+}
+uint32_t length(const char *tensor, uint64_t actual, uint64_t expected, tkh_error *err) {
+    if (actual != expected)
+        return fail(err, TKH_LENGTH, tensor, 0, expected, actual, "%s length is %llu, expected %llu",
+                    tensor, (unsigned long long)actual, (unsigned long long)expected);
+    return TKH_OK;
+}
+uint32_t invalid(const char *what, tkh_error *err) {
+    return fail(err, TKH_INVALID_PARAMETER, what, 0, 0, 0, "invalid parameter: %s", what);
+}
+uint32_t device_error(hipError_t e, const char *where, tkh_error *err) {
+    return fail(err, TKH_DEVICE, where, 0, 0, 0, "%s: %s", where, hipGetErrorString(e));
+}
+
+#define HIP_TRY(call, where)                                  \
+    do {                                                      \
+        hipError_t _e = (call);                               \
+        if (_e != hipSuccess) return device_error(_e, where, err); \
+    } while (0)
+
+int esize(tkh_dtype dt) { return dt == TKH_F32 ? 4 : 2; }
+bool valid_dtype(uint32_t dt) { return dt <= TKH_BF16; }
+
+int env_int(const char *name, int fallback) {
+    const char *v = std::getenv(name);
+    return v && *v ? std::atoi(v) : fallback;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- context
+
+struct tkh_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool synchronous = true;
+    uint32_t *status_dev = nullptr;
+    uint32_t *status_host = nullptr;
+    uint8_t *workspace = nullptr;
+    size_t workspace_bytes = 0;
+    tkh::Problem *ring_dev = nullptr;
+    tkh::Problem *ring_host = nullptr;
+    hipEvent_t ring_events[kSlots] = {};
+    bool ring_used[kSlots] = {};
+    int ring_next = 0;
+    int target_waves = 2048;
+    int split_keys_override = 0;
+    int force_generic = 0;
+    // profiling: event triples (before attention, after attention, after combine)
+    bool profiling = false;
+    std::vector<hipEvent_t> prof_events;
+    size_t prof_used = 0;
+    uint64_t prof_launches = 0;
+    double prof_attention_ms = 0, prof_combine_ms = 0;
+};
+
+namespace {
+
+// Completes queued work and turns the status word into an error code.
+uint32_t finish(tkh_context *ctx, tkh_error *err) {
+    hipError_t e = hipMemcpyAsync(ctx->status_host, ctx->status_dev, sizeof(uint32_t),
+                                  hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return device_error(e, "synchronize", err);
+    uint32_t st = *ctx->status_host;
+    if (st == 0) return ok(err);
+    // Clear the sticky word so the next call starts clean.
+    e = tkh_launch_fill_u32(ctx->status_dev, 0, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return device_error(e, "status reset", err);
+    if (st & tkh::ST_NONFINITE_INPUT)
+        return fail(err, TKH_NON_FINITE, "attention inputs", 0, 0, 0,
+                    "non-finite value in attention inputs or scores (status 0x%x)", st);
+    if (st & tkh::ST_BAD_MASS)
+        return fail(err, TKH_NON_FINITE, "attention probabilities", 0, 0, 0,
+                    "softmax mass is not finite and positive (status 0x%x)", st);
+    return fail(err, TKH_NON_FINITE, "attention context", 0, 0, 0,
+                "non-finite value in attention context (status 0x%x)", st);
+}
+
+uint32_t after_launch(tkh_context *ctx, tkh_error *err) {
+    if (ctx->synchronous) return finish(ctx, err);
+    return ok(err);
+}
+
+// A launch plan: problems sharing head geometry, dtype and mask parameters.
+struct Plan {
+    std::vector<tkh::Problem> problems;
+    tkh_dtype dtype = TKH_BF16;
+    int64_t query_heads = 0, kv_heads = 0, head_dim = 0;
+    bool has_window = false;
+    int64_t window = 0;
+    float scale = 1.0f;
+    float softcap = 0.0f;
+    int diag_mode = 0;
+    float *scores = nullptr;
+    float *probs = nullptr;
+};
+
+tkh::Problem make_problem(const void *q, float *out, int64_t q_row_stride, int64_t q_pos0,
+                          int64_t k_pos0, int64_t keys, int64_t queries) {
+    tkh::Problem p{};
+    p.q = q;
+    p.out = out;
+    p.q_row_stride = q_row_stride;
+    p.q_pos0 = q_pos0;
+    p.k_pos0 = k_pos0;
+    p.keys = keys;
+    p.queries = (int32_t)queries;
+    p.nseg = 0;
+    p.splits = 1;
+    p.split_keys = 0;
+    p.row_blocks = 1;
+    return p;
+}
+
+void add_segment(tkh::Problem &p, const void *k, const void *v, int64_t head_stride,
+                 int64_t row_stride, int64_t keys, int64_t start) {
+    tkh::Segment &s = p.seg[p.nseg++];
+    s.k = k;
+    s.v = v;
+    s.head_stride = head_stride;
+    s.row_stride = row_stride;
+    s.keys = keys;
+    s.start = start;
+}
+
+uint32_t upload(tkh_context *ctx, const tkh::Problem *probs, int count, tkh::Problem **dev,
+                tkh_error *err) {
+    int slot = ctx->ring_next;
+    ctx->ring_next = (ctx->ring_next + 1) % kSlots;
+    if (ctx->ring_used[slot]) HIP_TRY(hipEventSynchronize(ctx->ring_events[slot]), "problem ring");
+    tkh::Problem *host = ctx->ring_host + (size_t)slot * kSlotProblems;
+    *dev = ctx->ring_dev + (size_t)slot * kSlotProblems;
+    std::memcpy(host, probs, sizeof(tkh::Problem) * count);
+    HIP_TRY(hipMemcpyAsync(*dev, host, sizeof(tkh::Problem) * count, hipMemcpyHostToDevice,
+                           ctx->stream),
+            "problem upload");
+    HIP_TRY(hipEventRecord(ctx->ring_events[slot], ctx->stream), "problem ring");
+    ctx->ring_used[slot] = true;
+    return TKH_OK;
+}
+
+// Fold finished event triples into the totals.
+uint32_t profile_drain(tkh_context *ctx, tkh_error *err) {
+    if (ctx->prof_used == 0) return TKH_OK;
+    HIP_TRY(hipEventSynchronize(ctx->prof_events[3 * ctx->prof_used - 1]), "profile");
+    for (size_t i = 0; i < ctx->prof_used; ++i) {
+        float a = 0, c = 0;
+        HIP_TRY(hipEventElapsedTime(&a, ctx->prof_events[3 * i], ctx->prof_events[3 * i + 1]), "profile");
+        HIP_TRY(hipEventElapsedTime(&c, ctx->prof_events[3 * i + 1], ctx->prof_events[3 * i + 2]), "profile");
+        ctx->prof_attention_ms += a;
+        ctx->prof_combine_ms += c;
+        ctx->prof_launches += 1;
+    }
+    ctx->prof_used = 0;
+    return TKH_OK;
+}
+
+uint32_t profile_slot(tkh_context *ctx, hipEvent_t **ev, tkh_error *err) {
+    const size_t cap = 1024;
+    if (ctx->prof_events.empty()) {
+        ctx->prof_events.resize(3 * cap);
+        for (auto &e : ctx->prof_events) HIP_TRY(hipEventCreate(&e), "profile");
+    }
+    if (ctx->prof_used == cap) TRY(profile_drain(ctx, err));
+    *ev = &ctx->prof_events[3 * ctx->prof_used++];
+    return TKH_OK;
+}
+
+// Launch one group of problems (<= kSlotProblems) through the workspace.
+uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
+                      tkh_error *err) {
+    const int64_t D = plan.head_dim, Hq = plan.query_heads, Hkv = plan.kv_heads;
+    const int64_t G = Hq / Hkv;
+    const bool mfma = !ctx->force_generic && plan.diag_mode == 0 &&
+                      (plan.dtype == TKH_BF16 || plan.dtype == TKH_F16) &&
+                      (D == 64 || D == 128 || D == 256);
+    int nrb = 1;
+    int64_t max_rows = 0;
+    for (auto &p : group) max_rows = std::max<int64_t>(max_rows, (int64_t)p.queries * G);
+    if (mfma && D != 256 && max_rows > 16) nrb = 2;
+
+    const size_t ws_floats = ctx->workspace_bytes / sizeof(float);
+    int64_t split_keys = 0;
+    if (mfma) {
+        // Work in (row block x key) units; choose a key split that yields
+        // about target_waves waves, in multiples of the 32-key tile.
+        double work = 0;
+        int64_t base_tiles = 0;
+        for (auto &p : group) {
+            p.row_blocks = (int32_t)(((int64_t)p.queries * G + 16 * nrb - 1) / (16 * nrb));
+            base_tiles += Hkv * p.row_blocks;
+            work += (double)Hkv * p.row_blocks * (double)p.keys;
+        }
+        int64_t sk = (int64_t)std::ceil(work / std::max(1, ctx->target_waves));
+        sk = std::max<int64_t>(64, (sk + 31) / 32 * 32);
+        if (ctx->split_keys_override > 0) sk = (ctx->split_keys_override + 31) / 32 * 32;
+        for (;;) {
+            size_t need = 0;
+            for (auto &p : group) {
+                int64_t splits = (p.keys + sk - 1) / sk;
+                need += (size_t)p.queries * Hq * splits * (D + 2);
+            }
+            if (need <= ws_floats) break;
+            int64_t max_keys = 0;
+            for (auto &p : group) max_keys = std::max(max_keys, p.keys);
+            if (sk >= max_keys)
+                return fail(err, TKH_UNSUPPORTED, "workspace", 0, need * 4, ctx->workspace_bytes,
+                            "attention needs %zu workspace bytes, context has %zu", need * 4,
+                            ctx->workspace_bytes);
+            sk *= 2;
+        }
+        split_keys = sk;
+        (void)base_tiles;
+    } else {
+        size_t need = 0;
+        for (auto &p : group) need += (size_t)p.queries * Hq * (D + 2);
+        if (need > ws_floats)
+            return fail(err, TKH_UNSUPPORTED, "workspace", 0, need * 4, ctx->workspace_bytes,
+                        "attention needs %zu workspace bytes, context has %zu", need * 4,
+                        ctx->workspace_bytes);
+    }
+
+    int64_t tiles = 0, rows = 0, part_rows = 0;
+    for (auto &p : group) {
+        p.tile_base = tiles;
+        p.part_base = rows;
+        if (mfma) {
+            p.split_keys = (int32_t)split_keys;
+            p.splits = (int32_t)((p.keys + split_keys - 1) / split_keys);
+            tiles += Hkv * p.splits * p.row_blocks;
+        } else {
+            p.splits = 1;
+            p.row_blocks = 1;
+            tiles += (int64_t)p.queries * Hq;
+        }
+        p.slot_base = part_rows;
+        rows += (int64_t)p.queries * Hq;
+        part_rows += (int64_t)p.queries * Hq * p.splits;
+    }
+
+    tkh::Problem *dev = nullptr;
+    if (group.size() > 1) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
+
+    tkh::Params prm{};
+    prm.problems = dev;
+    if (group.size() == 1) prm.single = group[0];
+    prm.nproblems = (int32_t)group.size();
+    prm.query_heads = (int32_t)Hq;
+    prm.kv_heads = (int32_t)Hkv;
+    prm.head_dim = (int32_t)D;
+    prm.group = (int32_t)G;
+    prm.has_window = plan.has_window ? 1 : 0;
+    prm.window = plan.window;
+    prm.scale = plan.scale;
+    prm.scale_log2 = plan.scale * 1.4426950408889634f;
+    prm.softcap = plan.softcap;
+    prm.total_tiles = tiles;
+    prm.part_ml = reinterpret_cast<float *>(ctx->workspace);
+    prm.part_o = reinterpret_cast<float *>(ctx->workspace) + 2 * part_rows;
+    prm.status = ctx->status_dev;
+    prm.scores = plan.scores;
+    prm.probs = plan.probs;
+    prm.diag_mode = plan.diag_mode;
+
+    hipEvent_t *ev = nullptr;
+    if (ctx->profiling) TRY(profile_slot(ctx, &ev, err));
+    if (ev) HIP_TRY(hipEventRecord(ev[0], ctx->stream), "profile");
+    hipError_t e;
+    if (mfma) e = tkh_launch_mfma(&prm, (int)plan.dtype, (int)D, nrb, ctx->stream);
+    else e = tkh_launch_generic(&prm, (int)plan.dtype, ctx->stream);
+    if (e != hipSuccess) return device_error(e, "attention launch", err);
+    if (ev) HIP_TRY(hipEventRecord(ev[1], ctx->stream), "profile");
+    e = tkh_launch_combine(&prm, rows, ctx->stream);
+    if (e != hipSuccess) return device_error(e, "combine launch", err);
+    if (ev) HIP_TRY(hipEventRecord(ev[2], ctx->stream), "profile");
+    return TKH_OK;
+}
+
+uint32_t run(tkh_context *ctx, Plan &plan, tkh_error *err) {
+    if (hipSetDevice(ctx->device) != hipSuccess)
+        return fail(err, TKH_DEVICE, "device", 0, 0, 0, "hipSetDevice failed");
+    for (size_t i = 0; i < plan.problems.size(); i += kSlotProblems) {
+        size_t n = std::min<size_t>(kSlotProblems, plan.problems.size() - i);
+        std::vector<tkh::Problem> group(plan.problems.begin() + i, plan.problems.begin() + i + n);
+        TRY(launch_group(ctx, plan, group, err));
+    }
+    return after_launch(ctx, err);
+}
+
+
+// First visible key (absolute) of a query at `position` (window_attention.rs:105-107).
+uint64_t first_visible(uint64_t key_start, uint64_t position, bool has_window, uint64_t window) {
+    if (!has_window) return key_start;
+    uint64_t lower = position >= window - 1 ? position - (window - 1) : 0;
+    return std::max(key_start, lower);
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t tkh_abi_version(void) { return TKH_ABI_VERSION; }
+
+uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, int synchronous,
+                            tkh_context **out, tkh_error *err) {
+    if (!out) return invalid("context output", err);
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(err, TKH_DEVICE, "device", 0, 0, 0, "no HIP device is available");
+    if (device < 0 || device >= count) return invalid("device ordinal", err);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    auto *ctx = new tkh_context();
+    ctx->device = device;
+    ctx->synchronous = synchronous != 0;
+    ctx->workspace_bytes = workspace_bytes ? workspace_bytes : (size_t)256 << 20;
+    ctx->target_waves = env_int("TKH_TARGET_WAVES", 2048);
+    ctx->split_keys_override = env_int("TKH_SPLIT_KEYS", 0);
+    ctx->force_generic = env_int("TKH_FORCE_GENERIC", 0);
+    auto cleanup = [&](hipError_t e, const char *where) {
+        tkh_context_destroy(ctx);
+        return device_error(e, where, err);
+    };
+    hipError_t e;
+    // The caller's stream, or the device's null stream: work is ordered with
+    // whatever the caller queued there (no private stream, no priorities).
+    ctx->stream = reinterpret_cast<hipStream_t>(stream);
+    if ((e = hipMalloc(&ctx->status_dev, 256)) != hipSuccess) return cleanup(e, "status");
+    if ((e = hipMemset(ctx->status_dev, 0, 256)) != hipSuccess) return cleanup(e, "status");
+    if ((e = hipHostMalloc(&ctx->status_host, sizeof(uint32_t), hipHostMallocDefault)) != hipSuccess)
+        return cleanup(e, "status");
+    if ((e = hipMalloc(&ctx->workspace, ctx->workspace_bytes)) != hipSuccess)
+        return cleanup(e, "workspace");
+    size_t ring = sizeof(tkh::Problem) * kSlots * kSlotProblems;
+    if ((e = hipMalloc(&ctx->ring_dev, ring)) != hipSuccess) return cleanup(e, "problem ring");
+    if ((e = hipHostMalloc(&ctx->ring_host, ring, hipHostMallocDefault)) != hipSuccess)
+        return cleanup(e, "problem ring");
+    for (int i = 0; i < kSlots; ++i)
+        if ((e = hipEventCreateWithFlags(&ctx->ring_events[i], hipEventDisableTiming)) != hipSuccess)
+            return cleanup(e, "problem ring");
+    *out = ctx;
+    return ok(err);
+}
+
+void tkh_context_destroy(tkh_context *ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    if (ctx->stream) hipStreamSynchronize(ctx->stream);
+    for (int i = 0; i < kSlots; ++i)
+        if (ctx->ring_events[i]) hipEventDestroy(ctx->ring_events[i]);
+    for (auto &e : ctx->prof_events)
+        if (e) hipEventDestroy(e);
+    if (ctx->ring_host) hipHostFree(ctx->ring_host);
+    if (ctx->ring_dev) hipFree(ctx->ring_dev);
+    if (ctx->workspace) hipFree(ctx->workspace);
+    if (ctx->status_host) hipHostFree(ctx->status_host);
+    if (ctx->status_dev) hipFree(ctx->status_dev);
+    delete ctx;
+}
+
+uint32_t tkh_context_synchronize(tkh_context *ctx, tkh_error *err) {
+    if (!ctx) return invalid("context", err);
+    return finish(ctx, err);
+}
+
+void *tkh_context_stream(tkh_context *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+uint32_t tkh_context_profile(tkh_context *ctx, int enable, tkh_error *err) {
+    if (!ctx) return invalid("context", err);
+    TRY(profile_drain(ctx, err));
+    ctx->profiling = enable != 0;
+    ctx->prof_launches = 0;
+    ctx->prof_attention_ms = 0;
+    ctx->prof_combine_ms = 0;
+    return ok(err);
+}
+
+uint32_t tkh_context_profile_read(tkh_context *ctx, tkh_profile *out, tkh_error *err) {
+    if (!ctx || !out) return invalid("context", err);
+    TRY(profile_drain(ctx, err));
+    out->launches = ctx->prof_launches;
+    out->attention_ms = ctx->prof_attention_ms;
+    out->combine_ms = ctx->prof_combine_ms;
+    return ok(err);
+}
+
+// ---------------------------------------------------------------- operators
+
+uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, tkh_dtype dtype,
+                              const void *q, uint64_t q_len, const void *k, uint64_t k_len,
+                              const void *v, uint64_t v_len, float *context,
+                              uint64_t context_len, float *scores, uint64_t scores_len,
+                              float *probabilities, uint64_t probabilities_len, tkh_error *err) {
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    if (!shape) return invalid("shape", err);
+    const tkh_cached_shape s = *shape;
+    // src/cpu/attention.rs:218-251, in order.
+    TRY(nonzero(s.tokens, "tokens", err));
+    TRY(nonzero(s.query_heads, "query_heads", err));
+    TRY(nonzero(s.kv_heads, "kv_heads", err));
+    TRY(nonzero(s.head_dim, "head_dim", err));
+    TRY(nonzero(s.capacity, "cache capacity", err));
+    if (s.query_heads % s.kv_heads != 0) return invalid("query_heads must be divisible by kv_heads", err);
+    uint64_t end;
+    TRY(add(s.offset, s.tokens, &end, err));
+    if (end > s.capacity) return invalid("cache capacity exceeded", err);
+    uint64_t q_stride, q_count, head_stride, kv_count;
+    TRY(product(s.query_heads, s.head_dim, &q_stride, err));
+    TRY(product(s.tokens, q_stride, &q_count, err));
+    TRY(product(s.capacity, s.head_dim, &head_stride, err));
+    TRY(product(s.kv_heads, head_stride, &kv_count, err));
+    TRY(length("q", q_len, q_count, err));
+    TRY(length("k cache", k_len, kv_count, err));
+    TRY(length("v cache", v_len, kv_count, err));
+    TRY(length("attention context", context_len, q_count, err));
+    if (scores) TRY(length("attention scores", scores_len, s.capacity, err));
+    if (probabilities) TRY(length("attention probabilities", probabilities_len, s.capacity, err));
+    if (s.head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 0, 0, "head_dim above 512");
+    if (!ctx) return invalid("context", err);
+    Plan plan;
+    plan.dtype = dtype;
+    plan.query_heads = s.query_heads;
+    plan.kv_heads = s.kv_heads;
+    plan.head_dim = s.head_dim;
+    plan.scale = 1.0f / std::sqrt((float)s.head_dim);
+    plan.diag_mode = (scores || probabilities) ? 2 : 0;
+    plan.scores = scores;
+    plan.probs = probabilities;
+    tkh::Problem p = make_problem(q, context, q_stride, s.offset, 0, end, s.tokens);
+    add_segment(p, k, v, head_stride, s.head_dim, end, 0);
+    plan.problems.push_back(p);
+    return run(ctx, plan, err);
+}
+
+uint32_t tkh_attention(tkh_context *ctx, const tkh_attention_shape *shape, tkh_dtype dtype,
+                       const void *q, uint64_t q_len, const void *k, uint64_t k_len,
+                       const void *v, uint64_t v_len, float *context, uint64_t context_len,
+                       float *scores, uint64_t scores_len, float *probabilities,
+                       uint64_t probabilities_len, tkh_error *err) {
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    if (!shape) return invalid("shape", err);
+    const tkh_attention_shape s = *shape;
+    // src/cpu/attention.rs:102-134, in order.
+    TRY(nonzero(s.tokens, "tokens", err));
+    TRY(nonzero(s.query_heads, "query_heads", err));
+    TRY(nonzero(s.kv_heads, "kv_heads", err));
+    TRY(nonzero(s.head_dim, "head_dim", err));
+    if (s.query_heads % s.kv_heads != 0) return invalid("query_heads must be divisible by kv_heads", err);
+    uint64_t q_stride, kv_stride, q_count, kv_count, tmp, score_count;
+    TRY(product(s.query_heads, s.head_dim, &q_stride, err));
+    TRY(product(s.kv_heads, s.head_dim, &kv_stride, err));
+    TRY(product(s.tokens, q_stride, &q_count, err));
+    TRY(product(s.tokens, kv_stride, &kv_count, err));
+    TRY(product(s.query_heads, s.tokens, &tmp, err));
+    TRY(product(tmp, s.tokens, &score_count, err));
+    TRY(length("q", q_len, q_count, err));
+    TRY(length("k", k_len, kv_count, err));
+    TRY(length("v", v_len, kv_count, err));
+    TRY(length("attention context", context_len, q_count, err));
+    if (scores) TRY(length("attention scores", scores_len, score_count, err));
+    if (probabilities) TRY(length("attention probabilities", probabilities_len, score_count, err));
+    if (s.head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 0, 0, "head_dim above 512");
+    if (!ctx) return invalid("context", err);
+    Plan plan;
+    plan.dtype = dtype;
+    plan.query_heads = s.query_heads;
+    plan.kv_heads = s.kv_heads;
+    plan.head_dim = s.head_dim;
+    plan.scale = 1.0f / std::sqrt((float)s.head_dim);
+    plan.diag_mode = (scores || probabilities) ? 1 : 0;
+    plan.scores = scores;
+    plan.probs = probabilities;
+    tkh::Problem p = make_problem(q, context, q_stride, 0, 0, s.tokens, s.tokens);
+    add_segment(p, k, v, s.head_dim, kv_stride, s.tokens, 0);
+    plan.problems.push_back(p);
+    return run(ctx, plan, err);
+}
+
+uint32_t tkh_window_attention(tkh_context *ctx, const tkh_window_shape *shape, tkh_dtype dtype,
+                              const void *q, uint64_t q_len, const void *k, uint64_t k_len,
+                              const void *v, uint64_t v_len, float *context,
+                              uint64_t context_len, float *scores, uint64_t scores_len,
+                              float *probabilities, uint64_t probabilities_len, tkh_error *err) {
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    if (!shape) return invalid("shape", err);
+    const tkh_window_shape s = *shape;
+    // src/cpu/window_attention.rs:45-115, in order.
+    TRY(nonzero(s.queries, "queries", err));
+    TRY(nonzero(s.keys, "keys", err));
+    TRY(nonzero(s.query_heads, "query_heads", err));
+    TRY(nonzero(s.kv_heads, "kv_heads", err));
+    TRY(nonzero(s.head_dim, "head_dim", err));
+    if (s.keys > s.capacity || s.query_heads % s.kv_heads != 0)
+        return invalid("attention capacity/head mapping", err);
+    if ((s.has_window && s.window == 0) || !std::isfinite(s.scale) || s.scale <= 0.0f)
+        return invalid("attention window/scale", err);
+    if (s.softcap != 0.0f && (!std::isfinite(s.softcap) || s.softcap < 0.0f))
+        return invalid("attention score softcap", err);
+    uint64_t key_end, query_last;
+    TRY(add(s.key_start, s.keys - 1, &key_end, err));
+    TRY(add(s.query_start, s.queries - 1, &query_last, err));
+    uint64_t query_stride, query_count, kv_stride, kv_count, tmp, scratch_count;
+    TRY(product(s.query_heads, s.head_dim, &query_stride, err));
+    TRY(product(s.queries, query_stride, &query_count, err));
+    TRY(product(s.capacity, s.head_dim, &kv_stride, err));
+    TRY(product(s.kv_heads, kv_stride, &kv_count, err));
+    TRY(product(s.query_heads, s.queries, &tmp, err));
+    TRY(product(tmp, s.keys, &scratch_count, err));
+    TRY(length("attention query", q_len, query_count, err));
+    TRY(length("attention key", k_len, kv_count, err));
+    TRY(length("attention value", v_len, kv_count, err));
+    TRY(length("attention context", context_len, query_count, err));
+    if (scores) TRY(length("attention scores", scores_len, scratch_count, err));
+    if (probabilities) TRY(length("attention probabilities", probabilities_len, scratch_count, err));
+    for (uint64_t query = 0; query < s.queries; ++query) {
+        uint64_t position = s.query_start + query;
+        uint64_t first = first_visible(s.key_start, position, s.has_window, s.window);
+        uint64_t last = std::min(key_end, position);
+        if (first > last)
+            return fail(err, TKH_FULLY_MASKED, nullptr, query, 0, 0, "softmax row %llu is entirely masked",
+                        (unsigned long long)query);
+    }
+    if (s.head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 0, 0, "head_dim above 512");
+    if (!ctx) return invalid("context", err);
+    Plan plan;
+    plan.dtype = dtype;
+    plan.query_heads = s.query_heads;
+    plan.kv_heads = s.kv_heads;
+    plan.head_dim = s.head_dim;
+    plan.has_window = s.has_window != 0;
+    plan.window = (int64_t)s.window;
+    plan.scale = s.scale;
+    plan.softcap = s.softcap;
+    plan.diag_mode = (scores || probabilities) ? 1 : 0;
+    plan.scores = scores;
+    plan.probs = probabilities;
+    tkh::Problem p = make_problem(q, context, query_stride, s.query_start, s.key_start, s.keys,
+                                  s.queries);
+    add_segment(p, k, v, kv_stride, s.head_dim, s.keys, 0);
+    plan.problems.push_back(p);
+    return run(ctx, plan, err);
+}
+
+uint32_t tkh_span_attention(tkh_context *ctx, const tkh_span_shape *shape, tkh_dtype dtype,
+                            const void *q, uint64_t q_len, const tkh_segment segments[3],
+                            float *context, uint64_t context_len, float *scores,
+                            uint64_t scores_len, float *probabilities, uint64_t probabilities_len,
+                            tkh_error *err) {
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    if (!shape || !segments) return invalid("shape", err);
+    const tkh_span_shape s = *shape;
+    // src/cpu/span_attention.rs:50-138, in order.
+    TRY(nonzero(s.queries, "queries", err));
+    TRY(nonzero(s.keys, "keys", err));
+    TRY(nonzero(s.query_heads, "query_heads", err));
+    TRY(nonzero(s.kv_heads, "kv_heads", err));
+    TRY(nonzero(s.head_dim, "head_dim", err));
+    if (s.query_heads % s.kv_heads != 0 || (s.has_window && s.window == 0) ||
+        !std::isfinite(s.scale) || s.scale <= 0.0f)
+        return invalid("segmented attention heads/window/scale", err);
+    if (s.softcap != 0.0f && (!std::isfinite(s.softcap) || s.softcap < 0.0f))
+        return invalid("attention score softcap", err);
+    uint64_t key_end, query_last;
+    TRY(add(s.key_start, s.keys - 1, &key_end, err));
+    TRY(add(s.query_start, s.queries - 1, &query_last, err));
+    uint64_t query_stride, query_count, tmp, scratch_count;
+    TRY(product(s.query_heads, s.head_dim, &query_stride, err));
+    TRY(product(s.queries, query_stride, &query_count, err));
+    TRY(product(s.query_heads, s.queries, &tmp, err));
+    TRY(product(tmp, s.keys, &scratch_count, err));
+    TRY(length("attention query", q_len, query_count, err));
+    TRY(length("attention context", context_len, query_count, err));
+    if (scores) TRY(length("attention scores", scores_len, scratch_count, err));
+    if (probabilities) TRY(length("attention probabilities", probabilities_len, scratch_count, err));
+    uint64_t keys = 0;
+    for (int i = 0; i < 3; ++i) {
+        const tkh_segment &seg = segments[i];
+        uint64_t rows, expected = 0;
+        TRY(product(seg.keys, s.head_dim, &rows, err));
+        if (seg.keys != 0) {
+            if (seg.head_stride < rows) return invalid("attention segment heads overlap", err);
+            uint64_t start;
+            TRY(add(s.key_start, keys, &start, err));
+            if (seg.key_start != start) return invalid("attention segment logical origin", err);
+            uint64_t heads_part;
+            TRY(product(s.kv_heads - 1, seg.head_stride, &heads_part, err));
+            TRY(add(heads_part, rows, &expected, err));
+        }
+        TRY(length("attention segment key", seg.k_len, expected, err));
+        TRY(length("attention segment value", seg.v_len, expected, err));
+        TRY(add(keys, seg.keys, &keys, err));
+    }
+    TRY(length("attention segment keys", keys, s.keys, err));
+    for (uint64_t query = 0; query < s.queries; ++query) {
+        uint64_t position = s.query_start + query;
+        uint64_t first = first_visible(s.key_start, position, s.has_window, s.window);
+        uint64_t last = std::min(key_end, position);
+        if (first > last)
+            return fail(err, TKH_FULLY_MASKED, nullptr, query, 0, 0, "softmax row %llu is entirely masked",
+                        (unsigned long long)query);
+    }
+    if (s.head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 0, 0, "head_dim above 512");
+    if (!ctx) return invalid("context", err);
+    Plan plan;
+    plan.dtype = dtype;
+    plan.query_heads = s.query_heads;
+    plan.kv_heads = s.kv_heads;
+    plan.head_dim = s.head_dim;
+    plan.has_window = s.has_window != 0;
+    plan.window = (int64_t)s.window;
+    plan.scale = s.scale;
+    plan.softcap = s.softcap;
+    plan.diag_mode = (scores || probabilities) ? 1 : 0;
+    plan.scores = scores;
+    plan.probs = probabilities;
+    tkh::Problem p = make_problem(q, context, query_stride, s.query_start, s.key_start, s.keys,
+                                  s.queries);
+    uint64_t logical = 0;
+    for (int i = 0; i < 3; ++i) {
+        const tkh_segment &seg = segments[i];
+        if (seg.keys == 0) continue;
+        add_segment(p, seg.k, seg.v, seg.head_stride, s.head_dim, seg.keys, logical);
+        logical += seg.keys;
+    }
+    plan.problems.push_back(p);
+    return run(ctx, plan, err);
+}
+
+uint32_t tkh_logit_softcap(tkh_context *ctx, float *logits, uint64_t len, float cap,
+                           tkh_error *err) {
+    // src/cpu/softcap.rs:17-23
+    TRY(nonzero(len, "logit softcap width", err));
+    if (!std::isfinite(cap) || cap <= 0.0f) return invalid("logit softcap", err);
+    if (!ctx) return invalid("context", err);
+    HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    HIP_TRY(tkh_launch_softcap(logits, (int64_t)len, cap, ctx->status_dev, ctx->stream), "softcap");
+    return after_launch(ctx, err);
+}
+
+namespace {
+uint32_t batch_common(tkh_context *ctx, uint64_t batch, uint64_t tokens, uint64_t query_heads,
+                      uint64_t kv_heads, uint64_t head_dim, tkh_dtype dtype, float scale,
+                      tkh_error *err) {
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    TRY(nonzero(batch, "batch", err));
+    TRY(nonzero(tokens, "tokens", err));
+    TRY(nonzero(query_heads, "query_heads", err));
+    TRY(nonzero(kv_heads, "kv_heads", err));
+    TRY(nonzero(head_dim, "head_dim", err));
+    if (query_heads % kv_heads != 0) return invalid("query_heads must be divisible by kv_heads", err);
+    if (!std::isfinite(scale) || scale <= 0.0f) return invalid("attention scale", err);
+    if (head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 0, 0, "head_dim above 512");
+    if (!ctx) return invalid("context", err);
+    return TKH_OK;
+}
+}  // namespace
+
+uint32_t tkh_decode_batch(tkh_context *ctx, uint64_t batch, uint64_t query_heads,
+                          uint64_t kv_heads, uint64_t head_dim, tkh_dtype dtype, const void *q,
+                          const void *k_base, const void *v_base, const uint64_t *offsets,
+                          const uint64_t *head_strides, const uint64_t *lengths, float scale,
+                          float *context, tkh_error *err) {
+    TRY(batch_common(ctx, batch, 1, query_heads, kv_heads, head_dim, dtype, scale, err));
+    if (!offsets || !head_strides || !lengths) return invalid("batch descriptors", err);
+    Plan plan;
+    plan.dtype = dtype;
+    plan.query_heads = query_heads;
+    plan.kv_heads = kv_heads;
+    plan.head_dim = head_dim;
+    plan.scale = scale;
+    const int64_t es = esize(dtype);
+    const int64_t row = (int64_t)(query_heads * head_dim);
+    plan.problems.reserve(batch);
+    for (uint64_t b = 0; b < batch; ++b) {
+        if (lengths[b] == 0) return fail(err, TKH_ZERO_DIMENSION, "lengths", b, 0, 0, "session %llu has no keys", (unsigned long long)b);
+        if (head_strides[b] < lengths[b] * head_dim) return invalid("attention segment heads overlap", err);
+        tkh::Problem p = make_problem((const uint8_t *)q + b * row * es, context + b * row, row,
+                                      (int64_t)lengths[b] - 1, 0, (int64_t)lengths[b], 1);
+        add_segment(p, (const uint8_t *)k_base + offsets[b] * es,
+                    (const uint8_t *)v_base + offsets[b] * es, (int64_t)head_strides[b],
+                    (int64_t)head_dim, (int64_t)lengths[b], 0);
+        plan.problems.push_back(p);
+    }
+    return run(ctx, plan, err);
+}
+
+uint32_t tkh_prefill_batch(tkh_context *ctx, uint64_t batch, uint64_t tokens,
+                           uint64_t query_heads, uint64_t kv_heads, uint64_t head_dim,
+                           tkh_dtype dtype, const void *q, const void *k_base,
+                           const void *v_base, const uint64_t *offsets,
+                           const uint64_t *head_strides, const uint64_t *positions, float scale,
+                           float *context, tkh_error *err) {
+    TRY(batch_common(ctx, batch, tokens, query_heads, kv_heads, head_dim, dtype, scale, err));
+    if (!offsets || !head_strides || !positions) return invalid("batch descriptors", err);
+    Plan plan;
+    plan.dtype = dtype;
+    plan.query_heads = query_heads;
+    plan.kv_heads = kv_heads;
+    plan.head_dim = head_dim;
+    plan.scale = scale;
+    const int64_t es = esize(dtype);
+    const int64_t row = (int64_t)(query_heads * head_dim);
+    plan.problems.reserve(batch);
+    for (uint64_t b = 0; b < batch; ++b) {
+        int64_t keys = (int64_t)(positions[b] + tokens);
+        if (head_strides[b] < (uint64_t)keys * head_dim) return invalid("attention segment heads overlap", err);
+        tkh::Problem p = make_problem((const uint8_t *)q + b * tokens * row * es,
+                                      context + b * tokens * row, row, (int64_t)positions[b], 0,
+                                      keys, (int64_t)tokens);
+        add_segment(p, (const uint8_t *)k_base + offsets[b] * es,
+                    (const uint8_t *)v_base + offsets[b] * es, (int64_t)head_strides[b],
+                    (int64_t)head_dim, keys, 0);
+        plan.problems.push_back(p);
+    }
+    return run(ctx, plan, err);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- KV owners
+
+struct tkh_kv {
+    tkh_context *ctx = nullptr;
+    uint64_t heads = 0, dims = 0, capacity = 0, max_positions = 0;
+    bool has_window = false;
+    uint64_t window = 0;
+    tkh_dtype storage = TKH_BF16;
+    void *k = nullptr;
+    void *v = nullptr;
+    uint64_t offset = 0, generation = 0, owner = 0;
+    uint64_t allocated_bytes = 0;
+};
+
+namespace {
+
+std::atomic<uint64_t> g_next_owner{1};
+
+// capacity::KvOwner::at_capacity (src/capacity.rs:49-80) with copies and no guards.
+uint32_t owner_bytes(uint64_t heads, uint64_t head_dim, uint64_t capacity, bool has_window,
+                     uint64_t window, tkh_dtype storage, uint64_t copies, uint64_t *total,
+                     uint64_t *per_array, tkh_error *err) {
+    TRY(nonzero(capacity, "KV capacity", err));
+    TRY(nonzero(heads, "KV heads", err));
+    TRY(nonzero(head_dim, "KV head dimension", err));
+    TRY(nonzero(copies, "KV physical owners", err));
+    uint64_t retained = capacity;
+    if (has_window) {
+        TRY(nonzero(window, "KV window", err));
+        retained = std::min(capacity, window);
+    }
+    uint64_t elements, bytes, pair;
+    TRY(product(heads, retained, &elements, err));
+    TRY(product(elements, head_dim, &elements, err));
+    TRY(product(elements, (uint64_t)esize(storage), &bytes, err));
+    if (bytes > (uint64_t)INT64_MAX) return fail(err, TKH_SIZE_OVERFLOW, nullptr, 0, 0, 0, "tensor size arithmetic overflow");
+    TRY(product(bytes, 2, &pair, err));
+    TRY(product(pair, copies, total, err));
+    if (per_array) *per_array = bytes;
+    return TKH_OK;
+}
+
+// WindowKvCache::admit_tokens (src/model/window_cache.rs:214-237).
+uint32_t admit_tokens(const tkh_kv *kv, uint64_t tokens, uint64_t *elements, tkh_error *err) {
+    TRY(nonzero(tokens, "KV new tokens", err));
+    uint64_t after;
+    TRY(add(kv->offset, tokens, &after, err));
+    uint64_t limit = kv->has_window ? kv->max_positions : std::min(kv->capacity, kv->max_positions);
+    if (after > limit)
+        return fail(err, TKH_CAPACITY, "KV cache", kv->offset, limit, after,
+                    "offset %llu plus %llu tokens exceeds limit %llu",
+                    (unsigned long long)kv->offset, (unsigned long long)tokens,
+                    (unsigned long long)limit);
+    if (kv->generation == UINT64_MAX) return fail(err, TKH_SIZE_OVERFLOW, nullptr, 0, 0, 0, "KV generation exhausted");
+    uint64_t e;
+    TRY(product(kv->heads, tokens, &e, err));
+    TRY(product(e, kv->dims, &e, err));
+    *elements = e;
+    return TKH_OK;
+}
+
+// WindowKvCache::validate (src/model/window_cache.rs:239-254).
+uint32_t validate_frame(const tkh_kv *kv, const tkh_kv_frame *f, tkh_error *err) {
+    if (f->owner != kv->owner || f->generation != kv->generation || f->offset != kv->offset)
+        return fail(err, TKH_INVALID_CONFIG, "KV frame", 0, 0, 0, "stale or foreign KV proposal");
+    uint64_t elements;
+    return admit_tokens(kv, f->tokens, &elements, err);
+}
+
+// window_rows (src/model/window_rows.rs:24-88).
+uint64_t view_start(uint64_t offset, bool has_window, uint64_t window) {
+    if (!has_window) return 0;
+    return offset >= window - 1 ? offset - (window - 1) : 0;
+}
+void old_spans(uint64_t capacity, uint64_t offset, bool has_window, uint64_t window, uint64_t out[6]) {
+    uint64_t start = view_start(offset, has_window, window);
+    uint64_t old = offset - start;
+    uint64_t slot = start % capacity;
+    uint64_t first = std::min(old, capacity - slot);
+    out[0] = start; out[1] = slot; out[2] = first;
+    out[3] = start + first; out[4] = 0; out[5] = old - first;
+}
+void copy_runs(uint64_t capacity, uint64_t offset, uint64_t tokens, bool sliding, uint64_t out[6]) {
+    uint64_t first_new = sliding ? (tokens > capacity ? tokens - capacity : 0) : 0;
+    uint64_t slot = sliding ? (offset % capacity + first_new % capacity) % capacity : offset;
+    uint64_t count = tokens - first_new;
+    uint64_t first = std::min(count, capacity - slot);
+    out[0] = first_new; out[1] = slot; out[2] = first;
+    out[3] = first_new + first; out[4] = 0; out[5] = count - first;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t tkh_kv_planned_bytes(uint64_t heads, uint64_t head_dim, uint64_t capacity,
+                              uint32_t has_window, uint64_t window, tkh_dtype storage,
+                              uint64_t copies, uint64_t *total_bytes, tkh_error *err) {
+    if (!total_bytes) return invalid("total_bytes", err);
+    if (!valid_dtype(storage)) return invalid("dtype", err);
+    TRY(owner_bytes(heads, head_dim, capacity, has_window != 0, window, storage, copies,
+                    total_bytes, nullptr, err));
+    return ok(err);
+}
+
+uint32_t tkh_kv_create(tkh_context *ctx, uint64_t heads, uint64_t dims, uint64_t capacity,
+                       uint64_t max_positions, uint32_t has_window, uint64_t window,
+                       tkh_dtype storage, tkh_kv **out, tkh_error *err) {
+    if (!ctx) return invalid("context", err);
+    if (!out) return invalid("kv output", err);
+    if (!valid_dtype(storage)) return invalid("dtype", err);
+    *out = nullptr;
+    // WindowKvCache::planned_bytes (src/model/window_cache.rs:62-97).
+    TRY(nonzero(heads, "KV heads", err));
+    TRY(nonzero(dims, "KV head width", err));
+    TRY(nonzero(capacity, "KV capacity", err));
+    TRY(nonzero(max_positions, "KV maximum positions", err));
+    if (capacity > max_positions || (has_window && (window == 0 || window != capacity)))
+        return fail(err, TKH_INVALID_CONFIG, "KV capacity/window", 0, 0, 0, "invalid KV capacity/window");
+    uint64_t total, per_array;
+    TRY(owner_bytes(heads, dims, capacity, has_window != 0, window, storage, 1, &total, &per_array, err));
+    HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    auto *kv = new tkh_kv();
+    kv->ctx = ctx;
+    kv->heads = heads;
+    kv->dims = dims;
+    kv->capacity = capacity;
+    kv->max_positions = max_positions;
+    kv->has_window = has_window != 0;
+    kv->window = window;
+    kv->storage = storage;
+    hipError_t e = hipMalloc(&kv->k, per_array);
+    if (e == hipSuccess) e = hipMalloc(&kv->v, per_array);
+    if (e == hipSuccess) e = hipMemsetAsync(kv->k, 0, per_array, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(kv->v, 0, per_array, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        tkh_kv_destroy(kv);
+        return device_error(e, "KV allocation", err);
+    }
+    kv->allocated_bytes = total;
+    kv->owner = g_next_owner.fetch_add(1);
+    *out = kv;
+    return ok(err);
+}
+
+void tkh_kv_destroy(tkh_kv *kv) {
+    if (!kv) return;
+    if (kv->ctx) {
+        hipSetDevice(kv->ctx->device);
+        hipStreamSynchronize(kv->ctx->stream);
+    }
+    if (kv->k) hipFree(kv->k);
+    if (kv->v) hipFree(kv->v);
+    delete kv;
+}
+
+uint32_t tkh_kv_info_get(const tkh_kv *kv, tkh_kv_info *info) {
+    if (!kv || !info) return TKH_INVALID_PARAMETER;
+    info->heads = kv->heads;
+    info->dims = kv->dims;
+    info->capacity = kv->capacity;
+    info->max_positions = kv->max_positions;
+    info->window = kv->window;
+    info->offset = kv->offset;
+    info->generation = kv->generation;
+    info->owner = kv->owner;
+    info->has_window = kv->has_window ? 1 : 0;
+    info->storage = kv->storage;
+    info->k = kv->k;
+    info->v = kv->v;
+    info->allocated_bytes = kv->allocated_bytes;
+    return TKH_OK;
+}
+
+uint32_t tkh_kv_append(tkh_kv *kv, uint64_t offset, uint64_t tokens, tkh_dtype src_dtype,
+                       const void *k, const void *v, tkh_error *err) {
+    if (!kv) return invalid("kv", err);
+    if (!valid_dtype(src_dtype)) return invalid("dtype", err);
+    if (kv->has_window) return fail(err, TKH_INVALID_CONFIG, "KV cache", 0, 0, 0, "append needs a full-retention cache; use prepare/commit");
+    TRY(nonzero(tokens, "KV new tokens", err));
+    uint64_t end;
+    TRY(add(offset, tokens, &end, err));
+    if (end > kv->capacity)
+        return fail(err, TKH_CAPACITY, "KV cache", offset, kv->capacity, end, "cache capacity exceeded");
+    if (src_dtype != TKH_F32 && src_dtype != kv->storage) return invalid("append source dtype", err);
+    tkh_context *ctx = kv->ctx;
+    HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    HIP_TRY(tkh_launch_kv_append((int)src_dtype, (int)kv->storage, k, v, kv->k, kv->v,
+                                 (int64_t)tokens, (int)kv->heads, (int)kv->dims,
+                                 (int64_t)kv->capacity, (int64_t)offset, ctx->status_dev,
+                                 ctx->stream),
+            "KV append");
+    return after_launch(ctx, err);
+}
+
+uint32_t tkh_kv_prepare(const tkh_kv *kv, const void *k, uint64_t k_len, const void *v,
+                        uint64_t v_len, uint64_t tokens, tkh_kv_frame *frame, tkh_error *err) {
+    if (!kv || !frame) return invalid("kv", err);
+    uint64_t elements;
+    TRY(admit_tokens(kv, tokens, &elements, err));
+    TRY(length("new KV keys", k_len, elements, err));
+    TRY(length("new KV values", v_len, elements, err));
+    tkh_context *ctx = kv->ctx;
+    HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    HIP_TRY(tkh_launch_check_finite((int)kv->storage, k, v, (int64_t)elements, ctx->status_dev,
+                                    ctx->stream),
+            "KV prepare");
+    uint32_t rc = after_launch(ctx, err);
+    if (rc != TKH_OK) return rc;
+    frame->k = k;
+    frame->v = v;
+    frame->owner = kv->owner;
+    frame->generation = kv->generation;
+    frame->offset = kv->offset;
+    frame->tokens = tokens;
+    return ok(err);
+}
+
+uint32_t tkh_kv_view(const tkh_kv *kv, const tkh_kv_frame *frame, uint64_t query_heads,
+                     float scale, tkh_segment segments[3], tkh_span_shape *shape,
+                     tkh_error *err) {
+    if (!kv || !frame || !segments || !shape) return invalid("kv", err);
+    TRY(validate_frame(kv, frame, err));
+    const uint64_t es = (uint64_t)esize(kv->storage);
+    const uint64_t stride = kv->capacity * kv->dims;
+    uint64_t spans[6];
+    old_spans(kv->capacity, kv->offset, kv->has_window, kv->window, spans);
+    for (int i = 0; i < 2; ++i) {
+        uint64_t position = spans[3 * i], slot = spans[3 * i + 1], rows = spans[3 * i + 2];
+        tkh_segment &s = segments[i];
+        if (rows == 0) {
+            s = tkh_segment{nullptr, 0, nullptr, 0, 0, 0, kv->offset};
+            continue;
+        }
+        uint64_t begin = slot * kv->dims;
+        uint64_t len = (kv->heads - 1) * stride + rows * kv->dims;
+        s.k = (const uint8_t *)kv->k + begin * es;
+        s.v = (const uint8_t *)kv->v + begin * es;
+        s.k_len = len;
+        s.v_len = len;
+        s.keys = rows;
+        s.head_stride = stride;
+        s.key_start = position;
+    }
+    uint64_t len = kv->heads * frame->tokens * kv->dims;
+    segments[2] = tkh_segment{frame->k, len, frame->v, len, frame->tokens,
+                              frame->tokens * kv->dims, kv->offset};
+    uint64_t start = view_start(kv->offset, kv->has_window, kv->window);
+    // KvView::attention_shape (src/model/window_cache.rs:392-406).
+    shape->queries = frame->tokens;
+    shape->keys = kv->offset + frame->tokens - start;
+    shape->query_heads = query_heads;
+    shape->kv_heads = kv->heads;
+    shape->head_dim = kv->dims;
+    shape->query_start = kv->offset;
+    shape->key_start = start;
+    shape->has_window = kv->has_window ? 1 : 0;
+    shape->window = kv->window;
+    shape->scale = scale;
+    shape->softcap = 0.0f;
+    return ok(err);
+}
+
+uint32_t tkh_kv_commit_batch(tkh_kv *const *kvs, const tkh_kv_frame *frames, uint64_t count,
+                             tkh_error *err) {
+    if (count && (!kvs || !frames)) return invalid("kv batch", err);
+    for (uint64_t i = 0; i < count; ++i) {
+        if (!kvs[i]) return invalid("kv", err);
+        TRY(validate_frame(kvs[i], &frames[i], err));
+    }
+    for (uint64_t i = 0; i < count; ++i)
+        for (uint64_t j = i + 1; j < count; ++j)
+            if (kvs[i] == kvs[j])
+                return fail(err, TKH_INVALID_CONFIG, "KV frame", 0, 0, 0, "duplicate KV owner in commit");
+    // No fallible arithmetic remains: copy only the final min(tokens, W) rows.
+    for (uint64_t i = 0; i < count; ++i) {
+        tkh_kv *kv = kvs[i];
+        const tkh_kv_frame &f = frames[i];
+        uint64_t runs[6];
+        copy_runs(kv->capacity, kv->offset, f.tokens, kv->has_window, runs);
+        int64_t r[6];
+        for (int j = 0; j < 6; ++j) r[j] = (int64_t)runs[j];
+        tkh_context *ctx = kv->ctx;
+        HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+        HIP_TRY(tkh_launch_copy_runs(f.k, f.v, kv->k, kv->v, (int64_t)f.tokens, (int)kv->heads,
+                                     (int64_t)(kv->dims * esize(kv->storage)),
+                                     (int64_t)kv->capacity, r, ctx->stream),
+                "KV commit");
+        kv->offset += f.tokens;
+        kv->generation += 1;
+    }
+    for (uint64_t i = 0; i < count; ++i)
+        if (kvs[i]->ctx->synchronous) HIP_TRY(hipStreamSynchronize(kvs[i]->ctx->stream), "KV commit");
+    return ok(err);
+}
+
+uint32_t tkh_kv_reset_batch(tkh_kv *const *kvs, uint64_t count, tkh_error *err) {
+    if (count && !kvs) return invalid("kv batch", err);
+    for (uint64_t i = 0; i < count; ++i) {
+        if (!kvs[i]) return invalid("kv", err);
+        if (kvs[i]->generation == UINT64_MAX)
+            return fail(err, TKH_INVALID_CONFIG, "KV cache", 0, 0, 0, "KV reset generation exhausted");
+    }
+    for (uint64_t i = 0; i < count; ++i) {
+        kvs[i]->offset = 0;
+        kvs[i]->generation += 1;
+    }
+    return ok(err);
+}
+
+}  // extern "C"
