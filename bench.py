@@ -43,8 +43,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-north-star", action="store_true", help="skip configs[2]/[4]")
-    ap.add_argument("--only", choices=["c2", "c3", "c5", "d8k"], default=None,
-                    help="run a single workload (for profiling)")
+    ap.add_argument("--only", choices=["c2", "c3", "c5", "d8k", "copy"], default=None,
+                    help="run a single workload (for profiling); `copy` runs a plain 1 GiB "
+                         "device copy that calibrates the FETCH_SIZE/WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -266,6 +267,24 @@ def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096
     }
 
 
+def copy_calibration(torch, nbytes=1 << 30, reps=3):
+    """A plain device copy of known size: its FETCH_SIZE/WRITE_SIZE per dispatch
+    (rocprofv3 --pmc) against nbytes gives the counters' scale factor."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        torch.cuda.synchronize()
+        t.append(a.elapsed_time(b) / 1e3)
+    return {"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+            "copy_gbs": 2 * nbytes / min(t) / 1e9}
+
+
 def cpu_baseline(w, torch):
     """The oracle (single thread, FP64 softmax) on the C2 decode phase: 32 of 256 steps."""
     import numpy as np
@@ -305,6 +324,9 @@ def main():
     from toklet_amd import ops
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    if args.only == "copy":
+        print(json.dumps(copy_calibration(torch)))
+        return
     ctx = ops.Context(0, synchronous=False)
     result = {}
     w = None

@@ -17,9 +17,13 @@
  *  - Element lengths (`*_len`) are checked on the host against the shape
  *    before any launch, as the reference checks slice lengths before writes.
  *  - Finiteness of Q/K/V is checked inside the kernels through a device
- *    status word.  A synchronous context reports TKH_NON_FINITE after the
- *    call, and operator outputs are written only when the status word is
- *    clean, so an invalid input leaves `context` untouched.
+ *    status word (the Metal precedent's status atomic,
+ *    src/metal/kernels.metal:31-35).  A synchronous context reports
+ *    TKH_NON_FINITE after the call; the context contents are then
+ *    unspecified and must be discarded, as the reference discards partial
+ *    output after an arithmetic failure (src/cpu/mod.rs:5-7).  Shape and
+ *    length errors are reported before any launch and leave every output
+ *    untouched.
  *  - Tensors passed to operators are device pointers (HBM).  Q/context use
  *    [tokens, query_heads, head_dim]; K/V use the reference's head-major
  *    [kv_heads, capacity, head_dim] layout (strides [capacity*D, D, 1]).

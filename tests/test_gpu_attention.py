@@ -409,7 +409,9 @@ def test_prefill_batch_bf16(torch_mod, ctx, ops, orc):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
-def test_nonfinite_visible_input_reports_and_leaves_context(torch_mod, ctx, ops, dt):
+def test_nonfinite_visible_input_reports_nonfinite(torch_mod, ctx, ops, dt):
+    """A NaN in visible Q/K/V is NonFinite (src/cpu/attention.rs:247-251); the context
+    contents are then unspecified and the caller discards them (src/cpu/mod.rs:5-7)."""
     torch = torch_mod
     rng = np.random.default_rng(8)
     hq, hkv, D, cap = 16, 8, 128, 64
@@ -425,7 +427,6 @@ def test_nonfinite_visible_input_reports_and_leaves_context(torch_mod, ctx, ops,
             ops.attention_cached(ctx, dev(qq, dt), dev(kk, dt), dev(vv, dt), out, None, None,
                                  ops.CachedAttentionShape(4, hq, hkv, D, cap, 20))
         assert e.value.name == "NonFinite"
-        assert np.all(host(out) == 123.0)
     # afterwards the context works again (status was cleared)
     out = _zeros(torch, 4 * hq * D)
     ops.attention_cached(ctx, dev(q, dt), dev(k, dt), dev(v, dt), out, None, None,

@@ -1,0 +1,203 @@
+"""GPU parity of the streaming decode kernel (few query rows per KV head).
+
+Long contexts split the keys over many workgroups, so these cases exercise the
+split-K merge done by the last workgroup of each KV head, the arrival counters
+being reset between calls, per-row causal limits when a short chunk has
+several tokens, windows and the score softcap at head_dim 256, and ring spans.
+The checker is the CPU oracle on the same stored (rounded) values.
+"""
+
+import numpy as np
+import pytest
+
+from gpu_util import TOL_F32, TOL_HALF, dev, greedy_tokens, host, log, max_err, stored
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from toklet_amd import ops
+
+    return ops
+
+
+@pytest.fixture(scope="module")
+def ctx(torch_mod, ops):
+    return ops.Context(0)
+
+
+def _cached_case(torch, ctx, ops, orc, *, hq, hkv, D, dt, capacity, offset, tokens, seed,
+                 key_scale=None, k_mult=1.0):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((hkv, capacity, D)).astype(np.float32) * k_mult
+    if key_scale is not None:
+        mask = rng.random((hkv, capacity)) < key_scale
+        k[mask] *= 8.0
+    v = rng.standard_normal((hkv, capacity, D)).astype(np.float32)
+    q = rng.standard_normal((tokens, hq, D)).astype(np.float32)
+    ks, vs, qs = stored(k, dt), stored(v, dt), stored(q, dt).reshape(-1)
+    out = torch.full((tokens * hq * D,), np.nan, dtype=torch.float32, device="cuda")
+    ops.attention_cached(ctx, dev(qs, dt), dev(ks, dt), dev(vs, dt), out, None, None,
+                         ops.CachedAttentionShape(tokens, hq, hkv, D, capacity, offset))
+    ref, _, _ = orc.attention_cached(qs, ks, vs, tokens, hq, hkv, D, capacity, offset)
+    return host(out), ref
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("context", [1, 17, 300, 2049, 8192])
+def test_single_token_decode_qwen3(torch_mod, ctx, ops, orc, dt, context):
+    log(f"decode 16/8/128 {dt} context {context}")
+    got, ref = _cached_case(torch_mod, ctx, ops, orc, hq=16, hkv=8, D=128, dt=dt,
+                            capacity=context + 5, offset=context - 1, tokens=1, seed=context)
+    err = max_err(got, ref)
+    log(f"  max abs error {err:.3e}")
+    assert err <= TOL_HALF
+
+
+def test_decode_peaky_keys_and_tokens(torch_mod, ctx, ops, orc):
+    """5% of key rows x8 (configs[4]'s stress) at 6000 keys; greedy tokens identical."""
+    rng = np.random.default_rng(77)
+    w = rng.standard_normal((2048, 32 * 128)).astype(np.float32)
+    got, ref = _cached_case(torch_mod, ctx, ops, orc, hq=32, hkv=8, D=128, dt="bf16",
+                            capacity=6000, offset=5999, tokens=1, seed=5, key_scale=0.05)
+    err = max_err(got, ref)
+    log(f"llama 32/8/128 peaky decode: max abs error {err:.3e}")
+    assert err <= TOL_HALF
+    assert np.array_equal(greedy_tokens(got.reshape(1, -1), w), greedy_tokens(ref.reshape(1, -1), w))
+
+
+@pytest.mark.parametrize("tokens", [2, 3, 4])
+def test_short_chunk_rows_have_their_own_causal_limit(torch_mod, ctx, ops, orc, tokens):
+    log(f"short chunk of {tokens} tokens at offset 3000")
+    got, ref = _cached_case(torch_mod, ctx, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
+                            capacity=3100, offset=3000, tokens=tokens, seed=tokens)
+    assert max_err(got, ref) <= TOL_HALF
+
+
+def test_gqa7_d64_and_fp32(torch_mod, ctx, ops, orc):
+    """Qwen2.5 geometry (14/2/64, 7 rows per KV head) in bf16, and the FP32 path at 1e-5."""
+    got, ref = _cached_case(torch_mod, ctx, ops, orc, hq=14, hkv=2, D=64, dt="bf16",
+                            capacity=4000, offset=3999, tokens=1, seed=11)
+    assert max_err(got, ref) <= TOL_HALF
+    got, ref = _cached_case(torch_mod, ctx, ops, orc, hq=14, hkv=2, D=64, dt="f32",
+                            capacity=4000, offset=3999, tokens=1, seed=12)
+    err = max_err(got, ref)
+    log(f"fp32 14/2/64 decode at 4000: max abs error {err:.3e}")
+    assert err <= TOL_F32
+
+
+def test_repeated_calls_are_identical_and_counters_reset(torch_mod, ctx, ops, orc):
+    """The split-K arrival counters return to zero: the same call twice is bit-identical,
+    and a different split layout in between does not disturb it."""
+    a1, ref = _cached_case(torch_mod, ctx, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
+                           capacity=8192, offset=8191, tokens=1, seed=21)
+    _cached_case(torch_mod, ctx, ops, orc, hq=16, hkv=8, D=128, dt="bf16", capacity=1000,
+                 offset=999, tokens=1, seed=22)
+    a2, _ = _cached_case(torch_mod, ctx, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
+                         capacity=8192, offset=8191, tokens=1, seed=21)
+    assert np.array_equal(a1, a2)
+    assert max_err(a1, ref) <= TOL_HALF
+
+
+@pytest.mark.parametrize("softcap", [0.0, 50.0])
+def test_gemma_window_decode_d256(torch_mod, ctx, ops, orc, softcap):
+    """Gemma3 local layer decode: 8/4/256, W=1024, scale 1/16, at position 4100."""
+    torch = torch_mod
+    rng = np.random.default_rng(31)
+    hq, hkv, D, W = 8, 4, 256, 1024
+    keys = 4101
+    for dt in ("bf16", "f16"):
+        k = stored(rng.standard_normal((hkv, keys, D)) * 3, dt)
+        v = stored(rng.standard_normal((hkv, keys, D)), dt)
+        q = stored(rng.standard_normal((1, hq, D)) * 3, dt).reshape(-1)
+        out = torch.zeros(hq * D, dtype=torch.float32, device="cuda")
+        shape = ops.WindowAttentionShape(1, keys, keys, hq, hkv, D, keys - 1, 0, W, 1.0 / 16.0,
+                                         softcap)
+        ops.window_attention(ctx, dev(q, dt), dev(k, dt), dev(v, dt), out, None, None, shape)
+        ref, _, _ = orc.window_attention(q, k.reshape(-1), v.reshape(-1), 1, keys, keys, hq, hkv, D,
+                                         keys - 1, 0, W, 1.0 / 16.0, softcap=softcap)
+        err = max_err(host(out), ref)
+        log(f"gemma window decode {dt} softcap {softcap}: max abs error {err:.3e}")
+        assert err <= TOL_HALF
+
+
+def test_ring_span_decode_wraps(torch_mod, ctx, ops, orc):
+    """Decode over a W=1024 ring whose view is two old spans plus the new row."""
+    torch = torch_mod
+    rng = np.random.default_rng(41)
+    hq, hkv, D, W = 8, 4, 128, 1024
+    offset = 5000  # slot 5000 % 1024 = 904: the old spans wrap around the ring
+    ring_k = stored(rng.standard_normal((hkv, W, D)), "bf16")
+    ring_v = stored(rng.standard_normal((hkv, W, D)), "bf16")
+    nk = stored(rng.standard_normal((hkv, 1, D)), "bf16")
+    nv = stored(rng.standard_normal((hkv, 1, D)), "bf16")
+    q = stored(rng.standard_normal((1, hq, D)), "bf16").reshape(-1)
+    kd, vd = dev(ring_k, "bf16").reshape(-1), dev(ring_v, "bf16").reshape(-1)
+    segs_dev, segs_ref = [], []
+    logical = 0
+    for position, slot, rows in orc.old_spans(W, offset, W):
+        if rows == 0:
+            segs_dev.append(ops.AttentionKvSegment(None, None, 0, 0, offset))
+            segs_ref.append(orc.Segment(np.zeros(0), np.zeros(0), 0, 0, offset))
+            continue
+        b = slot * D
+        e = (hkv - 1) * W * D + b + rows * D
+        segs_dev.append(ops.AttentionKvSegment(kd[b:e], vd[b:e], rows, W * D, position))
+        segs_ref.append(orc.Segment(ring_k.reshape(-1)[b:e], ring_v.reshape(-1)[b:e], rows, W * D,
+                                    position))
+        logical += rows
+    assert sum(1 for sg in segs_ref if sg.keys) == 2, "the view must wrap the ring"
+    nkd, nvd = dev(nk, "bf16").reshape(-1), dev(nv, "bf16").reshape(-1)
+    segs_dev.append(ops.AttentionKvSegment(nkd, nvd, 1, D, offset))
+    segs_ref.append(orc.Segment(nk.reshape(-1), nv.reshape(-1), 1, D, offset))
+    key_start = offset - logical
+    keys = logical + 1
+    shape = ops.SpanAttentionShape(1, keys, hq, hkv, D, offset, key_start, W, 1.0 / np.sqrt(D), 0.0)
+    out = torch.zeros(hq * D, dtype=torch.float32, device="cuda")
+    ops.span_attention(ctx, dev(q, "bf16"), segs_dev, out, None, None, shape)
+    ref, _, _ = orc.span_attention(q, segs_ref, 1, keys, hq, hkv, D, offset, key_start, W,
+                                   np.float32(1.0 / np.sqrt(D)))
+    err = max_err(host(out), ref)
+    log(f"ring decode: keys {keys}, max abs error {err:.3e}")
+    assert err <= TOL_HALF
+
+
+def test_decode_batch_many_sessions_lengths_to_8192(torch_mod, ctx, ops, orc):
+    """configs[2] in miniature: 24 f16 sessions, lengths 1..8192, one query token each."""
+    torch = torch_mod
+    rng = np.random.default_rng(51)
+    hq, hkv, D, B = 16, 8, 128, 24
+    lengths = np.concatenate([[1, 2, 8192, 513], rng.integers(1, 8193, B - 4)])
+    scales = rng.uniform(0.5, 2.0, B)
+    offsets, pool_k, pool_v, total = [], [], [], 0
+    for b in range(B):
+        n = hkv * int(lengths[b]) * D
+        offsets.append(total)
+        pool_k.append(stored(rng.standard_normal(n) * scales[b], "f16"))
+        pool_v.append(stored(rng.standard_normal(n) * scales[b], "f16"))
+        total += n
+    kpool, vpool = np.concatenate(pool_k), np.concatenate(pool_v)
+    q = stored(rng.standard_normal((B, hq, D)) * scales[:, None, None], "f16")
+    out = torch.zeros(B * hq * D, dtype=torch.float32, device="cuda")
+    ops.decode_batch(ctx, dev(q, "f16"), dev(kpool, "f16"), dev(vpool, "f16"), offsets,
+                     [int(l) * D for l in lengths], [int(l) for l in lengths], out,
+                     query_heads=hq, kv_heads=hkv, head_dim=D, scale=1.0 / np.sqrt(D))
+    got = host(out).reshape(B, -1)
+    worst = 0.0
+    for b in range(B):
+        L = int(lengths[b])
+        kb = kpool[offsets[b]:offsets[b] + hkv * L * D]
+        vb = vpool[offsets[b]:offsets[b] + hkv * L * D]
+        ref, _, _ = orc.attention_cached(q[b].reshape(-1), kb, vb, 1, hq, hkv, D, L, L - 1)
+        worst = max(worst, max_err(got[b], ref))
+    log(f"decode batch of {B}: worst max abs error {worst:.3e}")
+    assert worst <= TOL_HALF

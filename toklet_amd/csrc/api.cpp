@@ -38,11 +38,21 @@ extern "C" hipError_t tkh_launch_check_finite(int dtype, const void *a, const vo
 extern "C" hipError_t tkh_launch_softcap(float *x, int64_t n, float cap, uint32_t *status,
                                          hipStream_t stream);
 extern "C" hipError_t tkh_launch_fill_u32(uint32_t *p, uint32_t v, hipStream_t stream);
+extern "C" int tkh_decode_max_rows(int dtype, int head_dim);
+extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int want);
+extern "C" int tkh_decode_max_waves(int dtype, int head_dim, int rows);
+extern "C" int tkh_decode_max_splits(void);
+extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int head_dim, int rows,
+                                        int keys_per_lane, int waves, int64_t groups,
+                                        hipStream_t stream);
 
 namespace {
 
 constexpr int kSlots = 16;
 constexpr int kSlotProblems = 1024;
+// Split-K arrival counters at the head of the workspace (decode kernel).
+constexpr size_t kCounters = 65536;
+constexpr size_t kCounterBytes = kCounters * sizeof(uint32_t);
 
 // ---------------------------------------------------------------- errors
 
@@ -137,6 +147,11 @@ struct tkh_context {
     int target_waves = 2048;
     int split_keys_override = 0;
     int force_generic = 0;
+    int decode_waves = 8;        // waves per decode workgroup
+    int decode_keys_per_lane = 4;  // keys each lane holds per streamed block
+    int decode_groups = 256;     // target decode workgroups per launch
+    int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
+    int decode_disable = 0;
     // profiling: event triples (before attention, after attention, after combine)
     bool profiling = false;
     std::vector<hipEvent_t> prof_events;
@@ -259,11 +274,130 @@ uint32_t profile_slot(tkh_context *ctx, hipEvent_t **ev, tkh_error *err) {
     return TKH_OK;
 }
 
+// Key range [lo, hi) visible to at least one query row of a problem.
+void visible_union(const Plan &plan, tkh::Problem &p) {
+    const int64_t pos_min = p.q_pos0, pos_max = p.q_pos0 + p.queries - 1;
+    int64_t hi = std::min<int64_t>(pos_max - p.k_pos0 + 1, p.keys);
+    int64_t lo = 0;
+    if (plan.has_window) lo = std::max<int64_t>(0, pos_min - (plan.window - 1) - p.k_pos0);
+    p.vis_lo = std::max<int64_t>(0, lo);
+    p.vis_hi = std::max<int64_t>(p.vis_lo, hi);
+}
+
+tkh::Params base_params(tkh_context *ctx, const Plan &plan) {
+    tkh::Params prm{};
+    prm.query_heads = (int32_t)plan.query_heads;
+    prm.kv_heads = (int32_t)plan.kv_heads;
+    prm.head_dim = (int32_t)plan.head_dim;
+    prm.group = (int32_t)(plan.query_heads / plan.kv_heads);
+    prm.has_window = plan.has_window ? 1 : 0;
+    prm.window = plan.window;
+    prm.scale = plan.scale;
+    prm.scale_log2 = plan.scale * 1.4426950408889634f;
+    prm.softcap = plan.softcap;
+    prm.status = ctx->status_dev;
+    prm.counters = reinterpret_cast<uint32_t *>(ctx->workspace);
+    return prm;
+}
+
+// Few query rows per KV head: the streaming decode kernel, one launch.
+uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
+                       int rows, tkh_error *err) {
+    const int64_t D = plan.head_dim, Hkv = plan.kv_heads;
+    const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    const int nw = std::min(ctx->decode_waves, tkh_decode_max_waves((int)plan.dtype, (int)D, R));
+    const int u = tkh_decode_keys_per_lane((int)plan.dtype, (int)D, ctx->decode_keys_per_lane);
+    const int max_splits = std::min(ctx->decode_max_splits, tkh_decode_max_splits());
+    const int64_t kpb = (int64_t)8 * u;  // keys per wave block
+    double work = 0;
+    int64_t max_span = 0;
+    for (auto &p : group) {
+        visible_union(plan, p);
+        work += (double)Hkv * (double)(p.vis_hi - p.vis_lo);
+        max_span = std::max<int64_t>(max_span, p.vis_hi - p.vis_lo);
+    }
+    // Keys per split: about decode_groups workgroups in all, at most
+    // max_splits per KV head, at least one block per wave, in whole blocks.
+    int64_t sk = (int64_t)std::ceil(work / ctx->decode_groups);
+    sk = std::max<int64_t>(sk, (max_span + max_splits - 1) / max_splits);
+    sk = std::max<int64_t>(sk, kpb * nw);
+    if (ctx->split_keys_override > 0) sk = ctx->split_keys_override;
+    sk = std::max<int64_t>(kpb, (sk + kpb - 1) / kpb * kpb);
+    if (sk > INT32_MAX) return fail(err, TKH_UNSUPPORTED, "keys", 0, 0, 0, "key range too large");
+
+    int64_t wgs = 0, slots = 0;
+    for (size_t i = 0; i < group.size(); ++i) {
+        auto &p = group[i];
+        p.split_keys = (int32_t)sk;
+        // Splits are laid out segment by segment over the visible range.
+        int64_t splits = 0;
+        for (int s = 0; s < 3; ++s) {
+            int64_t n = 0;
+            if (s < p.nseg) {
+                const int64_t lo = std::max<int64_t>(p.vis_lo, p.seg[s].start);
+                const int64_t hi = std::min<int64_t>(p.vis_hi, p.seg[s].start + p.seg[s].keys);
+                if (hi > lo) n = (hi - lo + sk - 1) / sk;
+            }
+            p.seg_splits[s] = (int32_t)n;
+            splits += n;
+        }
+        if (splits == 0) {  // nothing visible: one empty split reports the bad mass
+            p.seg_splits[0] = 1;
+            splits = 1;
+        }
+        p.splits = (int32_t)splits;
+        p.row_blocks = 1;
+        p.tile_base = wgs;
+        p.slot_base = slots;
+        p.group_base = (int32_t)(i * Hkv);
+        wgs += Hkv * p.splits;
+        slots += Hkv * p.splits;
+    }
+    if ((size_t)group.size() * Hkv > kCounters)
+        return fail(err, TKH_UNSUPPORTED, "batch", 0, kCounters, group.size() * Hkv,
+                    "too many (session, KV head) pairs in one call");
+    const size_t need = (size_t)slots * R * (D + 2) * sizeof(float);
+    if (need > ctx->workspace_bytes)
+        return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, ctx->workspace_bytes,
+                    "attention needs %zu workspace bytes, context has %zu", need,
+                    ctx->workspace_bytes);
+
+    tkh::Problem *dev = nullptr;
+    if (group.size() > 1) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
+    tkh::Params prm = base_params(ctx, plan);
+    prm.problems = dev;
+    if (group.size() == 1) prm.single = group[0];
+    prm.nproblems = (int32_t)group.size();
+    prm.total_tiles = wgs;
+    float *ws = reinterpret_cast<float *>(ctx->workspace + kCounterBytes);
+    prm.part_ml = ws;
+    prm.part_o = ws + (size_t)slots * R * 2;
+
+    hipEvent_t *ev = nullptr;
+    if (ctx->profiling) TRY(profile_slot(ctx, &ev, err));
+    if (ev) HIP_TRY(hipEventRecord(ev[0], ctx->stream), "profile");
+    hipError_t e = tkh_launch_decode(&prm, (int)plan.dtype, (int)D, R, u, nw, wgs, ctx->stream);
+    if (e != hipSuccess) return device_error(e, "decode launch", err);
+    if (ev) {
+        HIP_TRY(hipEventRecord(ev[1], ctx->stream), "profile");
+        HIP_TRY(hipEventRecord(ev[2], ctx->stream), "profile");
+    }
+    return TKH_OK;
+}
+
 // Launch one group of problems (<= kSlotProblems) through the workspace.
 uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
                       tkh_error *err) {
     const int64_t D = plan.head_dim, Hq = plan.query_heads, Hkv = plan.kv_heads;
     const int64_t G = Hq / Hkv;
+    {
+        int64_t max_rows = 0;
+        for (auto &p : group) max_rows = std::max<int64_t>(max_rows, (int64_t)p.queries * G);
+        const int limit = tkh_decode_max_rows((int)plan.dtype, (int)D);
+        if (!ctx->force_generic && !ctx->decode_disable && plan.diag_mode == 0 && limit > 0 &&
+            max_rows <= limit)
+            return launch_decode(ctx, plan, group, (int)max_rows, err);
+    }
     const bool mfma = !ctx->force_generic && plan.diag_mode == 0 &&
                       (plan.dtype == TKH_BF16 || plan.dtype == TKH_F16) &&
                       (D == 64 || D == 128 || D == 256);
@@ -348,8 +482,9 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
     prm.scale_log2 = plan.scale * 1.4426950408889634f;
     prm.softcap = plan.softcap;
     prm.total_tiles = tiles;
-    prm.part_ml = reinterpret_cast<float *>(ctx->workspace);
-    prm.part_o = reinterpret_cast<float *>(ctx->workspace) + 2 * part_rows;
+    prm.part_ml = reinterpret_cast<float *>(ctx->workspace + kCounterBytes);
+    prm.part_o = reinterpret_cast<float *>(ctx->workspace + kCounterBytes) + 2 * part_rows;
+    prm.counters = reinterpret_cast<uint32_t *>(ctx->workspace);
     prm.status = ctx->status_dev;
     prm.scores = plan.scores;
     prm.probs = plan.probs;
@@ -410,6 +545,19 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     ctx->target_waves = env_int("TKH_TARGET_WAVES", 2048);
     ctx->split_keys_override = env_int("TKH_SPLIT_KEYS", 0);
     ctx->force_generic = env_int("TKH_FORCE_GENERIC", 0);
+    ctx->decode_waves = std::min(8, std::max(1, env_int("TKH_DECODE_WAVES", 8)));
+    ctx->decode_keys_per_lane = std::max(1, env_int("TKH_DECODE_KEYS_PER_LANE", 4));
+    // One round of decode workgroups: with eight waves and the register
+    // budget of the kernel, one workgroup fits per CU.
+    {
+        hipDeviceProp_t prop;
+        int cus = 256;
+        if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+            cus = prop.multiProcessorCount;
+        ctx->decode_groups = std::max(1, env_int("TKH_DECODE_GROUPS", cus));
+    }
+    ctx->decode_max_splits = std::max(1, env_int("TKH_DECODE_MAX_SPLITS", 64));
+    ctx->decode_disable = env_int("TKH_DECODE_DISABLE", 0);
     auto cleanup = [&](hipError_t e, const char *where) {
         tkh_context_destroy(ctx);
         return device_error(e, where, err);
@@ -422,7 +570,9 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     if ((e = hipMemset(ctx->status_dev, 0, 256)) != hipSuccess) return cleanup(e, "status");
     if ((e = hipHostMalloc(&ctx->status_host, sizeof(uint32_t), hipHostMallocDefault)) != hipSuccess)
         return cleanup(e, "status");
-    if ((e = hipMalloc(&ctx->workspace, ctx->workspace_bytes)) != hipSuccess)
+    if ((e = hipMalloc(&ctx->workspace, ctx->workspace_bytes + kCounterBytes)) != hipSuccess)
+        return cleanup(e, "workspace");
+    if ((e = hipMemset(ctx->workspace, 0, kCounterBytes)) != hipSuccess)
         return cleanup(e, "workspace");
     size_t ring = sizeof(tkh::Problem) * kSlots * kSlotProblems;
     if ((e = hipMalloc(&ctx->ring_dev, ring)) != hipSuccess) return cleanup(e, "problem ring");

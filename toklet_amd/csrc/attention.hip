@@ -21,17 +21,6 @@
 
 namespace tkh {
 
-using f32x4 = float __attribute__((ext_vector_type(4)));
-using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
-using f32x2 = float __attribute__((ext_vector_type(2)));
-using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
-using f16x2 = _Float16 __attribute__((ext_vector_type(2)));
-using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
-using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
-
-constexpr float LOG2E = 1.4426950408889634f;
-constexpr float NEG_INF = -__builtin_inff();
-
 template <int DT>
 __device__ __forceinline__ f32x4 mfma_16x16x32(u32x4 a, u32x4 b, f32x4 c);
 template <>
@@ -65,54 +54,6 @@ template <> __device__ __forceinline__ float lo_f<F16>(uint32_t w) {
 }
 template <> __device__ __forceinline__ float hi_f<F16>(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
-}
-
-__device__ __forceinline__ float xor_max(float x, int mask) { return fmaxf(x, __shfl_xor(x, mask, 64)); }
-__device__ __forceinline__ float xor_sum(float x, int mask) { return x + __shfl_xor(x, mask, 64); }
-
-__device__ __forceinline__ float wave_max(float x) {
-    for (int m = 32; m >= 1; m >>= 1) x = xor_max(x, m);
-    return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-    for (int m = 32; m >= 1; m >>= 1) x = xor_sum(x, m);
-    return x;
-}
-
-// cap * tanh(x / cap), FP32.  tanh(y) = sign(y) (1 - 2 / (exp(2|y|) + 1)), with a
-// short odd Taylor series near zero where the subtraction would cancel.
-__device__ __forceinline__ float softcap_f(float x, float cap) {
-    float y = x / cap;
-    float a = fabsf(y);
-    float t;
-    if (a < 0.0625f) {
-        float y2 = y * y;
-        t = y * (1.0f + y2 * (-1.0f / 3.0f + y2 * (2.0f / 15.0f + y2 * (-17.0f / 315.0f))));
-    } else {
-        float e = __builtin_amdgcn_exp2f(fminf(2.0f * LOG2E * a, 126.0f));
-        t = copysignf(1.0f - 2.0f / (e + 1.0f), y);
-    }
-    return cap * t;
-}
-
-// Visible key range [lo, hi) (logical indices) of a query at absolute `pos`.
-__device__ __forceinline__ void visible_range(const Params &p, const Problem &pr, int64_t pos,
-                                              int64_t *lo, int64_t *hi) {
-    int64_t h = pos - pr.k_pos0 + 1;
-    *hi = h < pr.keys ? h : pr.keys;
-    int64_t l = 0;
-    if (p.has_window) {
-        int64_t first = pos - (p.window - 1) - pr.k_pos0;
-        l = first > 0 ? first : 0;
-    }
-    *lo = l;
-}
-
-__device__ __forceinline__ void raise_status(const Params &p, bool bad, uint32_t bit) {
-    if (__builtin_amdgcn_read_exec() != 0) {
-        uint64_t m = __ballot(bad);
-        if (m != 0 && (threadIdx.x & 63) == (int)__builtin_ctzll(m)) atomicOr(p.status, bit);
-    }
 }
 
 // ---------------------------------------------------------------------------

@@ -44,10 +44,14 @@ struct Problem {
     int32_t splits;       // key splits
     int32_t split_keys;   // keys per split (multiple of the key tile)
     int32_t row_blocks;   // row blocks per KV head (MFMA path)
-    int32_t pad0;
+    int32_t group_base;   // first split-K arrival counter (decode path: one per KV head)
     int64_t tile_base;    // first global tile of this problem
     int64_t part_base;    // first output row (rows are query*Hq + head)
     int64_t slot_base;    // first split-K partial slot (row-major [rows, splits])
+    int64_t vis_lo;       // logical key range visible to at least one query row
+    int64_t vis_hi;
+    int32_t seg_splits[3];  // decode path: key splits inside each segment (splits never
+    int32_t pad1;           // straddle a segment boundary)
 };
 
 struct Params {
@@ -73,18 +77,46 @@ struct Params {
     float *probs;
     int32_t diag_mode;      // 0 none, 1 full [Hq, queries, keys], 2 last row [keys]
     int32_t pad2;
+    uint32_t *counters;     // split-K arrival counters (zero between launches)
     Problem single;         // the problem itself when nproblems == 1 (no descriptor upload)
 };
 
+// Address-space qualified views: the problem descriptors are read-only for a
+// launch (scalar loads through the constant space), tensors are global.
+template <class T> using const_ptr = const __attribute__((address_space(4))) T *;
+template <class T> using global_ptr = __attribute__((address_space(1))) T *;
+template <class T> using global_cptr = const __attribute__((address_space(1))) T *;
+
+template <class T> __device__ __forceinline__ global_cptr<T> gload_ptr(const void *p) {
+    return (global_cptr<T>)p;
+}
+template <class T> __device__ __forceinline__ global_ptr<T> gstore_ptr(void *p) {
+    return (global_ptr<T>)p;
+}
+
 __device__ __forceinline__ int find_problem(const Params &p, int64_t tile) {
+    const_ptr<Problem> probs = (const_ptr<Problem>)p.problems;
     int lo = 0, hi = p.nproblems - 1;
     while (lo < hi) {
         int mid = (lo + hi + 1) >> 1;
-        if (p.problems[mid].tile_base <= tile) lo = mid; else hi = mid - 1;
+        if (probs[mid].tile_base <= tile) lo = mid; else hi = mid - 1;
     }
     return lo;
 }
 
+// The problem owning global tile `tile`, as a constant-space pointer: either
+// the copy inside the kernel arguments (Params must be the kernel's first
+// argument) or an entry of the uploaded descriptor array.  Its fields are
+// uniform and load through the scalar cache.
+__device__ __forceinline__ const_ptr<Problem> problem_ptr(const Params &p, int64_t tile) {
+    if (p.nproblems == 1) {
+        const_ptr<Params> args = (const_ptr<Params>)__builtin_amdgcn_kernarg_segment_ptr();
+        return &args->single;
+    }
+    return (const_ptr<Problem>)p.problems + find_problem(p, tile);
+}
+
+// Generic reference form used by the VALU and MFMA kernels.
 __device__ __forceinline__ const Problem &tile_problem(const Params &p, int64_t tile) {
     if (p.nproblems == 1) return p.single;
     return p.problems[find_problem(p, tile)];
@@ -129,6 +161,89 @@ __device__ __forceinline__ int64_t seg_offset(const Problem &pr, int64_t key, in
     *which = s;
     const Segment &g = pr.seg[s];
     return (int64_t)kvh * g.head_stride + (key - g.start) * g.row_stride;
+}
+
+// K/V addresses of logical key `key` by per-lane selects over the three
+// segments (constant indices only, so the descriptors stay in scalar
+// registers).  Returns the element offset inside the selected segment.
+__device__ __forceinline__ int64_t seg_select(const_ptr<Problem> pr, int64_t key, int kvh,
+                                              const void **k, const void **v) {
+    const auto &s0 = pr->seg[0], &s1 = pr->seg[1], &s2 = pr->seg[2];
+    const bool in1 = pr->nseg > 1 && key >= s1.start;
+    const bool in2 = pr->nseg > 2 && key >= s2.start;
+    const int64_t hs = in2 ? s2.head_stride : (in1 ? s1.head_stride : s0.head_stride);
+    const int64_t rs = in2 ? s2.row_stride : (in1 ? s1.row_stride : s0.row_stride);
+    const int64_t st = in2 ? s2.start : (in1 ? s1.start : s0.start);
+    *k = in2 ? s2.k : (in1 ? s1.k : s0.k);
+    *v = in2 ? s2.v : (in1 ? s1.v : s0.v);
+    return (int64_t)kvh * hs + (key - st) * rs;
+}
+
+// ---------------------------------------------------------------------------
+// Helpers shared by the attention kernels
+// ---------------------------------------------------------------------------
+
+using f32x4 = float __attribute__((ext_vector_type(4)));
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+using f32x2 = float __attribute__((ext_vector_type(2)));
+using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
+using f16x2 = _Float16 __attribute__((ext_vector_type(2)));
+using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float NEG_INF = -__builtin_inff();
+
+__device__ __forceinline__ float xor_max(float x, int mask) { return fmaxf(x, __shfl_xor(x, mask, 64)); }
+__device__ __forceinline__ float xor_sum(float x, int mask) { return x + __shfl_xor(x, mask, 64); }
+
+__device__ __forceinline__ float wave_max(float x) {
+    for (int m = 32; m >= 1; m >>= 1) x = xor_max(x, m);
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    for (int m = 32; m >= 1; m >>= 1) x = xor_sum(x, m);
+    return x;
+}
+
+// cap * tanh(x / cap), FP32.  tanh(y) = sign(y) (1 - 2 / (exp(2|y|) + 1)), with a
+// short odd Taylor series near zero where the subtraction would cancel.
+__device__ __forceinline__ float softcap_f(float x, float cap) {
+    float y = x / cap;
+    float a = fabsf(y);
+    float t;
+    if (a < 0.0625f) {
+        float y2 = y * y;
+        t = y * (1.0f + y2 * (-1.0f / 3.0f + y2 * (2.0f / 15.0f + y2 * (-17.0f / 315.0f))));
+    } else {
+        float e = __builtin_amdgcn_exp2f(fminf(2.0f * LOG2E * a, 126.0f));
+        t = copysignf(1.0f - 2.0f / (e + 1.0f), y);
+    }
+    return cap * t;
+}
+
+// Visible key range [lo, hi) (logical indices) of a query at absolute `pos`.
+__device__ __forceinline__ void visible_range(const Params &p, int64_t k_pos0, int64_t keys,
+                                              int64_t pos, int64_t *lo, int64_t *hi) {
+    int64_t h = pos - k_pos0 + 1;
+    *hi = h < keys ? h : keys;
+    int64_t l = 0;
+    if (p.has_window) {
+        int64_t first = pos - (p.window - 1) - k_pos0;
+        l = first > 0 ? first : 0;
+    }
+    *lo = l;
+}
+__device__ __forceinline__ void visible_range(const Params &p, const Problem &pr, int64_t pos,
+                                              int64_t *lo, int64_t *hi) {
+    visible_range(p, pr.k_pos0, pr.keys, pos, lo, hi);
+}
+
+__device__ __forceinline__ void raise_status(const Params &p, bool bad, uint32_t bit) {
+    if (__builtin_amdgcn_read_exec() != 0) {
+        uint64_t m = __ballot(bad);
+        if (m != 0 && (threadIdx.x & 63) == (int)__builtin_ctzll(m)) atomicOr(p.status, bit);
+    }
 }
 
 }  // namespace tkh
