@@ -39,6 +39,9 @@ extern "C" hipError_t tkh_launch_softcap(float *x, int64_t n, float cap, uint32_
                                          hipStream_t stream);
 extern "C" hipError_t tkh_launch_fill_u32(uint32_t *p, uint32_t v, hipStream_t stream);
 extern "C" int tkh_decode_max_rows(int dtype, int head_dim);
+extern "C" int tkh_prefill_rows_per_group(void);
+extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim,
+                                         int64_t groups, hipStream_t stream);
 extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int want);
 extern "C" int tkh_decode_max_waves(int dtype, int head_dim, int rows);
 extern "C" int tkh_decode_max_splits(void);
@@ -152,6 +155,9 @@ struct tkh_context {
     int decode_groups = 256;     // target decode workgroups per launch
     int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
     int decode_disable = 0;
+    int prefill_groups = 512;    // below this many row-block workgroups, split the keys
+    int prefill_max_splits = 16;
+    int prefill_min_keys = 256;  // keys per split at least
     // profiling: event triples (before attention, after attention, after combine)
     bool profiling = false;
     std::vector<hipEvent_t> prof_events;
@@ -385,6 +391,72 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     return TKH_OK;
 }
 
+// Many query rows per KV head (bf16/f16): the MFMA flash kernel, one launch.
+uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
+                        tkh_error *err) {
+    const int64_t D = plan.head_dim, Hkv = plan.kv_heads, G = plan.query_heads / plan.kv_heads;
+    const int64_t rows_per = tkh_prefill_rows_per_group();
+    int64_t base_groups = 0;
+    int64_t max_span = 0;
+    for (auto &p : group) {
+        visible_union(plan, p);
+        p.row_blocks = (int32_t)(((int64_t)p.queries * G + rows_per - 1) / rows_per);
+        base_groups += Hkv * p.row_blocks;
+        max_span = std::max<int64_t>(max_span, p.vis_hi - p.vis_lo);
+    }
+    // Too few row-block workgroups to fill the device: split the keys.
+    int64_t splits = 1;
+    if (base_groups < ctx->prefill_groups) {
+        splits = (ctx->prefill_groups + base_groups - 1) / base_groups;
+        splits = std::min<int64_t>(splits, ctx->prefill_max_splits);
+        splits = std::min<int64_t>(splits, std::max<int64_t>(1, max_span / ctx->prefill_min_keys));
+    }
+    int64_t sk = (max_span + splits - 1) / splits;
+    sk = std::max<int64_t>(32, (sk + 31) / 32 * 32);
+    if (ctx->split_keys_override > 0) sk = (ctx->split_keys_override + 31) / 32 * 32;
+    int64_t wgs = 0, slots = 0, counters = 0;
+    for (auto &p : group) {
+        p.split_keys = (int32_t)std::min<int64_t>(sk, INT32_MAX);
+        p.splits = (int32_t)std::max<int64_t>(1, (p.vis_hi - p.vis_lo + sk - 1) / sk);
+        p.tile_base = wgs;
+        p.slot_base = slots;
+        p.group_base = (int32_t)counters;
+        const int64_t g = Hkv * p.row_blocks;
+        wgs += g * p.splits;
+        if (p.splits > 1) slots += g * p.splits;
+        counters += g;
+    }
+    if (counters > (int64_t)kCounters)
+        return fail(err, TKH_UNSUPPORTED, "batch", 0, kCounters, counters,
+                    "too many (session, KV head, row block) groups in one call");
+    const size_t need = (size_t)slots * rows_per * (D + 2) * sizeof(float);
+    if (need > ctx->workspace_bytes)
+        return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, ctx->workspace_bytes,
+                    "attention needs %zu workspace bytes, context has %zu", need,
+                    ctx->workspace_bytes);
+    tkh::Problem *dev = nullptr;
+    if (group.size() > 1) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
+    tkh::Params prm = base_params(ctx, plan);
+    prm.problems = dev;
+    if (group.size() == 1) prm.single = group[0];
+    prm.nproblems = (int32_t)group.size();
+    prm.total_tiles = wgs;
+    float *ws = reinterpret_cast<float *>(ctx->workspace + kCounterBytes);
+    prm.part_ml = ws;
+    prm.part_o = ws + (size_t)slots * rows_per * 2;
+
+    hipEvent_t *ev = nullptr;
+    if (ctx->profiling) TRY(profile_slot(ctx, &ev, err));
+    if (ev) HIP_TRY(hipEventRecord(ev[0], ctx->stream), "profile");
+    hipError_t e = tkh_launch_prefill(&prm, (int)plan.dtype, (int)D, wgs, ctx->stream);
+    if (e != hipSuccess) return device_error(e, "prefill launch", err);
+    if (ev) {
+        HIP_TRY(hipEventRecord(ev[1], ctx->stream), "profile");
+        HIP_TRY(hipEventRecord(ev[2], ctx->stream), "profile");
+    }
+    return TKH_OK;
+}
+
 // Launch one group of problems (<= kSlotProblems) through the workspace.
 uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
                       tkh_error *err) {
@@ -397,6 +469,9 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
         if (!ctx->force_generic && !ctx->decode_disable && plan.diag_mode == 0 && limit > 0 &&
             max_rows <= limit)
             return launch_decode(ctx, plan, group, (int)max_rows, err);
+        if (!ctx->force_generic && plan.diag_mode == 0 &&
+            (plan.dtype == TKH_BF16 || plan.dtype == TKH_F16) && (D == 64 || D == 128 || D == 256))
+            return launch_prefill(ctx, plan, group, err);
     }
     const bool mfma = !ctx->force_generic && plan.diag_mode == 0 &&
                       (plan.dtype == TKH_BF16 || plan.dtype == TKH_F16) &&
@@ -558,6 +633,9 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     }
     ctx->decode_max_splits = std::max(1, env_int("TKH_DECODE_MAX_SPLITS", 64));
     ctx->decode_disable = env_int("TKH_DECODE_DISABLE", 0);
+    ctx->prefill_groups = std::max(1, env_int("TKH_PREFILL_GROUPS", 512));
+    ctx->prefill_max_splits = std::max(1, env_int("TKH_PREFILL_MAX_SPLITS", 16));
+    ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 256));
     auto cleanup = [&](hipError_t e, const char *where) {
         tkh_context_destroy(ctx);
         return device_error(e, where, err);
