@@ -301,6 +301,7 @@ tkh::Params base_params(tkh_context *ctx, const Plan &plan) {
     prm.scale = plan.scale;
     prm.scale_log2 = plan.scale * 1.4426950408889634f;
     prm.softcap = plan.softcap;
+    prm.softcap_inv = plan.softcap != 0.0f ? 1.0f / plan.softcap : 0.0f;
     prm.status = ctx->status_dev;
     prm.counters = reinterpret_cast<uint32_t *>(ctx->workspace);
     return prm;
@@ -556,6 +557,7 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
     prm.scale = plan.scale;
     prm.scale_log2 = plan.scale * 1.4426950408889634f;
     prm.softcap = plan.softcap;
+    prm.softcap_inv = plan.softcap != 0.0f ? 1.0f / plan.softcap : 0.0f;
     prm.total_tiles = tiles;
     prm.part_ml = reinterpret_cast<float *>(ctx->workspace + kCounterBytes);
     prm.part_o = reinterpret_cast<float *>(ctx->workspace + kCounterBytes) + 2 * part_rows;

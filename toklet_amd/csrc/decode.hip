@@ -148,7 +148,7 @@ constexpr int DECODE_MAX_SPLITS = 64;  // key splits per KV head (bounds the mer
 // row size leave room in the register file (256 VGPRs per lane), else four.
 constexpr int decode_waves_for(int row_bytes, int rows) { return rows <= 2 && row_bytes <= 512 ? 8 : 4; }
 
-template <int DT, int D, int R, int U>
+template <int DT, int D, int R, int U, bool CAP>
 __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void attn_decode(Params p) {
     constexpr int ES = Elem<DT>::size;
     constexpr int NWMAX = decode_waves_for(D * ES, R);
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     bool bad = false;
     const float scale_log2 = p.scale_log2;
     const float scale = p.scale;
-    const float softcap = p.softcap;
+    const float softcap = p.softcap, softcap_inv = p.softcap_inv;
 
     const int nblk = (span + KPB - 1) / KPB;
 
@@ -265,7 +265,9 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
                 float dot = 0.0f;
                 for (int c = 0; c < CPL; ++c) dot = chunk_dot<DT>(kb[u][c], q[r][c], dot);
                 dot = dpp_sum8(dot);
-                float x = softcap != 0.0f ? softcap_f(dot * scale, softcap) * LOG2E : dot * scale_log2;
+                float x;
+                if constexpr (CAP) x = softcap_fast(dot * scale, softcap, softcap_inv) * LOG2E;
+                else x = dot * scale_log2;
                 const bool vis = rel >= rlo[r] && rel < rhi[r];
                 bad |= vis && !is_finite_f(x);
                 s[u][r] = vis ? x : NEG_INF;
@@ -556,7 +558,10 @@ extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int hea
     dim3 grid((unsigned)groups), block(64 * waves);
 #define TKH_DEC(DT, DD, RR, UU)                                                             \
     if (dtype == DT && head_dim == DD && rows <= RR && keys_per_lane == UU) {               \
-        hipLaunchKernelGGL((attn_decode<DT, DD, RR, UU>), grid, block, 0, stream, *p);      \
+        if (p->softcap != 0.0f)                                                             \
+            hipLaunchKernelGGL((attn_decode<DT, DD, RR, UU, true>), grid, block, 0, stream, *p); \
+        else                                                                                \
+            hipLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false>), grid, block, 0, stream, *p); \
         return hipGetLastError();                                                           \
     }
 #define TKH_DEC_R(DT, DD, UU) TKH_DEC(DT, DD, 1, UU) TKH_DEC(DT, DD, 2, UU) TKH_DEC(DT, DD, 4, UU) TKH_DEC(DT, DD, 8, UU)

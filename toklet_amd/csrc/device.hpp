@@ -66,7 +66,7 @@ struct Params {
     float scale_log2;       // scale * log2(e): scores live in the exp2 domain
     float scale;
     float softcap;          // 0 disables cap*tanh(score/cap)
-    int32_t pad1;
+    float softcap_inv;      // 1 / softcap (0 when disabled)
     int64_t total_tiles;
     // split-K partials
     float *part_o;          // [rows, splits, D]
@@ -220,6 +220,19 @@ __device__ __forceinline__ float softcap_f(float x, float cap) {
         t = copysignf(1.0f - 2.0f / (e + 1.0f), y);
     }
     return cap * t;
+}
+
+// The same without divisions or branches, for the kernels' inner loops:
+// y = x * (1 / cap), tanh by the odd series below |y| = 1/16 and by
+// 1 - 2 / (e^{2|y|} + 1) (hardware reciprocal) above.
+__device__ __forceinline__ float softcap_fast(float x, float cap, float inv_cap) {
+    const float y = x * inv_cap;
+    const float a = fabsf(y);
+    const float y2 = y * y;
+    const float series = y * (1.0f + y2 * (-1.0f / 3.0f + y2 * (2.0f / 15.0f + y2 * (-17.0f / 315.0f))));
+    const float e = __builtin_amdgcn_exp2f(fminf(2.0f * LOG2E * a, 126.0f));
+    const float t = copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f), y);
+    return cap * (a < 0.0625f ? series : t);
 }
 
 // Visible key range [lo, hi) (logical indices) of a query at absolute `pos`.

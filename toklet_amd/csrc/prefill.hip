@@ -6,9 +6,9 @@
 //
 //  * One workgroup = four waves = 128 packed rows of one (problem, KV head),
 //    optionally one key split of it.  Each wave owns 32 rows.
-//  * K and V tiles of 32 keys are copied once per workgroup into padded LDS
-//    (double buffered: the next tile's global loads are in flight while the
-//    current tile is consumed) and read by all four waves.
+//  * K and V tiles of 32 keys are copied once per workgroup into an LDS ring
+//    by direct global->LDS loads, three tiles ahead of the one consumed, and
+//    read by all four waves.
 //  * Scores are formed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16: lane
 //    l holds query row l % 32 and sixteen keys of the tile, so the row's
 //    softmax state lives in one lane pair (one cross-lane step per tile).
@@ -89,19 +89,49 @@ constexpr int PF_WAVES = 4;
 constexpr int PF_ROWS = 32 * PF_WAVES;  // packed rows per workgroup
 constexpr int PF_KT = 32;               // keys per tile
 
+// LDS ring of K/V tiles.  Rows are unpadded (2D bytes) with the 16-byte
+// chunks XOR-swizzled by row, so the K-operand and transposed V reads spread
+// over the banks; direct global->LDS loads fill whole 1 KiB runs per wave
+// instruction.  Three tiles are in flight ahead of the one being consumed
+// (two for head_dim 256, where a stage is 32 KiB).
 template <int D> struct PrefillLds {
-    static constexpr int pitch = D * 2 + 16;            // bytes per staged row (bank spread)
-    static constexpr int tile = PF_KT * pitch;          // one K or V tile
-    static constexpr int stage = 2 * tile;              // K + V
-    static constexpr int bytes = 2 * stage;             // double buffered
+    static constexpr int row = D * 2;                      // bytes per staged row
+    static constexpr int chunks = row / 16;                // 16-byte chunks per row
+    static constexpr int swz = chunks < 32 ? chunks : 32;  // swizzle period
+    static constexpr int tile = PF_KT * row;               // one K or V tile
+    static constexpr int stage = 2 * tile;                 // K + V
+    static constexpr int stages = D >= 256 ? 3 : 4;
+    static constexpr int bytes = stages * stage;
+    static constexpr int runs = tile / 1024;               // 1 KiB runs per tile
+    static constexpr int runs_per_wave = runs / PF_WAVES;
+    static_assert(runs % PF_WAVES == 0, "tile runs must split evenly over the waves");
+    // Byte offset of chunk `c` of row `r` inside a tile.
+    __device__ static constexpr int at(int r, int c) { return r * row + ((c ^ (r % swz)) << 4); }
 };
 
-template <int DT, int D>
-__global__ __launch_bounds__(64 * PF_WAVES) void attn_prefill(Params p) {
+// Wait until at most `ahead` later tiles' direct loads of this wave are in
+// flight, then synchronise the workgroup.  Direct global->LDS loads count in
+// vmcnt; the compiler neither tracks nor orders them, hence the explicit wait
+// and the compiler fences around the barrier.
+template <int LPT> __device__ __forceinline__ void ring_sync(int ahead) {
+    static_assert(LPT * 2 < 64, "vmcnt field");
+    auto wait = [](auto n_tag) {
+        constexpr int n = decltype(n_tag)::value;
+        // gfx9 s_waitcnt: vmcnt in [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+    };
+    if (ahead >= 2) wait(std::integral_constant<int, 2 * LPT>{});
+    else if (ahead == 1) wait(std::integral_constant<int, LPT>{});
+    else wait(std::integral_constant<int, 0>{});
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+template <int DT, int D, bool CAP>
+__global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(Params p) {
     constexpr int KS = D / 16;        // QK k-steps (16 features each)
     constexpr int MB = D / 32;        // PV M-blocks (32 features each)
-    constexpr int CH = D * 2 / 16;    // 16-byte chunks per staged row
-    constexpr int PITCH = PrefillLds<D>::pitch;
     constexpr bool SPLIT_P = DT == BF16;
     static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
 
@@ -180,110 +210,151 @@ __global__ __launch_bounds__(64 * PF_WAVES) void attn_prefill(Params p) {
     for (int mb = 0; mb < MB; ++mb)
         for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
     float m_run = NEG_INF, l_run = 0.0f;
-    bool bad = false;
-    const float scale_log2 = p.scale_log2, scale = p.scale, softcap = p.softcap;
+    // Raw-score extremes over the visible range: +/-inf inputs show up here,
+    // NaN propagates into the mass and the context.
+    float raw_max = NEG_INF, raw_min = -NEG_INF;
+    const float scale = p.scale, softcap = p.softcap, softcap_inv = p.softcap_inv;
+    const float tmul = CAP ? 1.0f : p.scale_log2;  // t units -> log2 units
 
-    // ---- staging: each thread moves CPT 16-byte chunks of K and of V per tile
-    constexpr int CPT = (PF_KT * CH) / (64 * PF_WAVES);
-    static_assert(CPT >= 1 && (PF_KT * CH) % (64 * PF_WAVES) == 0, "tile/thread mismatch");
-    u32x4 stage_k[CPT], stage_v[CPT];
+    // ---- tiles: walk [k_lo, k_hi) segment by segment in steps of PF_KT keys.
+    using L = PrefillLds<D>;
+    constexpr int NS = L::stages;
+    constexpr int LPT = 2 * L::runs_per_wave;  // direct loads per wave per tile (K + V)
 
-    // Segment pieces of [k_lo, k_hi): tiles never straddle a segment.
-    int seg = 0;
-    int64_t tile_key = k_lo;  // first logical key of the next tile to load
-    auto seg_end = [&](int s) { return pr->seg[s].start + pr->seg[s].keys; };
-    auto advance_seg = [&]() {
-        while (seg < pr->nseg - 1 && tile_key >= seg_end(seg)) ++seg;
+    // The segment piece tiles are issued from, cached in scalars.
+    int iseg = 0;
+    const uint8_t *pk = nullptr, *pv = nullptr;  // row of logical key `pstart`, this KV head
+    int64_t pstart = 0, pend = 0;
+    int prow = 0;                                // bytes between consecutive keys
+    auto enter_piece = [&](int64_t key) {
+        while (iseg < pr->nseg - 1 && key >= pr->seg[iseg].start + pr->seg[iseg].keys) ++iseg;
+        const auto &sg = pr->seg[iseg];
+        pstart = sg.start;
+        pend = min(k_hi, sg.start + sg.keys);
+        prow = (int)(sg.row_stride * 2);
+        pk = reinterpret_cast<const uint8_t *>(sg.k) + (int64_t)kvh * sg.head_stride * 2;
+        pv = reinterpret_cast<const uint8_t *>(sg.v) + (int64_t)kvh * sg.head_stride * 2;
     };
-    advance_seg();
+    int64_t ikey = k_lo;  // first key of the next tile to issue
+    if (ikey < k_hi) enter_piece(ikey);
 
-    // Load the tile starting at `key0` (inside segment `s`) into registers.
-    auto load_tile = [&](int64_t key0, int s) {
-        const int64_t key_end = min(k_hi, seg_end(s));
-        const auto &sg = pr->seg[s];
-        const uint8_t *kb = reinterpret_cast<const uint8_t *>(sg.k);
-        const uint8_t *vb = reinterpret_cast<const uint8_t *>(sg.v);
-        const int64_t base = (int64_t)kvh * sg.head_stride + (key0 - sg.start) * sg.row_stride;
-        for (int c = 0; c < CPT; ++c) {
-            const int idx = threadIdx.x + c * 64 * PF_WAVES;
-            const int r = idx / CH, col = idx % CH;
-            u32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-            if (key0 + r < key_end) {
-                const int64_t off = (base + (int64_t)r * sg.row_stride) * 2 + col * 16;
-                kv = *gload_ptr<u32x4>(kb + off);
-                vv = *gload_ptr<u32x4>(vb + off);
-            }
-            stage_k[c] = kv;
-            stage_v[c] = vv;
-        }
-    };
-    auto store_tile = [&](int buf) {
-        lds_ptr<uint8_t> kt = lds + buf * PrefillLds<D>::stage;
-        lds_ptr<uint8_t> vt = kt + PrefillLds<D>::tile;
-        for (int c = 0; c < CPT; ++c) {
-            const int idx = threadIdx.x + c * 64 * PF_WAVES;
-            const int r = idx / CH, col = idx % CH;
-            *(lds_ptr<u32x4>)(kt + r * PITCH + col * 16) = stage_k[c];
-            *(lds_ptr<u32x4>)(vt + r * PITCH + col * 16) = stage_v[c];
-        }
-    };
-
-    // Tile list: walk the pieces; `cur_*` describe the tile in LDS buffer `buf`.
-    int buf = 0;
-    bool have = tile_key < k_hi;
-    int64_t cur_key = tile_key, cur_end = 0;
-    if (have) {
-        load_tile(tile_key, seg);
-        cur_end = min(k_hi, seg_end(seg));
-        tile_key = min(tile_key + PF_KT, cur_end);
-        store_tile(0);
+    // Per-lane part of the direct-load addresses (row in the tile, swizzled chunk).
+    int run_row[L::runs_per_wave], run_col[L::runs_per_wave];
+    for (int i = 0; i < L::runs_per_wave; ++i) {
+        const int pos = (wave * L::runs_per_wave + i) * 1024 + lane * 16;
+        run_row[i] = pos / L::row;
+        run_col[i] = (((pos % L::row) >> 4) ^ (run_row[i] % L::swz)) * 16;
     }
-    __syncthreads();
-    int cur_seg = seg;
-    (void)cur_seg;
-
-    while (have) {
-        // Next tile (if any) streams in while this one is consumed.
-        int64_t nxt_key = tile_key;
-        if (nxt_key >= cur_end) {  // this piece is done: move to the next segment
-            advance_seg();
+    // Issue the tile at `ikey` into stage `st`; returns its key count.
+    auto issue = [&](int st) -> int {
+        const int nk = (int)min<int64_t>(PF_KT, pend - ikey);
+        const int64_t first = (ikey - pstart) * prow;
+        const uint8_t *kb = pk + first, *vb = pv + first;
+        lds_ptr<uint8_t> kt = lds + st * L::stage;
+        for (int i = 0; i < L::runs_per_wave; ++i) {
+            const int run = wave * L::runs_per_wave + i;
+            const int re = run_row[i] < nk ? run_row[i] : nk - 1;  // past the keys: repeat a valid row
+            const uint32_t off = (uint32_t)(re * prow + run_col[i]);
+            __builtin_amdgcn_global_load_lds((global_ptr<void>)(kb + off), (lds_ptr<void>)(kt + run * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_ptr<void>)(vb + off), (lds_ptr<void>)(kt + L::tile + run * 1024), 16, 0, 0);
         }
-        const bool more = nxt_key < k_hi;
-        int64_t nxt_end = 0;
-        if (more) {
-            load_tile(nxt_key, seg);
-            nxt_end = min(k_hi, seg_end(seg));
+        ikey += nk;
+        if (ikey >= pend && ikey < k_hi) enter_piece(ikey);
+        return nk;
+    };
+
+    // Queue of issued tiles (first key, key count), oldest first.
+    int64_t qk[NS - 1];
+    int qn[NS - 1];
+    int queued = 0;
+    for (int i = 0; i < NS - 1; ++i) {
+        qk[i] = ikey;
+        qn[i] = 0;
+        if (ikey < k_hi) {
+            qn[i] = issue(i);
+            ++queued;
         }
+    }
+    // LDS offsets of this lane's operand reads (tile-relative).
+    int k_off[KS];
+    for (int ks = 0; ks < KS; ++ks) k_off[ks] = L::at(j, 2 * ks + h);
+    const int gi = lane >> 4, si = lane & 15;
+    int v_off[2][2][MB];
+    for (int stp = 0; stp < 2; ++stp) {
+        const int kr1 = 16 * stp + 4 * (gi >> 1) + (si >> 2);
+        const int dsub = 16 * (gi & 1) + 4 * (si & 3);
+        for (int mb = 0; mb < MB; ++mb) {
+            const int db = (32 * mb + dsub) * 2;  // byte offset of the 4 features in a row
+            v_off[stp][0][mb] = L::at(kr1, db >> 4) + (db & 15);
+            v_off[stp][1][mb] = L::at(kr1 + 8, db >> 4) + (db & 15);
+        }
+    }
 
-        lds_ptr<uint8_t> kt = lds + buf * PrefillLds<D>::stage;
-        lds_ptr<uint8_t> vt = kt + PrefillLds<D>::tile;
-        const int nkeys = (int)min<int64_t>(PF_KT, cur_end - cur_key);
+    int stage = 0;
+    while (queued > 0) {
+        const int64_t cur_key = qk[0];
+        const int nkeys = qn[0];
+        ring_sync<LPT>(queued - 1);
+        // Refill: the stage read in the previous iteration is free after the barrier.
+        const int64_t new_key = ikey;
+        int new_n = 0;
+        if (ikey < k_hi) new_n = issue((stage + NS - 1) % NS);
+        for (int i = 0; i < NS - 2; ++i) {
+            qk[i] = qk[i + 1];
+            qn[i] = qn[i + 1];
+        }
+        qk[NS - 2] = new_key;
+        qn[NS - 2] = new_n;
+        queued = queued - 1 + (new_n > 0 ? 1 : 0);
 
-        // ---- S^T = K Q^T (32 keys x 32 rows)
+        lds_ptr<uint8_t> kt = lds + stage * L::stage;
+        lds_ptr<uint8_t> vt = kt + L::tile;
+        stage = stage + 1 == NS ? 0 : stage + 1;
+
+        // ---- S^T = K Q^T (32 keys x 32 rows); lane: row j, keys 8q + 4h + r
         f32x16 st;
         for (int i = 0; i < 16; ++i) st[i] = 0.0f;
-        for (int ks = 0; ks < KS; ++ks) {
-            const u32x4 ka = *(lds_ptr<u32x4>)(kt + j * PITCH + 32 * ks + 16 * h);
-            st = mfma32<DT>(ka, qb[ks], st);
-        }
+        for (int ks = 0; ks < KS; ++ks)
+            st = mfma32<DT>(*(lds_ptr<u32x4>)(kt + k_off[ks]), qb[ks], st);
 
-        // ---- scores, mask, online softmax (lane: row j, keys 8q + 4h + r)
-        const bool full = nkeys == PF_KT && cur_key >= wfull_lo && cur_key + PF_KT <= wfull_hi;
-        float s[16];
-        float mt = NEG_INF;
+        // ---- scores, mask, online softmax.  t = raw dot (or, with the softcap,
+        // the capped score in log2 units); p = 2^(t * tmul - m * tmul), where
+        // both transforms are increasing so the tile maximum follows from the
+        // raw maximum.
+        float t[16];
         for (int i = 0; i < 16; ++i) {
-            const int kk = 8 * (i >> 2) + 4 * h + (i & 3);
-            float x = softcap != 0.0f ? softcap_f(st[i] * scale, softcap) * LOG2E : st[i] * scale_log2;
-            bool vis = true;
-            if (!full) {
-                const int64_t key = cur_key + kk;
-                vis = kk < nkeys && key >= r_lo && key < r_hi;
-            }
-            bad |= vis && !is_finite_f(x);
-            x = vis ? x : NEG_INF;
-            s[i] = x;
-            mt = fmaxf(mt, x);
+            if constexpr (CAP) t[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
+            else t[i] = st[i];
         }
+        const bool full = nkeys == PF_KT && cur_key >= wfull_lo && cur_key + PF_KT <= wfull_hi;
+        float hi, lo;
+        if (full) {
+            hi = fmaxf(fmaxf(st[0], st[1]), st[2]);
+            lo = fminf(fminf(st[0], st[1]), st[2]);
+            for (int i = 3; i < 16; ++i) {
+                hi = fmaxf(hi, st[i]);
+                lo = fminf(lo, st[i]);
+            }
+        } else {
+            // Visible keys of this row inside the tile: [lo_rel, hi_rel).
+            const int64_t a = r_lo - cur_key, b = min(r_hi, cur_key + nkeys) - cur_key;
+            const int lo_rel = (int)(a < 0 ? 0 : (a > PF_KT ? PF_KT : a));
+            const int hi_rel = (int)(b < 0 ? 0 : (b > PF_KT ? PF_KT : b));
+            hi = NEG_INF;
+            lo = -NEG_INF;
+            for (int i = 0; i < 16; ++i) {
+                const int kk = 8 * (i >> 2) + 4 * h + (i & 3);
+                const bool vis = kk >= lo_rel && kk < hi_rel;
+                hi = fmaxf(hi, vis ? st[i] : NEG_INF);
+                lo = fminf(lo, vis ? st[i] : -NEG_INF);
+                t[i] = vis ? t[i] : NEG_INF;
+            }
+        }
+        raw_max = fmaxf(raw_max, hi);
+        raw_min = fminf(raw_min, lo);
+        float mt;
+        if constexpr (CAP) mt = hi == NEG_INF ? NEG_INF : softcap_fast(hi * scale, softcap, softcap_inv) * LOG2E;
+        else mt = hi;
         {
             const uint32_t u = __builtin_bit_cast(uint32_t, mt);
             const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
@@ -292,58 +363,41 @@ __global__ __launch_bounds__(64 * PF_WAVES) void attn_prefill(Params p) {
         }
         const float m_new = fmaxf(m_run, mt);
         if (__ballot(m_new != m_run) != 0) {
-            const float base = m_new == NEG_INF ? 0.0f : m_new;
-            const float corr = __builtin_amdgcn_exp2f(m_run - base);
+            const float corr = m_new == NEG_INF ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * tmul);
             l_run *= corr;
             for (int mb = 0; mb < MB; ++mb)
                 for (int i = 0; i < 16; ++i) acc[mb][i] *= corr;
             m_run = m_new;
         }
-        const float base = m_run == NEG_INF ? 0.0f : m_run;
+        const float nbase = m_run == NEG_INF ? 0.0f : -m_run * tmul;
         uint32_t ph[8], pl[8];
         for (int i = 0; i < 8; ++i) {
-            const float e0 = __builtin_amdgcn_exp2f(s[2 * i] - base);
-            const float e1 = __builtin_amdgcn_exp2f(s[2 * i + 1] - base);
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(t[2 * i], tmul, nbase));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(t[2 * i + 1], tmul, nbase));
             ph[i] = pack2<DT>(e0, e1);
-            if constexpr (SPLIT_P) {
-                const float r0 = e0 - lo_f<DT>(ph[i]);
-                const float r1 = e1 - hi_f<DT>(ph[i]);
-                pl[i] = pack2<DT>(r0, r1);
-                l_run += (lo_f<DT>(ph[i]) + lo_f<DT>(pl[i])) + (hi_f<DT>(ph[i]) + hi_f<DT>(pl[i]));
-            } else {
-                l_run += lo_f<DT>(ph[i]) + hi_f<DT>(ph[i]);
-            }
+            if constexpr (SPLIT_P) pl[i] = pack2<DT>(e0 - lo_f<DT>(ph[i]), e1 - hi_f<DT>(ph[i]));
+            l_run += e0 + e1;
         }
 
         // ---- O^T += V^T P^T, two 16-key steps.  B slots 8h..8h+7 of step st
         // are keys {16 st + 4h + 0..3, 16 st + 8 + 4h + 0..3} = acc quads 2st, 2st+1.
-        const int gi = lane >> 4, si = lane & 15;
+        // V^T rows come transposed from LDS: group gi of 16 lanes reads features
+        // 32 mb + 16 (gi & 1) + 0..15 of keys kb..kb+3; source lane si supplies row
+        // kb + si / 4, features + 4 (si % 4).
         for (int stp = 0; stp < 2; ++stp) {
             const u32x4 bh = {ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
             u32x4 bl = {0, 0, 0, 0};
             if constexpr (SPLIT_P) bl = u32x4{pl[4 * stp], pl[4 * stp + 1], pl[4 * stp + 2], pl[4 * stp + 3]};
-            // Transposed reads: group gi covers features dbase + 0..15 of keys kb..kb+3;
-            // source lane si supplies row kb + si/4, features dbase + 4 (si % 4).
-            const int kb1 = 16 * stp + 4 * (gi >> 1);
-            const int dsub = 16 * (gi & 1) + 4 * (si & 3);
             for (int mb = 0; mb < MB; ++mb) {
-                const int dcol = (32 * mb + dsub) * 2;
-                const u32x2 r1 = read_tr(vt + (kb1 + (si >> 2)) * PITCH + dcol);
-                const u32x2 r2 = read_tr(vt + (kb1 + 8 + (si >> 2)) * PITCH + dcol);
+                const u32x2 r1 = read_tr(vt + v_off[stp][0][mb]);
+                const u32x2 r2 = read_tr(vt + v_off[stp][1][mb]);
                 const u32x4 va = {r1[0], r1[1], r2[0], r2[1]};
                 acc[mb] = mfma32<DT>(va, bh, acc[mb]);
                 if constexpr (SPLIT_P) acc[mb] = mfma32<DT>(va, bl, acc[mb]);
             }
         }
-
-        if (more) store_tile(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
-        have = more;
-        cur_key = nxt_key;
-        cur_end = nxt_end;
-        tile_key = min(nxt_key + PF_KT, nxt_end);
     }
+    bool bad = raw_max == -NEG_INF || raw_min == NEG_INF;  // an infinite visible score
 
     // ---- the two key halves of each row (lanes j and j + 32) share m_run; add l.
     {
@@ -442,10 +496,13 @@ extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int he
                                          int64_t groups, hipStream_t stream) {
     using namespace tkh;
     dim3 grid((unsigned)groups), block(64 * PF_WAVES);
-#define TKH_PF(DT, DD)                                                            \
-    if (dtype == DT && head_dim == DD) {                                          \
-        hipLaunchKernelGGL((attn_prefill<DT, DD>), grid, block, 0, stream, *p);   \
-        return hipGetLastError();                                                 \
+#define TKH_PF(DT, DD)                                                                  \
+    if (dtype == DT && head_dim == DD) {                                                \
+        if (p->softcap != 0.0f)                                                         \
+            hipLaunchKernelGGL((attn_prefill<DT, DD, true>), grid, block, 0, stream, *p);  \
+        else                                                                            \
+            hipLaunchKernelGGL((attn_prefill<DT, DD, false>), grid, block, 0, stream, *p); \
+        return hipGetLastError();                                                       \
     }
     TKH_PF(BF16, 64) TKH_PF(BF16, 128) TKH_PF(BF16, 256)
     TKH_PF(F16, 64) TKH_PF(F16, 128) TKH_PF(F16, 256)
