@@ -7,8 +7,9 @@
 //  * One workgroup = four waves = 128 packed rows of one (problem, KV head),
 //    optionally one key split of it.  Each wave owns 32 rows.
 //  * K and V tiles of 32 keys are copied once per workgroup into an LDS ring
-//    by direct global->LDS loads, three tiles ahead of the one consumed, and
-//    read by all four waves.
+//    by direct global->LDS loads, two tiles ahead of the two in use, and read
+//    by all four waves.  The scores of tile t + 1 are formed while the
+//    softmax and P.V of tile t run (software pipeline).
 //  * Scores are formed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16: lane
 //    l holds query row l % 32 and sixteen keys of the tile, so the row's
 //    softmax state lives in one lane pair (one cross-lane step per tile).
@@ -76,6 +77,21 @@ __device__ __forceinline__ u32x2 read_tr(lds_ptr<uint8_t> p) {
     return __builtin_bit_cast(u32x2, r);
 }
 
+// Direct global->LDS 16-byte load for each lane: lane i's 16 bytes land at
+// LDS address `l` + 16 i.  Issued as inline assembly so that the compiler,
+// which cannot prove these LDS writes apart from the tile being read, does not
+// put a full vmcnt(0) wait before every LDS read; ring_sync() orders them.
+__device__ __forceinline__ void dma16(const void *g, lds_ptr<uint8_t> l) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)l);  // wave-uniform
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ void coherent_store(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -97,7 +113,10 @@ constexpr int PF_KT = 32;               // keys per tile
 template <int D> struct PrefillLds {
     static constexpr int row = D * 2;                      // bytes per staged row
     static constexpr int chunks = row / 16;                // 16-byte chunks per row
-    static constexpr int swz = chunks < 32 ? chunks : 32;  // swizzle period
+    // Chunk swizzle of row r: XOR with (2r + r/4) mod 8.  Eight consecutive
+    // rows (a K-operand read) get eight distinct 16-byte bank groups, and the
+    // four rows of a transposed V read keep their two-chunk pairs disjoint.
+    __device__ static constexpr int swz(int r) { return (2 * r + (r >> 2)) & 7; }
     static constexpr int tile = PF_KT * row;               // one K or V tile
     static constexpr int stage = 2 * tile;                 // K + V
     static constexpr int stages = D >= 256 ? 3 : 4;
@@ -106,7 +125,7 @@ template <int D> struct PrefillLds {
     static constexpr int runs_per_wave = runs / PF_WAVES;
     static_assert(runs % PF_WAVES == 0, "tile runs must split evenly over the waves");
     // Byte offset of chunk `c` of row `r` inside a tile.
-    __device__ static constexpr int at(int r, int c) { return r * row + ((c ^ (r % swz)) << 4); }
+    __device__ static constexpr int at(int r, int c) { return r * row + ((c ^ swz(r)) << 4); }
 };
 
 // Wait until at most `ahead` later tiles' direct loads of this wave are in
@@ -195,6 +214,9 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         int64_t a, b;
         visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + w_first / G, &a, &wfull_hi);
         visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + w_last / G, &wfull_lo, &b);
+        // Wave-uniform by construction; say so, so the full-tile test is a scalar branch.
+        wfull_lo = uniform64(wfull_lo);
+        wfull_hi = uniform64(wfull_hi);
     }
 
     // Q^T B operands: lane holds row j, features 16 ks + 8 h .. + 7.
@@ -243,7 +265,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     for (int i = 0; i < L::runs_per_wave; ++i) {
         const int pos = (wave * L::runs_per_wave + i) * 1024 + lane * 16;
         run_row[i] = pos / L::row;
-        run_col[i] = (((pos % L::row) >> 4) ^ (run_row[i] % L::swz)) * 16;
+        run_col[i] = (((pos % L::row) >> 4) ^ L::swz(run_row[i])) * 16;
     }
     // Issue the tile at `ikey` into stage `st`; returns its key count.
     auto issue = [&](int st) -> int {
@@ -255,8 +277,8 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
             const int run = wave * L::runs_per_wave + i;
             const int re = run_row[i] < nk ? run_row[i] : nk - 1;  // past the keys: repeat a valid row
             const uint32_t off = (uint32_t)(re * prow + run_col[i]);
-            __builtin_amdgcn_global_load_lds((global_ptr<void>)(kb + off), (lds_ptr<void>)(kt + run * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((global_ptr<void>)(vb + off), (lds_ptr<void>)(kt + L::tile + run * 1024), 16, 0, 0);
+            dma16(kb + off, kt + run * 1024);
+            dma16(vb + off, kt + L::tile + run * 1024);
         }
         ikey += nk;
         if (ikey >= pend && ikey < k_hi) enter_piece(ikey);
@@ -290,32 +312,36 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         }
     }
 
+    // S^T = K Q^T of the tile in stage `stg` (32 keys x 32 rows); lane: row j,
+    // keys 8q + 4h + r.
+    auto scores_of = [&](int stg) {
+        lds_ptr<uint8_t> kt = lds + stg * L::stage;
+        f32x16 sc;
+        for (int i = 0; i < 16; ++i) sc[i] = 0.0f;
+        for (int ks = 0; ks < KS; ++ks)
+            sc = mfma32<DT>(*(lds_ptr<u32x4>)(kt + k_off[ks]), qb[ks], sc);
+        return sc;
+    };
+
+    // Software pipeline: iteration t forms the scores of tile t + 1 while it
+    // runs the softmax and P.V of tile t, so the matrix cores have independent
+    // work while the vector unit computes probabilities.
     int stage = 0;
+    f32x16 st;
+    if (queued > 0) {
+        ring_sync<LPT>(queued - 1);
+        st = scores_of(0);
+    }
     while (queued > 0) {
         const int64_t cur_key = qk[0];
         const int nkeys = qn[0];
-        ring_sync<LPT>(queued - 1);
-        // Refill: the stage read in the previous iteration is free after the barrier.
-        const int64_t new_key = ikey;
-        int new_n = 0;
-        if (ikey < k_hi) new_n = issue((stage + NS - 1) % NS);
-        for (int i = 0; i < NS - 2; ++i) {
-            qk[i] = qk[i + 1];
-            qn[i] = qn[i + 1];
-        }
-        qk[NS - 2] = new_key;
-        qn[NS - 2] = new_n;
-        queued = queued - 1 + (new_n > 0 ? 1 : 0);
-
-        lds_ptr<uint8_t> kt = lds + stage * L::stage;
-        lds_ptr<uint8_t> vt = kt + L::tile;
-        stage = stage + 1 == NS ? 0 : stage + 1;
-
-        // ---- S^T = K Q^T (32 keys x 32 rows); lane: row j, keys 8q + 4h + r
-        f32x16 st;
-        for (int i = 0; i < 16; ++i) st[i] = 0.0f;
-        for (int ks = 0; ks < KS; ++ks)
-            st = mfma32<DT>(*(lds_ptr<u32x4>)(kt + k_off[ks]), qb[ks], st);
+        const bool next = queued > 1;
+        f32x16 st_next;
+        const int stage_next = stage + 1 == NS ? 0 : stage + 1;
+        lds_ptr<uint8_t> vt = lds + stage * L::stage + L::tile;
+        lds_ptr<uint8_t> kn = lds + stage_next * L::stage;
+        const int stage_free = stage == 0 ? NS - 1 : stage - 1;
+        stage = stage_next;
 
         // ---- scores, mask, online softmax.  t = raw dot (or, with the softcap,
         // the capped score in log2 units); p = 2^(t * tmul - m * tmul), where
@@ -370,13 +396,46 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
             m_run = m_new;
         }
         const float nbase = m_run == NEG_INF ? 0.0f : -m_run * tmul;
+
+        if (next) {
+            // Tile t + 1 resident; everyone is done with tile t - 1, whose stage
+            // takes the next load.
+            ring_sync<LPT>(queued - 2);
+            const int64_t new_key = ikey;
+            int new_n = 0;
+            if (ikey < k_hi) new_n = issue(stage_free);
+            for (int i = 0; i < NS - 2; ++i) {
+                qk[i] = qk[i + 1];
+                qn[i] = qn[i + 1];
+            }
+            qk[NS - 2] = new_key;
+            qn[NS - 2] = new_n;
+            queued = queued - 1 + (new_n > 0 ? 1 : 0);
+        } else {
+            queued = 0;
+        }
+
+        // Scores of tile t + 1 interleaved with the probabilities of tile t:
+        // each QK MFMA (its K operand read one step ahead) is followed by a
+        // share of the exp/pack work, the order fixed by scheduling fences so
+        // the vector unit runs while the matrix core works.  With no next tile
+        // the stage holds stale data and the result is unused.
         uint32_t ph[8], pl[8];
-        for (int i = 0; i < 8; ++i) {
-            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(t[2 * i], tmul, nbase));
-            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(t[2 * i + 1], tmul, nbase));
-            ph[i] = pack2<DT>(e0, e1);
-            if constexpr (SPLIT_P) pl[i] = pack2<DT>(e0 - lo_f<DT>(ph[i]), e1 - hi_f<DT>(ph[i]));
-            l_run += e0 + e1;
+        for (int i = 0; i < 16; ++i) st_next[i] = 0.0f;
+        u32x4 kop = *(lds_ptr<u32x4>)(kn + k_off[0]);
+        for (int ks = 0; ks < KS; ++ks) {
+            const u32x4 kcur = kop;
+            if (ks + 1 < KS) kop = *(lds_ptr<u32x4>)(kn + k_off[ks + 1]);
+            st_next = mfma32<DT>(kcur, qb[ks], st_next);
+            __builtin_amdgcn_sched_barrier(0);
+            for (int i = 8 * ks / KS; i < 8 * (ks + 1) / KS; ++i) {
+                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(t[2 * i], tmul, nbase));
+                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(t[2 * i + 1], tmul, nbase));
+                ph[i] = pack2<DT>(e0, e1);
+                if constexpr (SPLIT_P) pl[i] = pack2<DT>(e0 - lo_f<DT>(ph[i]), e1 - hi_f<DT>(ph[i]));
+                l_run += e0 + e1;
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
 
         // ---- O^T += V^T P^T, two 16-key steps.  B slots 8h..8h+7 of step st
@@ -396,6 +455,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
                 if constexpr (SPLIT_P) acc[mb] = mfma32<DT>(va, bl, acc[mb]);
             }
         }
+        if (next) st = st_next;
     }
     bool bad = raw_max == -NEG_INF || raw_min == NEG_INF;  // an infinite visible score
 
