@@ -20,11 +20,10 @@
 #include "../../include/tokhip.h"
 #include "device.hpp"
 
-extern "C" hipError_t tkh_launch_mfma(const tkh::Params *p, int dtype, int head_dim, int nrb,
-                                      hipStream_t stream);
-extern "C" hipError_t tkh_launch_generic(const tkh::Params *p, int dtype, hipStream_t stream);
+extern "C" hipError_t tkh_launch_generic(const tkh::Params *p, int dtype, hipStream_t stream,
+                                         hipEvent_t start, hipEvent_t stop);
 extern "C" hipError_t tkh_launch_combine(const tkh::Params *p, int64_t total_rows,
-                                         hipStream_t stream);
+                                         hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 extern "C" hipError_t tkh_launch_kv_append(int src, int dst, const void *k, const void *v,
                                            void *kc, void *vc, int64_t tokens, int heads,
                                            int dims, int64_t capacity, int64_t offset,
@@ -41,13 +40,14 @@ extern "C" hipError_t tkh_launch_fill_u32(uint32_t *p, uint32_t v, hipStream_t s
 extern "C" int tkh_decode_max_rows(int dtype, int head_dim);
 extern "C" int tkh_prefill_rows_per_group(void);
 extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim,
-                                         int64_t groups, hipStream_t stream);
+                                         int64_t groups, hipStream_t stream, hipEvent_t start,
+                                         hipEvent_t stop);
 extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int want);
 extern "C" int tkh_decode_max_waves(int dtype, int head_dim, int rows);
 extern "C" int tkh_decode_max_splits(void);
 extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int head_dim, int rows,
                                         int keys_per_lane, int waves, int64_t groups,
-                                        hipStream_t stream);
+                                        hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 namespace {
 
@@ -147,7 +147,6 @@ struct tkh_context {
     hipEvent_t ring_events[kSlots] = {};
     bool ring_used[kSlots] = {};
     int ring_next = 0;
-    int target_waves = 2048;
     int split_keys_override = 0;
     int force_generic = 0;
     int decode_waves = 8;        // waves per decode workgroup
@@ -158,9 +157,10 @@ struct tkh_context {
     int prefill_groups = 512;    // below this many row-block workgroups, split the keys
     int prefill_max_splits = 16;
     int prefill_min_keys = 256;  // keys per split at least
-    // profiling: event triples (before attention, after attention, after combine)
+    // profiling: per launch, start/stop of the attention kernel and of the combine kernel
     bool profiling = false;
     std::vector<hipEvent_t> prof_events;
+    std::vector<char> prof_has_combine;
     size_t prof_used = 0;
     uint64_t prof_launches = 0;
     double prof_attention_ms = 0, prof_combine_ms = 0;
@@ -253,14 +253,17 @@ uint32_t upload(tkh_context *ctx, const tkh::Problem *probs, int count, tkh::Pro
     return TKH_OK;
 }
 
-// Fold finished event triples into the totals.
+// Fold finished event quads into the totals. Each launch slot holds the start
+// and stop events of the attention kernel and of the combine kernel; the
+// second pair is left unrecorded when the launch has no combine kernel.
 uint32_t profile_drain(tkh_context *ctx, tkh_error *err) {
     if (ctx->prof_used == 0) return TKH_OK;
-    HIP_TRY(hipEventSynchronize(ctx->prof_events[3 * ctx->prof_used - 1]), "profile");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "profile");
     for (size_t i = 0; i < ctx->prof_used; ++i) {
+        hipEvent_t *ev = &ctx->prof_events[4 * i];
         float a = 0, c = 0;
-        HIP_TRY(hipEventElapsedTime(&a, ctx->prof_events[3 * i], ctx->prof_events[3 * i + 1]), "profile");
-        HIP_TRY(hipEventElapsedTime(&c, ctx->prof_events[3 * i + 1], ctx->prof_events[3 * i + 2]), "profile");
+        HIP_TRY(hipEventElapsedTime(&a, ev[0], ev[1]), "profile");
+        if (ctx->prof_has_combine[i]) HIP_TRY(hipEventElapsedTime(&c, ev[2], ev[3]), "profile");
         ctx->prof_attention_ms += a;
         ctx->prof_combine_ms += c;
         ctx->prof_launches += 1;
@@ -269,14 +272,16 @@ uint32_t profile_drain(tkh_context *ctx, tkh_error *err) {
     return TKH_OK;
 }
 
-uint32_t profile_slot(tkh_context *ctx, hipEvent_t **ev, tkh_error *err) {
+uint32_t profile_slot(tkh_context *ctx, hipEvent_t **ev, bool combine, tkh_error *err) {
     const size_t cap = 1024;
     if (ctx->prof_events.empty()) {
-        ctx->prof_events.resize(3 * cap);
+        ctx->prof_events.resize(4 * cap);
+        ctx->prof_has_combine.resize(cap);
         for (auto &e : ctx->prof_events) HIP_TRY(hipEventCreate(&e), "profile");
     }
     if (ctx->prof_used == cap) TRY(profile_drain(ctx, err));
-    *ev = &ctx->prof_events[3 * ctx->prof_used++];
+    ctx->prof_has_combine[ctx->prof_used] = combine;
+    *ev = &ctx->prof_events[4 * ctx->prof_used++];
     return TKH_OK;
 }
 
@@ -381,14 +386,10 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     prm.part_o = ws + (size_t)slots * R * 2;
 
     hipEvent_t *ev = nullptr;
-    if (ctx->profiling) TRY(profile_slot(ctx, &ev, err));
-    if (ev) HIP_TRY(hipEventRecord(ev[0], ctx->stream), "profile");
-    hipError_t e = tkh_launch_decode(&prm, (int)plan.dtype, (int)D, R, u, nw, wgs, ctx->stream);
+    if (ctx->profiling) TRY(profile_slot(ctx, &ev, false, err));
+    hipError_t e = tkh_launch_decode(&prm, (int)plan.dtype, (int)D, R, u, nw, wgs, ctx->stream,
+                                     ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "decode launch", err);
-    if (ev) {
-        HIP_TRY(hipEventRecord(ev[1], ctx->stream), "profile");
-        HIP_TRY(hipEventRecord(ev[2], ctx->stream), "profile");
-    }
     return TKH_OK;
 }
 
@@ -447,14 +448,10 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
     prm.part_o = ws + (size_t)slots * rows_per * 2;
 
     hipEvent_t *ev = nullptr;
-    if (ctx->profiling) TRY(profile_slot(ctx, &ev, err));
-    if (ev) HIP_TRY(hipEventRecord(ev[0], ctx->stream), "profile");
-    hipError_t e = tkh_launch_prefill(&prm, (int)plan.dtype, (int)D, wgs, ctx->stream);
+    if (ctx->profiling) TRY(profile_slot(ctx, &ev, false, err));
+    hipError_t e = tkh_launch_prefill(&prm, (int)plan.dtype, (int)D, wgs, ctx->stream,
+                                      ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "prefill launch", err);
-    if (ev) {
-        HIP_TRY(hipEventRecord(ev[1], ctx->stream), "profile");
-        HIP_TRY(hipEventRecord(ev[2], ctx->stream), "profile");
-    }
     return TKH_OK;
 }
 
@@ -474,47 +471,10 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
             (plan.dtype == TKH_BF16 || plan.dtype == TKH_F16) && (D == 64 || D == 128 || D == 256))
             return launch_prefill(ctx, plan, group, err);
     }
-    const bool mfma = !ctx->force_generic && plan.diag_mode == 0 &&
-                      (plan.dtype == TKH_BF16 || plan.dtype == TKH_F16) &&
-                      (D == 64 || D == 128 || D == 256);
-    int nrb = 1;
-    int64_t max_rows = 0;
-    for (auto &p : group) max_rows = std::max<int64_t>(max_rows, (int64_t)p.queries * G);
-    if (mfma && D != 256 && max_rows > 16) nrb = 2;
-
+    // FP32, odd head sizes and diagnostics: one wave per (query, head), then a
+    // combine launch that publishes the context.
     const size_t ws_floats = ctx->workspace_bytes / sizeof(float);
-    int64_t split_keys = 0;
-    if (mfma) {
-        // Work in (row block x key) units; choose a key split that yields
-        // about target_waves waves, in multiples of the 32-key tile.
-        double work = 0;
-        int64_t base_tiles = 0;
-        for (auto &p : group) {
-            p.row_blocks = (int32_t)(((int64_t)p.queries * G + 16 * nrb - 1) / (16 * nrb));
-            base_tiles += Hkv * p.row_blocks;
-            work += (double)Hkv * p.row_blocks * (double)p.keys;
-        }
-        int64_t sk = (int64_t)std::ceil(work / std::max(1, ctx->target_waves));
-        sk = std::max<int64_t>(64, (sk + 31) / 32 * 32);
-        if (ctx->split_keys_override > 0) sk = (ctx->split_keys_override + 31) / 32 * 32;
-        for (;;) {
-            size_t need = 0;
-            for (auto &p : group) {
-                int64_t splits = (p.keys + sk - 1) / sk;
-                need += (size_t)p.queries * Hq * splits * (D + 2);
-            }
-            if (need <= ws_floats) break;
-            int64_t max_keys = 0;
-            for (auto &p : group) max_keys = std::max(max_keys, p.keys);
-            if (sk >= max_keys)
-                return fail(err, TKH_UNSUPPORTED, "workspace", 0, need * 4, ctx->workspace_bytes,
-                            "attention needs %zu workspace bytes, context has %zu", need * 4,
-                            ctx->workspace_bytes);
-            sk *= 2;
-        }
-        split_keys = sk;
-        (void)base_tiles;
-    } else {
+    {
         size_t need = 0;
         for (auto &p : group) need += (size_t)p.queries * Hq * (D + 2);
         if (need > ws_floats)
@@ -522,23 +482,16 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
                         "attention needs %zu workspace bytes, context has %zu", need * 4,
                         ctx->workspace_bytes);
     }
-
     int64_t tiles = 0, rows = 0, part_rows = 0;
     for (auto &p : group) {
         p.tile_base = tiles;
         p.part_base = rows;
-        if (mfma) {
-            p.split_keys = (int32_t)split_keys;
-            p.splits = (int32_t)((p.keys + split_keys - 1) / split_keys);
-            tiles += Hkv * p.splits * p.row_blocks;
-        } else {
-            p.splits = 1;
-            p.row_blocks = 1;
-            tiles += (int64_t)p.queries * Hq;
-        }
+        p.splits = 1;
+        p.row_blocks = 1;
+        tiles += (int64_t)p.queries * Hq;
         p.slot_base = part_rows;
         rows += (int64_t)p.queries * Hq;
-        part_rows += (int64_t)p.queries * Hq * p.splits;
+        part_rows += (int64_t)p.queries * Hq;
     }
 
     tkh::Problem *dev = nullptr;
@@ -568,16 +521,12 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
     prm.diag_mode = plan.diag_mode;
 
     hipEvent_t *ev = nullptr;
-    if (ctx->profiling) TRY(profile_slot(ctx, &ev, err));
-    if (ev) HIP_TRY(hipEventRecord(ev[0], ctx->stream), "profile");
-    hipError_t e;
-    if (mfma) e = tkh_launch_mfma(&prm, (int)plan.dtype, (int)D, nrb, ctx->stream);
-    else e = tkh_launch_generic(&prm, (int)plan.dtype, ctx->stream);
+    if (ctx->profiling) TRY(profile_slot(ctx, &ev, true, err));
+    hipError_t e = tkh_launch_generic(&prm, (int)plan.dtype, ctx->stream, ev ? ev[0] : nullptr,
+                                      ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "attention launch", err);
-    if (ev) HIP_TRY(hipEventRecord(ev[1], ctx->stream), "profile");
-    e = tkh_launch_combine(&prm, rows, ctx->stream);
+    e = tkh_launch_combine(&prm, rows, ctx->stream, ev ? ev[2] : nullptr, ev ? ev[3] : nullptr);
     if (e != hipSuccess) return device_error(e, "combine launch", err);
-    if (ev) HIP_TRY(hipEventRecord(ev[2], ctx->stream), "profile");
     return TKH_OK;
 }
 
@@ -619,7 +568,6 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     ctx->device = device;
     ctx->synchronous = synchronous != 0;
     ctx->workspace_bytes = workspace_bytes ? workspace_bytes : (size_t)256 << 20;
-    ctx->target_waves = env_int("TKH_TARGET_WAVES", 2048);
     ctx->split_keys_override = env_int("TKH_SPLIT_KEYS", 0);
     ctx->force_generic = env_int("TKH_FORCE_GENERIC", 0);
     ctx->decode_waves = std::min(8, std::max(1, env_int("TKH_DECODE_WAVES", 8)));

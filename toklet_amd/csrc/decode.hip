@@ -552,16 +552,16 @@ extern "C" int tkh_decode_max_splits(void) { return tkh::DECODE_MAX_SPLITS; }
 
 extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int head_dim, int rows,
                                         int keys_per_lane, int waves, int64_t groups,
-                                        hipStream_t stream) {
+                                        hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     using namespace tkh;
     if (waves < 1 || waves > tkh_decode_max_waves(dtype, head_dim, rows)) return hipErrorInvalidValue;
     dim3 grid((unsigned)groups), block(64 * waves);
 #define TKH_DEC(DT, DD, RR, UU)                                                             \
     if (dtype == DT && head_dim == DD && rows <= RR && keys_per_lane == UU) {               \
         if (p->softcap != 0.0f)                                                             \
-            hipLaunchKernelGGL((attn_decode<DT, DD, RR, UU, true>), grid, block, 0, stream, *p); \
+            hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, true>), grid, block, 0, stream, start, stop, 0, *p); \
         else                                                                                \
-            hipLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false>), grid, block, 0, stream, *p); \
+            hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false>), grid, block, 0, stream, start, stop, 0, *p); \
         return hipGetLastError();                                                           \
     }
 #define TKH_DEC_R(DT, DD, UU) TKH_DEC(DT, DD, 1, UU) TKH_DEC(DT, DD, 2, UU) TKH_DEC(DT, DD, 4, UU) TKH_DEC(DT, DD, 8, UU)

@@ -553,15 +553,16 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
 extern "C" int tkh_prefill_rows_per_group(void) { return tkh::PF_ROWS; }
 
 extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim,
-                                         int64_t groups, hipStream_t stream) {
+                                         int64_t groups, hipStream_t stream, hipEvent_t start,
+                                         hipEvent_t stop) {
     using namespace tkh;
     dim3 grid((unsigned)groups), block(64 * PF_WAVES);
 #define TKH_PF(DT, DD)                                                                  \
     if (dtype == DT && head_dim == DD) {                                                \
         if (p->softcap != 0.0f)                                                         \
-            hipLaunchKernelGGL((attn_prefill<DT, DD, true>), grid, block, 0, stream, *p);  \
+            hipExtLaunchKernelGGL((attn_prefill<DT, DD, true>), grid, block, 0, stream, start, stop, 0, *p);  \
         else                                                                            \
-            hipLaunchKernelGGL((attn_prefill<DT, DD, false>), grid, block, 0, stream, *p); \
+            hipExtLaunchKernelGGL((attn_prefill<DT, DD, false>), grid, block, 0, stream, start, stop, 0, *p); \
         return hipGetLastError();                                                       \
     }
     TKH_PF(BF16, 64) TKH_PF(BF16, 128) TKH_PF(BF16, 256)
