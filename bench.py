@@ -159,7 +159,9 @@ def bench_c2(torch, ops, kvmod, ctx, steps, warmup):
         "tokens_per_s": (w.total * steps) / job_s,
         "prefill_ms": pre_s / steps * 1e3,
         "prefill_tflops": flops * steps / pre_s / 1e12,
-        "prefill_kernel_tflops": flops * steps / (pre_prof["attention_ms"] / 1e3) / 1e12,
+        "prefill_kernel_tflops": flops * steps / ((pre_prof["attention_ms"] + pre_prof["combine_ms"]) / 1e3) / 1e12,
+        "prefill_kernel_us": pre_prof["attention_ms"] / max(1, pre_prof["launches"]) * 1e3,
+        "prefill_merge_us": pre_prof["combine_ms"] / max(1, pre_prof["launches"]) * 1e3,
         "decode_ms": dec_s / steps * 1e3,
         "decode_gbs": dbytes * steps / dec_s / 1e9,
         "decode_kernel_us": dec_prof["attention_ms"] / dec_prof["launches"] * 1e3,
@@ -255,12 +257,13 @@ def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096
     prof = ctx.profile_read()
     ctx.profile(False)
     ctx.synchronize()
-    kernel_s = prof["attention_ms"] / 1e3
+    kernel_s = (prof["attention_ms"] + prof["combine_ms"]) / 1e3
     return {
         "sessions": batch, "cached": cached, "new": tokens,
         "ms_per_step": s / steps * 1e3,
         "tflops": flops * steps / s / 1e12,
         "kernel_us": prof["attention_ms"] / max(1, prof["launches"]) * 1e3,
+        "merge_us": prof["combine_ms"] / max(1, prof["launches"]) * 1e3,
         "kernel_tflops": flops * steps / kernel_s / 1e12,
         "kernel_frac_mfma": flops * steps / kernel_s / 1e12 / PEAK_BF16_TFLOPS,
         "gflop_per_step": flops / 1e9,
@@ -283,6 +286,21 @@ def copy_calibration(torch, nbytes=1 << 30, reps=3):
         t.append(a.elapsed_time(b) / 1e3)
     return {"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
             "copy_gbs": 2 * nbytes / min(t) / 1e9}
+
+
+def measured_traffic(key):
+    """HBM bytes per launch of a workload's dominant kernel, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE passes of this script,
+    each scaled by what the counter reads for a plain copy of known size)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f).get(key)
+    except (OSError, ValueError):
+        return None, None
+    if not entry:
+        return None, None
+    return entry.get("bytes_per_launch"), entry
 
 
 def cpu_baseline(w, torch):
@@ -353,6 +371,7 @@ def main():
         return
 
     c2 = result["c2"]
+    traffic, traffic_entry = measured_traffic("c2_decode")
     line = {
         "metric": "decode attn GB/s (% HBM peak); prefill attn TFLOPS (% MFMA peak)",
         "value": round(c2["decode_gbs"], 2),
@@ -376,14 +395,16 @@ def main():
         "tokens_per_s": round(c2["tokens_per_s"], 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_mfma (decode launches of configs[1])",
+            "kernel": "attn_decode<bf16, D=128, 2 rows> (the 256 decode launches of configs[1])",
             "achieved": round(c2["decode_kernel_gbs"], 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(c2["decode_kernel_gbs"] / PEAK_HBM_GBS, 5),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": (traffic_entry or {}).get("source"),
             "avg_kernel_us": round(c2["decode_kernel_us"], 3),
             "algorithmic_bytes_per_launch": round(c2["decode_bytes_per_step_avg"]),
+            "timing": "hipExtLaunchKernelGGL start/stop events on the library's stream",
         },
         "prefill_roofline": {
             "bound": "mfma", "achieved": round(c2["prefill_kernel_tflops"], 3),

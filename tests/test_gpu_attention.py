@@ -9,8 +9,8 @@ import numpy as np
 import pytest
 
 from goldens import TINY_CASES, Golden, close, head_major_to_token_major
-from gpu_util import (TOL_F32, TOL_HALF, dev, greedy_tokens, head_major_cache, host, log, max_err,
-                      stored)
+from gpu_util import (TOL_F32, TOL_HALF, assert_tokens_agree, dev, head_major_cache, host, log,
+                      max_err, stored)
 
 pytestmark = pytest.mark.gpu
 
@@ -256,7 +256,7 @@ def test_mfma_qwen3_chunked_prefill_then_decode(torch_mod, ctx, ops, orc, dt):
     rng = np.random.default_rng(99)
     w = rng.standard_normal((4096, 16 * 128)).astype(np.float32)
     for got, ref in ctxs:
-        assert np.array_equal(greedy_tokens(got, w), greedy_tokens(ref, w))
+        assert_tokens_agree(got, ref, w)
     log(f"  worst max abs error {worst:.3e}")
 
 
@@ -478,5 +478,5 @@ def test_fp32_qwen25_prefill_decode_argmax(torch_mod, ctx, ops, orc):
         ref, _, _ = orc.attention_cached(q, np.nan_to_num(kc), np.nan_to_num(vc), n, hq, hkv, D, cap, start)
         got = host(out)
         assert max_err(got, ref) <= TOL_F32
-        assert np.array_equal(greedy_tokens(got.reshape(n, -1), w), greedy_tokens(ref.reshape(n, -1), w))
+        assert_tokens_agree(got.reshape(n, -1), ref.reshape(n, -1), w)
         start += n

@@ -10,7 +10,7 @@ The checker is the CPU oracle on the same stored (rounded) values.
 import numpy as np
 import pytest
 
-from gpu_util import TOL_F32, TOL_HALF, dev, greedy_tokens, host, log, max_err, stored
+from gpu_util import TOL_F32, TOL_HALF, assert_tokens_agree, dev, host, log, max_err, stored
 
 pytestmark = pytest.mark.gpu
 
@@ -72,7 +72,7 @@ def test_decode_peaky_keys_and_tokens(torch_mod, ctx, ops, orc):
     err = max_err(got, ref)
     log(f"llama 32/8/128 peaky decode: max abs error {err:.3e}")
     assert err <= TOL_HALF
-    assert np.array_equal(greedy_tokens(got.reshape(1, -1), w), greedy_tokens(ref.reshape(1, -1), w))
+    assert_tokens_agree(got.reshape(1, -1), ref.reshape(1, -1), w)
 
 
 @pytest.mark.parametrize("tokens", [2, 3, 4])

@@ -481,3 +481,17 @@ def test_proportional_rotary_reduces_to_rotary(orc):
     xr = x.reshape(3, 2, 8)
     cr = c.reshape(3, 2, 8)
     assert np.array_equal(cr[:, :, 2:4], xr[:, :, 2:4]) and np.array_equal(cr[:, :, 6:], xr[:, :, 6:])
+
+
+def test_token_agreement_gate_admits_rare_ties_only():
+    """The GPU tests' greedy-token gate: one tie within the context error passes,
+    a flip on many rows fails."""
+    from gpu_util import assert_tokens_agree
+
+    w = np.array([[1.0, 0.0], [0.0, 1.0]], np.float32)
+    tied = np.array([[1.0, 0.999]], np.float32)
+    assert assert_tokens_agree(np.array([[0.9995, 1.0]], np.float32), tied, w) == 1
+    ref = np.tile(np.array([[1.0, 0.5]], np.float32), (10, 1))
+    assert assert_tokens_agree(ref, ref, w) == 0
+    with pytest.raises(AssertionError):
+        assert_tokens_agree(ref[:, ::-1].copy(), ref, w)  # every row flips

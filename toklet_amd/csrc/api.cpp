@@ -19,6 +19,7 @@
 
 #include "../../include/tokhip.h"
 #include "device.hpp"
+#include "host.hpp"
 
 extern "C" hipError_t tkh_launch_generic(const tkh::Params *p, int dtype, hipStream_t stream,
                                          hipEvent_t start, hipEvent_t stop);
@@ -39,6 +40,11 @@ extern "C" hipError_t tkh_launch_softcap(float *x, int64_t n, float cap, uint32_
 extern "C" hipError_t tkh_launch_fill_u32(uint32_t *p, uint32_t v, hipStream_t stream);
 extern "C" int tkh_decode_max_rows(int dtype, int head_dim);
 extern "C" int tkh_prefill_rows_per_group(void);
+extern "C" int tkh_prefill_max_splits(void);
+extern "C" int tkh_prefill_merge_rows_per_block(int head_dim);
+extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int64_t blocks,
+                                               hipStream_t stream, hipEvent_t start,
+                                               hipEvent_t stop);
 extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim,
                                          int64_t groups, hipStream_t stream, hipEvent_t start,
                                          hipEvent_t stop);
@@ -49,122 +55,7 @@ extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int hea
                                         int keys_per_lane, int waves, int64_t groups,
                                         hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
-namespace {
-
-constexpr int kSlots = 16;
-constexpr int kSlotProblems = 1024;
-// Split-K arrival counters at the head of the workspace (decode kernel).
-constexpr size_t kCounters = 65536;
-constexpr size_t kCounterBytes = kCounters * sizeof(uint32_t);
-
-// ---------------------------------------------------------------- errors
-
-uint32_t fail(tkh_error *err, uint32_t code, const char *tensor, uint64_t index,
-              uint64_t expected, uint64_t actual, const char *fmt, ...) {
-    if (err) {
-        err->code = code;
-        err->index = index;
-        err->expected = expected;
-        err->actual = actual;
-        std::snprintf(err->tensor, sizeof err->tensor, "%s", tensor ? tensor : "");
-        va_list ap;
-        va_start(ap, fmt);
-        std::vsnprintf(err->message, sizeof err->message, fmt, ap);
-        va_end(ap);
-    }
-    return code;
-}
-
-uint32_t ok(tkh_error *err) {
-    if (err) {
-        std::memset(err, 0, sizeof *err);
-    }
-    return TKH_OK;
-}
-
-#define TRY(expr)                          \
-    do {                                   \
-        uint32_t _rc = (expr);             \
-        if (_rc != TKH_OK) return _rc;     \
-    } while (0)
-
-// src/cpu/mod.rs:84-114 restated for the C ABI.
-uint32_t nonzero(uint64_t value, const char *name, tkh_error *err) {
-    if (value == 0) return fail(err, TKH_ZERO_DIMENSION, name, 0, 0, 0, "%s must be nonzero", name);
-    return TKH_OK;
-}
-uint32_t product(uint64_t a, uint64_t b, uint64_t *out, tkh_error *err) {
-    if (__builtin_mul_overflow(a, b, out))
-        return fail(err, TKH_SIZE_OVERFLOW, nullptr, 0, 0, 0, "tensor size arithmetic overflow");
-    return TKH_OK;
-}
-uint32_t add(uint64_t a, uint64_t b, uint64_t *out, tkh_error *err) {
-    if (__builtin_add_overflow(a, b, out))
-        return fail(err, TKH_SIZE_OVERFLOW, nullptr, 0, 0, 0, "tensor size arithmetic overflow");
-    return TKH_OK;
-}
-uint32_t length(const char *tensor, uint64_t actual, uint64_t expected, tkh_error *err) {
-    if (actual != expected)
-        return fail(err, TKH_LENGTH, tensor, 0, expected, actual, "%s length is %llu, expected %llu",
-                    tensor, (unsigned long long)actual, (unsigned long long)expected);
-    return TKH_OK;
-}
-uint32_t invalid(const char *what, tkh_error *err) {
-    return fail(err, TKH_INVALID_PARAMETER, what, 0, 0, 0, "invalid parameter: %s", what);
-}
-uint32_t device_error(hipError_t e, const char *where, tkh_error *err) {
-    return fail(err, TKH_DEVICE, where, 0, 0, 0, "%s: %s", where, hipGetErrorString(e));
-}
-
-#define HIP_TRY(call, where)                                  \
-    do {                                                      \
-        hipError_t _e = (call);                               \
-        if (_e != hipSuccess) return device_error(_e, where, err); \
-    } while (0)
-
-int esize(tkh_dtype dt) { return dt == TKH_F32 ? 4 : 2; }
-bool valid_dtype(uint32_t dt) { return dt <= TKH_BF16; }
-
-int env_int(const char *name, int fallback) {
-    const char *v = std::getenv(name);
-    return v && *v ? std::atoi(v) : fallback;
-}
-
-}  // namespace
-
-// ---------------------------------------------------------------- context
-
-struct tkh_context {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    bool synchronous = true;
-    uint32_t *status_dev = nullptr;
-    uint32_t *status_host = nullptr;
-    uint8_t *workspace = nullptr;
-    size_t workspace_bytes = 0;
-    tkh::Problem *ring_dev = nullptr;
-    tkh::Problem *ring_host = nullptr;
-    hipEvent_t ring_events[kSlots] = {};
-    bool ring_used[kSlots] = {};
-    int ring_next = 0;
-    int split_keys_override = 0;
-    int force_generic = 0;
-    int decode_waves = 8;        // waves per decode workgroup
-    int decode_keys_per_lane = 4;  // keys each lane holds per streamed block
-    int decode_groups = 256;     // target decode workgroups per launch
-    int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
-    int decode_disable = 0;
-    int prefill_groups = 512;    // below this many row-block workgroups, split the keys
-    int prefill_max_splits = 16;
-    int prefill_min_keys = 256;  // keys per split at least
-    // profiling: per launch, start/stop of the attention kernel and of the combine kernel
-    bool profiling = false;
-    std::vector<hipEvent_t> prof_events;
-    std::vector<char> prof_has_combine;
-    size_t prof_used = 0;
-    uint64_t prof_launches = 0;
-    double prof_attention_ms = 0, prof_combine_ms = 0;
-};
+using namespace tkh_host;
 
 namespace {
 
@@ -416,21 +307,26 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
     int64_t sk = (max_span + splits - 1) / splits;
     sk = std::max<int64_t>(32, (sk + 31) / 32 * 32);
     if (ctx->split_keys_override > 0) sk = (ctx->split_keys_override + 31) / 32 * 32;
-    int64_t wgs = 0, slots = 0, counters = 0;
+    // Splits of one row block are combined by a second kernel, in merge blocks
+    // of a few rows; Problem::part_base is the problem's first merge block.
+    const int64_t merge_rows = tkh_prefill_merge_rows_per_block((int)D);
+    int64_t wgs = 0, slots = 0, merge_blocks = 0;
     for (auto &p : group) {
         p.split_keys = (int32_t)std::min<int64_t>(sk, INT32_MAX);
         p.splits = (int32_t)std::max<int64_t>(1, (p.vis_hi - p.vis_lo + sk - 1) / sk);
+        if (p.splits > tkh_prefill_max_splits())
+            return fail(err, TKH_UNSUPPORTED, "batch", 0, tkh_prefill_max_splits(), p.splits,
+                        "prefill key splits exceed the merge limit");
         p.tile_base = wgs;
         p.slot_base = slots;
-        p.group_base = (int32_t)counters;
+        p.part_base = merge_blocks;
         const int64_t g = Hkv * p.row_blocks;
         wgs += g * p.splits;
-        if (p.splits > 1) slots += g * p.splits;
-        counters += g;
+        if (p.splits > 1) {
+            slots += g * p.splits;
+            merge_blocks += g * (rows_per / merge_rows);
+        }
     }
-    if (counters > (int64_t)kCounters)
-        return fail(err, TKH_UNSUPPORTED, "batch", 0, kCounters, counters,
-                    "too many (session, KV head, row block) groups in one call");
     const size_t need = (size_t)slots * rows_per * (D + 2) * sizeof(float);
     if (need > ctx->workspace_bytes)
         return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, ctx->workspace_bytes,
@@ -448,10 +344,15 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
     prm.part_o = ws + (size_t)slots * rows_per * 2;
 
     hipEvent_t *ev = nullptr;
-    if (ctx->profiling) TRY(profile_slot(ctx, &ev, false, err));
+    if (ctx->profiling) TRY(profile_slot(ctx, &ev, merge_blocks > 0, err));
     hipError_t e = tkh_launch_prefill(&prm, (int)plan.dtype, (int)D, wgs, ctx->stream,
                                       ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "prefill launch", err);
+    if (merge_blocks > 0) {
+        e = tkh_launch_prefill_merge(&prm, (int)D, merge_blocks, ctx->stream, ev ? ev[2] : nullptr,
+                                     ev ? ev[3] : nullptr);
+        if (e != hipSuccess) return device_error(e, "prefill merge launch", err);
+    }
     return TKH_OK;
 }
 
@@ -584,7 +485,8 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     ctx->decode_max_splits = std::max(1, env_int("TKH_DECODE_MAX_SPLITS", 64));
     ctx->decode_disable = env_int("TKH_DECODE_DISABLE", 0);
     ctx->prefill_groups = std::max(1, env_int("TKH_PREFILL_GROUPS", 512));
-    ctx->prefill_max_splits = std::max(1, env_int("TKH_PREFILL_MAX_SPLITS", 16));
+    ctx->prefill_max_splits =
+        std::min(tkh_prefill_max_splits(), std::max(1, env_int("TKH_PREFILL_MAX_SPLITS", 16)));
     ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 256));
     auto cleanup = [&](hipError_t e, const char *where) {
         tkh_context_destroy(ctx);
@@ -990,17 +892,6 @@ uint32_t tkh_prefill_batch(tkh_context *ctx, uint64_t batch, uint64_t tokens,
 
 // ---------------------------------------------------------------- KV owners
 
-struct tkh_kv {
-    tkh_context *ctx = nullptr;
-    uint64_t heads = 0, dims = 0, capacity = 0, max_positions = 0;
-    bool has_window = false;
-    uint64_t window = 0;
-    tkh_dtype storage = TKH_BF16;
-    void *k = nullptr;
-    void *v = nullptr;
-    uint64_t offset = 0, generation = 0, owner = 0;
-    uint64_t allocated_bytes = 0;
-};
 
 namespace {
 

@@ -1,0 +1,143 @@
+// host.hpp - host-side internals shared by the C ABI translation units:
+// error reporting in the reference's check order, the context and the KV
+// owner objects behind the opaque handles of include/tokhip.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "../../include/tokhip.h"
+#include "device.hpp"
+
+namespace tkh_host {
+
+inline constexpr int kSlots = 16;
+inline constexpr int kSlotProblems = 1024;
+// Split-K arrival counters at the head of the workspace (decode kernel).
+inline constexpr size_t kCounters = 65536;
+inline constexpr size_t kCounterBytes = kCounters * sizeof(uint32_t);
+
+// ---------------------------------------------------------------- errors
+
+inline uint32_t fail(tkh_error *err, uint32_t code, const char *tensor, uint64_t index,
+              uint64_t expected, uint64_t actual, const char *fmt, ...) {
+    if (err) {
+        err->code = code;
+        err->index = index;
+        err->expected = expected;
+        err->actual = actual;
+        std::snprintf(err->tensor, sizeof err->tensor, "%s", tensor ? tensor : "");
+        va_list ap;
+        va_start(ap, fmt);
+        std::vsnprintf(err->message, sizeof err->message, fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+inline uint32_t ok(tkh_error *err) {
+    if (err) {
+        std::memset(err, 0, sizeof *err);
+    }
+    return TKH_OK;
+}
+
+#define TRY(expr)                          \
+    do {                                   \
+        uint32_t _rc = (expr);             \
+        if (_rc != TKH_OK) return _rc;     \
+    } while (0)
+
+// src/cpu/mod.rs:84-114 restated for the C ABI.
+inline uint32_t nonzero(uint64_t value, const char *name, tkh_error *err) {
+    if (value == 0) return fail(err, TKH_ZERO_DIMENSION, name, 0, 0, 0, "%s must be nonzero", name);
+    return TKH_OK;
+}
+inline uint32_t product(uint64_t a, uint64_t b, uint64_t *out, tkh_error *err) {
+    if (__builtin_mul_overflow(a, b, out))
+        return fail(err, TKH_SIZE_OVERFLOW, nullptr, 0, 0, 0, "tensor size arithmetic overflow");
+    return TKH_OK;
+}
+inline uint32_t add(uint64_t a, uint64_t b, uint64_t *out, tkh_error *err) {
+    if (__builtin_add_overflow(a, b, out))
+        return fail(err, TKH_SIZE_OVERFLOW, nullptr, 0, 0, 0, "tensor size arithmetic overflow");
+    return TKH_OK;
+}
+inline uint32_t length(const char *tensor, uint64_t actual, uint64_t expected, tkh_error *err) {
+    if (actual != expected)
+        return fail(err, TKH_LENGTH, tensor, 0, expected, actual, "%s length is %llu, expected %llu",
+                    tensor, (unsigned long long)actual, (unsigned long long)expected);
+    return TKH_OK;
+}
+inline uint32_t invalid(const char *what, tkh_error *err) {
+    return fail(err, TKH_INVALID_PARAMETER, what, 0, 0, 0, "invalid parameter: %s", what);
+}
+inline uint32_t device_error(hipError_t e, const char *where, tkh_error *err) {
+    return fail(err, TKH_DEVICE, where, 0, 0, 0, "%s: %s", where, hipGetErrorString(e));
+}
+
+#define HIP_TRY(call, where)                                  \
+    do {                                                      \
+        hipError_t _e = (call);                               \
+        if (_e != hipSuccess) return device_error(_e, where, err); \
+    } while (0)
+
+inline int esize(tkh_dtype dt) { return dt == TKH_F32 ? 4 : 2; }
+inline bool valid_dtype(uint32_t dt) { return dt <= TKH_BF16; }
+
+inline int env_int(const char *name, int fallback) {
+    const char *v = std::getenv(name);
+    return v && *v ? std::atoi(v) : fallback;
+}
+
+}  // namespace tkh_host
+using namespace tkh_host;
+
+// ---------------------------------------------------------------- context
+
+struct tkh_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool synchronous = true;
+    uint32_t *status_dev = nullptr;
+    uint32_t *status_host = nullptr;
+    uint8_t *workspace = nullptr;
+    size_t workspace_bytes = 0;
+    tkh::Problem *ring_dev = nullptr;
+    tkh::Problem *ring_host = nullptr;
+    hipEvent_t ring_events[kSlots] = {};
+    bool ring_used[kSlots] = {};
+    int ring_next = 0;
+    int split_keys_override = 0;
+    int force_generic = 0;
+    int decode_waves = 8;        // waves per decode workgroup
+    int decode_keys_per_lane = 4;  // keys each lane holds per streamed block
+    int decode_groups = 256;     // target decode workgroups per launch
+    int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
+    int decode_disable = 0;
+    int prefill_groups = 512;    // below this many row-block workgroups, split the keys
+    int prefill_max_splits = 16;
+    int prefill_min_keys = 256;  // keys per split at least
+    // profiling: per launch, start/stop of the attention kernel and of the combine kernel
+    bool profiling = false;
+    std::vector<hipEvent_t> prof_events;
+    std::vector<char> prof_has_combine;
+    size_t prof_used = 0;
+    uint64_t prof_launches = 0;
+    double prof_attention_ms = 0, prof_combine_ms = 0;
+};
+
+struct tkh_kv {
+    tkh_context *ctx = nullptr;
+    uint64_t heads = 0, dims = 0, capacity = 0, max_positions = 0;
+    bool has_window = false;
+    uint64_t window = 0;
+    tkh_dtype storage = TKH_BF16;
+    void *k = nullptr;
+    void *v = nullptr;
+    uint64_t offset = 0, generation = 0, owner = 0;
+    uint64_t allocated_bytes = 0;
+};

@@ -25,8 +25,9 @@
 //  * Workgroups are mapped XCD-major (dispatch slot b runs on XCD b % 8) so
 //    the row blocks of one (problem, KV head) sit on one XCD and share its
 //    L2 for the K/V stream.
-//  * Split-K partials (max, mass, unnormalised context) use device-coherent
-//    stores; the last workgroup of a row block to arrive merges them.
+//  * Split-K partials (max, mass, unnormalised context) go to the workspace
+//    and a second, fully parallel kernel (attn_prefill_merge) combines them,
+//    so no single workgroup reads a whole row block's partials.
 #include <type_traits>
 
 #include "device.hpp"
@@ -155,7 +156,6 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
 
     __shared__ __attribute__((aligned(16))) uint8_t lds_raw[PrefillLds<D>::bytes];
-    __shared__ int lds_last;
     lds_ptr<uint8_t> lds = (lds_ptr<uint8_t>)lds_raw;
 
     const int wave = threadIdx.x >> 6;
@@ -494,56 +494,95 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     }
 
     // ---- split-K partial: slot (row block, split) holds PF_ROWS x (D + 2)
+    // floats, merged by attn_prefill_merge after this kernel.
+    raise_status(p, bad, ST_NONFINITE_INPUT);
     const int64_t group = (int64_t)kvh * pr->row_blocks + rb;
     const int64_t slot = pr->slot_base + group * pr->splits + split;
-    {
-        float *po = p.part_o + (slot * PF_ROWS + wave * 32 + j) * D;
-        for (int mb = 0; mb < MB; ++mb)
-            for (int q = 0; q < 4; ++q)
-                for (int r = 0; r < 4; ++r) coherent_store(po + 32 * mb + 8 * q + 4 * h + r, acc[mb][4 * q + r]);
-        if (h == 0) {
-            coherent_store(p.part_ml + (slot * PF_ROWS + wave * 32 + j) * 2, m_run);
-            coherent_store(p.part_ml + (slot * PF_ROWS + wave * 32 + j) * 2 + 1, l_run);
+    float *po = p.part_o + (slot * PF_ROWS + wave * 32 + j) * D;
+    for (int mb = 0; mb < MB; ++mb)
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 v = {acc[mb][4 * q], acc[mb][4 * q + 1], acc[mb][4 * q + 2], acc[mb][4 * q + 3]};
+            *gstore_ptr<f32x4>(po + 32 * mb + 8 * q + 4 * h) = v;
         }
+    if (h == 0) {
+        const f32x2 ml = {m_run, l_run};
+        *gstore_ptr<f32x2>(p.part_ml + (slot * PF_ROWS + wave * 32 + j) * 2) = ml;
     }
-    raise_status(p, bad, ST_NONFINITE_INPUT);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    uint32_t *counter = p.counters + pr->group_base + group;
-    if (threadIdx.x == 0)
-        lds_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   (uint32_t)(pr->splits - 1);
-    __syncthreads();
-    if (!lds_last) return;
+}
 
-    // ---- merge: thread per (row, 4 features); splits read in batches.
-    const int S = pr->splits;
-    const int64_t slot0 = pr->slot_base + group * pr->splits;
-    constexpr int F4 = D / 4;
-    for (int i = threadIdx.x; i < PF_ROWS * F4; i += 64 * PF_WAVES) {
-        const int r = i / F4, f = (i % F4) * 4;
-        const int prow = rb * PF_ROWS + r;
-        if (prow >= m_kv) continue;
-        float M = NEG_INF;
-        for (int sp = 0; sp < S; ++sp) M = fmaxf(M, coherent_load(p.part_ml + ((slot0 + sp) * PF_ROWS + r) * 2));
-        const float mbase = M == NEG_INF ? 0.0f : M;
-        float L = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int sp = 0; sp < S; ++sp) {
-            const int64_t srow = (slot0 + sp) * PF_ROWS + r;
-            const float w = __builtin_amdgcn_exp2f(coherent_load(p.part_ml + srow * 2) - mbase);
-            L += w * coherent_load(p.part_ml + srow * 2 + 1);
-            for (int e = 0; e < 4; ++e) o[e] += w * coherent_load(p.part_o + srow * D + f + e);
+// Merge of the split-K partials of attn_prefill.  Merge block b covers
+// PF_MERGE_ROWS packed rows of one (problem, KV head, row block); each thread
+// owns four features of one row and reads the S partials of its row at once
+// (one round trip): m and l of every split, then the weighted sum of the
+// unnormalised contexts.  Problem::part_base is the problem's first merge block.
+template <int D>
+__global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t blocks) {
+    constexpr int TPR = D / 4;                  // threads per row
+    constexpr int RPB = 256 / TPR;              // rows per merge block
+    constexpr int MAXS = 16;
+    const int64_t b = blockIdx.x;
+    if (b >= blocks) return;
+    const_ptr<Problem> pr;
+    if (p.nproblems == 1) {
+        pr = &((const_ptr<Params>)__builtin_amdgcn_kernarg_segment_ptr())->single;
+    } else {
+        const_ptr<Problem> probs = (const_ptr<Problem>)p.problems;
+        int lo = 0, hi = p.nproblems - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (probs[mid].part_base <= b) lo = mid; else hi = mid - 1;
         }
-        bad_mass |= !(L > 0.0f) || !is_finite_f(L);
-        const int t = prow / G, hh = kvh * G + prow % G;
-        f32x4 v;
-        for (int e = 0; e < 4; ++e) {
-            v[e] = o[e] / L;
-            bad_out |= !is_finite_f(v[e]);
-        }
-        *gstore_ptr<f32x4>(pr->out + ((int64_t)t * Hq + hh) * D + f) = v;
+        pr = probs + lo;
     }
-    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int G = p.group, Hq = p.query_heads;
+    const int m_kv = pr->queries * G;
+    const int64_t local = b - pr->part_base;
+    const int blocks_per_rb = PF_ROWS / RPB;
+    const int64_t group = local / blocks_per_rb;          // kvh * row_blocks + rb
+    const int kvh = (int)(group / pr->row_blocks), rb = (int)(group % pr->row_blocks);
+    const int r = (int)(local % blocks_per_rb) * RPB + (int)(threadIdx.x / TPR);
+    const int f = (int)(threadIdx.x % TPR) * 4;
+    const int prow = rb * PF_ROWS + r;
+    if (prow >= m_kv) return;
+    const int S = pr->splits;
+    const int64_t slot0 = pr->slot_base + group * S;
+
+    f32x2 ml[MAXS];
+    f32x4 po[MAXS];
+#pragma unroll
+    for (int sp = 0; sp < MAXS; ++sp) {
+        if (sp < S) {
+            const int64_t srow = (slot0 + sp) * PF_ROWS + r;
+            ml[sp] = *gload_ptr<f32x2>(p.part_ml + srow * 2);
+            po[sp] = *gload_ptr<f32x4>(p.part_o + srow * D + f);
+        }
+    }
+    float M = NEG_INF;
+#pragma unroll
+    for (int sp = 0; sp < MAXS; ++sp)
+        if (sp < S) M = fmaxf(M, ml[sp][0]);
+    const float mbase = M == NEG_INF ? 0.0f : M;
+    const float tmul = p.softcap != 0.0f ? 1.0f : p.scale_log2;
+    float L = 0.0f;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int sp = 0; sp < MAXS; ++sp) {
+        if (sp < S) {
+            const float w = ml[sp][0] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f((ml[sp][0] - mbase) * tmul);
+            L += w * ml[sp][1];
+            for (int e = 0; e < 4; ++e) o[e] += w * po[sp][e];
+        }
+    }
+    const bool bad_mass = !(L > 0.0f) || !is_finite_f(L);
+    const float inv = 1.0f / L;
+    bool bad_out = false;
+    f32x4 v;
+    for (int e = 0; e < 4; ++e) {
+        v[e] = o[e] * inv;
+        bad_out |= !is_finite_f(v[e]);
+    }
+    const int t = prow / G, hh = kvh * G + prow % G;
+    *gstore_ptr<f32x4>(pr->out + ((int64_t)t * Hq + hh) * D + f) = v;
     raise_status(p, bad_mass, ST_BAD_MASS);
     raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
 }
@@ -551,6 +590,23 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
 }  // namespace tkh
 
 extern "C" int tkh_prefill_rows_per_group(void) { return tkh::PF_ROWS; }
+extern "C" int tkh_prefill_max_splits(void) { return 16; }
+extern "C" int tkh_prefill_merge_rows_per_block(int head_dim) { return 256 / (head_dim / 4); }
+
+extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int64_t blocks,
+                                               hipStream_t stream, hipEvent_t start,
+                                               hipEvent_t stop) {
+    using namespace tkh;
+    dim3 grid((unsigned)blocks), block(256);
+    if (head_dim == 64)
+        hipExtLaunchKernelGGL((attn_prefill_merge<64>), grid, block, 0, stream, start, stop, 0, *p, blocks);
+    else if (head_dim == 128)
+        hipExtLaunchKernelGGL((attn_prefill_merge<128>), grid, block, 0, stream, start, stop, 0, *p, blocks);
+    else if (head_dim == 256)
+        hipExtLaunchKernelGGL((attn_prefill_merge<256>), grid, block, 0, stream, start, stop, 0, *p, blocks);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
 
 extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim,
                                          int64_t groups, hipStream_t stream, hipEvent_t start,
