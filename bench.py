@@ -66,46 +66,40 @@ def qk_producer(torch, x, weight, positions, theta):
 
 
 class C2:
-    """Qwen3-shaped single session."""
+    """Qwen3-shaped single session driven through the native session:
+    per chunk and layer, the producer (per-head RMSNorm, rotary 1e6, bf16 rounding,
+    K/V append) and the attention kernel, issued by tkh_session_evaluate."""
     hq, hkv, d = 16, 8, 128
     prefill, chunk, decode = 2048, 128, 256
 
-    def __init__(self, torch, ops, kvmod, ctx, seed=1234):
-        self.torch, self.ops, self.ctx = torch, ops, ctx
+    def __init__(self, torch, ops, sessmod, ctx, seed=1234):
+        self.torch, self.ops, self.ctx, self.sessmod = torch, ops, ctx, sessmod
         g = torch.Generator(device="cuda").manual_seed(seed)
         total = self.prefill + self.decode
         self.total = total
-        pos = torch.arange(total, device="cuda")
-        wq = 1.0 + 0.02 * torch.randn(self.d, generator=g, device="cuda")
-        wk = 1.0 + 0.02 * torch.randn(self.d, generator=g, device="cuda")
-        q = torch.randn(total, self.hq, self.d, generator=g, device="cuda")
-        k = torch.randn(total, self.hkv, self.d, generator=g, device="cuda")
-        v = torch.randn(total, self.hkv, self.d, generator=g, device="cuda")
-        self.q = qk_producer(torch, q, wq, pos, 1e6).to(torch.bfloat16).contiguous()
-        self.k = qk_producer(torch, k, wk, pos, 1e6).to(torch.bfloat16).contiguous()
-        self.v = v.to(torch.bfloat16).contiguous()
-        self.layer = kvmod.LayerKv(ctx, self.hkv, self.d, total, torch.bfloat16)
+        # Projections (the producer's inputs) resident in HBM, N(0, 1); norm weights N(1, 0.02).
+        self.q_proj = torch.randn(total, self.hq, self.d, generator=g, device="cuda")
+        self.k_proj = torch.randn(total, self.hkv, self.d, generator=g, device="cuda")
+        self.v_proj = torch.randn(total, self.hkv, self.d, generator=g, device="cuda")
+        self.wq = 1.0 + 0.02 * torch.randn(self.d, generator=g, device="cuda")
+        self.wk = 1.0 + 0.02 * torch.randn(self.d, generator=g, device="cuda")
         self.out = torch.zeros(total, self.hq * self.d, dtype=torch.float32, device="cuda")
-        self.shape = ops.CachedAttentionShape
+        self.session = sessmod.Session(ctx, sessmod.Options(
+            capacity=total, prefill_chunk_size=self.chunk, vocab_size=151936, layers=1,
+            query_heads=self.hq, kv_heads=self.hkv, head_dim=self.d, storage="bf16",
+            norm_epsilon=1e-6, theta=1e6))
+        self.io = [sessmod.LayerIo(self.q_proj, self.k_proj, self.v_proj, self.out, self.wq,
+                                   self.wk)]
+        self.tokens = torch.randint(0, 151936, (total,), generator=torch.Generator().manual_seed(seed)).tolist()
 
     def run_prefill(self):
-        ops, layer = self.ops, self.layer
-        kbuf, vbuf = layer.committed()
-        for start in range(0, self.prefill, self.chunk):
-            n = self.chunk
-            layer.append(self.k[start:start + n], self.v[start:start + n], start)
-            ops.attention_cached(self.ctx, self.q[start:start + n], kbuf, vbuf,
-                                 self.out[start:start + n], None, None,
-                                 self.shape(n, self.hq, self.hkv, self.d, self.total, start))
+        self.session.reset()
+        self.session.set_tokens(self.tokens[:self.prefill])
+        self.session.evaluate(self.io)
 
     def run_decode(self):
-        ops, layer = self.ops, self.layer
-        kbuf, vbuf = layer.committed()
-        for start in range(self.prefill, self.total):
-            layer.append(self.k[start:start + 1], self.v[start:start + 1], start)
-            ops.attention_cached(self.ctx, self.q[start:start + 1], kbuf, vbuf,
-                                 self.out[start:start + 1], None, None,
-                                 self.shape(1, self.hq, self.hkv, self.d, self.total, start))
+        self.session.append(self.tokens[self.prefill:])
+        self.session.evaluate(self.io, chunk_limit=1)
 
     def prefill_flops(self):
         pairs = sum(sum(start + t + 1 for t in range(self.chunk))
@@ -134,24 +128,38 @@ def time_region(torch, fn, steps, warmup):
     return start.elapsed_time(end) / 1e3, wall
 
 
-def bench_c2(torch, ops, kvmod, ctx, steps, warmup):
-    w = C2(torch, ops, kvmod, ctx)
-    log("c2: qwen3 16/8/128 bf16, prefill 2048 in 128-token chunks + 256 decode steps")
-    # whole-job step timing
+def bench_c2(torch, ops, sessmod, ctx, steps, warmup):
+    w = C2(torch, ops, sessmod, ctx)
+    log("c2: qwen3 16/8/128 bf16, prefill 2048 in 128-token chunks + 256 decode steps "
+        "(native session: producer + attention per chunk)")
+
     def step():
         w.run_prefill()
         w.run_decode()
+        w.session.synchronize()
     job_s, job_wall = time_region(torch, step, steps, warmup)
-    ctx.synchronize()
-    # phase timing (same calls), with the kernel profile of each phase
-    ctx.profile(True)
-    pre_s, _ = time_region(torch, w.run_prefill, steps, 0)
-    pre_prof = ctx.profile_read()
-    ctx.profile(True)
-    dec_s, _ = time_region(torch, w.run_decode, steps, 0)
-    dec_prof = ctx.profile_read()
+    # Phase timing (same calls), with the attention kernels' dispatch-recorded events.
+    pre_s = dec_s = 0.0
+    pre_prof = {"attention_ms": 0.0, "combine_ms": 0.0, "launches": 0}
+    dec_prof = dict(pre_prof)
+    for _ in range(steps):
+        ctx.profile(True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        w.run_prefill()
+        w.session.synchronize()
+        pre_s += time.perf_counter() - t0
+        p = ctx.profile_read()
+        ctx.profile(True)
+        t0 = time.perf_counter()
+        w.run_decode()
+        w.session.synchronize()
+        dec_s += time.perf_counter() - t0
+        d = ctx.profile_read()
+        for acc, src in ((pre_prof, p), (dec_prof, d)):
+            for k in acc:
+                acc[k] += src[k]
     ctx.profile(False)
-    ctx.synchronize()
     flops = w.prefill_flops()
     dbytes = w.decode_bytes()
     res = {
@@ -164,6 +172,7 @@ def bench_c2(torch, ops, kvmod, ctx, steps, warmup):
         "prefill_merge_us": pre_prof["combine_ms"] / max(1, pre_prof["launches"]) * 1e3,
         "decode_ms": dec_s / steps * 1e3,
         "decode_gbs": dbytes * steps / dec_s / 1e9,
+        "decode_us_per_token": dec_s / steps / w.decode * 1e6,
         "decode_kernel_us": dec_prof["attention_ms"] / dec_prof["launches"] * 1e3,
         "decode_combine_us": dec_prof["combine_ms"] / dec_prof["launches"] * 1e3,
         "decode_kernel_gbs": dbytes * steps / (dec_prof["attention_ms"] / 1e3) / 1e9,
@@ -304,28 +313,47 @@ def measured_traffic(key):
 
 
 def cpu_baseline(w, torch):
-    """The oracle (single thread, FP64 softmax) on the C2 decode phase: 32 of 256 steps."""
+    """The reference's CPU path for configs[1]'s decode steps, restated by the oracle
+    (single thread): per step rmsnorm + rotary of the new Q/K rows (FP64), append into
+    FP32 head-major caches (the reference's CPU storage), attention_cached (FP32 dot,
+    FP64 softmax).  32 of the 256 steps, after an untimed 2048-token prefix."""
     import numpy as np
 
     import oracle
 
     oracle.lib()
-    hq, hkv, d, cap = w.hq, w.hkv, w.d, w.total
-    k = w.layer.committed()[0].float().cpu().numpy()
-    v = w.layer.committed()[1].float().cpu().numpy()
-    q = w.q.float().cpu().numpy().reshape(w.total, -1)
+    hq, hkv, d, cap, pre = w.hq, w.hkv, w.d, w.total, w.prefill
+    qp = w.q_proj.cpu().numpy()
+    kp = w.k_proj.cpu().numpy()
+    vp = w.v_proj.cpu().numpy()
+    wq = w.wq.cpu().numpy()
+    wk = w.wk.cpu().numpy()
+
+    def produce(x, wt, t0, n, heads):
+        y = oracle.rmsnorm(x[t0:t0 + n].reshape(-1), wt, n * heads, d, 1e-6)
+        return oracle.rotary(y, n, heads, d, t0, 1e6).reshape(n, heads, d)
+
+    kc = np.zeros((hkv, cap, d), np.float32)
+    vc = np.zeros((hkv, cap, d), np.float32)
+    kc[:, :pre] = produce(kp, wk, 0, pre, hkv).transpose(1, 0, 2)
+    vc[:, :pre] = vp[:pre].transpose(1, 0, 2)
     steps = 32
-    positions = list(range(w.prefill, w.prefill + steps))
+    positions = list(range(pre, pre + steps))
     t0 = time.perf_counter()
     for p in positions:
-        oracle.attention_cached(q[p], k, v, 1, hq, hkv, d, cap, p)
+        q = produce(qp, wq, p, 1, hq)
+        kc[:, p] = produce(kp, wk, p, 1, hkv)[0]
+        vc[:, p] = vp[p]
+        oracle.attention_cached(q.reshape(-1), kc, vc, 1, hq, hkv, d, cap, p)
     dt = time.perf_counter() - t0
     nbytes = sum(w.decode_bytes_per_step(p + 1) for p in positions)
     return {
         "value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": f"C2 decode, 1 layer, {steps} of 256 steps (context {positions[0] + 1}..{positions[-1] + 1}), "
-                  f"oracle attention_cached (FP32 dot, FP64 softmax), {dt:.2f} s",
+        "sample": f"configs[1] decode, 1 layer, {steps} of 256 steps (context {positions[0] + 1}.."
+                  f"{positions[-1] + 1}): oracle rmsnorm + rotary + append + attention_cached "
+                  f"(FP32 KV, FP64 softmax), {dt:.2f} s; bytes counted as the GPU's bf16 bytes",
         "seconds": dt,
+        "us_per_token": dt / steps * 1e6,
         "host_cpus": os.cpu_count(),
     }
 
@@ -338,8 +366,8 @@ def main():
         sys.exit(2)
     import torch
 
-    from toklet_amd import kv as kvmod
     from toklet_amd import ops
+    from toklet_amd import session as sessmod
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     if args.only == "copy":
@@ -349,7 +377,7 @@ def main():
     result = {}
     w = None
     if args.only in (None, "c2"):
-        c2, w = bench_c2(torch, ops, kvmod, ctx, args.steps, args.warmup)
+        c2, w = bench_c2(torch, ops, sessmod, ctx, args.steps, args.warmup)
         log(json.dumps(c2))
         result["c2"] = c2
     if not args.no_north_star and args.only in (None, "d8k"):
@@ -393,6 +421,7 @@ def main():
         "prefill_frac_mfma": round(c2["prefill_tflops"] / PEAK_BF16_TFLOPS, 5),
         "decode_frac_hbm": round(c2["decode_gbs"] / PEAK_HBM_GBS, 5),
         "tokens_per_s": round(c2["tokens_per_s"], 1),
+        "decode_us_per_token": round(c2["decode_us_per_token"], 3),
         "roofline": {
             "bound": "hbm",
             "kernel": "attn_decode<bf16, D=128, 2 rows> (the 256 decode launches of configs[1])",

@@ -272,6 +272,126 @@ uint32_t tkh_kv_commit_batch(tkh_kv *const *kvs, const tkh_kv_frame *frames, uin
 /* reset_batch (src/model/window_cache.rs:342-350): offset 0, new generation. */
 uint32_t tkh_kv_reset_batch(tkh_kv *const *kvs, uint64_t count, tkh_error *err);
 
+/* ---------------- producer (the step before attention) ---------------- */
+
+/* Rotary variants: none, Qwen split-half (src/cpu/attention.rs:10-64) and
+ * proportional (src/cpu/proportional_rotary.rs:32-91). */
+typedef enum tkh_rotary { TKH_ROTARY_NONE = 0, TKH_ROTARY_SPLIT_HALF = 1, TKH_ROTARY_PROPORTIONAL = 2 } tkh_rotary;
+
+/* Per-layer producer of Model::run (src/model/mod.rs:611-662): optional
+ * per-head RMSNorm of Q and K (cpu::rmsnorm, src/cpu/reductions.rs:8-49,
+ * FP64), then rotary at absolute positions position..position+tokens-1. */
+typedef struct tkh_producer_shape {
+    uint64_t tokens, query_heads, kv_heads, head_dim;
+    uint64_t position;
+    float norm_epsilon;  /* used when norm weights are given */
+    uint32_t rotary;     /* tkh_rotary */
+    float theta;         /* split-half theta, or proportional base */
+    uint64_t rotated_dims; /* proportional only */
+    float factor;          /* proportional only */
+} tkh_producer_shape;
+
+/* Replaces the rmsnorm -> rotary -> LayerKv::append sequence of Model::run
+ * for one layer and chunk, fused into one launch (no reference counterpart
+ * as a single call).  q/k/v_proj: device FP32 token-major [tokens, H, D].
+ * q_norm/k_norm: device FP32 [D] or NULL (no norm).  q_out: [tokens, Hq, D]
+ * in `dtype`; k_out/v_out: element (h, t, d) at h*out_head_stride + t*D + d
+ * in `dtype` (a cache's rows at an offset: base + offset*D, stride
+ * capacity*D).  Non-finite inputs or results: TKH_NON_FINITE at the next
+ * status check (synchronous contexts: on return). */
+uint32_t tkh_produce_qkv(tkh_context *ctx, const tkh_producer_shape *shape, tkh_dtype dtype,
+                         const float *q_proj, const float *k_proj, const float *v_proj,
+                         const float *q_norm, const float *k_norm, void *q_out, void *k_out,
+                         void *v_out, uint64_t out_head_stride, tkh_error *err);
+
+/* ---------------- session (src/session.rs) ---------------- */
+
+typedef struct tkh_session tkh_session;
+
+/* Options of session::Options (src/session.rs:38-62) plus the attention
+ * geometry the session's KV owners need.  layer_windows (per layer, 0 = full
+ * retention) select ring caches for sliding layers (WindowKvCache).
+ * score_scale 0 selects attention_cached semantics (dot / sqrt(D), no
+ * softcap) for full layers; otherwise every layer uses window/span semantics
+ * with this scale and the optional score softcap. */
+typedef struct tkh_session_options {
+    uint64_t capacity;
+    uint64_t prefill_chunk_size;
+    uint64_t position_offset;
+    uint64_t vocab_size;      /* token admission (Session::validate) */
+    uint64_t layers, query_heads, kv_heads, head_dim;
+    tkh_dtype storage;
+    float score_scale;
+    float softcap;
+    float norm_epsilon;
+    uint32_t rotary;          /* tkh_rotary */
+    float theta;
+    uint64_t rotated_dims;
+    float factor;
+} tkh_session_options;
+
+/* Session::new (src/session.rs:205-245): validates, then allocates every
+ * device buffer the session will use (KV owners, Q scratch, ring staging).
+ * ctx may be NULL: a host-only session that runs the token state machine
+ * alone (evaluation commits state and computes nothing), for planning and
+ * for testing transitions without a device. */
+uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_options *options,
+                            const uint64_t *layer_windows, tkh_session **out, tkh_error *err);
+void tkh_session_destroy(tkh_session *s);
+
+/* Session::append / set_tokens (src/session.rs:320-356). */
+uint32_t tkh_session_append(tkh_session *s, const uint32_t *tokens, uint64_t count,
+                            tkh_error *err);
+uint32_t tkh_session_set_tokens(tkh_session *s, const uint32_t *tokens, uint64_t count,
+                                tkh_error *err);
+/* Session::discard_pending / reset (src/session.rs:428-446). */
+void tkh_session_discard_pending(tkh_session *s);
+void tkh_session_reset(tkh_session *s);
+
+typedef struct tkh_session_state {
+    uint64_t history_len, evaluated_len, pending_len, capacity;
+    uint32_t distribution_valid; /* Session::logits().is_some() */
+    uint64_t kv_bytes, scratch_bytes;
+} tkh_session_state;
+uint32_t tkh_session_state_get(const tkh_session *s, tkh_session_state *out);
+/* Copies min(capacity_tokens, history_len) tokens of Session::history(). */
+uint64_t tkh_session_history(const tkh_session *s, uint32_t *tokens, uint64_t capacity_tokens);
+
+/* Tokens the next chunk evaluates: positions [start, start + count) of the
+ * history, count = min(pending, prefill_chunk_size) (src/session.rs:384). */
+uint32_t tkh_session_next_chunk(const tkh_session *s, uint64_t *start, uint64_t *count);
+
+/* One layer's inputs for a chunk.  Projections are device FP32 token-major
+ * [rows, H, D]; context receives [rows, Hq, D] FP32.  `rows` start at the
+ * chunk's first token (chunk-relative) in tkh_session_evaluate_next_chunk and
+ * at session position 0 in tkh_session_evaluate. */
+typedef struct tkh_layer_io {
+    const float *q_proj, *k_proj, *v_proj;
+    const float *q_norm, *k_norm; /* [D] or NULL */
+    float *context;
+} tkh_layer_io;
+
+/* Session::evaluate_next_chunk (src/session.rs:364-418) for the attention
+ * path: per layer, produce Q/K/V, stage or append K/V, attend; then commit
+ * every layer (ring frames and evaluated_len) together.  With a synchronous
+ * context the status word is checked before the commit and a failure leaves
+ * the committed prefix and the pending history as they were.  With a queued
+ * context the commit is provisional until tkh_session_synchronize.
+ * *count receives the evaluated token count (0 when nothing is pending). */
+uint32_t tkh_session_evaluate_next_chunk(tkh_session *s, const tkh_layer_io *layers,
+                                         uint64_t *count, tkh_error *err);
+
+/* Session::evaluate (src/session.rs:420-423) with a per-call chunk limit
+ * (<= prefill_chunk_size; 1 evaluates pending tokens one decode step at a
+ * time): every pending token, with position-indexed layer inputs. */
+uint32_t tkh_session_evaluate(tkh_session *s, const tkh_layer_io *layers, uint64_t chunk_limit,
+                              uint64_t *evaluated, tkh_error *err);
+
+/* Waits for queued chunks and checks the status word.  On failure the
+ * session returns to the last checked prefix (sessions with sliding layers
+ * check every chunk and never hold provisional commits). */
+uint32_t tkh_session_synchronize(tkh_session *s, tkh_error *err);
+
 #ifdef __cplusplus
 }
 #endif

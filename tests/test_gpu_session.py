@@ -1,0 +1,266 @@
+"""GPU parity of the producer (RMSNorm -> rotary -> cache rounding) and of the
+session driver (tkh_session) against the CPU oracle.
+
+The producer is compared with the oracle's rmsnorm and rotary on the same FP32
+projections; the session's per-layer contexts with full-prefix attention over
+the oracle-produced (and cache-rounded) Q/K/V, which is what the reference's
+session equals (tests/session.rs:262-306, src/cpu/attention.rs:194-195).
+"""
+
+import numpy as np
+import pytest
+
+from gpu_util import TOL_HALF, host, log, max_err, stored
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from toklet_amd import ops
+
+    return ops
+
+
+@pytest.fixture(scope="module")
+def sess_mod():
+    from toklet_amd import session
+
+    return session
+
+
+@pytest.fixture(scope="module")
+def ctx(torch_mod, ops):
+    return ops.Context(0)
+
+
+def _t(torch, a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to("cuda")
+    return t if dtype is None else t.to(dtype)
+
+
+def _oracle_produce(orc, x, w, tokens, heads, D, position, *, eps=1e-6, rotary="split",
+                    theta=1e6, rotated=0, factor=1.0):
+    y = orc.rmsnorm(x.reshape(-1), w, tokens * heads, D, eps) if w is not None else x.reshape(-1)
+    if rotary == "split":
+        y = orc.rotary(y, tokens, heads, D, position, theta)
+    elif rotary == "proportional":
+        y = orc.proportional_rotary(y, tokens, heads, D, rotated, position, theta, factor)
+    return y.reshape(tokens, heads, D)
+
+
+def _ulp_diff_f32(a, b):
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ai - bi)
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_producer_qwen3_norm_rotary_f32(torch_mod, ctx, ops, orc, norm):
+    """FP32 outputs against the oracle within 1 ulp (FP64 sum order and device
+    sin/cos/pow may move a rounding tie); V copied exactly; K/V head-major."""
+    torch = torch_mod
+    rng = np.random.default_rng(1)
+    T, hq, hkv, D, pos, cap = 37, 16, 8, 128, 2000, 64
+    q = rng.standard_normal((T, hq, D)).astype(np.float32) * 3
+    k = rng.standard_normal((T, hkv, D)).astype(np.float32) * 3
+    v = rng.standard_normal((T, hkv, D)).astype(np.float32)
+    wq = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32) if norm else None
+    wk = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32) if norm else None
+    qo = torch.zeros(T * hq * D, dtype=torch.float32, device="cuda")
+    kc = torch.full((hkv, cap, D), np.nan, dtype=torch.float32, device="cuda")
+    vc = torch.full((hkv, cap, D), np.nan, dtype=torch.float32, device="cuda")
+    off = 9
+    ops.produce_qkv(ctx, ops.ProducerShape(T, hq, hkv, D, pos), _t(torch, q), _t(torch, k),
+                    _t(torch, v), _t(torch, wq) if norm else None, _t(torch, wk) if norm else None,
+                    qo, kc[:, off:], vc[:, off:], cap * D)
+    rq = _oracle_produce(orc, q, wq, T, hq, D, pos)
+    rk = _oracle_produce(orc, k, wk, T, hkv, D, pos)
+    gq = host(qo).reshape(T, hq, D)
+    gk = host(kc)[:, off:off + T].transpose(1, 0, 2)
+    gv = host(vc)[:, off:off + T].transpose(1, 0, 2)
+    for name, g, r in (("q", gq, rq), ("k", gk, rk)):
+        u = _ulp_diff_f32(g, r)
+        log(f"{name}: exact {np.mean(u == 0):.6f}, max ulp {u.max()}")
+        assert u.max() <= 1 and np.mean(u == 0) > 0.999
+    assert np.array_equal(gv, v)
+    assert np.isnan(host(kc)[:, :off]).all() and np.isnan(host(kc)[:, off + T:]).all()
+
+
+def test_producer_proportional_partial_bf16(torch_mod, ctx, ops, orc):
+    """Gemma geometry (8/4/256), proportional rotary on 64 of 256 features, bf16 outputs:
+    equal to the oracle's FP32 result rounded once, up to one bf16 ulp at ties."""
+    torch = torch_mod
+    rng = np.random.default_rng(2)
+    T, hq, hkv, D, pos = 20, 8, 4, 256, 4000
+    q = rng.standard_normal((T, hq, D)).astype(np.float32)
+    k = rng.standard_normal((T, hkv, D)).astype(np.float32)
+    v = rng.standard_normal((T, hkv, D)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    qo = torch.zeros(T * hq * D, dtype=torch.bfloat16, device="cuda")
+    ko = torch.zeros(hkv * T * D, dtype=torch.bfloat16, device="cuda")
+    vo = torch.zeros(hkv * T * D, dtype=torch.bfloat16, device="cuda")
+    shape = ops.ProducerShape(T, hq, hkv, D, pos, 1e-6, ops.ROTARY_PROPORTIONAL, 1e6, 64, 8.0)
+    ops.produce_qkv(ctx, shape, _t(torch, q), _t(torch, k), _t(torch, v), _t(torch, w), _t(torch, w),
+                    qo, ko, vo, T * D)
+    rq = stored(_oracle_produce(orc, q, w, T, hq, D, pos, rotary="proportional", rotated=64, factor=8.0), "bf16")
+    rk = stored(_oracle_produce(orc, k, w, T, hkv, D, pos, rotary="proportional", rotated=64, factor=8.0), "bf16")
+    gq = host(qo).reshape(T, hq, D)
+    gk = host(ko).reshape(hkv, T, D).transpose(1, 0, 2)
+    for g, r in ((gq, rq), (gk, rk)):
+        d = np.abs(g - r)
+        assert np.mean(d == 0) > 0.999
+        assert np.all(d <= np.abs(r) * 2.0 ** -7 + 1e-30)
+    assert np.array_equal(host(vo).reshape(hkv, T, D).transpose(1, 0, 2), stored(v, "bf16"))
+
+
+def test_producer_nonfinite_input_reports(torch_mod, ctx, ops):
+    torch = torch_mod
+    T, hq, hkv, D = 2, 2, 1, 64
+    q = np.ones((T, hq, D), np.float32)
+    q[1, 1, 5] = np.inf
+    k = np.ones((T, hkv, D), np.float32)
+    v = np.ones((T, hkv, D), np.float32)
+    out = [torch.zeros(n, dtype=torch.float32, device="cuda") for n in (T * hq * D, T * hkv * D, T * hkv * D)]
+    with pytest.raises(ops.TkhError) as e:
+        ops.produce_qkv(ctx, ops.ProducerShape(T, hq, hkv, D, 0), _t(torch, q), _t(torch, k),
+                        _t(torch, v), None, None, out[0], out[1], out[2], T * D)
+    assert e.value.name == "NonFinite"
+
+
+def _session_inputs(rng, layers, total, hq, hkv, D, scale=1.0):
+    qs = [rng.standard_normal((total, hq, D)).astype(np.float32) * scale for _ in range(layers)]
+    ks = [rng.standard_normal((total, hkv, D)).astype(np.float32) * scale for _ in range(layers)]
+    vs = [rng.standard_normal((total, hkv, D)).astype(np.float32) for _ in range(layers)]
+    wq = [(1 + 0.02 * rng.standard_normal(D)).astype(np.float32) for _ in range(layers)]
+    wk = [(1 + 0.02 * rng.standard_normal(D)).astype(np.float32) for _ in range(layers)]
+    return qs, ks, vs, wq, wk
+
+
+def test_session_qwen3_prefill_chunks_then_decode_steps(torch_mod, ctx, ops, sess_mod, orc):
+    """Two Qwen3-shaped layers (16/8/128, bf16 KV, QK-norm, rotary 1e6, position offset 7):
+    300 prompt tokens in 128-token chunks, then 6 single-token decode steps.  Each
+    layer's contexts equal full-prefix attention over the oracle-produced Q/K/V."""
+    torch = torch_mod
+    rng = np.random.default_rng(3)
+    L, hq, hkv, D, prompt, steps, off = 2, 16, 8, 128, 300, 6, 7
+    total = prompt + steps
+    qs, ks, vs, wq, wk = _session_inputs(rng, L, total, hq, hkv, D)
+    opts = sess_mod.Options(capacity=total + 10, prefill_chunk_size=128, position_offset=off,
+                            vocab_size=1000, layers=L, query_heads=hq, kv_heads=hkv, head_dim=D,
+                            storage="bf16")
+    s = sess_mod.Session(ctx, opts)
+    ctxs = [torch.full((total, hq * D), np.nan, dtype=torch.float32, device="cuda") for _ in range(L)]
+    io = [sess_mod.LayerIo(_t(torch, qs[l]), _t(torch, ks[l]), _t(torch, vs[l]), ctxs[l],
+                           _t(torch, wq[l]), _t(torch, wk[l])) for l in range(L)]
+    tokens = list(rng.integers(0, 1000, total))
+    s.set_tokens(tokens[:prompt])
+    assert s.evaluate(io) == prompt
+    s.append(tokens[prompt:])
+    assert s.evaluate(io, chunk_limit=1) == steps
+    assert (s.evaluated_len(), s.pending_len()) == (total, 0) and s.distribution_valid()
+    for l in range(L):
+        q = stored(_oracle_produce(orc, qs[l], wq[l], total, hq, D, off), "bf16")
+        k = stored(_oracle_produce(orc, ks[l], wk[l], total, hkv, D, off), "bf16")
+        v = stored(vs[l], "bf16")
+        ref, _, _ = orc.attention(q.reshape(-1), k.reshape(-1), v.reshape(-1), total, hq, hkv, D)
+        err = max_err(host(ctxs[l]).reshape(-1), ref)
+        log(f"layer {l}: max abs error {err:.3e}")
+        assert err <= TOL_HALF
+
+
+def test_session_sliding_and_global_layers_gemma_shape(torch_mod, ctx, ops, sess_mod, orc):
+    """A sliding (W=64, ring cache) and a global layer at 8/4/256, scale 1/16, score
+    softcap 50, proportional rotary: 200 prompt tokens in 64-token chunks, 5 decode steps."""
+    torch = torch_mod
+    rng = np.random.default_rng(4)
+    L, hq, hkv, D, prompt, steps, W = 2, 8, 4, 256, 200, 5, 64
+    total = prompt + steps
+    qs, ks, vs, wq, wk = _session_inputs(rng, L, total, hq, hkv, D, scale=2.0)
+    opts = sess_mod.Options(capacity=total, prefill_chunk_size=64, vocab_size=100, layers=L,
+                            query_heads=hq, kv_heads=hkv, head_dim=D, storage="bf16",
+                            score_scale=1.0 / 16.0, softcap=50.0, rotary=2, theta=1e6,
+                            rotated_dims=128, factor=8.0, layer_windows=[W, 0])
+    s = sess_mod.Session(ctx, opts)
+    ctxs = [torch.full((total, hq * D), np.nan, dtype=torch.float32, device="cuda") for _ in range(L)]
+    io = [sess_mod.LayerIo(_t(torch, qs[l]), _t(torch, ks[l]), _t(torch, vs[l]), ctxs[l],
+                           _t(torch, wq[l]), _t(torch, wk[l])) for l in range(L)]
+    s.set_tokens([1] * prompt)
+    assert s.evaluate(io) == prompt
+    s.append([2] * steps)
+    assert s.evaluate(io, chunk_limit=1) == steps
+    for l, window in enumerate([W, None]):
+        kw = dict(rotary="proportional", theta=1e6, rotated=128, factor=8.0)
+        q = stored(_oracle_produce(orc, qs[l], wq[l], total, hq, D, 0, **kw), "bf16")
+        k = stored(_oracle_produce(orc, ks[l], wk[l], total, hkv, D, 0, **kw), "bf16")
+        v = stored(vs[l], "bf16")
+        kh = k.transpose(1, 0, 2).copy()
+        vh = v.transpose(1, 0, 2).copy()
+        ref, _, _ = orc.window_attention(q.reshape(-1), kh.reshape(-1), vh.reshape(-1), total, total,
+                                         total, hq, hkv, D, 0, 0, window, 1.0 / 16.0, softcap=50.0)
+        err = max_err(host(ctxs[l]).reshape(-1), ref)
+        log(f"layer {l} window {window}: max abs error {err:.3e}")
+        assert err <= TOL_HALF
+
+
+def test_session_failed_chunk_commits_nothing_and_retry_succeeds(torch_mod, ctx, ops, sess_mod, orc):
+    """src/session.rs:357-363: a chunk whose layer fails leaves the committed prefix
+    and the pending history; fixing the input and evaluating again succeeds."""
+    torch = torch_mod
+    rng = np.random.default_rng(5)
+    L, hq, hkv, D, total = 1, 4, 2, 64, 40
+    qs, ks, vs, wq, wk = _session_inputs(rng, L, total, hq, hkv, D)
+    opts = sess_mod.Options(capacity=64, prefill_chunk_size=16, vocab_size=10, layers=L,
+                            query_heads=hq, kv_heads=hkv, head_dim=D, storage="f32")
+    s = sess_mod.Session(ctx, opts)
+    out = torch.zeros((total, hq * D), dtype=torch.float32, device="cuda")
+    kbad = ks[0].copy()
+    kbad[20, 1, 3] = np.nan
+    io = [sess_mod.LayerIo(_t(torch, qs[0]), _t(torch, kbad), _t(torch, vs[0]), out, None, None)]
+    s.set_tokens([3] * total)
+    assert s.evaluate_next_chunk(io) == 16   # rows 0..15 are clean
+    with pytest.raises(ops.TkhError) as e:
+        s.evaluate(io)
+    assert e.value.name == "NonFinite"
+    assert (s.evaluated_len(), s.pending_len()) == (16, 24)
+    io[0].k_proj = _t(torch, ks[0])
+    assert s.evaluate(io) == 24
+    q = _oracle_produce(orc, qs[0], None, total, hq, D, 0)
+    k = _oracle_produce(orc, ks[0], None, total, hkv, D, 0)
+    ref, _, _ = orc.attention(q.reshape(-1), k.reshape(-1), vs[0].reshape(-1), total, hq, hkv, D)
+    err = max_err(host(out).reshape(-1), ref)
+    log(f"fp32 session after retry: max abs error {err:.3e}")
+    assert err <= 1e-5
+
+
+def test_session_queued_context_matches_synchronous(torch_mod, ops, sess_mod):
+    """A queued context evaluates without per-chunk host waits; after synchronize the
+    contexts are bit-identical to a synchronous context's."""
+    torch = torch_mod
+    rng = np.random.default_rng(6)
+    L, hq, hkv, D, total = 1, 16, 8, 128, 150
+    qs, ks, vs, wq, wk = _session_inputs(rng, L, total, hq, hkv, D)
+    outs = []
+    for sync in (True, False):
+        c = ops.Context(0, synchronous=sync)
+        s = sess_mod.Session(c, sess_mod.Options(capacity=total, prefill_chunk_size=128, layers=1,
+                                                 query_heads=hq, kv_heads=hkv, head_dim=D))
+        out = torch.zeros((total, hq * D), dtype=torch.float32, device="cuda")
+        io = [sess_mod.LayerIo(_t(torch, qs[0]), _t(torch, ks[0]), _t(torch, vs[0]), out,
+                               _t(torch, wq[0]), _t(torch, wk[0]))]
+        s.set_tokens([1] * 140)
+        s.evaluate(io)
+        s.append([1] * 10)
+        s.evaluate(io, chunk_limit=1)
+        s.synchronize()
+        assert s.evaluated_len() == total
+        outs.append(host(out))
+    assert np.array_equal(outs[0], outs[1])

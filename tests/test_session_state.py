@@ -1,0 +1,177 @@
+"""Session state machine (tkh_session) against the reference's transition tests.
+
+A host-only session (no device context) runs the token state machine alone:
+evaluation commits state and computes nothing.  The expected values are the
+ones src/session.rs's tests assert (tests/session.rs:343-502), with
+`logits().is_some()` read as `distribution_valid()`.
+"""
+
+import pytest
+
+from toklet_amd import _lib
+from toklet_amd.ops import TkhError
+from toklet_amd.session import Options, Session
+
+BASE = [1, 7, 13, 3, 47, 11]
+
+
+def host_session(capacity, chunk, offset=0, vocab=64):
+    return Session(None, Options(capacity=capacity, prefill_chunk_size=chunk,
+                                 position_offset=offset, vocab_size=vocab, layers=1,
+                                 query_heads=4, kv_heads=2, head_dim=8))
+
+
+def test_reusable_prefix_edits_and_shortening_match_reference_table():
+    """tests/session.rs:343-380: (tokens, kept prefix) after a fully evaluated BASE."""
+    for offset in (0, 5):
+        s = host_session(27, 3, offset)
+        for tokens, keep in [(BASE, 6), ([1, 7, 13, 3, 47, 12], 5), ([1, 8, 13, 3], 1),
+                             ([2, 7, 13], 0), (BASE[:4], 3), (BASE[:1], 0), ([], 0)]:
+            s.reset()
+            s.set_tokens(BASE)
+            s.evaluate(None)
+            s.set_tokens(tokens)
+            assert s.evaluated_len() == keep, (tokens, keep)
+            assert s.history() == tokens
+            if keep < len(tokens):
+                assert not s.distribution_valid()
+            s.evaluate(None)
+            assert s.evaluated_len() == len(tokens)
+            assert s.distribution_valid() == (len(tokens) > 0)
+
+
+def test_pending_sampled_token_is_not_committed_kv():
+    """tests/session.rs:381-408."""
+    s = host_session(27, 3)
+    for pending in (47, 48):
+        s.reset()
+        s.set_tokens(BASE)
+        s.evaluate(None)
+        s.append([47])
+        s.set_tokens(BASE + [pending])
+        assert (s.evaluated_len(), s.pending_len()) == (6, 1)
+        s.evaluate(None)
+        assert s.distribution_valid()
+    s.reset()
+    s.set_tokens(BASE)
+    s.evaluate(None)
+    s.append([47])
+    s.set_tokens(BASE)
+    assert (s.evaluated_len(), s.pending_len()) == (6, 0)
+    assert s.distribution_valid()
+
+
+def test_cancelled_edit_discard_stages_one_replay_token():
+    """tests/session.rs:405-450: discard after an edited request replays one token."""
+    s = host_session(27, 3)
+    s.set_tokens(BASE)
+    s.evaluate(None)
+    s.set_tokens([1, 7, 13, 3, 47, 12])
+    assert s.evaluated_len() == 5
+    assert not s.distribution_valid()
+    s.discard_pending()
+    assert s.history() == BASE[:5]
+    assert (s.evaluated_len(), s.pending_len()) == (4, 1)
+    assert not s.distribution_valid()
+    s.discard_pending()
+    assert s.history() == BASE[:5]
+    assert (s.evaluated_len(), s.pending_len()) == (4, 1)
+    s.append([12, 13])
+    s.discard_pending()
+    s.discard_pending()
+    assert s.history() == BASE[:5]
+    assert (s.evaluated_len(), s.pending_len()) == (4, 1)
+    s.set_tokens(s.history())
+    s.discard_pending()
+    assert s.history() == BASE[:5]
+    assert (s.evaluated_len(), s.pending_len()) == (4, 1)
+    s.evaluate(None)
+    assert s.distribution_valid() and s.evaluated_len() == 5
+    # A fully cached request at the truncated boundary still needs its replay.
+    s.set_tokens([1, 7, 13, 3, 48])
+    assert s.evaluated_len() == 4
+    s.set_tokens(BASE[:4])
+    assert (s.evaluated_len(), s.pending_len()) == (3, 1)
+    s.discard_pending()
+    s.discard_pending()
+    assert s.history() == BASE[:4]
+    assert (s.evaluated_len(), s.pending_len()) == (3, 1)
+    s.evaluate(None)
+    assert s.distribution_valid()
+
+
+def test_chunk_boundaries_cached_prompt_and_reset():
+    """tests/session.rs:455-502 (options(32, 2, 0))."""
+    s = host_session(32, 2)
+    s.set_tokens([1, 7, 13, 3])
+    assert s.next_chunk() == (0, 2)
+    assert s.evaluate_next_chunk(None) == 2
+    assert (s.evaluated_len(), s.pending_len()) == (2, 2)
+    s.evaluate(None)
+    assert s.distribution_valid()
+    s.set_tokens([1, 7, 13, 3])
+    assert s.evaluated_len() == 4
+    assert s.evaluate_next_chunk(None) == 0
+    assert s.distribution_valid()
+    s.set_tokens([1, 7, 13, 3, 47, 11])
+    assert s.evaluated_len() == 4
+    s.discard_pending()
+    assert s.distribution_valid() and s.history() == [1, 7, 13, 3]
+    s.set_tokens([1, 7, 13, 17])
+    assert s.evaluated_len() == 3
+    assert not s.distribution_valid()
+    s.evaluate(None)
+    s.set_tokens([1, 7])
+    assert s.evaluated_len() == 1
+    s.evaluate(None)
+    s.reset()
+    assert s.history() == [] and not s.distribution_valid()
+    assert s.evaluate_next_chunk(None) == 0
+    s.set_tokens([11])
+    s.evaluate(None)
+    assert s.distribution_valid()
+    s.set_tokens([])
+    assert not s.distribution_valid()
+
+
+def test_requests_are_admitted_before_mutation():
+    """tests/session.rs:504-583: capacity and vocabulary errors change nothing."""
+    s = host_session(4, 2, vocab=64)
+    s.set_tokens([1, 2, 3])
+    s.evaluate(None)
+    before = (s.history(), s.evaluated_len(), s.distribution_valid())
+    with pytest.raises(TkhError) as e:
+        s.set_tokens([64])
+    assert e.value.code == _lib.TOKEN and e.value.index == 0
+    with pytest.raises(TkhError) as e:
+        s.set_tokens([1, 2, 3, 4, 5])
+    assert e.value.code == _lib.CAPACITY
+    with pytest.raises(TkhError) as e:
+        s.append([5, 6])
+    assert e.value.code == _lib.CAPACITY
+    with pytest.raises(TkhError) as e:
+        s.append([64])
+    assert e.value.code == _lib.TOKEN and e.value.index == 3
+    assert (s.history(), s.evaluated_len(), s.distribution_valid()) == before
+
+
+def test_evaluate_with_chunk_limit_walks_decode_steps():
+    """Teacher-forced decode: pending tokens evaluated one position at a time."""
+    s = host_session(16, 8)
+    s.set_tokens(list(range(1, 11)))
+    assert s.evaluate(None) == 10 and s.evaluated_len() == 10
+    s.append([5, 6, 7])
+    assert s.next_chunk() == (10, 3)
+    assert s.evaluate(None, chunk_limit=1) == 3
+    assert (s.evaluated_len(), s.pending_len()) == (13, 0)
+
+
+def test_invalid_options_are_rejected():
+    with pytest.raises(TkhError) as e:
+        Session(None, Options(capacity=0))
+    assert e.value.code == _lib.ZERO_DIMENSION
+    with pytest.raises(TkhError) as e:
+        Session(None, Options(capacity=8, query_heads=6, kv_heads=4))
+    assert e.value.code == _lib.INVALID_PARAMETER
+    with pytest.raises(TkhError):
+        Session(None, Options(capacity=8, layers=2, layer_windows=[4, 0]))  # needs a score scale

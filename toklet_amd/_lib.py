@@ -71,6 +71,29 @@ class KvFrame(ctypes.Structure):
                 ("tokens", u64)]
 
 
+class ProducerShape(ctypes.Structure):
+    _fields_ = [(n, u64) for n in ("tokens", "query_heads", "kv_heads", "head_dim", "position")] + [
+        ("norm_epsilon", f32), ("rotary", u32), ("theta", f32), ("rotated_dims", u64),
+        ("factor", f32)]
+
+
+class SessionOptions(ctypes.Structure):
+    _fields_ = [(n, u64) for n in ("capacity", "prefill_chunk_size", "position_offset",
+                                   "vocab_size", "layers", "query_heads", "kv_heads",
+                                   "head_dim")] + [
+        ("storage", ctypes.c_int), ("score_scale", f32), ("softcap", f32), ("norm_epsilon", f32),
+        ("rotary", u32), ("theta", f32), ("rotated_dims", u64), ("factor", f32)]
+
+
+class SessionState(ctypes.Structure):
+    _fields_ = [(n, u64) for n in ("history_len", "evaluated_len", "pending_len", "capacity")] + [
+        ("distribution_valid", u32), ("kv_bytes", u64), ("scratch_bytes", u64)]
+
+
+class LayerIo(ctypes.Structure):
+    _fields_ = [(n, vp) for n in ("q_proj", "k_proj", "v_proj", "q_norm", "k_norm", "context")]
+
+
 P = ctypes.POINTER
 E = P(Error)
 
@@ -104,6 +127,20 @@ SIGNATURES = {
     "tkh_kv_view": (u32, [vp, P(KvFrame), u64, f32, P(Segment), P(SpanShape), E]),
     "tkh_kv_commit_batch": (u32, [P(vp), P(KvFrame), u64, E]),
     "tkh_kv_reset_batch": (u32, [P(vp), u64, E]),
+    "tkh_produce_qkv": (u32, [vp, P(ProducerShape), ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp,
+                              u64, E]),
+    "tkh_session_create": (u32, [vp, P(SessionOptions), P(u64), P(vp), E]),
+    "tkh_session_destroy": (None, [vp]),
+    "tkh_session_append": (u32, [vp, P(u32), u64, E]),
+    "tkh_session_set_tokens": (u32, [vp, P(u32), u64, E]),
+    "tkh_session_discard_pending": (None, [vp]),
+    "tkh_session_reset": (None, [vp]),
+    "tkh_session_state_get": (u32, [vp, P(SessionState)]),
+    "tkh_session_history": (u64, [vp, P(u32), u64]),
+    "tkh_session_next_chunk": (u32, [vp, P(u64), P(u64)]),
+    "tkh_session_evaluate_next_chunk": (u32, [vp, P(LayerIo), P(u64), E]),
+    "tkh_session_evaluate": (u32, [vp, P(LayerIo), u64, P(u64), E]),
+    "tkh_session_synchronize": (u32, [vp, E]),
 }
 
 _lib = None

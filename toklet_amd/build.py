@@ -19,7 +19,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtokhip.so")
-SOURCES = ["api.cpp", "attention.hip", "decode.hip", "prefill.hip", "kv.hip"]
+SOURCES = ["api.cpp", "session.cpp", "attention.hip", "decode.hip", "prefill.hip", "kv.hip", "produce.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -55,6 +55,23 @@ struct Problem {
     int32_t pad1;           // straddle a segment boundary)
 };
 
+// Producer launch (produce.hip): per-head RMSNorm, rotary, cache rounding.
+struct ProduceParams {
+    const float *q, *k, *v;   // [T, Hq, D], [T, Hkv, D], [T, Hkv, D] FP32, token-major
+    const float *q_norm;      // [D] or null (no norm)
+    const float *k_norm;
+    void *q_out;              // [T, Hq, D] in the cache dtype
+    void *k_out, *v_out;      // element (h, t, d) at h * out_head_stride + t * D + d
+    int64_t out_head_stride;
+    int64_t tokens;
+    int64_t position;         // absolute rotary position of token 0
+    int32_t hq, hkv, d;
+    int32_t rotary;           // 0 none, 1 split-half, 2 proportional
+    int32_t rotated_dims;     // proportional: rotated features (even, <= D)
+    float eps, theta, factor; // theta: split-half theta or proportional base
+    uint32_t *status;
+};
+
 struct Params {
     const Problem *problems;
     int32_t nproblems;
@@ -253,11 +270,14 @@ __device__ __forceinline__ void visible_range(const Params &p, const Problem &pr
     visible_range(p, pr.k_pos0, pr.keys, pos, lo, hi);
 }
 
-__device__ __forceinline__ void raise_status(const Params &p, bool bad, uint32_t bit) {
+__device__ __forceinline__ void raise_status(uint32_t *status, bool bad, uint32_t bit) {
     if (__builtin_amdgcn_read_exec() != 0) {
         uint64_t m = __ballot(bad);
-        if (m != 0 && (threadIdx.x & 63) == (int)__builtin_ctzll(m)) atomicOr(p.status, bit);
+        if (m != 0 && (threadIdx.x & 63) == (int)__builtin_ctzll(m)) atomicOr(status, bit);
     }
+}
+__device__ __forceinline__ void raise_status(const Params &p, bool bad, uint32_t bit) {
+    raise_status(p.status, bad, bit);
 }
 
 }  // namespace tkh

@@ -1,0 +1,126 @@
+// produce.hip - the step before attention on the session path: per-head
+// RMSNorm of Q and K, rotary position embedding, rounding to the cache dtype,
+// and the K/V append into head-major rows, in one launch.
+//
+// Order and arithmetic follow Model::run (src/model/mod.rs:611-662):
+//  * rmsnorm (src/cpu/reductions.rs:8-49): squares and their sum in FP64,
+//    denominator sqrt(sum / D + eps) in FP64, value = f32(x / den * w) in FP64;
+//  * rotary (src/cpu/attention.rs:10-64): frequency theta^(-2j/D), angle =
+//    position * frequency and sine/cosine in FP64, rounded to FP32; rotation
+//    a*c - b*s, b*c + a*s in FP32 with separate roundings (no contraction);
+//  * proportional rotary (src/cpu/proportional_rotary.rs:32-91): inverse
+//    frequency base^(-2j/D) / factor for pairs j < rotated_dims / 2, other
+//    features copied;
+//  * LayerKv::append (src/model/cache.rs:64-85): token-major new rows into
+//    head-major cache rows, here rounded once to the cache dtype.
+// The FP64 sum runs in a different order than the reference's sequential one;
+// the denominator can differ in its last FP64 bit, which reaches an FP32
+// result only at a rounding tie.
+//
+// One wave per (token, head slot): slots [0, Hq) are query heads, [Hq,
+// Hq + Hkv) key heads, the rest value heads.  Non-finite inputs or results set
+// the device status word (the reference returns Error::NonFinite).
+#include "device.hpp"
+
+namespace tkh {
+
+
+namespace {
+
+template <int DT> __device__ __forceinline__ void store_out(void *base, int64_t i, float x);
+template <> __device__ __forceinline__ void store_out<F32>(void *base, int64_t i, float x) {
+    reinterpret_cast<float *>(base)[i] = x;
+}
+template <> __device__ __forceinline__ void store_out<F16>(void *base, int64_t i, float x) {
+    reinterpret_cast<_Float16 *>(base)[i] = (_Float16)x;
+}
+template <> __device__ __forceinline__ void store_out<BF16>(void *base, int64_t i, float x) {
+    reinterpret_cast<__bf16 *>(base)[i] = (__bf16)x;  // round to nearest even
+}
+
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+    return x;
+}
+
+}  // namespace
+
+template <int DT>
+__global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
+#pragma clang fp contract(off)
+    __shared__ float row[512];
+    const int lane = threadIdx.x;
+    const int D = p.d;
+    const int slots = p.hq + 2 * p.hkv;
+    const int64_t t = blockIdx.x / slots;
+    const int slot = (int)(blockIdx.x % slots);
+    if (t >= p.tokens) return;
+    const int kind = slot < p.hq ? 0 : (slot < p.hq + p.hkv ? 1 : 2);  // q, k, v
+    const int h = kind == 0 ? slot : (kind == 1 ? slot - p.hq : slot - p.hq - p.hkv);
+    const int heads = kind == 0 ? p.hq : p.hkv;
+    const float *src = (kind == 0 ? p.q : (kind == 1 ? p.k : p.v)) + (t * heads + h) * D;
+    void *dst = kind == 0 ? p.q_out : (kind == 1 ? p.k_out : p.v_out);
+    const int64_t dst0 = kind == 0 ? (t * p.hq + h) * D : h * p.out_head_stride + t * D;
+
+    bool bad = false;
+    for (int i = lane; i < D; i += 64) {
+        const float x = src[i];
+        bad |= !is_finite_f(x);
+        row[i] = x;
+    }
+    if (kind == 2) {
+        for (int i = lane; i < D; i += 64) store_out<DT>(dst, dst0 + i, row[i]);
+        raise_status(p.status, bad, ST_NONFINITE_INPUT);
+        return;
+    }
+    const float *w = kind == 0 ? p.q_norm : p.k_norm;
+    if (w) {
+        double ss = 0.0;
+        for (int i = lane; i < D; i += 64) {
+            const double x = (double)row[i];
+            ss += x * x;
+        }
+        ss = wave_sum_f64(ss);
+        const double den = sqrt(ss / (double)D + (double)p.eps);
+        for (int i = lane; i < D; i += 64) {
+            const float y = (float)((double)row[i] / den * (double)w[i]);
+            bad |= !is_finite_f(y) || !is_finite_f(w[i]);
+            row[i] = y;
+        }
+    }
+    __syncthreads();
+    const int half = D / 2;
+    const int pairs = p.rotary == 1 ? half : (p.rotary == 2 ? p.rotated_dims / 2 : 0);
+    const double pos = (double)(p.position + t);
+    for (int j = lane; j < half; j += 64) {
+        const float a = row[j], b = row[j + half];
+        float x = a, y = b;
+        if (j < pairs) {
+            double inv = pow((double)p.theta, -(2.0 * (double)j) / (double)D);
+            if (p.rotary == 2) inv = inv / (double)p.factor;
+            const double angle = pos * inv;
+            const float s = (float)sin(angle), c = (float)cos(angle);
+            const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
+            x = ac - bs;
+            y = bc + as;
+            bad |= !is_finite_f(x) || !is_finite_f(y);
+        }
+        store_out<DT>(dst, dst0 + j, x);
+        store_out<DT>(dst, dst0 + j + half, y);
+    }
+    raise_status(p.status, bad, ST_NONFINITE_INPUT);
+}
+
+}  // namespace tkh
+
+extern "C" hipError_t tkh_launch_produce(const tkh::ProduceParams *p, int dtype, hipStream_t stream) {
+    using namespace tkh;
+    const int64_t blocks = p->tokens * (p->hq + 2 * p->hkv);
+    if (blocks <= 0 || p->d > 512 || p->d % 2) return hipErrorInvalidValue;
+    dim3 grid((unsigned)blocks), block(64);
+    if (dtype == F32) hipLaunchKernelGGL((produce_qkv<F32>), grid, block, 0, stream, *p);
+    else if (dtype == F16) hipLaunchKernelGGL((produce_qkv<F16>), grid, block, 0, stream, *p);
+    else if (dtype == BF16) hipLaunchKernelGGL((produce_qkv<BF16>), grid, block, 0, stream, *p);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}

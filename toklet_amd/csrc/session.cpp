@@ -1,0 +1,526 @@
+// session.cpp - the session state machine of the attention path and the
+// fused Q/K/V producer entry point (include/tokhip.h, "producer" and
+// "session").
+//
+// tkh_session mirrors toklet's Session (src/session.rs:192-446) for what the
+// attention path needs: token history with longest-prefix reuse, one pending
+// chunk evaluated per call, every layer committed together, discard and
+// reset.  The model around attention (embeddings, projections, MLP, logits)
+// stays with the caller: a chunk's evaluation takes each layer's Q/K/V
+// projections and returns its attention context.  Per layer it runs the
+// producer (RMSNorm, rotary, cache rounding), appends or stages K/V, and
+// attends; ring caches of sliding layers commit after every layer succeeded,
+// as the reference commits a Gemma step's frames in one batch
+// (src/model/gemma3/forward.rs:401).
+#include <algorithm>
+#include <cmath>
+
+#include "host.hpp"
+
+extern "C" hipError_t tkh_launch_produce(const tkh::ProduceParams *p, int dtype, hipStream_t stream);
+
+using namespace tkh_host;
+
+namespace {
+
+uint32_t check_producer(const tkh_producer_shape *sh, tkh_error *err) {
+    if (!sh) return invalid("producer shape", err);
+    TRY(nonzero(sh->tokens, "tokens", err));
+    TRY(nonzero(sh->query_heads, "query_heads", err));
+    TRY(nonzero(sh->kv_heads, "kv_heads", err));
+    TRY(nonzero(sh->head_dim, "head_dim", err));
+    if (sh->query_heads % sh->kv_heads != 0)
+        return invalid("query heads must be a multiple of KV heads", err);
+    if (sh->head_dim % 2 != 0) return invalid("rotary head_dim must be even", err);
+    if (sh->head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 512, sh->head_dim,
+                                        "head_dim above 512 is not supported");
+    if (sh->rotary > TKH_ROTARY_PROPORTIONAL) return invalid("rotary kind", err);
+    if (sh->rotary != TKH_ROTARY_NONE && (!std::isfinite(sh->theta) || sh->theta <= 0.0f))
+        return invalid("theta must be finite and positive", err);
+    if (sh->rotary == TKH_ROTARY_PROPORTIONAL) {
+        if (sh->rotated_dims % 2 != 0 || sh->rotated_dims > sh->head_dim)
+            return invalid("proportional rotary dimensions", err);
+        if (!std::isfinite(sh->factor) || sh->factor <= 0.0f)
+            return invalid("proportional rotary base/factor", err);
+    }
+    uint64_t last;
+    TRY(add(sh->position, sh->tokens - 1, &last, err));
+    if (last > (uint64_t{1} << 53)) return invalid("rotary positions must be at most 2^53", err);
+    return TKH_OK;
+}
+
+uint32_t launch_producer(tkh_context *ctx, const tkh_producer_shape *sh, tkh_dtype dtype,
+                         const float *q, const float *k, const float *v, const float *qn,
+                         const float *kn, void *q_out, void *k_out, void *v_out,
+                         uint64_t head_stride, tkh_error *err) {
+    tkh::ProduceParams p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.q_norm = qn;
+    p.k_norm = kn;
+    p.q_out = q_out;
+    p.k_out = k_out;
+    p.v_out = v_out;
+    p.out_head_stride = (int64_t)head_stride;
+    p.tokens = (int64_t)sh->tokens;
+    p.position = (int64_t)sh->position;
+    p.hq = (int32_t)sh->query_heads;
+    p.hkv = (int32_t)sh->kv_heads;
+    p.d = (int32_t)sh->head_dim;
+    p.rotary = (int32_t)sh->rotary;
+    p.rotated_dims = (int32_t)sh->rotated_dims;
+    p.eps = sh->norm_epsilon;
+    p.theta = sh->theta;
+    p.factor = sh->factor;
+    p.status = ctx->status_dev;
+    HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    HIP_TRY(tkh_launch_produce(&p, (int)dtype, ctx->stream), "producer launch");
+    return TKH_OK;
+}
+
+}  // namespace
+
+extern "C" uint32_t tkh_produce_qkv(tkh_context *ctx, const tkh_producer_shape *shape,
+                                    tkh_dtype dtype, const float *q_proj, const float *k_proj,
+                                    const float *v_proj, const float *q_norm, const float *k_norm,
+                                    void *q_out, void *k_out, void *v_out,
+                                    uint64_t out_head_stride, tkh_error *err) {
+    if (!ctx) return invalid("context", err);
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    TRY(check_producer(shape, err));
+    if ((q_norm || k_norm) && (!std::isfinite(shape->norm_epsilon) || shape->norm_epsilon <= 0.0f))
+        return invalid("epsilon must be finite and positive", err);
+    if (!q_proj || !k_proj || !v_proj || !q_out || !k_out || !v_out)
+        return invalid("producer buffers", err);
+    uint64_t rows;
+    TRY(product(shape->tokens, shape->head_dim, &rows, err));
+    if (out_head_stride < rows) return invalid("output head stride below tokens * head_dim", err);
+    TRY(launch_producer(ctx, shape, dtype, q_proj, k_proj, v_proj, q_norm, k_norm, q_out, k_out,
+                        v_out, out_head_stride, err));
+    if (ctx->synchronous) return tkh_context_synchronize(ctx, err);
+    return ok(err);
+}
+
+// ---------------------------------------------------------------- session
+
+struct tkh_session {
+    tkh_context *ctx = nullptr;
+    tkh_session_options opt{};
+    std::vector<uint64_t> windows;  // per layer, 0 = full retention
+    std::vector<tkh_kv *> kv;       // per layer owner
+    std::vector<uint32_t> history;
+    uint64_t evaluated = 0;
+    bool dist_valid = false, dist_replay = false;
+    // Queued contexts: the prefix (and distribution validity) confirmed by the
+    // last status check.
+    uint64_t checked = 0;
+    bool checked_valid = false;
+    bool rings = false;                        // some layer keeps a ring cache
+    void *q_scratch = nullptr;                 // [chunk, Hq, D] cache dtype
+    std::vector<void *> stage_k, stage_v;      // sliding layers: [Hkv, chunk, D]
+    uint64_t scratch_bytes = 0, kv_bytes = 0;
+};
+
+namespace {
+
+void free_session(tkh_session *s) {
+    if (!s) return;
+    if (s->ctx) hipSetDevice(s->ctx->device);
+    for (auto *k : s->kv) tkh_kv_destroy(k);
+    if (s->q_scratch) hipFree(s->q_scratch);
+    for (auto *p : s->stage_k)
+        if (p) hipFree(p);
+    for (auto *p : s->stage_v)
+        if (p) hipFree(p);
+    delete s;
+}
+
+// Session::validate (src/session.rs:292-318): capacity, then every token id.
+uint32_t validate_tokens(const tkh_session *s, const uint32_t *tokens, uint64_t count,
+                         uint64_t base, tkh_error *err) {
+    uint64_t end;
+    TRY(add(base, count, &end, err));
+    if (end > s->opt.capacity)
+        return fail(err, TKH_CAPACITY, "session", base, s->opt.capacity, end,
+                    "offset %llu plus %llu tokens exceeds capacity %llu", (unsigned long long)base,
+                    (unsigned long long)count, (unsigned long long)s->opt.capacity);
+    if (count && !tokens) return invalid("tokens", err);
+    for (uint64_t i = 0; i < count; ++i)
+        if (tokens[i] >= s->opt.vocab_size)
+            return fail(err, TKH_TOKEN, "token", base + i, s->opt.vocab_size, tokens[i],
+                        "token %u at position %llu is outside vocabulary %llu", tokens[i],
+                        (unsigned long long)(base + i), (unsigned long long)s->opt.vocab_size);
+    return TKH_OK;
+}
+
+// session::reusable_prefix (src/session.rs:17-36).
+void reusable_prefix(const std::vector<uint32_t> &history, uint64_t evaluated,
+                     const uint32_t *tokens, uint64_t count, bool distribution_valid,
+                     uint64_t *keep, bool *recover) {
+    uint64_t shared = 0;
+    while (shared < evaluated && shared < count && history[shared] == tokens[shared]) ++shared;
+    if (shared == count && (shared < evaluated || !distribution_valid)) {
+        *keep = shared > 0 ? shared - 1 : 0;
+        *recover = shared > 0;
+    } else {
+        *keep = shared;
+        *recover = false;
+    }
+}
+
+// The committed prefix moves back to `keep`.  Linear caches need nothing
+// (only the evaluated length defines validity, src/model/cache.rs:9-10).  A
+// ring of window W at committed length E holds positions [E - W, E); a chunk
+// starting at `keep` needs [keep - W + 1, keep), present only for keep >= E - 1.
+// Deeper rewinds restart every ring (and the prefix) from position 0.
+uint64_t rewind(tkh_session *s, uint64_t keep) {
+    if (!s->rings) return keep;
+    bool restart = false;
+    for (auto *kv : s->kv)
+        if (kv->has_window && keep + 1 < kv->offset) restart = true;
+    for (auto *kv : s->kv) {
+        if (!kv->has_window) continue;
+        kv->offset = restart ? 0 : std::min(kv->offset, keep);
+        kv->generation += 1;  // frames prepared before the rewind are stale
+    }
+    return restart ? 0 : keep;
+}
+
+}  // namespace
+
+extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_options *o,
+                                       const uint64_t *layer_windows, tkh_session **out,
+                                       tkh_error *err) {
+    if (!out || !o) return invalid("session options", err);
+    *out = nullptr;
+    TRY(nonzero(o->capacity, "capacity", err));
+    TRY(nonzero(o->prefill_chunk_size, "prefill_chunk_size", err));
+    TRY(nonzero(o->vocab_size, "vocab_size", err));
+    TRY(nonzero(o->layers, "layers", err));
+    if (!valid_dtype(o->storage)) return invalid("dtype", err);
+    tkh_producer_shape sh{};
+    sh.tokens = 1;
+    sh.query_heads = o->query_heads;
+    sh.kv_heads = o->kv_heads;
+    sh.head_dim = o->head_dim;
+    sh.rotary = o->rotary;
+    sh.theta = o->theta;
+    sh.rotated_dims = o->rotated_dims;
+    sh.factor = o->factor;
+    TRY(check_producer(&sh, err));
+    uint64_t last;
+    TRY(add(o->position_offset, o->capacity, &last, err));
+    if (last > (uint64_t{1} << 53)) return invalid("rotary positions must be at most 2^53", err);
+    if (o->score_scale != 0.0f && !(std::isfinite(o->score_scale) && o->score_scale > 0.0f))
+        return invalid("score scale must be finite and positive", err);
+    if (!(o->softcap == 0.0f || (std::isfinite(o->softcap) && o->softcap > 0.0f)))
+        return invalid("softcap must be finite and positive (0 disables)", err);
+    auto *s = new tkh_session();
+    s->ctx = ctx;
+    s->opt = *o;
+    s->opt.prefill_chunk_size = std::min(o->prefill_chunk_size, o->capacity);
+    // windows: the attention mask of each layer.  A window shorter than the
+    // capacity also selects a ring cache of that many rows.
+    s->windows.assign(o->layers, 0);
+    if (layer_windows)
+        for (uint64_t l = 0; l < o->layers; ++l) s->windows[l] = layer_windows[l];
+    bool windowed = false;
+    for (uint64_t w : s->windows) windowed |= w != 0;
+    if (windowed && o->score_scale == 0.0f) {
+        free_session(s);
+        return invalid("windowed layers need an explicit score scale", err);
+    }
+    s->history.reserve(o->capacity);
+    if (ctx) {
+        const uint64_t D = o->head_dim, es = (uint64_t)esize(o->storage);
+        const uint64_t chunk = s->opt.prefill_chunk_size;
+        s->kv.assign(o->layers, nullptr);
+        s->stage_k.assign(o->layers, nullptr);
+        s->stage_v.assign(o->layers, nullptr);
+        for (uint64_t l = 0; l < o->layers; ++l) {
+            const uint64_t w = s->windows[l];
+            const bool ring = w != 0 && w < o->capacity;
+            uint32_t rc = tkh_kv_create(ctx, o->kv_heads, D, ring ? w : o->capacity, o->capacity,
+                                        ring ? 1u : 0u, ring ? w : 0, o->storage, &s->kv[l], err);
+            if (rc != TKH_OK) {
+                free_session(s);
+                return rc;
+            }
+            s->kv_bytes += s->kv[l]->allocated_bytes;
+            s->rings |= ring;
+        }
+        hipError_t e = hipMalloc(&s->q_scratch, chunk * o->query_heads * D * es);
+        s->scratch_bytes = chunk * o->query_heads * D * es;
+        for (uint64_t l = 0; e == hipSuccess && l < o->layers; ++l) {
+            if (!s->kv[l]->has_window) continue;
+            const size_t bytes = chunk * o->kv_heads * D * es;
+            e = hipMalloc(&s->stage_k[l], bytes);
+            if (e == hipSuccess) e = hipMalloc(&s->stage_v[l], bytes);
+            s->scratch_bytes += 2 * bytes;
+        }
+        if (e != hipSuccess) {
+            free_session(s);
+            return device_error(e, "session allocation", err);
+        }
+    }
+    *out = s;
+    return ok(err);
+}
+
+extern "C" void tkh_session_destroy(tkh_session *s) { free_session(s); }
+
+extern "C" uint32_t tkh_session_append(tkh_session *s, const uint32_t *tokens, uint64_t count,
+                                       tkh_error *err) {
+    if (!s) return invalid("session", err);
+    TRY(validate_tokens(s, tokens, count, s->history.size(), err));
+    s->history.insert(s->history.end(), tokens, tokens + count);
+    return ok(err);
+}
+
+extern "C" uint32_t tkh_session_set_tokens(tkh_session *s, const uint32_t *tokens, uint64_t count,
+                                           tkh_error *err) {
+    if (!s) return invalid("session", err);
+    TRY(validate_tokens(s, tokens, count, 0, err));
+    uint64_t keep;
+    bool recover;
+    reusable_prefix(s->history, s->evaluated, tokens, count, s->dist_valid, &keep, &recover);
+    // Option<&u32> equality of tokens.get(keep) and history.get(keep): two
+    // absent values compare equal.
+    const bool t_has = keep < count, h_has = keep < s->history.size();
+    const bool same_next = t_has == h_has && (!t_has || tokens[keep] == s->history[keep]);
+    recover = recover || (s->dist_replay && keep == s->evaluated && same_next);
+    if (keep < s->evaluated) s->dist_valid = false;
+    const uint64_t kept = rewind(s, keep);
+    if (kept != keep) recover = false;  // every token is pending again
+    s->evaluated = kept;
+    s->checked = std::min(s->checked, kept);
+    s->dist_replay = recover;
+    s->history.assign(tokens, tokens + count);
+    return ok(err);
+}
+
+extern "C" void tkh_session_discard_pending(tkh_session *s) {
+    if (!s) return;
+    s->history.resize(std::min<uint64_t>(s->history.size(), s->evaluated + (s->dist_replay ? 1 : 0)));
+    if (s->dist_replay) return;
+    if (!s->dist_valid && s->evaluated > 0) {
+        // A one-position rewind, which every ring can take.
+        s->evaluated = rewind(s, s->evaluated - 1);
+        s->checked = std::min(s->checked, s->evaluated);
+        s->dist_replay = true;
+    }
+}
+
+extern "C" void tkh_session_reset(tkh_session *s) {
+    if (!s) return;
+    s->history.clear();
+    s->evaluated = 0;
+    s->checked = 0;
+    s->checked_valid = false;
+    s->dist_valid = false;
+    s->dist_replay = false;
+    std::vector<tkh_kv *> rings;
+    for (auto *kv : s->kv)
+        if (kv->has_window) rings.push_back(kv);
+    if (!rings.empty()) tkh_kv_reset_batch(rings.data(), rings.size(), nullptr);
+}
+
+extern "C" uint32_t tkh_session_state_get(const tkh_session *s, tkh_session_state *out) {
+    if (!s || !out) return TKH_INVALID_PARAMETER;
+    out->history_len = s->history.size();
+    out->evaluated_len = s->evaluated;
+    out->pending_len = s->history.size() - s->evaluated;
+    out->capacity = s->opt.capacity;
+    out->distribution_valid = s->dist_valid && s->evaluated > 0 && out->pending_len == 0;
+    out->kv_bytes = s->kv_bytes;
+    out->scratch_bytes = s->scratch_bytes;
+    return TKH_OK;
+}
+
+extern "C" uint64_t tkh_session_history(const tkh_session *s, uint32_t *tokens,
+                                        uint64_t capacity_tokens) {
+    if (!s) return 0;
+    const uint64_t n = std::min<uint64_t>(capacity_tokens, s->history.size());
+    if (tokens && n) std::memcpy(tokens, s->history.data(), n * sizeof(uint32_t));
+    return s->history.size();
+}
+
+extern "C" uint32_t tkh_session_next_chunk(const tkh_session *s, uint64_t *start, uint64_t *count) {
+    if (!s || !start || !count) return TKH_INVALID_PARAMETER;
+    *start = s->evaluated;
+    *count = std::min<uint64_t>(s->history.size() - s->evaluated, s->opt.prefill_chunk_size);
+    return TKH_OK;
+}
+
+namespace {
+
+// The commit of Session::evaluate_chunk (src/session.rs:413-417).
+void commit_state(tkh_session *s, uint64_t count) {
+    s->evaluated += count;
+    s->dist_valid = true;
+    s->dist_replay = false;
+    s->checked = s->evaluated;
+    s->checked_valid = true;
+}
+
+// One chunk of `count` tokens at session position `start`: every layer, then
+// the status check (when required) and the joint commit.
+uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t start,
+                        uint64_t count, bool position_indexed, tkh_error *err) {
+    tkh_context *ctx = s->ctx;
+    const tkh_session_options &o = s->opt;
+    const uint64_t Hq = o.query_heads, Hkv = o.kv_heads, D = o.head_dim;
+    const uint64_t es = (uint64_t)esize(o.storage);
+    const uint64_t row0 = position_indexed ? start : 0;
+    tkh_producer_shape sh{};
+    sh.tokens = count;
+    sh.query_heads = Hq;
+    sh.kv_heads = Hkv;
+    sh.head_dim = D;
+    sh.position = o.position_offset + start;
+    sh.norm_epsilon = o.norm_epsilon;
+    sh.rotary = o.rotary;
+    sh.theta = o.theta;
+    sh.rotated_dims = o.rotated_dims;
+    sh.factor = o.factor;
+    const uint64_t checked = s->checked;
+    const bool checked_valid = s->checked_valid;
+    std::vector<tkh_kv *> ring_kv;
+    std::vector<tkh_kv_frame> frames;
+    for (uint64_t l = 0; l < o.layers; ++l) {
+        const tkh_layer_io &io = layers[l];
+        if (!io.q_proj || !io.k_proj || !io.v_proj || !io.context)
+            return invalid("layer inputs", err);
+        if ((io.q_norm || io.k_norm) && (!std::isfinite(o.norm_epsilon) || o.norm_epsilon <= 0.0f))
+            return invalid("epsilon must be finite and positive", err);
+        const float *q = io.q_proj + row0 * Hq * D;
+        const float *k = io.k_proj + row0 * Hkv * D;
+        const float *v = io.v_proj + row0 * Hkv * D;
+        float *context = io.context + row0 * Hq * D;
+        tkh_kv *kv = s->kv[l];
+        const bool ring = kv->has_window;
+        const uint64_t window = s->windows[l];
+        if (!ring) {
+            uint8_t *kb = (uint8_t *)kv->k + start * D * es, *vb = (uint8_t *)kv->v + start * D * es;
+            TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
+                                kb, vb, kv->capacity * D, err));
+            if (o.score_scale == 0.0f) {
+                // Model::run -> LayerKv::attend -> attention_cached (src/model/mod.rs:645-662).
+                tkh_cached_shape cs{count, Hq, Hkv, D, kv->capacity, start};
+                TRY(tkh_attention_cached(ctx, &cs, o.storage, s->q_scratch, count * Hq * D, kv->k,
+                                         Hkv * kv->capacity * D, kv->v, Hkv * kv->capacity * D,
+                                         context, count * Hq * D, nullptr, 0, nullptr, 0, err));
+            } else {
+                tkh_window_shape ws{};
+                ws.queries = count;
+                ws.keys = start + count;
+                ws.capacity = kv->capacity;
+                ws.query_heads = Hq;
+                ws.kv_heads = Hkv;
+                ws.head_dim = D;
+                ws.query_start = start;
+                ws.key_start = 0;
+                ws.has_window = window != 0;
+                ws.window = window;
+                ws.scale = o.score_scale;
+                ws.softcap = o.softcap;
+                TRY(tkh_window_attention(ctx, &ws, o.storage, s->q_scratch, count * Hq * D, kv->k,
+                                         Hkv * kv->capacity * D, kv->v, Hkv * kv->capacity * D,
+                                         context, count * Hq * D, nullptr, 0, nullptr, 0, err));
+            }
+        } else {
+            // Sliding layer: stage the chunk, attend over the ring's old spans
+            // plus the staged rows (WindowKvCache::view), commit later.
+            if (kv->offset != start)
+                return fail(err, TKH_INVALID_CONFIG, "KV frame", l, start, kv->offset,
+                            "ring cache of layer %llu is at %llu, chunk starts at %llu",
+                            (unsigned long long)l, (unsigned long long)kv->offset,
+                            (unsigned long long)start);
+            TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
+                                s->stage_k[l], s->stage_v[l], count * D, err));
+            tkh_kv_frame f{};
+            f.k = s->stage_k[l];
+            f.v = s->stage_v[l];
+            f.owner = kv->owner;
+            f.generation = kv->generation;
+            f.offset = kv->offset;
+            f.tokens = count;
+            tkh_segment segs[3];
+            tkh_span_shape span{};
+            TRY(tkh_kv_view(kv, &f, Hq, o.score_scale, segs, &span, err));
+            span.softcap = o.softcap;
+            TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
+                                   context, count * Hq * D, nullptr, 0, nullptr, 0, err));
+            ring_kv.push_back(kv);
+            frames.push_back(f);
+        }
+    }
+    // Commit only after every layer of the chunk succeeded.  Sliding layers
+    // overwrite ring rows on commit, so their sessions check the status first
+    // even on a queued context.
+    if (ctx->synchronous || !ring_kv.empty()) TRY(tkh_context_synchronize(ctx, err));
+    if (!ring_kv.empty()) TRY(tkh_kv_commit_batch(ring_kv.data(), frames.data(), ring_kv.size(), err));
+    commit_state(s, count);
+    if (!ctx->synchronous && !s->rings) {
+        // Provisional until tkh_session_synchronize confirms the status word.
+        s->checked = checked;
+        s->checked_valid = checked_valid;
+    }
+    return ok(err);
+}
+
+}  // namespace
+
+extern "C" uint32_t tkh_session_evaluate_next_chunk(tkh_session *s, const tkh_layer_io *layers,
+                                                    uint64_t *count, tkh_error *err) {
+    if (!s) return invalid("session", err);
+    if (count) *count = 0;
+    const uint64_t n = std::min<uint64_t>(s->history.size() - s->evaluated, s->opt.prefill_chunk_size);
+    if (n == 0) return ok(err);
+    if (!s->ctx) {
+        commit_state(s, n);
+    } else {
+        if (!layers) return invalid("layer inputs", err);
+        TRY(evaluate_chunk(s, layers, s->evaluated, n, false, err));
+    }
+    if (count) *count = n;
+    return ok(err);
+}
+
+extern "C" uint32_t tkh_session_evaluate(tkh_session *s, const tkh_layer_io *layers,
+                                         uint64_t chunk_limit, uint64_t *evaluated, tkh_error *err) {
+    if (!s) return invalid("session", err);
+    if (evaluated) *evaluated = 0;
+    TRY(nonzero(chunk_limit, "chunk limit", err));
+    const uint64_t limit = std::min<uint64_t>(chunk_limit, s->opt.prefill_chunk_size);
+    uint64_t done = 0;
+    while (s->history.size() > s->evaluated) {
+        const uint64_t n = std::min<uint64_t>(s->history.size() - s->evaluated, limit);
+        if (!s->ctx) {
+            commit_state(s, n);
+        } else {
+            if (!layers) return invalid("layer inputs", err);
+            TRY(evaluate_chunk(s, layers, s->evaluated, n, true, err));
+        }
+        done += n;
+        if (evaluated) *evaluated = done;
+    }
+    return ok(err);
+}
+
+extern "C" uint32_t tkh_session_synchronize(tkh_session *s, tkh_error *err) {
+    if (!s) return invalid("session", err);
+    if (!s->ctx) return ok(err);
+    uint32_t rc = tkh_context_synchronize(s->ctx, err);
+    if (rc == TKH_OK) {
+        s->checked = s->evaluated;
+        s->checked_valid = s->dist_valid;
+        return rc;
+    }
+    // Provisional chunks since the last check are not committed.
+    s->evaluated = s->checked;
+    s->dist_valid = s->checked_valid;
+    s->dist_replay = false;
+    return rc;
+}

@@ -279,3 +279,42 @@ def prefill_batch(ctx: Context, q, k_base, v_base, offsets, head_strides, positi
         _ptr(q), _ptr(k_base), _ptr(v_base), _u64s(offsets), _u64s(head_strides),
         _u64s(positions), scale, _fptr(context), ctypes.byref(err))
     _check(rc, err)
+
+
+# ---- producer: the step before attention (Model::run, src/model/mod.rs:611-662) ----
+
+ROTARY_NONE, ROTARY_SPLIT_HALF, ROTARY_PROPORTIONAL = 0, 1, 2
+
+
+@dataclass
+class ProducerShape:
+    """Per-layer producer geometry: norm epsilon, rotary kind and its parameters
+    (split-half theta, or proportional base / rotated_dims / factor)."""
+    tokens: int
+    query_heads: int
+    kv_heads: int
+    head_dim: int
+    position: int
+    norm_epsilon: float = 1e-6
+    rotary: int = ROTARY_SPLIT_HALF
+    theta: float = 1e6
+    rotated_dims: int = 0
+    factor: float = 1.0
+
+    def c(self):
+        return _lib.ProducerShape(self.tokens, self.query_heads, self.kv_heads, self.head_dim,
+                                  self.position, self.norm_epsilon, self.rotary, self.theta,
+                                  self.rotated_dims, self.factor)
+
+
+def produce_qkv(ctx: Context, shape: ProducerShape, q_proj, k_proj, v_proj, q_norm, k_norm,
+                q_out, k_out, v_out, out_head_stride: int):
+    """rmsnorm (optional) -> rotary -> rounding of Q, and the K/V append into head-major
+    rows, in one launch.  k_out/v_out may be views into a cache at a row offset."""
+    err = _lib.Error()
+    s = shape.c()
+    rc = _lib.load().tkh_produce_qkv(
+        ctx.handle, ctypes.byref(s), dtype_of(q_out, k_out, v_out), _ptr(q_proj), _ptr(k_proj),
+        _ptr(v_proj), _ptr(q_norm), _ptr(k_norm), _ptr(q_out), _ptr(k_out), _ptr(v_out),
+        out_head_stride, ctypes.byref(err))
+    _check(rc, err)
