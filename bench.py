@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-north-star", action="store_true", help="skip configs[2]/[4]")
-    ap.add_argument("--only", choices=["c2", "c3", "c5", "d8k", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "d8k", "copy"], default=None,
                     help="run a single workload (for profiling); `copy` runs a plain 1 GiB "
                          "device copy that calibrates the FETCH_SIZE/WRITE_SIZE counters")
     return ap.parse_args()
@@ -279,6 +279,68 @@ def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096
     }
 
 
+def bench_c4(torch, ops, sessmod, ctx, steps, warmup, softcap=50.0, seed=5):
+    """Gemma3-style 6-layer group (5 sliding W=1024 + 1 global), 8/4/256 bf16,
+    scale 1/16, score softcap 50, through the native session: prefill 4096 in 128-token
+    chunks, then 128 single-token decode steps."""
+    hq, hkv, d, W, prompt, dec, layers = 8, 4, 256, 1024, 4096, 128, 6
+    total = prompt + dec
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    io, outs = [], []
+    for _ in range(layers):
+        out = torch.zeros(total, hq * d, dtype=torch.float32, device="cuda")
+        io.append(sessmod.LayerIo(torch.randn(total, hq, d, generator=g, device="cuda"),
+                                  torch.randn(total, hkv, d, generator=g, device="cuda"),
+                                  torch.randn(total, hkv, d, generator=g, device="cuda"), out))
+        outs.append(out)
+    windows = [W] * 5 + [0]
+    sess = sessmod.Session(ctx, sessmod.Options(
+        capacity=total, prefill_chunk_size=128, vocab_size=262144, layers=layers, query_heads=hq,
+        kv_heads=hkv, head_dim=d, storage="bf16", score_scale=1.0 / 16.0, softcap=softcap,
+        theta=1e6, layer_windows=windows))
+    tokens = [1] * total
+
+    def prefill():
+        sess.reset()
+        sess.set_tokens(tokens[:prompt])
+        sess.evaluate(io)
+        sess.synchronize()
+
+    def decode():
+        sess.append(tokens[prompt:])
+        sess.evaluate(io, chunk_limit=1)
+        sess.synchronize()
+
+    for _ in range(warmup):
+        prefill()
+        decode()
+    pre_s = dec_s = 0.0
+    for _ in range(steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        prefill()
+        pre_s += time.perf_counter() - t0
+        t0 = time.perf_counter()
+        decode()
+        dec_s += time.perf_counter() - t0
+    pairs_global = sum(p + 1 for p in range(prompt))
+    pairs_sliding = sum(min(p + 1, W) for p in range(prompt))
+    flops = 4.0 * hq * d * (pairs_global + 5 * pairs_sliding)
+    per_key = 2 * hkv * d * 2
+    dbytes = sum(per_key * ((p + 1) + 5 * min(p + 1, W)) + layers * hq * d * 6
+                 for p in range(prompt, total))
+    return {
+        "layers": "5 sliding (W=1024) + 1 global", "softcap": softcap,
+        "prefill_ms": pre_s / steps * 1e3,
+        "prefill_tflops": flops * steps / pre_s / 1e12,
+        "prefill_gflop": flops / 1e9,
+        "decode_ms": dec_s / steps * 1e3,
+        "decode_us_per_token": dec_s / steps / dec * 1e6,
+        "decode_gbs": dbytes * steps / dec_s / 1e9,
+        "tokens_per_s": total * steps / (pre_s + dec_s),
+    }
+
+
 def copy_calibration(torch, nbytes=1 << 30, reps=3):
     """A plain device copy of known size: its FETCH_SIZE/WRITE_SIZE per dispatch
     (rocprofv3 --pmc) against nbytes gives the counters' scale factor."""
@@ -390,6 +452,10 @@ def main():
                                 dtype=torch.float16)
         log("c3: " + json.dumps(c3))
         result["c3"] = c3
+    if not args.no_north_star and args.only in (None, "c4"):
+        c4 = bench_c4(torch, ops, sessmod, ctx, 2, 1)
+        log("c4: " + json.dumps(c4))
+        result["c4"] = c4
     if not args.no_north_star and args.only in (None, "c5"):
         c5 = bench_prefill_batch(torch, ops, ctx, 10, 2)
         log("c5: " + json.dumps(c5))
@@ -440,7 +506,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(c2["prefill_kernel_tflops"] / PEAK_BF16_TFLOPS, 5),
         },
-        "north_star": {k: result[k] for k in ("decode_8k", "c3", "c5") if k in result},
+        "north_star": {k: result[k] for k in ("decode_8k", "c3", "c4", "c5") if k in result},
         "detail": c2,
     }
     if not args.no_cpu and w is not None:

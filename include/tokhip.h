@@ -388,8 +388,11 @@ uint32_t tkh_session_evaluate(tkh_session *s, const tkh_layer_io *layers, uint64
                               uint64_t *evaluated, tkh_error *err);
 
 /* Waits for queued chunks and checks the status word.  On failure the
- * session returns to the last checked prefix (sessions with sliding layers
- * check every chunk and never hold provisional commits). */
+ * provisional chunks are dropped: the session returns to the last checked
+ * prefix, or, with sliding layers, to the end of the last chunk whose ring
+ * commit ran before the failure (ring commits of a queued context run on the
+ * device only while the status word is clean).  set_tokens,
+ * discard_pending and reset settle provisional chunks first. */
 uint32_t tkh_session_synchronize(tkh_session *s, tkh_error *err);
 
 #ifdef __cplusplus

@@ -263,4 +263,74 @@ def test_session_queued_context_matches_synchronous(torch_mod, ops, sess_mod):
         s.synchronize()
         assert s.evaluated_len() == total
         outs.append(host(out))
+        s.close()
+        c.close()
     assert np.array_equal(outs[0], outs[1])
+
+
+def test_queued_ring_session_failure_rolls_back_to_last_ring_commit(torch_mod, ops, sess_mod, orc):
+    """Queued context, a sliding (W=32, ring) and a global layer, chunks of 16: a NaN in
+    the fourth chunk's keys surfaces at synchronize; the session stands at the end of
+    the third chunk (its last ring commit), and evaluating again from there with clean
+    inputs matches the oracle, so the rings held exactly the committed chunks."""
+    torch = torch_mod
+    rng = np.random.default_rng(7)
+    L, hq, hkv, D, total, W = 2, 4, 2, 64, 100, 32
+    qs, ks, vs, wq, wk = _session_inputs(rng, L, total, hq, hkv, D)
+    c = ops.Context(0, synchronous=False)
+    s = sess_mod.Session(c, sess_mod.Options(capacity=total, prefill_chunk_size=16, vocab_size=10,
+                                             layers=L, query_heads=hq, kv_heads=hkv, head_dim=D,
+                                             storage="f16", score_scale=0.125,
+                                             layer_windows=[W, 0]))
+    ctxs = [torch.zeros((total, hq * D), dtype=torch.float32, device="cuda") for _ in range(L)]
+    kbad = ks[0].copy()
+    kbad[50, 0, 7] = np.nan   # chunk [48, 64)
+    io = [sess_mod.LayerIo(_t(torch, qs[l]), _t(torch, kbad if l == 0 else ks[l]), _t(torch, vs[l]),
+                           ctxs[l], _t(torch, wq[l]), _t(torch, wk[l])) for l in range(L)]
+    s.set_tokens([1] * total)
+    assert s.evaluate(io) == total          # queued: nothing checked yet
+    with pytest.raises(ops.TkhError) as e:
+        s.synchronize()
+    assert e.value.name == "NonFinite"
+    assert (s.evaluated_len(), s.pending_len()) == (48, total - 48)
+    io[0].k_proj = _t(torch, ks[0])
+    assert s.evaluate(io) == total - 48
+    s.synchronize()
+    for l, window in enumerate([W, None]):
+        q = stored(_oracle_produce(orc, qs[l], wq[l], total, hq, D, 0), "f16")
+        k = stored(_oracle_produce(orc, ks[l], wk[l], total, hkv, D, 0), "f16")
+        v = stored(vs[l], "f16")
+        ref, _, _ = orc.window_attention(q.reshape(-1), k.transpose(1, 0, 2).reshape(-1),
+                                         v.transpose(1, 0, 2).reshape(-1), total, total, total, hq,
+                                         hkv, D, 0, 0, window, 0.125)
+        err = max_err(host(ctxs[l]).reshape(-1), ref)
+        log(f"queued ring session layer {l}: max abs error {err:.3e}")
+        assert err <= TOL_HALF
+    s.close()
+    c.close()
+
+
+def test_queued_linear_session_failure_returns_to_checked_prefix(torch_mod, ops, sess_mod):
+    torch = torch_mod
+    rng = np.random.default_rng(8)
+    hq, hkv, D, total = 4, 2, 64, 64
+    qs, ks, vs, wq, wk = _session_inputs(rng, 1, total, hq, hkv, D)
+    c = ops.Context(0, synchronous=False)
+    s = sess_mod.Session(c, sess_mod.Options(capacity=total, prefill_chunk_size=16, vocab_size=10,
+                                             layers=1, query_heads=hq, kv_heads=hkv, head_dim=D,
+                                             storage="bf16"))
+    out = torch.zeros((total, hq * D), dtype=torch.float32, device="cuda")
+    vbad = vs[0].copy()
+    vbad[40, 1, 0] = np.inf
+    io = [sess_mod.LayerIo(_t(torch, qs[0]), _t(torch, ks[0]), _t(torch, vbad), out, None, None)]
+    s.set_tokens([1] * 32)
+    s.evaluate(io)
+    s.synchronize()                          # 32 tokens checked
+    s.append([1] * 32)
+    s.evaluate(io)
+    with pytest.raises(ops.TkhError):
+        s.synchronize()
+    assert (s.evaluated_len(), s.pending_len()) == (32, 32)
+    assert not s.distribution_valid()
+    s.close()
+    c.close()

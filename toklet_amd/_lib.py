@@ -6,8 +6,10 @@ an error: there is no CPU fallback behind these bindings.
 
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
+import weakref
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtokhip.so")
@@ -161,3 +163,25 @@ def load():
             fn.argtypes = args
         _lib = lib
     return _lib
+
+
+# Handles still open when the interpreter exits are closed here, before the
+# HIP runtime's own teardown: sessions, then KV owners, then contexts (an
+# object kept alive only by a reference cycle would otherwise be finalised
+# after the runtime is gone).
+_live = {0: weakref.WeakSet(), 1: weakref.WeakSet(), 2: weakref.WeakSet()}
+SESSION, KV_OWNER, CONTEXT = 0, 1, 2
+
+
+def track(obj, order: int):
+    _live[order].add(obj)
+
+
+@atexit.register
+def _close_all():
+    for order in (SESSION, KV_OWNER, CONTEXT):
+        for obj in list(_live[order]):
+            try:
+                obj.close()
+            except Exception:
+                pass

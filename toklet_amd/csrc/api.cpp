@@ -32,7 +32,9 @@ extern "C" hipError_t tkh_launch_kv_append(int src, int dst, const void *k, cons
 extern "C" hipError_t tkh_launch_copy_runs(const void *src_k, const void *src_v, void *dst_k,
                                            void *dst_v, int64_t tokens, int heads,
                                            int64_t row_bytes, int64_t capacity,
-                                           const int64_t runs[6], hipStream_t stream);
+                                           const int64_t runs[6], const uint32_t *gate,
+                                           uint64_t *committed, uint64_t committed_value,
+                                           hipStream_t stream);
 extern "C" hipError_t tkh_launch_check_finite(int dtype, const void *a, const void *b, int64_t n,
                                               uint32_t *status, hipStream_t stream);
 extern "C" hipError_t tkh_launch_softcap(float *x, int64_t n, float cap, uint32_t *status,
@@ -1143,8 +1145,15 @@ uint32_t tkh_kv_view(const tkh_kv *kv, const tkh_kv_frame *frame, uint64_t query
     return ok(err);
 }
 
-uint32_t tkh_kv_commit_batch(tkh_kv *const *kvs, const tkh_kv_frame *frames, uint64_t count,
-                             tkh_error *err) {
+}  // extern "C"
+
+// commit_batch with an optional device gate: the copies of a gated commit run
+// only while the status word is clean, and the last one records
+// `committed_value` in `committed` (queued sessions read it back after a
+// failure to learn which chunks reached the rings).
+uint32_t tkh_host::commit_frames(tkh_kv *const *kvs, const tkh_kv_frame *frames, uint64_t count,
+                                 const uint32_t *gate, uint64_t *committed,
+                                 uint64_t committed_value, tkh_error *err) {
     if (count && (!kvs || !frames)) return invalid("kv batch", err);
     for (uint64_t i = 0; i < count; ++i) {
         if (!kvs[i]) return invalid("kv", err);
@@ -1166,7 +1175,9 @@ uint32_t tkh_kv_commit_batch(tkh_kv *const *kvs, const tkh_kv_frame *frames, uin
         HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
         HIP_TRY(tkh_launch_copy_runs(f.k, f.v, kv->k, kv->v, (int64_t)f.tokens, (int)kv->heads,
                                      (int64_t)(kv->dims * esize(kv->storage)),
-                                     (int64_t)kv->capacity, r, ctx->stream),
+                                     (int64_t)kv->capacity, r, gate,
+                                     i + 1 == count ? committed : nullptr, committed_value,
+                                     ctx->stream),
                 "KV commit");
         kv->offset += f.tokens;
         kv->generation += 1;
@@ -1174,6 +1185,13 @@ uint32_t tkh_kv_commit_batch(tkh_kv *const *kvs, const tkh_kv_frame *frames, uin
     for (uint64_t i = 0; i < count; ++i)
         if (kvs[i]->ctx->synchronous) HIP_TRY(hipStreamSynchronize(kvs[i]->ctx->stream), "KV commit");
     return ok(err);
+}
+
+extern "C" {
+
+uint32_t tkh_kv_commit_batch(tkh_kv *const *kvs, const tkh_kv_frame *frames, uint64_t count,
+                             tkh_error *err) {
+    return commit_frames(kvs, frames, count, nullptr, nullptr, 0, err);
 }
 
 uint32_t tkh_kv_reset_batch(tkh_kv *const *kvs, uint64_t count, tkh_error *err) {

@@ -141,3 +141,10 @@ struct tkh_kv {
     uint64_t offset = 0, generation = 0, owner = 0;
     uint64_t allocated_bytes = 0;
 };
+
+namespace tkh_host {
+// tkh_kv_commit_batch with an optional device gate (api.cpp).
+uint32_t commit_frames(tkh_kv *const *kvs, const tkh_kv_frame *frames, uint64_t count,
+                       const uint32_t *gate, uint64_t *committed, uint64_t committed_value,
+                       tkh_error *err);
+}  // namespace tkh_host

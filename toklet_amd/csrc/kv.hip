@@ -60,7 +60,14 @@ __global__ __launch_bounds__(256) void kv_copy_runs(const uint8_t *src_k, const 
                                                     int64_t row_bytes, int64_t capacity,
                                                     int64_t r0_src, int64_t r0_slot,
                                                     int64_t r0_rows, int64_t r1_src,
-                                                    int64_t r1_slot, int64_t r1_rows) {
+                                                    int64_t r1_slot, int64_t r1_rows,
+                                                    const uint32_t *gate, uint64_t *committed,
+                                                    uint64_t committed_value) {
+    // Gated commit (queued sessions): nothing is copied once the status word
+    // reports a failure in this or an earlier chunk; otherwise the session's
+    // device-side committed length moves to the end of this chunk.
+    if (gate && *(volatile const uint32_t *)gate != 0) return;
+    if (committed && blockIdx.x == 0 && threadIdx.x == 0) *committed = committed_value;
     const int64_t words = row_bytes / 2;  // rows are whole 2-byte units
     const int64_t rows = r0_rows + r1_rows;
     const int64_t total = (int64_t)heads * rows * words;
@@ -112,6 +119,7 @@ __global__ __launch_bounds__(256) void convert_from_f32(const float *src, void *
 }
 
 __global__ void fill_u32(uint32_t *p, uint32_t v) { *p = v; }
+__global__ void fill_u64(uint64_t *p, uint64_t v) { *p = v; }
 
 }  // namespace tkh
 
@@ -144,13 +152,16 @@ extern "C" hipError_t tkh_launch_kv_append(int src, int dst, const void *k, cons
 extern "C" hipError_t tkh_launch_copy_runs(const void *src_k, const void *src_v, void *dst_k,
                                            void *dst_v, int64_t tokens, int heads,
                                            int64_t row_bytes, int64_t capacity,
-                                           const int64_t runs[6], hipStream_t stream) {
-    int64_t rows = runs[2] + runs[5];
-    if (rows == 0) return hipSuccess;
-    dim3 grid(grid_for(heads * rows * (row_bytes / 2))), block(256);
+                                           const int64_t runs[6], const uint32_t *gate,
+                                           uint64_t *committed, uint64_t committed_value,
+                                           hipStream_t stream) {
+    const int64_t rows = runs[2] + runs[5];
+    if (rows == 0 && !committed) return hipSuccess;
+    dim3 grid(rows ? grid_for(heads * rows * (row_bytes / 2)) : 1), block(256);
     hipLaunchKernelGGL(kv_copy_runs, grid, block, 0, stream, (const uint8_t *)src_k,
                        (const uint8_t *)src_v, (uint8_t *)dst_k, (uint8_t *)dst_v, tokens, heads,
-                       row_bytes, capacity, runs[0], runs[1], runs[2], runs[3], runs[4], runs[5]);
+                       row_bytes, capacity, runs[0], runs[1], runs[2], runs[3], runs[4], runs[5],
+                       gate, committed, committed_value);
     return hipGetLastError();
 }
 
@@ -177,6 +188,11 @@ extern "C" hipError_t tkh_launch_convert(int dtype, const float *src, void *dst,
     else if (dtype == BF16) hipLaunchKernelGGL((convert_from_f32<BF16>), grid, block, 0, stream, src, dst, n);
     else if (dtype == F32) hipLaunchKernelGGL((convert_from_f32<F32>), grid, block, 0, stream, src, dst, n);
     else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+extern "C" hipError_t tkh_launch_fill_u64(uint64_t *p, uint64_t v, hipStream_t stream) {
+    hipLaunchKernelGGL(fill_u64, dim3(1), dim3(1), 0, stream, p, v);
     return hipGetLastError();
 }
 

@@ -18,6 +18,7 @@
 #include "host.hpp"
 
 extern "C" hipError_t tkh_launch_produce(const tkh::ProduceParams *p, int dtype, hipStream_t stream);
+extern "C" hipError_t tkh_launch_fill_u64(uint64_t *p, uint64_t v, hipStream_t stream);
 
 using namespace tkh_host;
 
@@ -117,6 +118,9 @@ struct tkh_session {
     uint64_t checked = 0;
     bool checked_valid = false;
     bool rings = false;                        // some layer keeps a ring cache
+    // Queued ring sessions: the end of the last chunk whose ring commit ran
+    // with a clean status word (written by the gated commit on the device).
+    uint64_t *committed_dev = nullptr;
     void *q_scratch = nullptr;                 // [chunk, Hq, D] cache dtype
     std::vector<void *> stage_k, stage_v;      // sliding layers: [Hkv, chunk, D]
     uint64_t scratch_bytes = 0, kv_bytes = 0;
@@ -129,6 +133,7 @@ void free_session(tkh_session *s) {
     if (s->ctx) hipSetDevice(s->ctx->device);
     for (auto *k : s->kv) tkh_kv_destroy(k);
     if (s->q_scratch) hipFree(s->q_scratch);
+    if (s->committed_dev) hipFree(s->committed_dev);
     for (auto *p : s->stage_k)
         if (p) hipFree(p);
     for (auto *p : s->stage_v)
@@ -179,12 +184,58 @@ uint64_t rewind(tkh_session *s, uint64_t keep) {
     bool restart = false;
     for (auto *kv : s->kv)
         if (kv->has_window && keep + 1 < kv->offset) restart = true;
+    const uint64_t kept = restart ? 0 : keep;
     for (auto *kv : s->kv) {
         if (!kv->has_window) continue;
-        kv->offset = restart ? 0 : std::min(kv->offset, keep);
+        kv->offset = std::min(kv->offset, kept);
         kv->generation += 1;  // frames prepared before the rewind are stale
     }
-    return restart ? 0 : keep;
+    if (s->committed_dev) tkh_launch_fill_u64(s->committed_dev, kept, s->ctx->stream);
+    return kept;
+}
+
+uint32_t synchronize(tkh_session *s, tkh_error *err);
+
+// Queued contexts: state edits first settle the provisional chunks, so that
+// a late failure cannot land on an edited history.
+void settle(tkh_session *s) {
+    if (s->ctx && !s->ctx->synchronous && s->checked != s->evaluated) synchronize(s, nullptr);
+}
+
+// Waits for queued work and checks the status word.  On failure the
+// provisional chunks are dropped: linear-cache sessions return to the last
+// checked prefix; ring sessions to the last chunk whose gated ring commit ran
+// (read back from the device), which is where their rings stand.
+uint32_t synchronize(tkh_session *s, tkh_error *err) {
+    if (!s->ctx) return ok(err);
+    uint32_t rc = tkh_context_synchronize(s->ctx, err);
+    if (rc == TKH_OK) {
+        s->checked = s->evaluated;
+        s->checked_valid = s->dist_valid;
+        return rc;
+    }
+    if (rc != TKH_NON_FINITE) return rc;
+    uint64_t back = s->checked;
+    bool valid = s->checked_valid;
+    if (s->rings) {
+        uint64_t c = s->checked;
+        if (hipMemcpy(&c, s->committed_dev, sizeof c, hipMemcpyDeviceToHost) == hipSuccess &&
+            c >= s->checked && c <= s->evaluated) {
+            valid = c > s->checked ? true : s->checked_valid;
+            back = c;
+        }
+        for (auto *kv : s->kv) {
+            if (!kv->has_window) continue;
+            kv->offset = back;
+            kv->generation += 1;
+        }
+    }
+    s->evaluated = back;
+    s->checked = back;
+    s->dist_valid = valid && back > 0;
+    s->checked_valid = s->dist_valid;
+    s->dist_replay = false;
+    return rc;
 }
 
 }  // namespace
@@ -251,6 +302,8 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
             s->rings |= ring;
         }
         hipError_t e = hipMalloc(&s->q_scratch, chunk * o->query_heads * D * es);
+        if (e == hipSuccess) e = hipMalloc(&s->committed_dev, sizeof(uint64_t));
+        if (e == hipSuccess) e = tkh_launch_fill_u64(s->committed_dev, 0, ctx->stream);
         s->scratch_bytes = chunk * o->query_heads * D * es;
         for (uint64_t l = 0; e == hipSuccess && l < o->layers; ++l) {
             if (!s->kv[l]->has_window) continue;
@@ -282,6 +335,7 @@ extern "C" uint32_t tkh_session_set_tokens(tkh_session *s, const uint32_t *token
                                            tkh_error *err) {
     if (!s) return invalid("session", err);
     TRY(validate_tokens(s, tokens, count, 0, err));
+    settle(s);
     uint64_t keep;
     bool recover;
     reusable_prefix(s->history, s->evaluated, tokens, count, s->dist_valid, &keep, &recover);
@@ -302,6 +356,7 @@ extern "C" uint32_t tkh_session_set_tokens(tkh_session *s, const uint32_t *token
 
 extern "C" void tkh_session_discard_pending(tkh_session *s) {
     if (!s) return;
+    settle(s);
     s->history.resize(std::min<uint64_t>(s->history.size(), s->evaluated + (s->dist_replay ? 1 : 0)));
     if (s->dist_replay) return;
     if (!s->dist_valid && s->evaluated > 0) {
@@ -314,6 +369,7 @@ extern "C" void tkh_session_discard_pending(tkh_session *s) {
 
 extern "C" void tkh_session_reset(tkh_session *s) {
     if (!s) return;
+    settle(s);
     s->history.clear();
     s->evaluated = 0;
     s->checked = 0;
@@ -324,6 +380,7 @@ extern "C" void tkh_session_reset(tkh_session *s) {
     for (auto *kv : s->kv)
         if (kv->has_window) rings.push_back(kv);
     if (!rings.empty()) tkh_kv_reset_batch(rings.data(), rings.size(), nullptr);
+    if (s->committed_dev) tkh_launch_fill_u64(s->committed_dev, 0, s->ctx->stream);
 }
 
 extern "C" uint32_t tkh_session_state_get(const tkh_session *s, tkh_session_state *out) {
@@ -456,13 +513,18 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
             frames.push_back(f);
         }
     }
-    // Commit only after every layer of the chunk succeeded.  Sliding layers
-    // overwrite ring rows on commit, so their sessions check the status first
-    // even on a queued context.
-    if (ctx->synchronous || !ring_kv.empty()) TRY(tkh_context_synchronize(ctx, err));
-    if (!ring_kv.empty()) TRY(tkh_kv_commit_batch(ring_kv.data(), frames.data(), ring_kv.size(), err));
+    // Commit only after every layer of the chunk succeeded.
+    if (ctx->synchronous) TRY(tkh_context_synchronize(ctx, err));
+    if (!ring_kv.empty()) {
+        // Queued: the ring copies run on the device only while the status word
+        // is clean, and record how far the rings got.
+        const bool gated = !ctx->synchronous;
+        TRY(commit_frames(ring_kv.data(), frames.data(), ring_kv.size(),
+                          gated ? ctx->status_dev : nullptr, gated ? s->committed_dev : nullptr,
+                          start + count, err));
+    }
     commit_state(s, count);
-    if (!ctx->synchronous && !s->rings) {
+    if (!ctx->synchronous) {
         // Provisional until tkh_session_synchronize confirms the status word.
         s->checked = checked;
         s->checked_valid = checked_valid;
@@ -511,16 +573,5 @@ extern "C" uint32_t tkh_session_evaluate(tkh_session *s, const tkh_layer_io *lay
 
 extern "C" uint32_t tkh_session_synchronize(tkh_session *s, tkh_error *err) {
     if (!s) return invalid("session", err);
-    if (!s->ctx) return ok(err);
-    uint32_t rc = tkh_context_synchronize(s->ctx, err);
-    if (rc == TKH_OK) {
-        s->checked = s->evaluated;
-        s->checked_valid = s->dist_valid;
-        return rc;
-    }
-    // Provisional chunks since the last check are not committed.
-    s->evaluated = s->checked;
-    s->dist_valid = s->checked_valid;
-    s->dist_replay = false;
-    return rc;
+    return synchronize(s, err);
 }

@@ -65,6 +65,7 @@ class _Owner:
                err)
         self.handle = handle
         self.storage = storage
+        _lib.track(self, _lib.KV_OWNER)
 
     def info(self) -> _lib.KvInfo:
         info = _lib.KvInfo()

@@ -61,6 +61,7 @@ class Context:
         _check(lib.tkh_context_create(device, ctypes.c_void_p(stream.cuda_stream), workspace_bytes,
                                       int(synchronous), ctypes.byref(handle), ctypes.byref(err)), err)
         self.handle = handle
+        _lib.track(self, _lib.CONTEXT)
 
     def synchronize(self):
         err = _lib.Error()

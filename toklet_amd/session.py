@@ -10,7 +10,7 @@ the per-chunk driver (producer, KV append or ring staging, attention, joint
 commit) are native code in libtokhip (``tkh_session_*``).
 
 ``Session(None, ...)`` builds a host-only session: its token state machine
-runs without a GPU, evaluation raises ``Unsupported``.
+runs without a GPU, and evaluation commits state without computing anything.
 """
 
 from __future__ import annotations
@@ -95,6 +95,7 @@ class Session:
         _check(lib.tkh_session_create(ctx.handle if ctx is not None else None, ctypes.byref(o),
                                       windows, ctypes.byref(handle), ctypes.byref(err)), err)
         self.handle = handle
+        _lib.track(self, _lib.SESSION)
 
     # ---- state (InferenceSession accessors)
     def _state(self):
