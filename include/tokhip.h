@@ -227,6 +227,7 @@ uint32_t tkh_kv_planned_bytes(uint64_t heads, uint64_t head_dim, uint64_t capaci
 uint32_t tkh_kv_create(tkh_context *ctx, uint64_t heads, uint64_t dims, uint64_t capacity,
                        uint64_t max_positions, uint32_t has_window, uint64_t window,
                        tkh_dtype storage, tkh_kv **out, tkh_error *err);
+/* Safe in any order with tkh_context_destroy of the owning context. */
 void tkh_kv_destroy(tkh_kv *kv);
 
 typedef struct tkh_kv_info {
@@ -337,6 +338,7 @@ typedef struct tkh_session_options {
  * for testing transitions without a device. */
 uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_options *options,
                             const uint64_t *layer_windows, tkh_session **out, tkh_error *err);
+/* Safe in any order with tkh_context_destroy of the owning context. */
 void tkh_session_destroy(tkh_session *s);
 
 /* Session::append / set_tokens (src/session.rs:320-356). */

@@ -1005,6 +1005,7 @@ uint32_t tkh_kv_create(tkh_context *ctx, uint64_t heads, uint64_t dims, uint64_t
     HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
     auto *kv = new tkh_kv();
     kv->ctx = ctx;
+    kv->device = ctx->device;
     kv->heads = heads;
     kv->dims = dims;
     kv->capacity = capacity;
@@ -1029,10 +1030,9 @@ uint32_t tkh_kv_create(tkh_context *ctx, uint64_t heads, uint64_t dims, uint64_t
 
 void tkh_kv_destroy(tkh_kv *kv) {
     if (!kv) return;
-    if (kv->ctx) {
-        hipSetDevice(kv->ctx->device);
-        hipStreamSynchronize(kv->ctx->stream);
-    }
+    // The owning context is not touched: it may already be destroyed.  hipFree
+    // waits for work still using the memory.
+    hipSetDevice(kv->device);
     if (kv->k) hipFree(kv->k);
     if (kv->v) hipFree(kv->v);
     delete kv;

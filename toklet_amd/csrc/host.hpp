@@ -132,6 +132,7 @@ struct tkh_context {
 
 struct tkh_kv {
     tkh_context *ctx = nullptr;
+    int device = 0;
     uint64_t heads = 0, dims = 0, capacity = 0, max_positions = 0;
     bool has_window = false;
     uint64_t window = 0;

@@ -107,6 +107,7 @@ extern "C" uint32_t tkh_produce_qkv(tkh_context *ctx, const tkh_producer_shape *
 
 struct tkh_session {
     tkh_context *ctx = nullptr;
+    int device = 0;
     tkh_session_options opt{};
     std::vector<uint64_t> windows;  // per layer, 0 = full retention
     std::vector<tkh_kv *> kv;       // per layer owner
@@ -130,7 +131,8 @@ namespace {
 
 void free_session(tkh_session *s) {
     if (!s) return;
-    if (s->ctx) hipSetDevice(s->ctx->device);
+    // Like tkh_kv_destroy, the context is not touched (it may be gone first).
+    if (s->ctx) hipSetDevice(s->device);
     for (auto *k : s->kv) tkh_kv_destroy(k);
     if (s->q_scratch) hipFree(s->q_scratch);
     if (s->committed_dev) hipFree(s->committed_dev);
@@ -269,6 +271,7 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
         return invalid("softcap must be finite and positive (0 disables)", err);
     auto *s = new tkh_session();
     s->ctx = ctx;
+    s->device = ctx ? ctx->device : 0;
     s->opt = *o;
     s->opt.prefill_chunk_size = std::min(o->prefill_chunk_size, o->capacity);
     // windows: the attention mask of each layer.  A window shorter than the
