@@ -236,7 +236,7 @@ def bench_decode_batch(torch, ops, ctx, steps, warmup, *, batch, lmin, lmax, dty
 
 
 def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096, tokens=128,
-                        seed=11):
+                        seed=11, dtype=None):
     """32 sessions x (4096 cached + 128 new causal), Llama-3-8B heads, bf16."""
     hq, hkv, d = 32, 8, 128
     gd = torch.Generator(device="cuda").manual_seed(seed)
@@ -244,9 +244,10 @@ def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096
     per = hkv * cap * d
     k = torch.randn(batch, hkv, cap, d, generator=gd, device="cuda")
     mask = torch.rand(batch, hkv, cap, 1, generator=gd, device="cuda") < 0.05
-    k = torch.where(mask, k * 8.0, k).to(torch.bfloat16).reshape(-1)
-    v = torch.randn(batch * per, generator=gd, device="cuda").to(torch.bfloat16)
-    q = torch.randn(batch, tokens, hq, d, generator=gd, device="cuda").to(torch.bfloat16)
+    dtype = dtype or torch.bfloat16
+    k = torch.where(mask, k * 8.0, k).to(dtype).reshape(-1)
+    v = torch.randn(batch * per, generator=gd, device="cuda").to(dtype)
+    q = torch.randn(batch, tokens, hq, d, generator=gd, device="cuda").to(dtype)
     out = torch.zeros(batch * tokens * hq * d, dtype=torch.float32, device="cuda")
     offsets = [b * per for b in range(batch)]
     strides = [cap * d] * batch

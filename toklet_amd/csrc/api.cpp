@@ -309,16 +309,42 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
     int64_t sk = (max_span + splits - 1) / splits;
     sk = std::max<int64_t>(32, (sk + 31) / 32 * 32);
     if (ctx->split_keys_override > 0) sk = (ctx->split_keys_override + 31) / 32 * 32;
+    // Splits are laid out segment by segment and never straddle a segment
+    // boundary (one base pointer per workgroup), so a view of several segments
+    // needs at least one split each; grow the split size until every problem
+    // fits the merge limit.
+    auto seg_split_counts = [&](tkh::Problem &p, int64_t keys_per_split) {
+        int64_t n_all = 0;
+        for (int sgi = 0; sgi < 3; ++sgi) {
+            int64_t n = 0;
+            if (sgi < p.nseg) {
+                const int64_t lo = std::max<int64_t>(p.vis_lo, p.seg[sgi].start);
+                const int64_t hi = std::min<int64_t>(p.vis_hi, p.seg[sgi].start + p.seg[sgi].keys);
+                if (hi > lo) n = (hi - lo + keys_per_split - 1) / keys_per_split;
+            }
+            p.seg_splits[sgi] = (int32_t)n;
+            n_all += n;
+        }
+        if (n_all == 0) {  // nothing visible: one empty split reports the bad mass
+            p.seg_splits[0] = 1;
+            n_all = 1;
+        }
+        return n_all;
+    };
+    for (;;) {
+        int64_t worst = 0;
+        for (auto &p : group) worst = std::max<int64_t>(worst, seg_split_counts(p, sk));
+        if (worst <= tkh_prefill_max_splits()) break;
+        sk *= 2;
+    }
     // Splits of one row block are combined by a second kernel, in merge blocks
     // of a few rows; Problem::part_base is the problem's first merge block.
     const int64_t merge_rows = tkh_prefill_merge_rows_per_block((int)D);
     int64_t wgs = 0, slots = 0, merge_blocks = 0;
     for (auto &p : group) {
-        p.split_keys = (int32_t)std::min<int64_t>(sk, INT32_MAX);
-        p.splits = (int32_t)std::max<int64_t>(1, (p.vis_hi - p.vis_lo + sk - 1) / sk);
-        if (p.splits > tkh_prefill_max_splits())
-            return fail(err, TKH_UNSUPPORTED, "batch", 0, tkh_prefill_max_splits(), p.splits,
-                        "prefill key splits exceed the merge limit");
+        if (sk > INT32_MAX) return fail(err, TKH_UNSUPPORTED, "keys", 0, 0, 0, "key range too large");
+        p.split_keys = (int32_t)sk;
+        p.splits = (int32_t)seg_split_counts(p, sk);
         p.tile_base = wgs;
         p.slot_base = slots;
         p.part_base = merge_blocks;

@@ -148,14 +148,27 @@ template <int LPT> __device__ __forceinline__ void ring_sync(int ahead) {
     __asm__ volatile("" ::: "memory");
 }
 
+// The running maximum of a row is moved (and O and l rescaled) only when a
+// tile's maximum exceeds it by more than 2^RESCALE_SLACK in probability: until
+// then probabilities up to 2^RESCALE_SLACK are accumulated against the stale
+// maximum, which bf16/f16 P and the FP32 accumulators hold exactly.  The final
+// division by l is unchanged, so the result is the same softmax.
+constexpr float RESCALE_SLACK = 8.0f;
+
+__device__ __forceinline__ int uniform32(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
 template <int DT, int D, bool CAP>
 __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(Params p) {
     constexpr int KS = D / 16;        // QK k-steps (16 features each)
     constexpr int MB = D / 32;        // PV M-blocks (32 features each)
     constexpr bool SPLIT_P = DT == BF16;
     static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
+    using L = PrefillLds<D>;
+    constexpr int NS = L::stages;
+    constexpr int RPW = L::runs_per_wave;
+    constexpr int LPT = 2 * RPW;      // direct loads per wave per tile (K + V)
 
-    __shared__ __attribute__((aligned(16))) uint8_t lds_raw[PrefillLds<D>::bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_raw[L::bytes];
     lds_ptr<uint8_t> lds = (lds_ptr<uint8_t>)lds_raw;
 
     const int wave = threadIdx.x >> 6;
@@ -183,14 +196,32 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     const int Hq = p.query_heads;
     const int m_kv = pr->queries * G;
 
+    // This split's segment: splits are laid out segment by segment over the
+    // visible range and never straddle a boundary, so one base pointer and
+    // row stride serve every tile of the workgroup.
+    int seg = 0, sidx = split;
+    if (sidx >= pr->seg_splits[0]) {
+        sidx -= pr->seg_splits[0];
+        seg = 1;
+        if (sidx >= pr->seg_splits[1]) {
+            sidx -= pr->seg_splits[1];
+            seg = 2;
+        }
+    }
+    const int64_t seg_start = pr->seg[seg].start;
+    const int64_t seg_end = seg_start + pr->seg[seg].keys;
+    const int64_t seg_lo = seg_start > pr->vis_lo ? seg_start : pr->vis_lo;
+    const int64_t seg_hi = seg_end < pr->vis_hi ? seg_end : pr->vis_hi;
+    const int64_t s_lo = seg_lo + (int64_t)sidx * pr->split_keys;
+    const int64_t s_hi = s_lo + pr->split_keys < seg_hi ? s_lo + pr->split_keys : seg_hi;
+
     // This lane's query row.
     const int row = rb * PF_ROWS + wave * 32 + j;
     const bool rvalid = row < m_kv;
     const int rrow = rvalid ? row : m_kv - 1;
     const int t_row = rrow / G, h_row = kvh * G + rrow % G;
-    const int64_t pos = pr->q_pos0 + t_row;
     int64_t r_lo, r_hi;
-    visible_range(p, pr->k_pos0, pr->keys, pos, &r_lo, &r_hi);
+    visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + t_row, &r_lo, &r_hi);
     if (!rvalid) r_hi = r_lo;  // no visible keys: never contributes, never stored
 
     // Key range of the workgroup: the union over its rows, clipped to the split.
@@ -199,24 +230,34 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     int64_t k_lo, k_hi, tmp;
     visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + wg_row_first / G, &k_lo, &tmp);
     visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + wg_row_last / G, &tmp, &k_hi);
+    if (k_lo < s_lo) k_lo = s_lo;
+    if (k_hi > s_hi) k_hi = s_hi;
+    if (k_hi < k_lo) k_hi = k_lo;
+    const int nkeys = uniform32((int)(k_hi - k_lo));
+    const int ntiles = (nkeys + PF_KT - 1) / PF_KT;
+    const int nlast = nkeys - (ntiles - 1) * PF_KT;  // keys of the last tile
+    // Tiles [tf_lo, tf_hi) are visible to every row of this wave (no mask).
+    int tf_lo, tf_hi;
     {
-        const int64_t s_lo = pr->vis_lo + (int64_t)split * pr->split_keys;
-        const int64_t s_hi = s_lo + pr->split_keys;
-        if (k_lo < s_lo) k_lo = s_lo;
-        if (k_hi > s_hi) k_hi = s_hi;
-        if (k_hi < k_lo) k_hi = k_lo;
+        const int w_first = min(wg_row_first + wave * 32, m_kv - 1);
+        const int w_last = min(wg_row_first + wave * 32 + 31, m_kv - 1);
+        int64_t a, b, full_lo, full_hi;
+        visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + w_first / G, &a, &full_hi);
+        visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + w_last / G, &full_lo, &b);
+        int64_t lo_t = full_lo - k_lo;
+        lo_t = lo_t <= 0 ? 0 : (lo_t + PF_KT - 1) / PF_KT;
+        int64_t hi_t = full_hi - k_lo;
+        hi_t = hi_t <= 0 ? 0 : hi_t / PF_KT;
+        if (hi_t > ntiles - (nlast < PF_KT ? 1 : 0)) hi_t = ntiles - (nlast < PF_KT ? 1 : 0);
+        tf_lo = uniform32((int)(lo_t < ntiles ? lo_t : ntiles));
+        tf_hi = uniform32((int)hi_t);
     }
-    // Keys the whole wave sees (tiles inside this need no mask).
-    const int w_first = min(wg_row_first + wave * 32, m_kv - 1);
-    const int w_last = min(wg_row_first + wave * 32 + 31, m_kv - 1);
-    int64_t wfull_lo, wfull_hi;
+    // This row's visible keys relative to k_lo.
+    int rlo0, rhi0;
     {
-        int64_t a, b;
-        visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + w_first / G, &a, &wfull_hi);
-        visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + w_last / G, &wfull_lo, &b);
-        // Wave-uniform by construction; say so, so the full-tile test is a scalar branch.
-        wfull_lo = uniform64(wfull_lo);
-        wfull_hi = uniform64(wfull_hi);
+        int64_t x = r_lo - k_lo, y = r_hi - k_lo;
+        rlo0 = (int)(x < 0 ? 0 : (x > nkeys ? nkeys : x));
+        rhi0 = (int)(y < 0 ? 0 : (y > nkeys ? nkeys : y));
     }
 
     // Q^T B operands: lane holds row j, features 16 ks + 8 h .. + 7.
@@ -232,71 +273,47 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     for (int mb = 0; mb < MB; ++mb)
         for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
     float m_run = NEG_INF, l_run = 0.0f;
-    // Raw-score extremes over the visible range: +/-inf inputs show up here,
-    // NaN propagates into the mass and the context.
-    float raw_max = NEG_INF, raw_min = -NEG_INF;
+    bool bad = false;  // an infinite visible score (NaN reaches the mass and the context)
     const float scale = p.scale, softcap = p.softcap, softcap_inv = p.softcap_inv;
     const float tmul = CAP ? 1.0f : p.scale_log2;  // t units -> log2 units
+    const float slack = RESCALE_SLACK / tmul;      // in t units
+    float m_thr = NEG_INF;                         // rescale when a tile maximum exceeds this
 
-    // ---- tiles: walk [k_lo, k_hi) segment by segment in steps of PF_KT keys.
-    using L = PrefillLds<D>;
-    constexpr int NS = L::stages;
-    constexpr int LPT = 2 * L::runs_per_wave;  // direct loads per wave per tile (K + V)
-
-    // The segment piece tiles are issued from, cached in scalars.
-    int iseg = 0;
-    const uint8_t *pk = nullptr, *pv = nullptr;  // row of logical key `pstart`, this KV head
-    int64_t pstart = 0, pend = 0;
-    int prow = 0;                                // bytes between consecutive keys
-    auto enter_piece = [&](int64_t key) {
-        while (iseg < pr->nseg - 1 && key >= pr->seg[iseg].start + pr->seg[iseg].keys) ++iseg;
-        const auto &sg = pr->seg[iseg];
-        pstart = sg.start;
-        pend = min(k_hi, sg.start + sg.keys);
-        prow = (int)(sg.row_stride * 2);
-        pk = reinterpret_cast<const uint8_t *>(sg.k) + (int64_t)kvh * sg.head_stride * 2;
-        pv = reinterpret_cast<const uint8_t *>(sg.v) + (int64_t)kvh * sg.head_stride * 2;
-    };
-    int64_t ikey = k_lo;  // first key of the next tile to issue
-    if (ikey < k_hi) enter_piece(ikey);
-
-    // Per-lane part of the direct-load addresses (row in the tile, swizzled chunk).
-    int run_row[L::runs_per_wave], run_col[L::runs_per_wave];
-    for (int i = 0; i < L::runs_per_wave; ++i) {
-        const int pos = (wave * L::runs_per_wave + i) * 1024 + lane * 16;
-        run_row[i] = pos / L::row;
-        run_col[i] = (((pos % L::row) >> 4) ^ L::swz(run_row[i])) * 16;
+    // ---- K/V tiles: PF_KT keys each, issued into an NS-stage LDS ring.
+    const int prow = uniform32((int)(pr->seg[seg].row_stride * 2));  // bytes between keys
+    const int64_t first = (int64_t)kvh * pr->seg[seg].head_stride + (k_lo - seg_start) * pr->seg[seg].row_stride;
+    const uint8_t *k_next = reinterpret_cast<const uint8_t *>(pr->seg[seg].k) + uniform64(first * 2);
+    const uint8_t *v_next = reinterpret_cast<const uint8_t *>(pr->seg[seg].v) + uniform64(first * 2);
+    // Per-lane offsets of the direct loads (row in the tile, swizzled chunk);
+    // rows past the last tile's keys repeat a valid row.
+    int off_full[RPW], off_last[RPW];
+    for (int i = 0; i < RPW; ++i) {
+        const int pos = (wave * RPW + i) * 1024 + lane * 16;
+        const int rr = pos / L::row;
+        const int cc = (((pos % L::row) >> 4) ^ L::swz(rr)) * 16;
+        off_full[i] = rr * prow + cc;
+        off_last[i] = (rr < nlast ? rr : nlast - 1) * prow + cc;
     }
-    // Issue the tile at `ikey` into stage `st`; returns its key count.
-    auto issue = [&](int st) -> int {
-        const int nk = (int)min<int64_t>(PF_KT, pend - ikey);
-        const int64_t first = (ikey - pstart) * prow;
-        const uint8_t *kb = pk + first, *vb = pv + first;
+    int t_next = 0;
+    auto issue = [&](int st) {
+        const bool last = t_next == ntiles - 1;
         lds_ptr<uint8_t> kt = lds + st * L::stage;
-        for (int i = 0; i < L::runs_per_wave; ++i) {
-            const int run = wave * L::runs_per_wave + i;
-            const int re = run_row[i] < nk ? run_row[i] : nk - 1;  // past the keys: repeat a valid row
-            const uint32_t off = (uint32_t)(re * prow + run_col[i]);
-            dma16(kb + off, kt + run * 1024);
-            dma16(vb + off, kt + L::tile + run * 1024);
+        for (int i = 0; i < RPW; ++i) {
+            const int run = wave * RPW + i;
+            const uint32_t off = (uint32_t)(last ? off_last[i] : off_full[i]);
+            dma16(k_next + off, kt + run * 1024);
+            dma16(v_next + off, kt + L::tile + run * 1024);
         }
-        ikey += nk;
-        if (ikey >= pend && ikey < k_hi) enter_piece(ikey);
-        return nk;
+        k_next += PF_KT * prow;
+        v_next += PF_KT * prow;
+        ++t_next;
+    };
+    // Wait for tile `t` (issued earlier) and synchronise the workgroup.
+    auto wait_tile = [&](int t) {
+        const int ahead = t_next - 1 - t;  // later tiles still allowed in flight
+        ring_sync<LPT>(ahead);
     };
 
-    // Queue of issued tiles (first key, key count), oldest first.
-    int64_t qk[NS - 1];
-    int qn[NS - 1];
-    int queued = 0;
-    for (int i = 0; i < NS - 1; ++i) {
-        qk[i] = ikey;
-        qn[i] = 0;
-        if (ikey < k_hi) {
-            qn[i] = issue(i);
-            ++queued;
-        }
-    }
     // LDS offsets of this lane's operand reads (tile-relative).
     int k_off[KS];
     for (int ks = 0; ks < KS; ++ks) k_off[ks] = L::at(j, 2 * ks + h);
@@ -312,153 +329,182 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         }
     }
 
-    // S^T = K Q^T of the tile in stage `stg` (32 keys x 32 rows); lane: row j,
-    // keys 8q + 4h + r.
-    auto scores_of = [&](int stg) {
-        lds_ptr<uint8_t> kt = lds + stg * L::stage;
-        f32x16 sc;
-        for (int i = 0; i < 16; ++i) sc[i] = 0.0f;
-        for (int ks = 0; ks < KS; ++ks)
-            sc = mfma32<DT>(*(lds_ptr<u32x4>)(kt + k_off[ks]), qb[ks], sc);
-        return sc;
-    };
-
-    // Software pipeline: iteration t forms the scores of tile t + 1 while it
-    // runs the softmax and P.V of tile t, so the matrix cores have independent
-    // work while the vector unit computes probabilities.
-    int stage = 0;
+    // Software pipeline.  Iteration t:
+    //   1. P.V of tile t - 1 on the matrix cores, with the statistics of tile
+    //      t's scores (mask, maximum, rescale decision) and the first half of
+    //      its probabilities on the vector unit between those MFMAs;
+    //   2. wait for tile t + 1 and hand the stage of tile t - 1 to a new load;
+    //   3. the scores of tile t + 1 (QK MFMAs) with the second half of tile t's
+    //      probabilities between them;
+    //   4. read tile t's V^T operands for step 1 of the next iteration.
+    // Scheduling fences keep that interleave; every MFMA slot is a compile-time
+    // position.  In iteration 0 step 1 multiplies zero operands, and after the
+    // last tile step 3 scores stale LDS data (of a stage that holds an earlier
+    // tile) that is never used.
+    constexpr int NPV = 2 * MB * (SPLIT_P ? 2 : 1);  // P.V MFMAs per tile
+    constexpr int W = SPLIT_P ? 2 : 1;
+    for (int t = 0; t < NS - 1 && t < ntiles; ++t) issue(t);
     f32x16 st;
-    if (queued > 0) {
-        ring_sync<LPT>(queued - 1);
-        st = scores_of(0);
+    for (int i = 0; i < 16; ++i) st[i] = 0.0f;
+    if (ntiles > 0) {
+        wait_tile(0);
+        for (int ks = 0; ks < KS; ++ks) st = mfma32<DT>(*(lds_ptr<u32x4>)(lds + k_off[ks]), qb[ks], st);
     }
-    while (queued > 0) {
-        const int64_t cur_key = qk[0];
-        const int nkeys = qn[0];
-        const bool next = queued > 1;
-        f32x16 st_next;
+    u32x4 vop[2][MB];                  // V^T operands of the tile whose P.V is pending
+    uint32_t ph[8], pl[8];             // its probabilities (bf16: head and remainder)
+    for (int stp = 0; stp < 2; ++stp)
+        for (int mb = 0; mb < MB; ++mb) vop[stp][mb] = u32x4{0, 0, 0, 0};
+    for (int i = 0; i < 8; ++i) {
+        ph[i] = 0u;
+        pl[i] = 0u;
+    }
+    int stage = 0;
+    for (int t = 0; t < ntiles; ++t) {
         const int stage_next = stage + 1 == NS ? 0 : stage + 1;
         lds_ptr<uint8_t> vt = lds + stage * L::stage + L::tile;
         lds_ptr<uint8_t> kn = lds + stage_next * L::stage;
-        const int stage_free = stage == 0 ? NS - 1 : stage - 1;
-        stage = stage_next;
 
-        // ---- scores, mask, online softmax.  t = raw dot (or, with the softcap,
-        // the capped score in log2 units); p = 2^(t * tmul - m * tmul), where
-        // both transforms are increasing so the tile maximum follows from the
-        // raw maximum.
-        float t[16];
-        for (int i = 0; i < 16; ++i) {
-            if constexpr (CAP) t[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
-            else t[i] = st[i];
-        }
-        const bool full = nkeys == PF_KT && cur_key >= wfull_lo && cur_key + PF_KT <= wfull_hi;
-        float hi, lo;
-        if (full) {
-            hi = fmaxf(fmaxf(st[0], st[1]), st[2]);
-            lo = fminf(fminf(st[0], st[1]), st[2]);
-            for (int i = 3; i < 16; ++i) {
-                hi = fmaxf(hi, st[i]);
-                lo = fminf(lo, st[i]);
+        // ---- step 1.  t = raw dot (or, with the softcap, the capped score in
+        // log2 units); p = 2^(t * tmul - m * tmul).  Both transforms are
+        // increasing, so the tile maximum follows from the raw one.
+        float tv[CAP ? 16 : 1];  // softcapped scores (the raw scores serve otherwise)
+        float hi = NEG_INF, corr = 1.0f, nbase = 0.0f;
+        bool rescale = false;
+        uint32_t nh[4], nl[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < NPV; ++k) {
+            {
+                const int stp = k / (MB * W), mb = (k / W) % MB, part = k % W;
+                const u32x4 bv = part ? u32x4{pl[4 * stp], pl[4 * stp + 1], pl[4 * stp + 2], pl[4 * stp + 3]}
+                                      : u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
+                acc[mb] = mfma32<DT>(vop[stp][mb], bv, acc[mb]);
             }
-        } else {
-            // Visible keys of this row inside the tile: [lo_rel, hi_rel).
-            const int64_t a = r_lo - cur_key, b = min(r_hi, cur_key + nkeys) - cur_key;
-            const int lo_rel = (int)(a < 0 ? 0 : (a > PF_KT ? PF_KT : a));
-            const int hi_rel = (int)(b < 0 ? 0 : (b > PF_KT ? PF_KT : b));
-            hi = NEG_INF;
-            lo = -NEG_INF;
-            for (int i = 0; i < 16; ++i) {
-                const int kk = 8 * (i >> 2) + 4 * h + (i & 3);
-                const bool vis = kk >= lo_rel && kk < hi_rel;
-                hi = fmaxf(hi, vis ? st[i] : NEG_INF);
-                lo = fminf(lo, vis ? st[i] : -NEG_INF);
-                t[i] = vis ? t[i] : NEG_INF;
+            __builtin_amdgcn_sched_barrier(0);
+            if (k == 0) {
+                if (t >= tf_lo && t < tf_hi) {
+                    hi = fmaxf(fmaxf(st[0], st[1]), st[2]);
+                    float lo = fminf(fminf(st[0], st[1]), st[2]);
+                    for (int i = 3; i < 16; ++i) {
+                        hi = fmaxf(hi, st[i]);
+                        lo = fminf(lo, st[i]);
+                    }
+                    bad |= lo == NEG_INF;
+                    if constexpr (CAP)
+                        for (int i = 0; i < 16; ++i) tv[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
+                } else {
+                    // Visible keys of this row inside the tile: [lo_rel, hi_rel).
+                    const int lo_rel = min(max(rlo0 - t * PF_KT, 0), PF_KT);
+                    const int hi_rel = min(max(rhi0 - t * PF_KT, 0), PF_KT);
+                    for (int i = 0; i < 16; ++i) {
+                        const int kk = 8 * (i >> 2) + 4 * h + (i & 3);
+                        const bool vis = kk >= lo_rel && kk < hi_rel;
+                        bad |= vis && st[i] == NEG_INF;
+                        hi = fmaxf(hi, vis ? st[i] : NEG_INF);
+                        if constexpr (CAP) tv[i] = vis ? softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E : NEG_INF;
+                        else st[i] = vis ? st[i] : NEG_INF;  // masked in place: no copy of the scores
+                    }
+                }
             }
+            if (k == (NPV > 1 ? 1 : 0)) {
+                bad |= hi == -NEG_INF;
+                float mt;
+                if constexpr (CAP) mt = hi == NEG_INF ? NEG_INF : softcap_fast(hi * scale, softcap, softcap_inv) * LOG2E;
+                else mt = hi;
+                const uint32_t u = __builtin_bit_cast(uint32_t, mt);
+                const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+                const uint32_t a0 = pr32[0], a1 = pr32[1];
+                mt = fmaxf(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+                // Rare: a maximum moved past the slack.  l and the maximum change
+                // now; O, which still receives tile t - 1's P.V, after step 1.
+                if (__ballot(mt > m_thr) != 0) {
+                    const float m_new = fmaxf(m_run, mt);
+                    if (m_new != m_run) {
+                        corr = m_run == NEG_INF ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * tmul);
+                        l_run *= corr;
+                        m_run = m_new;
+                        m_thr = m_new == NEG_INF ? NEG_INF : m_new + slack;
+                    }
+                    rescale = true;
+                }
+                nbase = m_run == NEG_INF ? 0.0f : -m_run * tmul;
+            }
+            // First half of tile t's probabilities (tile t - 1's are still being read).
+            for (int i = 0; i < 4; ++i) {
+                if (k == (NPV > 2 ? 2 + (i * (NPV - 2)) / 4 : NPV - 1)) {
+                    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
+                    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
+                    nh[i] = pack2<DT>(e0, e1);
+                    if constexpr (SPLIT_P) nl[i] = pack2<DT>(e0 - lo_f<DT>(nh[i]), e1 - hi_f<DT>(nh[i]));
+                    l_run += e0 + e1;
+                    // Pin the pair here: the compiler would otherwise sink it to
+                    // its use after step 1, out of the MFMA shadow.
+                    asm volatile("" : "+v"(nh[i]), "+v"(nl[i]), "+v"(l_run));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        raw_max = fmaxf(raw_max, hi);
-        raw_min = fminf(raw_min, lo);
-        float mt;
-        if constexpr (CAP) mt = hi == NEG_INF ? NEG_INF : softcap_fast(hi * scale, softcap, softcap_inv) * LOG2E;
-        else mt = hi;
-        {
-            const uint32_t u = __builtin_bit_cast(uint32_t, mt);
-            const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-            const uint32_t a0 = pr32[0], a1 = pr32[1];
-            mt = fmaxf(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
-        }
-        const float m_new = fmaxf(m_run, mt);
-        if (__ballot(m_new != m_run) != 0) {
-            const float corr = m_new == NEG_INF ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * tmul);
-            l_run *= corr;
+        if (rescale)
             for (int mb = 0; mb < MB; ++mb)
                 for (int i = 0; i < 16; ++i) acc[mb][i] *= corr;
-            m_run = m_new;
-        }
-        const float nbase = m_run == NEG_INF ? 0.0f : -m_run * tmul;
-
-        if (next) {
-            // Tile t + 1 resident; everyone is done with tile t - 1, whose stage
-            // takes the next load.
-            ring_sync<LPT>(queued - 2);
-            const int64_t new_key = ikey;
-            int new_n = 0;
-            if (ikey < k_hi) new_n = issue(stage_free);
-            for (int i = 0; i < NS - 2; ++i) {
-                qk[i] = qk[i + 1];
-                qn[i] = qn[i + 1];
-            }
-            qk[NS - 2] = new_key;
-            qn[NS - 2] = new_n;
-            queued = queued - 1 + (new_n > 0 ? 1 : 0);
-        } else {
-            queued = 0;
+        for (int i = 0; i < 4; ++i) {
+            ph[i] = nh[i];
+            if constexpr (SPLIT_P) pl[i] = nl[i];
         }
 
-        // Scores of tile t + 1 interleaved with the probabilities of tile t:
-        // each QK MFMA (its K operand read one step ahead) is followed by a
-        // share of the exp/pack work, the order fixed by scheduling fences so
-        // the vector unit runs while the matrix core works.  With no next tile
-        // the stage holds stale data and the result is unused.
-        uint32_t ph[8], pl[8];
+        // ---- step 2: tile t + 1 resident; everyone is done with tile t - 1,
+        // whose stage takes the next load.
+        if (t + 1 < ntiles) {
+            wait_tile(t + 1);
+            if (t_next < ntiles) issue(stage == 0 ? NS - 1 : stage - 1);
+        }
+
+        // ---- step 3: scores of tile t + 1 (K operands read KPRE steps ahead),
+        // second half of tile t's probabilities.
+        constexpr int KPRE = CAP ? 2 : 3;
+        f32x16 st_next;
         for (int i = 0; i < 16; ++i) st_next[i] = 0.0f;
-        u32x4 kop = *(lds_ptr<u32x4>)(kn + k_off[0]);
+        u32x4 kq[KPRE];
+        for (int i = 0; i < KPRE && i < KS; ++i) kq[i] = *(lds_ptr<u32x4>)(kn + k_off[i]);
+#pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const u32x4 kcur = kop;
-            if (ks + 1 < KS) kop = *(lds_ptr<u32x4>)(kn + k_off[ks + 1]);
+            const u32x4 kcur = kq[ks % KPRE];
+            if (ks + KPRE < KS) kq[ks % KPRE] = *(lds_ptr<u32x4>)(kn + k_off[ks + KPRE]);
             st_next = mfma32<DT>(kcur, qb[ks], st_next);
             __builtin_amdgcn_sched_barrier(0);
-            for (int i = 8 * ks / KS; i < 8 * (ks + 1) / KS; ++i) {
-                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(t[2 * i], tmul, nbase));
-                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(t[2 * i + 1], tmul, nbase));
+            for (int i = 4 + 4 * ks / KS; i < 4 + 4 * (ks + 1) / KS; ++i) {
+                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
+                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
                 ph[i] = pack2<DT>(e0, e1);
                 if constexpr (SPLIT_P) pl[i] = pack2<DT>(e0 - lo_f<DT>(ph[i]), e1 - hi_f<DT>(ph[i]));
                 l_run += e0 + e1;
+                asm volatile("" : "+v"(ph[i]), "+v"(pl[i]), "+v"(l_run));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        // ---- O^T += V^T P^T, two 16-key steps.  B slots 8h..8h+7 of step st
-        // are keys {16 st + 4h + 0..3, 16 st + 8 + 4h + 0..3} = acc quads 2st, 2st+1.
-        // V^T rows come transposed from LDS: group gi of 16 lanes reads features
+        // ---- step 4: tile t's V^T operands.  Group gi of 16 lanes reads features
         // 32 mb + 16 (gi & 1) + 0..15 of keys kb..kb+3; source lane si supplies row
-        // kb + si / 4, features + 4 (si % 4).
-        for (int stp = 0; stp < 2; ++stp) {
-            const u32x4 bh = {ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
-            u32x4 bl = {0, 0, 0, 0};
-            if constexpr (SPLIT_P) bl = u32x4{pl[4 * stp], pl[4 * stp + 1], pl[4 * stp + 2], pl[4 * stp + 3]};
+        // kb + si / 4, features + 4 (si % 4).  B slots 8h..8h+7 of step stp are
+        // keys {16 stp + 4h + 0..3, 16 stp + 8 + 4h + 0..3}.
+        for (int stp = 0; stp < 2; ++stp)
             for (int mb = 0; mb < MB; ++mb) {
                 const u32x2 r1 = read_tr(vt + v_off[stp][0][mb]);
                 const u32x2 r2 = read_tr(vt + v_off[stp][1][mb]);
-                const u32x4 va = {r1[0], r1[1], r2[0], r2[1]};
-                acc[mb] = mfma32<DT>(va, bh, acc[mb]);
-                if constexpr (SPLIT_P) acc[mb] = mfma32<DT>(va, bl, acc[mb]);
+                vop[stp][mb] = u32x4{r1[0], r1[1], r2[0], r2[1]};
             }
-        }
-        if (next) st = st_next;
+        st = st_next;
+        stage = stage_next;
     }
-    bool bad = raw_max == -NEG_INF || raw_min == NEG_INF;  // an infinite visible score
-
+    // P.V of the last tile.
+    if (ntiles > 0) {
+#pragma unroll
+        for (int k = 0; k < NPV; ++k) {
+            const int stp = k / (MB * W), mb = (k / W) % MB, part = k % W;
+            const u32x4 bv = part ? u32x4{pl[4 * stp], pl[4 * stp + 1], pl[4 * stp + 2], pl[4 * stp + 3]}
+                                  : u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
+            acc[mb] = mfma32<DT>(vop[stp][mb], bv, acc[mb]);
+        }
+    }
     // ---- the two key halves of each row (lanes j and j + 32) share m_run; add l.
     {
         const uint32_t u = __builtin_bit_cast(uint32_t, l_run);
