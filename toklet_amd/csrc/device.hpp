@@ -70,6 +70,11 @@ struct ProduceParams {
     int32_t rotated_dims;     // proportional: rotated features (even, <= D)
     float eps, theta, factor; // theta: split-half theta or proportional base
     uint32_t *status;
+    // Optional precomputed (cos, sin) per (position, pair), rows from absolute
+    // position rope_pos0, `pairs` entries per row (the same FP64 formulas,
+    // evaluated once per session); null: computed in the kernel.
+    const float *rope;
+    int64_t rope_pos0;
 };
 
 struct Params {

@@ -27,6 +27,23 @@ namespace tkh {
 
 namespace {
 
+__device__ __forceinline__ int rotary_pairs(int rotary, int D, int rotated_dims) {
+    return rotary == 1 ? D / 2 : (rotary == 2 ? rotated_dims / 2 : 0);
+}
+
+// Rotation of pair j at absolute position pos: frequency theta^(-2j/D) (divided
+// by factor for the proportional form), angle and sine/cosine in FP64,
+// rounded once to FP32 (src/cpu/attention.rs:41-46,
+// src/cpu/proportional_rotary.rs:68-74).
+__device__ __forceinline__ void rotary_cos_sin(int rotary, float theta, float factor, int D,
+                                               int64_t pos, int j, float *c, float *s) {
+    double inv = pow((double)theta, -(2.0 * (double)j) / (double)D);
+    if (rotary == 2) inv = inv / (double)factor;
+    const double angle = (double)pos * inv;
+    *s = (float)sin(angle);
+    *c = (float)cos(angle);
+}
+
 template <int DT> __device__ __forceinline__ void store_out(void *base, int64_t i, float x);
 template <> __device__ __forceinline__ void store_out<F32>(void *base, int64_t i, float x) {
     reinterpret_cast<float *>(base)[i] = x;
@@ -90,16 +107,19 @@ __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
     }
     __syncthreads();
     const int half = D / 2;
-    const int pairs = p.rotary == 1 ? half : (p.rotary == 2 ? p.rotated_dims / 2 : 0);
-    const double pos = (double)(p.position + t);
+    const int pairs = rotary_pairs(p.rotary, D, p.rotated_dims);
     for (int j = lane; j < half; j += 64) {
         const float a = row[j], b = row[j + half];
         float x = a, y = b;
         if (j < pairs) {
-            double inv = pow((double)p.theta, -(2.0 * (double)j) / (double)D);
-            if (p.rotary == 2) inv = inv / (double)p.factor;
-            const double angle = pos * inv;
-            const float s = (float)sin(angle), c = (float)cos(angle);
+            float c, s;
+            if (p.rope) {
+                const float *cs = p.rope + 2 * ((p.position + t - p.rope_pos0) * pairs + j);
+                c = cs[0];
+                s = cs[1];
+            } else {
+                rotary_cos_sin(p.rotary, p.theta, p.factor, D, p.position + t, j, &c, &s);
+            }
             const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
             x = ac - bs;
             y = bc + as;
@@ -111,7 +131,40 @@ __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
     raise_status(p.status, bad, ST_NONFINITE_INPUT);
 }
 
+// (cos, sin) of every (position, pair) for rows [pos0, pos0 + rows): the
+// producer's table, filled once per session with the same FP64 formulas.
+__global__ __launch_bounds__(256) void rotary_table(float *out, int64_t pos0, int64_t rows,
+                                                    int pairs, int rotary, float theta,
+                                                    float factor, int D) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * pairs) return;
+    const int64_t r = i / pairs;
+    const int j = (int)(i % pairs);
+    float c, s;
+    rotary_cos_sin(rotary, theta, factor, D, pos0 + r, j, &c, &s);
+    out[2 * i] = c;
+    out[2 * i + 1] = s;
+}
+
 }  // namespace tkh
+
+extern "C" int tkh_rotary_pairs(int rotary, int head_dim, int rotated_dims) {
+    return rotary == 1 ? head_dim / 2 : (rotary == 2 ? rotated_dims / 2 : 0);
+}
+
+extern "C" hipError_t tkh_launch_rotary_table(float *out, int64_t pos0, int64_t rows, int rotary,
+                                              float theta, float factor, int head_dim,
+                                              int rotated_dims, hipStream_t stream) {
+    using namespace tkh;
+    const int pairs = tkh_rotary_pairs(rotary, head_dim, rotated_dims);
+    const int64_t n = rows * pairs;
+    if (n <= 0) return hipSuccess;
+    dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    hipLaunchKernelGGL(rotary_table, grid, block, 0, stream, out, pos0, rows, pairs, rotary, theta,
+                       factor, head_dim);
+    return hipGetLastError();
+}
 
 extern "C" hipError_t tkh_launch_produce(const tkh::ProduceParams *p, int dtype, hipStream_t stream) {
     using namespace tkh;

@@ -19,6 +19,10 @@
 
 extern "C" hipError_t tkh_launch_produce(const tkh::ProduceParams *p, int dtype, hipStream_t stream);
 extern "C" hipError_t tkh_launch_fill_u64(uint64_t *p, uint64_t v, hipStream_t stream);
+extern "C" int tkh_rotary_pairs(int rotary, int head_dim, int rotated_dims);
+extern "C" hipError_t tkh_launch_rotary_table(float *out, int64_t pos0, int64_t rows, int rotary,
+                                              float theta, float factor, int head_dim,
+                                              int rotated_dims, hipStream_t stream);
 
 using namespace tkh_host;
 
@@ -53,8 +57,11 @@ uint32_t check_producer(const tkh_producer_shape *sh, tkh_error *err) {
 uint32_t launch_producer(tkh_context *ctx, const tkh_producer_shape *sh, tkh_dtype dtype,
                          const float *q, const float *k, const float *v, const float *qn,
                          const float *kn, void *q_out, void *k_out, void *v_out,
-                         uint64_t head_stride, tkh_error *err) {
+                         uint64_t head_stride, tkh_error *err, const float *rope = nullptr,
+                         uint64_t rope_pos0 = 0) {
     tkh::ProduceParams p{};
+    p.rope = rope;
+    p.rope_pos0 = (int64_t)rope_pos0;
     p.q = q;
     p.k = k;
     p.v = v;
@@ -123,6 +130,7 @@ struct tkh_session {
     // with a clean status word (written by the gated commit on the device).
     uint64_t *committed_dev = nullptr;
     void *q_scratch = nullptr;                 // [chunk, Hq, D] cache dtype
+    float *rope = nullptr;                     // (cos, sin) per (position, pair), or null
     std::vector<void *> stage_k, stage_v;      // sliding layers: [Hkv, chunk, D]
     uint64_t scratch_bytes = 0, kv_bytes = 0;
 };
@@ -136,6 +144,7 @@ void free_session(tkh_session *s) {
     for (auto *k : s->kv) tkh_kv_destroy(k);
     if (s->q_scratch) hipFree(s->q_scratch);
     if (s->committed_dev) hipFree(s->committed_dev);
+    if (s->rope) hipFree(s->rope);
     for (auto *p : s->stage_k)
         if (p) hipFree(p);
     for (auto *p : s->stage_v)
@@ -307,6 +316,18 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
         hipError_t e = hipMalloc(&s->q_scratch, chunk * o->query_heads * D * es);
         if (e == hipSuccess) e = hipMalloc(&s->committed_dev, sizeof(uint64_t));
         if (e == hipSuccess) e = tkh_launch_fill_u64(s->committed_dev, 0, ctx->stream);
+        // The rotary (cos, sin) of every session position, once.
+        const int pairs = tkh_rotary_pairs((int)o->rotary, (int)D, (int)o->rotated_dims);
+        if (e == hipSuccess && pairs > 0) {
+            const size_t bytes = (size_t)o->capacity * pairs * 2 * sizeof(float);
+            e = hipMalloc(&s->rope, bytes);
+            if (e == hipSuccess)
+                e = tkh_launch_rotary_table(s->rope, (int64_t)o->position_offset, (int64_t)o->capacity,
+                                            (int)o->rotary, o->theta, o->factor, (int)D,
+                                            (int)o->rotated_dims, ctx->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+            s->scratch_bytes += bytes;
+        }
         s->scratch_bytes = chunk * o->query_heads * D * es;
         for (uint64_t l = 0; e == hipSuccess && l < o->layers; ++l) {
             if (!s->kv[l]->has_window) continue;
@@ -464,7 +485,7 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
         if (!ring) {
             uint8_t *kb = (uint8_t *)kv->k + start * D * es, *vb = (uint8_t *)kv->v + start * D * es;
             TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
-                                kb, vb, kv->capacity * D, err));
+                                kb, vb, kv->capacity * D, err, s->rope, o.position_offset));
             if (o.score_scale == 0.0f) {
                 // Model::run -> LayerKv::attend -> attention_cached (src/model/mod.rs:645-662).
                 tkh_cached_shape cs{count, Hq, Hkv, D, kv->capacity, start};
@@ -498,7 +519,8 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
                             (unsigned long long)l, (unsigned long long)kv->offset,
                             (unsigned long long)start);
             TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
-                                s->stage_k[l], s->stage_v[l], count * D, err));
+                                s->stage_k[l], s->stage_v[l], count * D, err, s->rope,
+                                o.position_offset));
             tkh_kv_frame f{};
             f.k = s->stage_k[l];
             f.v = s->stage_v[l];
