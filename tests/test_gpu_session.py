@@ -334,3 +334,55 @@ def test_queued_linear_session_failure_returns_to_checked_prefix(torch_mod, ops,
     assert not s.distribution_valid()
     s.close()
     c.close()
+
+
+@pytest.mark.parametrize("storage,hq,hkv,D", [("bf16", 16, 8, 128), ("f32", 8, 2, 64), ("f16", 8, 1, 64),
+                                              ("bf16", 32, 8, 128)])
+def test_decode_steps_with_fused_producer_match_separate_producer(torch_mod, ops, sess_mod, orc,
+                                                                  storage, hq, hkv, D):
+    """Decode steps run the producer inside the decode kernel; the contexts match the
+    separate producer launch to rounding and the oracle within tolerance (1e-5 for
+    FP32 storage).  Later steps read the rows earlier steps appended, so a wrong
+    append shows up as an oracle mismatch."""
+    import os
+
+    torch = torch_mod
+    rng = np.random.default_rng(9)
+    prompt, steps = 70, 5
+    total = prompt + steps
+    qs, ks, vs, wq, wk = _session_inputs(rng, 1, total, hq, hkv, D)
+    outs = []
+    for fused in ("1", "0"):
+        saved = os.environ.get("TKH_FUSED_DECODE")
+        os.environ["TKH_FUSED_DECODE"] = fused
+        try:
+            c = ops.Context(0)
+            s = sess_mod.Session(c, sess_mod.Options(capacity=total, prefill_chunk_size=32,
+                                                     position_offset=3, layers=1, query_heads=hq,
+                                                     kv_heads=hkv, head_dim=D, storage=storage))
+        finally:
+            if saved is None:
+                os.environ.pop("TKH_FUSED_DECODE", None)
+            else:
+                os.environ["TKH_FUSED_DECODE"] = saved
+        out = torch.zeros((total, hq * D), dtype=torch.float32, device="cuda")
+        io = [sess_mod.LayerIo(_t(torch, qs[0]), _t(torch, ks[0]), _t(torch, vs[0]), out,
+                               _t(torch, wq[0]), _t(torch, wk[0]))]
+        s.set_tokens([1] * prompt)
+        s.evaluate(io)
+        s.append([1] * steps)
+        assert s.evaluate(io, chunk_limit=1) == steps
+        outs.append(host(out))
+        s.close()
+        c.close()
+    q = stored(_oracle_produce(orc, qs[0], wq[0], total, hq, D, 3), storage)
+    k = stored(_oracle_produce(orc, ks[0], wk[0], total, hkv, D, 3), storage)
+    v = stored(vs[0], storage)
+    ref, _, _ = orc.attention(q.reshape(-1), k.reshape(-1), v.reshape(-1), total, hq, hkv, D)
+    errs = [max_err(o.reshape(-1), ref) for o in outs]
+    log(f"{storage} {hq}/{hkv}/{D} decode steps, fused / separate producer: max abs error "
+        f"{errs[0]:.3e} / {errs[1]:.3e}")
+    assert max(errs) <= (1e-5 if storage == "f32" else TOL_HALF)
+    # The new key is summed in a different order (after the stream, in one wave),
+    # so the two agree to rounding, not bitwise.
+    assert max_err(outs[0], outs[1]) <= 1e-5

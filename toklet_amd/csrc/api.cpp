@@ -54,7 +54,7 @@ extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int want);
 extern "C" int tkh_decode_max_waves(int dtype, int head_dim, int rows);
 extern "C" int tkh_decode_max_splits(void);
 extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int head_dim, int rows,
-                                        int keys_per_lane, int waves, int64_t groups,
+                                        int keys_per_lane, int waves, int64_t groups, int fused,
                                         hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 using namespace tkh_host;
@@ -100,6 +100,7 @@ struct Plan {
     int diag_mode = 0;
     float *scores = nullptr;
     float *probs = nullptr;
+    const tkh::FusedDecode *fused = nullptr;  // decode with the producer folded in
 };
 
 tkh::Problem make_problem(const void *q, float *out, int64_t q_row_stride, int64_t q_pos0,
@@ -280,8 +281,10 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
 
     hipEvent_t *ev = nullptr;
     if (ctx->profiling) TRY(profile_slot(ctx, &ev, false, err));
-    hipError_t e = tkh_launch_decode(&prm, (int)plan.dtype, (int)D, R, u, nw, wgs, ctx->stream,
-                                     ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
+    if (plan.fused) prm.fused = *plan.fused;
+    hipError_t e = tkh_launch_decode(&prm, (int)plan.dtype, (int)D, R, u, nw, wgs,
+                                     plan.fused ? 1 : 0, ctx->stream, ev ? ev[0] : nullptr,
+                                     ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "decode launch", err);
     return TKH_OK;
 }
@@ -393,6 +396,12 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
         int64_t max_rows = 0;
         for (auto &p : group) max_rows = std::max<int64_t>(max_rows, (int64_t)p.queries * G);
         const int limit = tkh_decode_max_rows((int)plan.dtype, (int)D);
+        if (plan.fused) {
+            if (limit <= 0 || max_rows > limit || plan.diag_mode != 0 || plan.softcap != 0.0f)
+                return fail(err, TKH_UNSUPPORTED, "fused decode", 0, limit, max_rows,
+                            "fused producer decode needs the streaming decode kernel");
+            return launch_decode(ctx, plan, group, (int)max_rows, err);
+        }
         if (!ctx->force_generic && !ctx->decode_disable && plan.diag_mode == 0 && limit > 0 &&
             max_rows <= limit)
             return launch_decode(ctx, plan, group, (int)max_rows, err);
@@ -632,6 +641,43 @@ uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, t
     plan.problems.push_back(p);
     return run(ctx, plan, err);
 }
+
+}  // extern "C"
+
+// attention_cached for one new token whose producer (RMSNorm, rotary, rounding,
+// cache append) runs inside the decode kernel (session decode steps).  The
+// shape is validated as tkh_attention_cached validates it.
+uint32_t tkh_host::attention_cached_fused(tkh_context *ctx, const tkh_cached_shape *shape,
+                                          tkh_dtype dtype, const void *k, const void *v,
+                                          float *context, const tkh::FusedDecode &fused,
+                                          tkh_error *err) {
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    if (!shape || !ctx) return invalid("shape", err);
+    const tkh_cached_shape s = *shape;
+    TRY(nonzero(s.tokens, "tokens", err));
+    TRY(nonzero(s.query_heads, "query_heads", err));
+    TRY(nonzero(s.kv_heads, "kv_heads", err));
+    TRY(nonzero(s.head_dim, "head_dim", err));
+    TRY(nonzero(s.capacity, "cache capacity", err));
+    if (s.tokens != 1) return invalid("fused decode takes one token", err);
+    if (s.query_heads % s.kv_heads != 0) return invalid("query_heads must be divisible by kv_heads", err);
+    uint64_t end;
+    TRY(add(s.offset, s.tokens, &end, err));
+    if (end > s.capacity) return invalid("cache capacity exceeded", err);
+    Plan plan;
+    plan.dtype = dtype;
+    plan.query_heads = s.query_heads;
+    plan.kv_heads = s.kv_heads;
+    plan.head_dim = s.head_dim;
+    plan.scale = 1.0f / std::sqrt((float)s.head_dim);
+    plan.fused = &fused;
+    tkh::Problem p = make_problem(nullptr, context, s.query_heads * s.head_dim, s.offset, 0, end, 1);
+    add_segment(p, k, v, s.capacity * s.head_dim, s.head_dim, end, 0);
+    plan.problems.push_back(p);
+    return run(ctx, plan, err);
+}
+
+extern "C" {
 
 uint32_t tkh_attention(tkh_context *ctx, const tkh_attention_shape *shape, tkh_dtype dtype,
                        const void *q, uint64_t q_len, const void *k, uint64_t k_len,

@@ -131,6 +131,131 @@ template <> __device__ __forceinline__ void widen<F32>(u32x4 w, float *out) {
 
 __device__ __forceinline__ u32x4 load16(const uint8_t *p) { return *gload_ptr<u32x4>(p); }
 
+// Round a chunk's worth of FP32 values to the storage dtype (RNE) and pack them.
+template <int DT> __device__ __forceinline__ u32x4 pack_chunk(const float *x);
+template <> __device__ __forceinline__ u32x4 pack_chunk<BF16>(const float *x) {
+    u32x4 w;
+    for (int j = 0; j < 4; ++j) {
+        const f32x2 v = {x[2 * j], x[2 * j + 1]};
+        w[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    }
+    return w;
+}
+template <> __device__ __forceinline__ u32x4 pack_chunk<F16>(const float *x) {
+    u32x4 w;
+    for (int j = 0; j < 4; ++j) {
+        const f32x2 v = {x[2 * j], x[2 * j + 1]};
+        w[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+    }
+    return w;
+}
+template <> __device__ __forceinline__ u32x4 pack_chunk<F32>(const float *x) {
+    u32x4 w;
+    for (int j = 0; j < 4; ++j) w[j] = __builtin_bit_cast(uint32_t, x[j]);
+    return w;
+}
+
+// The producer for one head row, in this kernel's lane layout: lane `sub` of
+// an eight-lane group holds the 16-byte chunks at byte offsets 128 c + 16 sub,
+// i.e. elements c * (128 / ES) + sub * EPC + i.  Loading (produce_load) is
+// separate from the arithmetic (produce_row) so a caller can put every load
+// in flight first.  Per-head RMSNorm (FP64 sum over the eight lanes, FP64
+// scaling by the reciprocal root and the weight, rounded to FP32), then the
+// rotary of pair j (elements j and j + D/2) with the given (cos, sin) and FP32
+// products and sums rounded separately, then rounding to the cache dtype.
+// Matches produce_qkv element for element.
+template <int DT, int D> struct ProduceLayout {
+    static constexpr int ES = Elem<DT>::size;
+    static constexpr int CPL = D * ES / 128;
+    static constexpr int EPC = 16 / ES;
+    static constexpr int EPL = CPL * EPC;
+    static constexpr int CE = 128 / ES;  // elements per chunk column
+    // (cos, sin) floats per lane: two per first-half slot (with one chunk per
+    // lane every slot of the lane is a first-half slot of its pair).
+    static constexpr int CS = 2 * (CPL >= 2 ? CPL / 2 : 1) * EPC;
+    // Pair index of element slot (c, i) of lane `sub` for the rotary's first
+    // half; the second half's slots hold the partners.
+    __device__ static int pair_of(int sub, int c, int i) {
+        return CPL >= 2 ? c * CE + sub * EPC + i : (sub & 3) * EPC + i;
+    }
+};
+
+// This lane's elements of a row (EPL floats).
+template <int DT, int D> __device__ __forceinline__ void produce_load(const float *src, int sub, float *x) {
+    using PL = ProduceLayout<DT, D>;
+    for (int c = 0; c < PL::CPL; ++c)
+        for (int i = 0; i < PL::EPC; i += 4) {
+            const f32x4 v = *gload_ptr<f32x4>(src + c * PL::CE + sub * PL::EPC + i);
+            for (int e = 0; e < 4; ++e) x[c * PL::EPC + i + e] = v[e];
+        }
+}
+// This lane's (cos, sin) pairs, in the order produce_row consumes them
+// (ProduceLayout::CS floats).
+template <int DT, int D> __device__ __forceinline__ void produce_load_rope(const float *rope, int sub, float *cs) {
+    using PL = ProduceLayout<DT, D>;
+    constexpr int SLOTS = PL::CPL >= 2 ? PL::CPL / 2 : 1;
+    for (int c = 0; c < SLOTS; ++c)
+        for (int i = 0; i < PL::EPC; i += 2) {
+            const f32x4 v = *gload_ptr<f32x4>(rope + 2 * PL::pair_of(sub, c, i));
+            for (int e = 0; e < 4; ++e) cs[2 * (c * PL::EPC + i) + e] = v[e];
+        }
+}
+
+template <int DT, int D>
+__device__ __forceinline__ void produce_row(float *x, bool norm, const float *w, float eps,
+                                            bool rotate, const float *cs, int pairs, int sub,
+                                            u32x4 *out, bool &bad) {
+#pragma clang fp contract(off)
+    using PL = ProduceLayout<DT, D>;
+    constexpr int CPL = PL::CPL, EPC = PL::EPC, EPL = PL::EPL;
+    for (int e = 0; e < EPL; ++e) bad |= !is_finite_f(x[e]);
+    if (norm) {
+        double ss = 0.0;
+        for (int e = 0; e < EPL; ++e) {
+            const double d = (double)x[e];
+            ss += d * d;
+        }
+        for (int m = 1; m < 8; m <<= 1) ss += __shfl_xor(ss, m, 64);
+        const double inv = 1.0 / sqrt(ss / (double)D + (double)eps);
+        for (int e = 0; e < EPL; ++e) {
+            const float y = (float)((double)x[e] * inv * (double)w[e]);
+            bad |= !is_finite_f(y) || !is_finite_f(w[e]);
+            x[e] = y;
+        }
+    }
+    if (rotate && pairs > 0) {
+        if constexpr (CPL >= 2) {
+            // Pair partner in the same lane, CPL / 2 chunks on.
+            for (int c = 0; c < CPL / 2; ++c)
+                for (int i = 0; i < EPC; ++i) {
+                    if (PL::pair_of(sub, c, i) < pairs) {
+                        const float co = cs[2 * (c * EPC + i)], sn = cs[2 * (c * EPC + i) + 1];
+                        const float a = x[c * EPC + i], b = x[(c + CPL / 2) * EPC + i];
+                        const float ac = a * co, bs = b * sn, bc = b * co, as = a * sn;
+                        x[c * EPC + i] = ac - bs;
+                        x[(c + CPL / 2) * EPC + i] = bc + as;
+                        bad |= !is_finite_f(ac - bs) || !is_finite_f(bc + as);
+                    }
+                }
+        } else {
+            // One chunk per lane: element e pairs with e + D/2 in lane sub ^ 4.
+            for (int i = 0; i < EPC; ++i) {
+                const float mine = x[i];
+                const float other = __shfl_xor(mine, 4, 64);
+                const bool first = sub < 4;
+                if (PL::pair_of(sub, 0, i) < pairs) {
+                    const float co = cs[2 * i], sn = cs[2 * i + 1];
+                    const float a = first ? mine : other, b = first ? other : mine;
+                    const float ac = a * co, bs = b * sn, bc = b * co, as = a * sn;
+                    x[i] = first ? ac - bs : bc + as;
+                    bad |= !is_finite_f(x[i]);
+                }
+            }
+        }
+    }
+    for (int c = 0; c < CPL; ++c) out[c] = pack_chunk<DT>(x + c * EPC);
+}
+
 // Device-coherent (agent scope) store and load of split-K partials: sc1
 // write-through stores and sc1 loads, visible across the XCDs' L2 caches.
 __device__ __forceinline__ void coherent_store(float *p, float v) {
@@ -148,7 +273,7 @@ constexpr int DECODE_MAX_SPLITS = 64;  // key splits per KV head (bounds the mer
 // row size leave room in the register file (256 VGPRs per lane), else four.
 constexpr int decode_waves_for(int row_bytes, int rows) { return rows <= 2 && row_bytes <= 512 ? 8 : 4; }
 
-template <int DT, int D, int R, int U, bool CAP>
+template <int DT, int D, int R, int U, bool CAP, bool FUSED>
 __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void attn_decode(Params p) {
     constexpr int ES = Elem<DT>::size;
     constexpr int NWMAX = decode_waves_for(D * ES, R);
@@ -165,6 +290,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     __shared__ float lds_l[DECODE_MAX_SPLITS * R];
     __shared__ float lds_mass[R];
     __shared__ int lds_last;
+    __shared__ u32x4 lds_new[FUSED ? 2 * CPL * 8 : 1];  // fused: the new K/V row (chunk c of lane sub)
 
     const int nw = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6;
@@ -206,6 +332,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     const uint8_t *vseg = reinterpret_cast<const uint8_t *>(pr->seg[seg].v) + seg_first * ES + 16 * sub;
     const int64_t row_bytes = pr->seg[seg].row_stride * ES;
 
+    bool bad = false;
     // Rows: visible range relative to a, and the query chunks in registers.
     int rlo[R], rhi[R];
     u32x4 q[R][CPL];
@@ -222,10 +349,63 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
             hi -= a;
             rlo[r] = (int)(lo < 0 ? 0 : (lo > span ? span : lo));
             rhi[r] = (int)(hi < 0 ? 0 : (hi > span ? span : hi));
-            const uint8_t *qrow = qbase + ((int64_t)t * pr->q_row_stride + (int64_t)h * D) * ES;
-            for (int c = 0; c < CPL; ++c) q[r][c] = load16(qrow + 128 * c + 16 * sub);
+            if constexpr (!FUSED) {
+                const uint8_t *qrow = qbase + ((int64_t)t * pr->q_row_stride + (int64_t)h * D) * ES;
+                for (int c = 0; c < CPL; ++c) q[r][c] = load16(qrow + 128 * c + 16 * sub);
+            }
         }
     }
+    // Fused producer: the new key is the last of the visible range, so it
+    // falls in the last split.  Wave 0 of that workgroup makes its K/V row,
+    // stores it into the cache, keeps a copy in LDS, and scores it after the
+    // stream of the older keys (which the stream below leaves out).
+    int rel_new = -1;
+    int stream_span = span;
+    if constexpr (FUSED) {
+        const int64_t rn = p.fused.new_key - a;
+        if (rn >= 0 && rn < span) {
+            rel_new = (int)rn;
+            stream_span = rel_new;  // keys after the new one: none (it is the last)
+        }
+    }
+    // The producer's work, after the first K/V block is in flight (below).
+    auto produce = [&]() {
+        if constexpr (FUSED) {
+            // Every load first (Q rows, and for wave 0 of the workgroup holding
+            // the new key its K and V rows), then the arithmetic.
+            const FusedDecode &f = p.fused;
+            const bool make_kv = rel_new >= 0 && wave == 0;
+            float xq[R][EPL], wq[EPL], cs[ProduceLayout<DT, D>::CS], xk[EPL], wk[EPL], xv[EPL];
+            for (int r = 0; r < R; ++r)
+                if (r < nrows) produce_load<DT, D>(f.q_proj + (int64_t)(kvh * G + r % G) * D, sub, xq[r]);
+            if (f.q_norm) produce_load<DT, D>(f.q_norm, sub, wq);
+            if (f.rope) produce_load_rope<DT, D>(f.rope, sub, cs);
+            if (make_kv) {
+                produce_load<DT, D>(f.k_proj + (int64_t)kvh * D, sub, xk);
+                produce_load<DT, D>(f.v_proj + (int64_t)kvh * D, sub, xv);
+                if (f.k_norm) produce_load<DT, D>(f.k_norm, sub, wk);
+            }
+            const bool rot = f.rope != nullptr;
+            for (int r = 0; r < R; ++r)
+                if (r < nrows)
+                    produce_row<DT, D>(xq[r], f.q_norm != nullptr, wq, f.eps, rot, cs, f.pairs, sub,
+                                       q[r], bad);
+            if (make_kv) {
+                u32x4 knew[CPL], vnew[CPL];
+                produce_row<DT, D>(xk, f.k_norm != nullptr, wk, f.eps, rot, cs, f.pairs, sub, knew, bad);
+                produce_row<DT, D>(xv, false, wk, 0.0f, false, cs, 0, sub, vnew, bad);
+                if (kg == 0) {
+                    const int64_t row0 = ((int64_t)kvh * f.head_stride + f.new_key * D) * ES;
+                    for (int c = 0; c < CPL; ++c) {
+                        *gstore_ptr<u32x4>(reinterpret_cast<uint8_t *>(f.k_cache) + row0 + 128 * c + 16 * sub) = knew[c];
+                        *gstore_ptr<u32x4>(reinterpret_cast<uint8_t *>(f.v_cache) + row0 + 128 * c + 16 * sub) = vnew[c];
+                        lds_new[(0 * CPL + c) * 8 + sub] = knew[c];
+                        lds_new[(1 * CPL + c) * 8 + sub] = vnew[c];
+                    }
+                }
+            }
+        }
+    };
 
     float m[R], l[R], acc[R][EPL];
     for (int r = 0; r < R; ++r) {
@@ -233,17 +413,16 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         l[r] = 0.0f;
         for (int e = 0; e < EPL; ++e) acc[r][e] = 0.0f;
     }
-    bool bad = false;
     const float scale_log2 = p.scale_log2;
     const float scale = p.scale;
     const float softcap = p.softcap, softcap_inv = p.softcap_inv;
 
-    const int nblk = (span + KPB - 1) / KPB;
+    const int nblk = (stream_span + KPB - 1) / KPB;
 
     auto load_block = [&](int blk, u32x4 (&kb)[U][CPL], u32x4 (&vb)[U][CPL]) {
         for (int u = 0; u < U; ++u) {
             const int rel = blk * KPB + kg + 8 * u;
-            if (rel < span) {
+            if (rel < stream_span) {
                 const uint8_t *kp = kseg + rel * row_bytes;
                 const uint8_t *vp = vseg + rel * row_bytes;
                 for (int c = 0; c < CPL; ++c) kb[u][c] = load16(kp + 128 * c);
@@ -307,11 +486,20 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         }
     };
 
+    // The stream covers keys [0, stream_span): keys past it are never visible
+    // to it (their K/V are not loaded).
+    int rhi_all[R];
+    for (int r = 0; r < R; ++r) {
+        rhi_all[r] = rhi[r];
+        if (rhi[r] > stream_span) rhi[r] = stream_span;
+    }
+
     // Block blk + nw streams in while block blk is consumed.
     int blk = wave;
+    u32x4 kc[U][CPL], vc[U][CPL];
+    if (blk < nblk) load_block(blk, kc, vc);
+    produce();
     if (blk < nblk) {
-        u32x4 kc[U][CPL], vc[U][CPL];
-        load_block(blk, kc, vc);
         for (;;) {
             const bool more = blk + nw < nblk;
             u32x4 kn[U][CPL], vn[U][CPL];
@@ -324,6 +512,30 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
                     vc[u][c] = vn[u][c];
                 }
             blk += nw;
+        }
+    }
+
+    // Fused producer: wave 0 of the workgroup holding the new key scores it
+    // (lanes kg == 0 hold its chunks; the other key lanes add nothing).
+    if constexpr (FUSED) {
+        if (rel_new >= 0 && wave == 0) {
+            u32x4 kb[U][CPL], vb[U][CPL];
+            for (int u = 0; u < U; ++u)
+                for (int c = 0; c < CPL; ++c) {
+                    kb[u][c] = u == 0 && kg == 0 ? lds_new[(0 * CPL + c) * 8 + sub] : u32x4{0, 0, 0, 0};
+                    vb[u][c] = u == 0 && kg == 0 ? lds_new[(1 * CPL + c) * 8 + sub] : u32x4{0, 0, 0, 0};
+                }
+            // A block index whose lane kg == 0, u == 0 key is rel_new: the
+            // consume() key of (kg, u) is blk * KPB + kg + 8 u, so shift the
+            // visibility bounds instead of the block.
+            const int shift = rel_new;
+            for (int r = 0; r < R; ++r) {
+                rlo[r] -= shift;
+                rhi[r] = rhi_all[r] - shift;
+            }
+            for (int r = 0; r < R; ++r)
+                if (kg != 0) rhi[r] = rlo[r];  // only the key lanes that hold the row
+            consume(0, kb, vb);
         }
     }
 
@@ -550,19 +762,43 @@ extern "C" int tkh_decode_max_waves(int dtype, int head_dim, int rows) {
 }
 extern "C" int tkh_decode_max_splits(void) { return tkh::DECODE_MAX_SPLITS; }
 
+namespace {
+// The softcap and fused-producer variants of one geometry.  The producer is
+// folded in only for rows of at most 256 bytes (its per-lane row copy fits the
+// register budget there).
+template <int DT, int DD, int RR, int UU>
+hipError_t launch_variant(const tkh::Params *p, int fused, dim3 grid, dim3 block,
+                          hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+    using namespace tkh;
+    if (fused) {
+        if constexpr (DD * Elem<DT>::size <= 256) {
+            if (p->softcap != 0.0f) return hipErrorInvalidValue;
+            hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false, true>), grid, block, 0, stream,
+                                  start, stop, 0, *p);
+            return hipGetLastError();
+        } else {
+            return hipErrorInvalidValue;
+        }
+    }
+    if (p->softcap != 0.0f)
+        hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, true, false>), grid, block, 0, stream,
+                              start, stop, 0, *p);
+    else
+        hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false, false>), grid, block, 0, stream,
+                              start, stop, 0, *p);
+    return hipGetLastError();
+}
+}  // namespace
+
 extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int head_dim, int rows,
-                                        int keys_per_lane, int waves, int64_t groups,
+                                        int keys_per_lane, int waves, int64_t groups, int fused,
                                         hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     using namespace tkh;
     if (waves < 1 || waves > tkh_decode_max_waves(dtype, head_dim, rows)) return hipErrorInvalidValue;
     dim3 grid((unsigned)groups), block(64 * waves);
 #define TKH_DEC(DT, DD, RR, UU)                                                             \
     if (dtype == DT && head_dim == DD && rows <= RR && keys_per_lane == UU) {               \
-        if (p->softcap != 0.0f)                                                             \
-            hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, true>), grid, block, 0, stream, start, stop, 0, *p); \
-        else                                                                                \
-            hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false>), grid, block, 0, stream, start, stop, 0, *p); \
-        return hipGetLastError();                                                           \
+        return launch_variant<DT, DD, RR, UU>(p, fused, grid, block, stream, start, stop); \
     }
 #define TKH_DEC_R(DT, DD, UU) TKH_DEC(DT, DD, 1, UU) TKH_DEC(DT, DD, 2, UU) TKH_DEC(DT, DD, 4, UU) TKH_DEC(DT, DD, 8, UU)
 #define TKH_DEC_R4(DT, DD, UU) TKH_DEC(DT, DD, 1, UU) TKH_DEC(DT, DD, 2, UU) TKH_DEC(DT, DD, 4, UU)

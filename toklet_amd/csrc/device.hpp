@@ -77,6 +77,26 @@ struct ProduceParams {
     int64_t rope_pos0;
 };
 
+// Decode steps of a session with the producer folded in: one new token whose
+// Q/K/V projections are normalised, rotated and rounded inside the decode
+// kernel (every workgroup makes the Q rows it needs; the workgroup whose key
+// split holds the new key makes that K/V row, uses it, and stores it into the
+// cache row `new_key`).
+struct FusedDecode {
+    const float *q_proj;   // [Hq, D] FP32
+    const float *k_proj;   // [Hkv, D]
+    const float *v_proj;   // [Hkv, D]
+    const float *q_norm;   // [D] or null
+    const float *k_norm;
+    const float *rope;     // (cos, sin) of the token's position, `pairs` entries, or null
+    int32_t pairs;
+    float eps;
+    void *k_cache;         // cache bases; element (h, key, d) at h * head_stride + key * D + d
+    void *v_cache;
+    int64_t head_stride;
+    int64_t new_key;       // logical key index of the new token
+};
+
 struct Params {
     const Problem *problems;
     int32_t nproblems;
@@ -101,6 +121,7 @@ struct Params {
     int32_t diag_mode;      // 0 none, 1 full [Hq, queries, keys], 2 last row [keys]
     int32_t pad2;
     uint32_t *counters;     // split-K arrival counters (zero between launches)
+    FusedDecode fused;      // decode kernel built with FUSED only
     Problem single;         // the problem itself when nproblems == 1 (no descriptor upload)
 };
 

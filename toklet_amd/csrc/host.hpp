@@ -144,6 +144,11 @@ struct tkh_kv {
 };
 
 namespace tkh_host {
+// attention_cached of one token with the producer folded into the decode
+// kernel (api.cpp); used by the session for decode steps.
+uint32_t attention_cached_fused(tkh_context *ctx, const tkh_cached_shape *shape, tkh_dtype dtype,
+                                const void *k, const void *v, float *context,
+                                const tkh::FusedDecode &fused, tkh_error *err);
 // tkh_kv_commit_batch with an optional device gate (api.cpp).
 uint32_t commit_frames(tkh_kv *const *kvs, const tkh_kv_frame *frames, uint64_t count,
                        const uint32_t *gate, uint64_t *committed, uint64_t committed_value,

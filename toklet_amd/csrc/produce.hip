@@ -4,7 +4,9 @@
 //
 // Order and arithmetic follow Model::run (src/model/mod.rs:611-662):
 //  * rmsnorm (src/cpu/reductions.rs:8-49): squares and their sum in FP64,
-//    denominator sqrt(sum / D + eps) in FP64, value = f32(x / den * w) in FP64;
+//    denominator sqrt(sum / D + eps) in FP64, value = f32(x * (1 / den) * w) in
+//    FP64 (the reference divides by den; the reciprocal form can move the FP64
+//    value by an ulp, which changes the FP32 result only at a rounding tie);
 //  * rotary (src/cpu/attention.rs:10-64): frequency theta^(-2j/D), angle =
 //    position * frequency and sine/cosine in FP64, rounded to FP32; rotation
 //    a*c - b*s, b*c + a*s in FP32 with separate roundings (no contraction);
@@ -98,9 +100,9 @@ __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
             ss += x * x;
         }
         ss = wave_sum_f64(ss);
-        const double den = sqrt(ss / (double)D + (double)p.eps);
+        const double inv = 1.0 / sqrt(ss / (double)D + (double)p.eps);
         for (int i = lane; i < D; i += 64) {
-            const float y = (float)((double)row[i] / den * (double)w[i]);
+            const float y = (float)((double)row[i] * inv * (double)w[i]);
             bad |= !is_finite_f(y) || !is_finite_f(w[i]);
             row[i] = y;
         }

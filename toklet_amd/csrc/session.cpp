@@ -131,6 +131,7 @@ struct tkh_session {
     uint64_t *committed_dev = nullptr;
     void *q_scratch = nullptr;                 // [chunk, Hq, D] cache dtype
     float *rope = nullptr;                     // (cos, sin) per (position, pair), or null
+    bool fused_decode = false;                 // decode steps fold the producer into attention
     std::vector<void *> stage_k, stage_v;      // sliding layers: [Hkv, chunk, D]
     uint64_t scratch_bytes = 0, kv_bytes = 0;
 };
@@ -295,6 +296,16 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
         return invalid("windowed layers need an explicit score scale", err);
     }
     s->history.reserve(o->capacity);
+    // Decode steps with the producer inside the decode kernel: head sizes of
+    // that kernel, GQA groups whose rows' producer inputs fit the registers
+    // (at most 1 KiB of cache-dtype rows per lane group), no softcap.
+    {
+        const uint64_t G = o->query_heads / o->kv_heads;
+        const uint64_t rowb = o->head_dim * (uint64_t)esize(o->storage);
+        const uint64_t limit = rowb <= 256 ? 8 : (rowb <= 512 ? 4 : 2);
+        s->fused_decode = (o->head_dim == 64 || o->head_dim == 128) && rowb <= 256 &&
+                          G <= limit && G * rowb <= 1024 && env_int("TKH_FUSED_DECODE", 1) != 0;
+    }
     if (ctx) {
         const uint64_t D = o->head_dim, es = (uint64_t)esize(o->storage);
         const uint64_t chunk = s->opt.prefill_chunk_size;
@@ -482,7 +493,24 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
         tkh_kv *kv = s->kv[l];
         const bool ring = kv->has_window;
         const uint64_t window = s->windows[l];
-        if (!ring) {
+        if (!ring && count == 1 && o.score_scale == 0.0f && s->fused_decode) {
+            // A decode step: the producer runs inside the decode kernel.
+            tkh::FusedDecode f{};
+            f.q_proj = q;
+            f.k_proj = k;
+            f.v_proj = v;
+            f.q_norm = io.q_norm;
+            f.k_norm = io.k_norm;
+            f.pairs = tkh_rotary_pairs((int)o.rotary, (int)D, (int)o.rotated_dims);
+            f.rope = f.pairs > 0 ? s->rope + 2 * start * (uint64_t)f.pairs : nullptr;
+            f.eps = o.norm_epsilon;
+            f.k_cache = kv->k;
+            f.v_cache = kv->v;
+            f.head_stride = (int64_t)(kv->capacity * D);
+            f.new_key = (int64_t)start;
+            tkh_cached_shape cs{1, Hq, Hkv, D, kv->capacity, start};
+            TRY(attention_cached_fused(ctx, &cs, o.storage, kv->k, kv->v, context, f, err));
+        } else if (!ring) {
             uint8_t *kb = (uint8_t *)kv->k + start * D * es, *vb = (uint8_t *)kv->v + start * D * es;
             TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
                                 kb, vb, kv->capacity * D, err, s->rope, o.position_offset));
