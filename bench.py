@@ -128,6 +128,19 @@ def time_region(torch, fn, steps, warmup):
     return start.elapsed_time(end) / 1e3, wall
 
 
+def profiled(torch, ctx, fn, steps):
+    """The attention kernels' dispatch-recorded durations over `steps` calls of
+    fn, in a pass separate from the timed region (the events add work)."""
+    torch.cuda.synchronize()
+    ctx.profile(True)
+    for _ in range(steps):
+        fn()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    ctx.synchronize()
+    return prof
+
+
 def bench_c2(torch, ops, sessmod, ctx, steps, warmup):
     w = C2(torch, ops, sessmod, ctx)
     log("c2: qwen3 16/8/128 bf16, prefill 2048 in 128-token chunks + 256 decode steps "
@@ -138,23 +151,30 @@ def bench_c2(torch, ops, sessmod, ctx, steps, warmup):
         w.run_decode()
         w.session.synchronize()
     job_s, job_wall = time_region(torch, step, steps, warmup)
-    # Phase timing (same calls), with the attention kernels' dispatch-recorded events.
+    # Phase timing (same calls, no event recording: the phase rates).
     pre_s = dec_s = 0.0
-    pre_prof = {"attention_ms": 0.0, "combine_ms": 0.0, "launches": 0}
-    dec_prof = dict(pre_prof)
     for _ in range(steps):
-        ctx.profile(True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         w.run_prefill()
         w.session.synchronize()
         pre_s += time.perf_counter() - t0
-        p = ctx.profile_read()
-        ctx.profile(True)
         t0 = time.perf_counter()
         w.run_decode()
         w.session.synchronize()
         dec_s += time.perf_counter() - t0
+    # Kernel durations: a second pass with the attention kernels'
+    # dispatch-recorded events (which add host and queue work of their own).
+    pre_prof = {"attention_ms": 0.0, "combine_ms": 0.0, "launches": 0}
+    dec_prof = dict(pre_prof)
+    for _ in range(steps):
+        ctx.profile(True)
+        w.run_prefill()
+        w.session.synchronize()
+        p = ctx.profile_read()
+        ctx.profile(True)
+        w.run_decode()
+        w.session.synchronize()
         d = ctx.profile_read()
         for acc, src in ((pre_prof, p), (dec_prof, d)):
             for k in acc:
@@ -217,13 +237,12 @@ def bench_decode_batch(torch, ops, ctx, steps, warmup, *, batch, lmin, lmax, dty
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    ctx.profile(True)
     start_lengths = list(cur)
     s, _ = time_region(torch, step, steps, 0)
-    prof = ctx.profile_read()
-    ctx.profile(False)
-    ctx.synchronize()
     total_bytes = sum(bytes_of([l + i + 1 for l in start_lengths]) for i in range(steps))
+    # Kernel durations over the same lengths, in a pass of their own.
+    cur[:] = start_lengths
+    prof = profiled(torch, ctx, step, steps)
     return {
         "batch": batch, "sum_keys": sum(start_lengths), "dtype": str(dtype).replace("torch.", ""),
         "ms_per_step": s / steps * 1e3,
@@ -262,11 +281,8 @@ def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    ctx.profile(True)
     s, _ = time_region(torch, step, steps, 0)
-    prof = ctx.profile_read()
-    ctx.profile(False)
-    ctx.synchronize()
+    prof = profiled(torch, ctx, step, steps)
     kernel_s = (prof["attention_ms"] + prof["combine_ms"]) / 1e3
     return {
         "sessions": batch, "cached": cached, "new": tokens,

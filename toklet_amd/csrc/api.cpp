@@ -40,6 +40,7 @@ extern "C" hipError_t tkh_launch_check_finite(int dtype, const void *a, const vo
 extern "C" hipError_t tkh_launch_softcap(float *x, int64_t n, float cap, uint32_t *status,
                                          hipStream_t stream);
 extern "C" hipError_t tkh_launch_fill_u32(uint32_t *p, uint32_t v, hipStream_t stream);
+extern "C" hipError_t tkh_launch_zero_u64(uint64_t *p, int64_t words, hipStream_t stream);
 extern "C" int tkh_decode_max_rows(int dtype, int head_dim);
 extern "C" int tkh_prefill_rows_per_group(void);
 extern "C" int tkh_prefill_max_splits(void);
@@ -73,6 +74,9 @@ uint32_t finish(tkh_context *ctx, tkh_error *err) {
     e = tkh_launch_fill_u32(ctx->status_dev, 0, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return device_error(e, "status reset", err);
+    if (st & tkh::ST_SPLIT_TIMEOUT)
+        return fail(err, TKH_DEVICE, "decode splits", 0, 0, 0,
+                    "a decode merge timed out waiting for its key splits (status 0x%x)", st);
     if (st & tkh::ST_NONFINITE_INPUT)
         return fail(err, TKH_NON_FINITE, "attention inputs", 0, 0, 0,
                     "non-finite value in attention inputs or scores (status 0x%x)", st);
@@ -202,7 +206,6 @@ tkh::Params base_params(tkh_context *ctx, const Plan &plan) {
     prm.softcap = plan.softcap;
     prm.softcap_inv = plan.softcap != 0.0f ? 1.0f / plan.softcap : 0.0f;
     prm.status = ctx->status_dev;
-    prm.counters = reinterpret_cast<uint32_t *>(ctx->workspace);
     return prm;
 }
 
@@ -211,7 +214,8 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
                        int rows, tkh_error *err) {
     const int64_t D = plan.head_dim, Hkv = plan.kv_heads;
     const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
-    const int nw = std::min(ctx->decode_waves, tkh_decode_max_waves((int)plan.dtype, (int)D, R));
+    const int nw_max = std::min(ctx->decode_waves, tkh_decode_max_waves((int)plan.dtype, (int)D, R));
+    int nw = nw_max;
     const int u = tkh_decode_keys_per_lane((int)plan.dtype, (int)D, ctx->decode_keys_per_lane);
     const int max_splits = std::min(ctx->decode_max_splits, tkh_decode_max_splits());
     const int64_t kpb = (int64_t)8 * u;  // keys per wave block
@@ -223,19 +227,21 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
         max_span = std::max<int64_t>(max_span, p.vis_hi - p.vis_lo);
     }
     // Keys per split: about decode_groups workgroups in all, at most
-    // max_splits per KV head, at least one block per wave, in whole blocks.
+    // max_splits per KV head, in whole blocks; then as many waves (up to nw)
+    // as the split has blocks, so no wave starts without work.  Short spans
+    // thus spread over more, narrower workgroups.
     int64_t sk = (int64_t)std::ceil(work / ctx->decode_groups);
     sk = std::max<int64_t>(sk, (max_span + max_splits - 1) / max_splits);
-    sk = std::max<int64_t>(sk, kpb * nw);
     if (ctx->split_keys_override > 0) sk = ctx->split_keys_override;
     sk = std::max<int64_t>(kpb, (sk + kpb - 1) / kpb * kpb);
     if (sk > INT32_MAX) return fail(err, TKH_UNSUPPORTED, "keys", 0, 0, 0, "key range too large");
+    nw = (int)std::min<int64_t>(nw, sk / kpb);
 
+    // Splits of every problem, laid out segment by segment over its visible range.
     int64_t wgs = 0, slots = 0;
     for (size_t i = 0; i < group.size(); ++i) {
         auto &p = group[i];
         p.split_keys = (int32_t)sk;
-        // Splits are laid out segment by segment over the visible range.
         int64_t splits = 0;
         for (int s = 0; s < 3; ++s) {
             int64_t n = 0;
@@ -259,14 +265,20 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
         wgs += Hkv * p.splits;
         slots += Hkv * p.splits;
     }
-    if ((size_t)group.size() * Hkv > kCounters)
-        return fail(err, TKH_UNSUPPORTED, "batch", 0, kCounters, group.size() * Hkv,
-                    "too many (session, KV head) pairs in one call");
-    const size_t need = (size_t)slots * R * (D + 2) * sizeof(float);
-    if (need > ctx->workspace_bytes)
-        return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, ctx->workspace_bytes,
-                    "attention needs %zu workspace bytes, context has %zu", need,
-                    ctx->workspace_bytes);
+    // The merging workgroup of a split launch reads 64 outputs per wave: one
+    // wave per 64 outputs (within the kernel's limit) makes the merge one pass.
+    bool any_split = false;
+    for (auto &p : group) any_split |= p.splits > 1;
+    if (any_split) nw = std::max(nw, std::min(nw_max, (int)((R * D + 63) / 64)));
+
+    // Decode partials: completion flags, then (max, mass) and contexts, in the
+    // decode half of the workspace.
+    const size_t flag_bytes = ((size_t)slots * sizeof(uint32_t) + 255) / 256 * 256;
+    const size_t need = flag_bytes + (size_t)slots * R * (D + 2) * sizeof(float);
+    if (need > decode_region_bytes(ctx))
+        return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, decode_region_bytes(ctx),
+                    "decode needs %zu workspace bytes, context has %zu for it", need,
+                    decode_region_bytes(ctx));
 
     tkh::Problem *dev = nullptr;
     if (group.size() > 1) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
@@ -275,7 +287,18 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     if (group.size() == 1) prm.single = group[0];
     prm.nproblems = (int32_t)group.size();
     prm.total_tiles = wgs;
-    float *ws = reinterpret_cast<float *>(ctx->workspace + kCounterBytes);
+    bool split = false;
+    for (auto &p : group) split |= p.splits > 1;
+    if (split && ++ctx->epoch == 0) {
+        // The epoch wrapped: clear every flag so no stale one can match again.
+        HIP_TRY(tkh_launch_zero_u64(reinterpret_cast<uint64_t *>(decode_region(ctx)),
+                                    (int64_t)(decode_region_bytes(ctx) / sizeof(uint64_t)), ctx->stream),
+                "decode workspace clear");
+        ctx->epoch = 1;
+    }
+    prm.epoch = ctx->epoch;
+    prm.flags = reinterpret_cast<uint32_t *>(decode_region(ctx));
+    float *ws = reinterpret_cast<float *>(decode_region(ctx) + flag_bytes);
     prm.part_ml = ws;
     prm.part_o = ws + (size_t)slots * R * 2;
 
@@ -359,10 +382,10 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
         }
     }
     const size_t need = (size_t)slots * rows_per * (D + 2) * sizeof(float);
-    if (need > ctx->workspace_bytes)
-        return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, ctx->workspace_bytes,
-                    "attention needs %zu workspace bytes, context has %zu", need,
-                    ctx->workspace_bytes);
+    if (need > split_region_bytes(ctx))
+        return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, split_region_bytes(ctx),
+                    "attention needs %zu workspace bytes, context has %zu for it", need,
+                    split_region_bytes(ctx));
     tkh::Problem *dev = nullptr;
     if (group.size() > 1) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
     tkh::Params prm = base_params(ctx, plan);
@@ -370,7 +393,13 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
     if (group.size() == 1) prm.single = group[0];
     prm.nproblems = (int32_t)group.size();
     prm.total_tiles = wgs;
-    float *ws = reinterpret_cast<float *>(ctx->workspace + kCounterBytes);
+    bool split = false;
+    for (auto &p : group) split |= p.splits > 1;
+    if (split) {
+        if (++ctx->epoch == 0) ctx->epoch = 1;
+        prm.epoch = ctx->epoch;
+    }
+    float *ws = reinterpret_cast<float *>(ctx->workspace);
     prm.part_ml = ws;
     prm.part_o = ws + (size_t)slots * rows_per * 2;
 
@@ -411,7 +440,7 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
     }
     // FP32, odd head sizes and diagnostics: one wave per (query, head), then a
     // combine launch that publishes the context.
-    const size_t ws_floats = ctx->workspace_bytes / sizeof(float);
+    const size_t ws_floats = split_region_bytes(ctx) / sizeof(float);
     {
         size_t need = 0;
         for (auto &p : group) need += (size_t)p.queries * Hq * (D + 2);
@@ -450,9 +479,8 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
     prm.softcap = plan.softcap;
     prm.softcap_inv = plan.softcap != 0.0f ? 1.0f / plan.softcap : 0.0f;
     prm.total_tiles = tiles;
-    prm.part_ml = reinterpret_cast<float *>(ctx->workspace + kCounterBytes);
-    prm.part_o = reinterpret_cast<float *>(ctx->workspace + kCounterBytes) + 2 * part_rows;
-    prm.counters = reinterpret_cast<uint32_t *>(ctx->workspace);
+    prm.part_ml = reinterpret_cast<float *>(ctx->workspace);
+    prm.part_o = reinterpret_cast<float *>(ctx->workspace) + 2 * part_rows;
     prm.status = ctx->status_dev;
     prm.scores = plan.scores;
     prm.probs = plan.probs;
@@ -537,9 +565,10 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     if ((e = hipMemset(ctx->status_dev, 0, 256)) != hipSuccess) return cleanup(e, "status");
     if ((e = hipHostMalloc(&ctx->status_host, sizeof(uint32_t), hipHostMallocDefault)) != hipSuccess)
         return cleanup(e, "status");
-    if ((e = hipMalloc(&ctx->workspace, ctx->workspace_bytes + kCounterBytes)) != hipSuccess)
+    if ((e = hipMalloc(&ctx->workspace, ctx->workspace_bytes)) != hipSuccess)
         return cleanup(e, "workspace");
-    if ((e = hipMemset(ctx->workspace, 0, kCounterBytes)) != hipSuccess)
+    // Decode tags start at 0, which no launch epoch equals.
+    if ((e = hipMemset(decode_region(ctx), 0, decode_region_bytes(ctx))) != hipSuccess)
         return cleanup(e, "workspace");
     size_t ring = sizeof(tkh::Problem) * kSlots * kSlotProblems;
     if ((e = hipMalloc(&ctx->ring_dev, ring)) != hipSuccess) return cleanup(e, "problem ring");

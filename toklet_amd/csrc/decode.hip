@@ -19,11 +19,11 @@
 //  * Online softmax runs per lane over the keys it sees (exp2 domain).  The
 //    rescale of the running context is skipped for a block unless some
 //    lane's running maximum moved, which after the first blocks is rare.
-//  * At the end the eight key lanes merge by xor shuffles, the waves merge
+//  * At the end the eight key lanes merge by lane swaps, the waves merge
 //    through LDS, and a split either writes the context directly (one split)
-//    or writes an unnormalised partial; the last workgroup of a KV head to
-//    arrive (device-scope counter) merges the partials and writes the
-//    context, then resets the counter.  One launch per call.
+//    or writes an unnormalised partial and a completion flag; the last split
+//    of a KV head (its highest block index) waits for the other flags, merges
+//    the partials and writes the context.  No atomics, one launch per call.
 #include <type_traits>
 
 #include "device.hpp"
@@ -155,117 +155,176 @@ template <> __device__ __forceinline__ u32x4 pack_chunk<F32>(const float *x) {
     return w;
 }
 
-// The producer for one head row, in this kernel's lane layout: lane `sub` of
-// an eight-lane group holds the 16-byte chunks at byte offsets 128 c + 16 sub,
-// i.e. elements c * (128 / ES) + sub * EPC + i.  Loading (produce_load) is
-// separate from the arithmetic (produce_row) so a caller can put every load
-// in flight first.  Per-head RMSNorm (FP64 sum over the eight lanes, FP64
-// scaling by the reciprocal root and the weight, rounded to FP32), then the
-// rotary of pair j (elements j and j + D/2) with the given (cos, sin) and FP32
-// products and sums rounded separately, then rounding to the cache dtype.
-// Matches produce_qkv element for element.
-template <int DT, int D> struct ProduceLayout {
-    static constexpr int ES = Elem<DT>::size;
-    static constexpr int CPL = D * ES / 128;
-    static constexpr int EPC = 16 / ES;
-    static constexpr int EPL = CPL * EPC;
-    static constexpr int CE = 128 / ES;  // elements per chunk column
-    // (cos, sin) floats per lane: two per first-half slot (with one chunk per
-    // lane every slot of the lane is a first-half slot of its pair).
-    static constexpr int CS = 2 * (CPL >= 2 ? CPL / 2 : 1) * EPC;
-    // Pair index of element slot (c, i) of lane `sub` for the rotary's first
-    // half; the second half's slots hold the partners.
-    __device__ static int pair_of(int sub, int c, int i) {
-        return CPL >= 2 ? c * CE + sub * EPC + i : (sub & 3) * EPC + i;
-    }
-};
-
-// This lane's elements of a row (EPL floats).
-template <int DT, int D> __device__ __forceinline__ void produce_load(const float *src, int sub, float *x) {
-    using PL = ProduceLayout<DT, D>;
-    for (int c = 0; c < PL::CPL; ++c)
-        for (int i = 0; i < PL::EPC; i += 4) {
-            const f32x4 v = *gload_ptr<f32x4>(src + c * PL::CE + sub * PL::EPC + i);
-            for (int e = 0; e < 4; ++e) x[c * PL::EPC + i + e] = v[e];
-        }
-}
-// This lane's (cos, sin) pairs, in the order produce_row consumes them
-// (ProduceLayout::CS floats).
-template <int DT, int D> __device__ __forceinline__ void produce_load_rope(const float *rope, int sub, float *cs) {
-    using PL = ProduceLayout<DT, D>;
-    constexpr int SLOTS = PL::CPL >= 2 ? PL::CPL / 2 : 1;
-    for (int c = 0; c < SLOTS; ++c)
-        for (int i = 0; i < PL::EPC; i += 2) {
-            const f32x4 v = *gload_ptr<f32x4>(rope + 2 * PL::pair_of(sub, c, i));
-            for (int e = 0; e < 4; ++e) cs[2 * (c * PL::EPC + i) + e] = v[e];
-        }
-}
-
-template <int DT, int D>
-__device__ __forceinline__ void produce_row(float *x, bool norm, const float *w, float eps,
-                                            bool rotate, const float *cs, int pairs, int sub,
-                                            u32x4 *out, bool &bad) {
+// The producer for one head row, by one whole wave, in produce_qkv's own
+// arithmetic and order (so both give the same bits): lane l takes elements
+// l, l + 64, ... into a per-wave LDS row; per-head RMSNorm with the squares
+// summed in FP64 per lane and then by the same xor butterfly (wave_sum_f64), the reciprocal
+// root in FP64 and value = f32(x * inv * w) in FP64; then the rotary of pair
+// j (elements j and j + D/2) with the row's (cos, sin) from the session's
+// table and FP32 products and sums rounded separately.  The caller packs the
+// row to the cache dtype.  A wave's LDS accesses complete in program order,
+// so the row needs no barrier between the steps.
+template <int D>
+__device__ __forceinline__ void wave_produce_row(const float *src, const float *w, float eps,
+                                                 const float *rope, int pairs, float *row, int lane,
+                                                 bool &bad) {
 #pragma clang fp contract(off)
-    using PL = ProduceLayout<DT, D>;
-    constexpr int CPL = PL::CPL, EPC = PL::EPC, EPL = PL::EPL;
-    for (int e = 0; e < EPL; ++e) bad |= !is_finite_f(x[e]);
-    if (norm) {
+    for (int i = lane; i < D; i += 64) {
+        const float x = src[i];
+        bad |= !is_finite_f(x);
+        row[i] = x;
+    }
+    if (w) {
         double ss = 0.0;
-        for (int e = 0; e < EPL; ++e) {
-            const double d = (double)x[e];
-            ss += d * d;
+        for (int i = lane; i < D; i += 64) {
+            const double x = (double)row[i];
+            ss += x * x;
         }
-        for (int m = 1; m < 8; m <<= 1) ss += __shfl_xor(ss, m, 64);
+        ss = wave_sum_f64(ss);
         const double inv = 1.0 / sqrt(ss / (double)D + (double)eps);
-        for (int e = 0; e < EPL; ++e) {
-            const float y = (float)((double)x[e] * inv * (double)w[e]);
-            bad |= !is_finite_f(y) || !is_finite_f(w[e]);
-            x[e] = y;
+        for (int i = lane; i < D; i += 64) {
+            const float y = (float)((double)row[i] * inv * (double)w[i]);
+            bad |= !is_finite_f(y) || !is_finite_f(w[i]);
+            row[i] = y;
         }
     }
-    if (rotate && pairs > 0) {
-        if constexpr (CPL >= 2) {
-            // Pair partner in the same lane, CPL / 2 chunks on.
-            for (int c = 0; c < CPL / 2; ++c)
-                for (int i = 0; i < EPC; ++i) {
-                    if (PL::pair_of(sub, c, i) < pairs) {
-                        const float co = cs[2 * (c * EPC + i)], sn = cs[2 * (c * EPC + i) + 1];
-                        const float a = x[c * EPC + i], b = x[(c + CPL / 2) * EPC + i];
-                        const float ac = a * co, bs = b * sn, bc = b * co, as = a * sn;
-                        x[c * EPC + i] = ac - bs;
-                        x[(c + CPL / 2) * EPC + i] = bc + as;
-                        bad |= !is_finite_f(ac - bs) || !is_finite_f(bc + as);
-                    }
-                }
-        } else {
-            // One chunk per lane: element e pairs with e + D/2 in lane sub ^ 4.
-            for (int i = 0; i < EPC; ++i) {
-                const float mine = x[i];
-                const float other = __shfl_xor(mine, 4, 64);
-                const bool first = sub < 4;
-                if (PL::pair_of(sub, 0, i) < pairs) {
-                    const float co = cs[2 * i], sn = cs[2 * i + 1];
-                    const float a = first ? mine : other, b = first ? other : mine;
-                    const float ac = a * co, bs = b * sn, bc = b * co, as = a * sn;
-                    x[i] = first ? ac - bs : bc + as;
-                    bad |= !is_finite_f(x[i]);
-                }
-            }
+    if (rope) {
+        constexpr int half = D / 2;
+        for (int j = lane; j < half && j < pairs; j += 64) {
+            const float a = row[j], b = row[j + half];
+            const float c = rope[2 * j], sn = rope[2 * j + 1];
+            const float ac = a * c, bs = b * sn, bc = b * c, as = a * sn;
+            const float x = ac - bs, y = bc + as;
+            bad |= !is_finite_f(x) || !is_finite_f(y);
+            row[j] = x;
+            row[j + half] = y;
         }
     }
-    for (int c = 0; c < CPL; ++c) out[c] = pack_chunk<DT>(x + c * EPC);
 }
 
-// Device-coherent (agent scope) store and load of split-K partials: sc1
-// write-through stores and sc1 loads, visible across the XCDs' L2 caches.
-__device__ __forceinline__ void coherent_store(float *p, float v) {
+// Split-K partials and completion flags: agent-scope accesses, which on
+// gfx950 are sc1 stores and loads (the merge reads partials with sc1 buffer
+// loads).  They bypass the CU's vector L1 (a
+// workgroup-scope sc0 load may be served from it, so a poll with one can read
+// a stale line for ever) and are coherent across the XCDs.  A partial is read
+// only after its writer's stores were acknowledged and its flag seen: a line
+// read while a store to it is still on its way can stay stale in the reader's
+// caches for microseconds.
+__device__ __forceinline__ void split_store(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float coherent_load(const float *p) {
+__device__ __forceinline__ void flag_store(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t flag_load(const uint32_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Buffer resource word 3 for raw 32-bit-element buffers on gfx9, the cache
+// policy operand of a buffer load that makes it an sc1 (device-coherent),
+// non-temporal load (the partials are read once), and an offset past every
+// buffer range (the load returns zeros).
+constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
+constexpr int CPOL_SC1_NT = 16 | 2;
+constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
+
+// Maximum / sum over the whole wave in registers: DPP inside groups of eight,
+// then the lane swaps of lane_pair (no LDS round trips).
+__device__ __forceinline__ float dpp_max8(float x) {
+    int v = __builtin_bit_cast(int, x);
+    x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false)));
+    v = __builtin_bit_cast(int, x);
+    x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false)));
+    v = __builtin_bit_cast(int, x);
+    x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false)));
+    return x;
+}
+__device__ __forceinline__ float wave_max_regs(float x) {
+    float a, b;
+    x = dpp_max8(x);
+    lane_pair<8>(x, a, b);
+    x = fmaxf(a, b);
+    lane_pair<16>(x, a, b);
+    x = fmaxf(a, b);
+    lane_pair<32>(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float wave_sum_regs(float x) {
+    float a, b;
+    x = dpp_sum8(x);
+    lane_pair<8>(x, a, b);
+    x = a + b;
+    lane_pair<16>(x, a, b);
+    x = a + b;
+    lane_pair<32>(x, a, b);
+    return a + b;
+}
+
+// Longest wait of a merging workgroup for the other splits of its KV head
+// (s_memrealtime ticks, 100 MHz): half a second, far beyond any split's work,
+// after which the launch reports ST_SPLIT_TIMEOUT instead of waiting on.
+constexpr uint64_t SPLIT_WAIT_TICKS = 50000000ull;
+
 }  // namespace
+
+// A key segment's fields the decode kernel reads (Segment minus nothing it
+// needs), and the problem fields its first K/V and Q loads depend on.
+struct DecodeSegment {
+    const void *k, *v;
+    int64_t head_stride, row_stride, keys, start;
+};
+struct DecodeView {
+    int64_t tile_base, vis_lo, vis_hi, k_pos0, keys, q_pos0, q_row_stride;
+    const void *q;
+    int32_t splits, split_keys, seg_splits0, seg_splits1, queries;
+    DecodeSegment seg0;
+};
+__device__ __forceinline__ DecodeSegment decode_segment(const_ptr<Problem> pr, int s) {
+    const auto &g = pr->seg[s];
+    return DecodeSegment{g.k, g.v, g.head_stride, g.row_stride, g.keys, g.start};
+}
+// Held in scalar registers at this point: an empty asm that reads and
+// "writes" the value keeps its load ahead of what follows.
+template <class T> __device__ __forceinline__ void pin_scalar(T &x) { asm volatile("" : "+s"(x)); }
+__device__ __forceinline__ void pin_view(DecodeView &v) {
+    pin_scalar(v.tile_base);
+    pin_scalar(v.vis_lo);
+    pin_scalar(v.vis_hi);
+    pin_scalar(v.k_pos0);
+    pin_scalar(v.keys);
+    pin_scalar(v.q_pos0);
+    pin_scalar(v.q_row_stride);
+    pin_scalar(v.q);
+    pin_scalar(v.splits);
+    pin_scalar(v.split_keys);
+    pin_scalar(v.seg_splits0);
+    pin_scalar(v.seg_splits1);
+    pin_scalar(v.queries);
+    pin_scalar(v.seg0.k);
+    pin_scalar(v.seg0.v);
+    pin_scalar(v.seg0.head_stride);
+    pin_scalar(v.seg0.row_stride);
+    pin_scalar(v.seg0.keys);
+    pin_scalar(v.seg0.start);
+}
+__device__ __forceinline__ DecodeView decode_view(const_ptr<Problem> pr) {
+    DecodeView v;
+    v.tile_base = pr->tile_base;
+    v.vis_lo = pr->vis_lo;
+    v.vis_hi = pr->vis_hi;
+    v.k_pos0 = pr->k_pos0;
+    v.keys = pr->keys;
+    v.q_pos0 = pr->q_pos0;
+    v.q_row_stride = pr->q_row_stride;
+    v.q = pr->q;
+    v.splits = pr->splits;
+    v.split_keys = pr->split_keys;
+    v.seg_splits0 = pr->seg_splits[0];
+    v.seg_splits1 = pr->seg_splits[1];
+    v.queries = pr->queries;
+    v.seg0 = decode_segment(pr, 0);
+    return v;
+}
 
 constexpr int DECODE_MAX_SPLITS = 64;  // key splits per KV head (bounds the merge)
 
@@ -286,11 +345,14 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
 
     __shared__ float lds_o[NWMAX * R * D];
     __shared__ float lds_ml[NWMAX * R * 2];
-    __shared__ float lds_w[DECODE_MAX_SPLITS * R];
-    __shared__ float lds_l[DECODE_MAX_SPLITS * R];
-    __shared__ float lds_mass[R];
-    __shared__ int lds_last;
-    __shared__ u32x4 lds_new[FUSED ? 2 * CPL * 8 : 1];  // fused: the new K/V row (chunk c of lane sub)
+    // The merging split's own partial (context, (max, mass) per row) and its
+    // flag-wait outcome.
+    __shared__ __attribute__((aligned(16))) float lds_own[R * D + 2 * R + 1];
+    // Fused producer: the new K/V rows and the Q rows in 16-byte chunks
+    // (chunk 8 c + sub is lane sub's chunk c), and one staging row per wave.
+    __shared__ u32x4 lds_new[FUSED ? 2 * CPL * 8 : 1];
+    __shared__ u32x4 lds_q[FUSED ? R * CPL * 8 : 1];
+    __shared__ float lds_prow[FUSED ? NWMAX * D : 1];
 
     const int nw = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6;
@@ -298,45 +360,90 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     const int sub = lane & 7;   // which chunks of the row
     const int kg = lane >> 3;   // which key of the block
 
-    const_ptr<Problem> pr = problem_ptr(p, blockIdx.x);
-    const int64_t local = (int64_t)blockIdx.x - pr->tile_base;
-    const int split = (int)(local % pr->splits);
-    const int kvh = (int)(local / pr->splits);
+    // The scalars the first K/V load depends on arrive in one batch: the
+    // problem inside the kernel arguments is read together with the problem
+    // count (a single-problem launch needs nothing else), and a batched launch
+    // then finds its problem by a wave-parallel search and reads it again.
+    // Segments past the first load only when the split lies in one (rings).
+    const_ptr<Params> args = (const_ptr<Params>)__builtin_amdgcn_kernarg_segment_ptr();
+    const_ptr<Problem> pr = &args->single;
+    DecodeView pv = decode_view(pr);
+    int nproblems = args->nproblems;
+    pin_scalar(nproblems);
+    pin_view(pv);
+    // The fused producer's descriptor, in the same batch (a kernel-argument
+    // line first touched later costs another memory round trip).
+    FusedDecode fz{};
+    if constexpr (FUSED) {
+        const auto &fa = args->fused;
+        fz.q_proj = fa.q_proj;
+        fz.k_proj = fa.k_proj;
+        fz.v_proj = fa.v_proj;
+        fz.q_norm = fa.q_norm;
+        fz.k_norm = fa.k_norm;
+        fz.rope = fa.rope;
+        fz.pairs = fa.pairs;
+        fz.eps = fa.eps;
+        fz.k_cache = fa.k_cache;
+        fz.v_cache = fa.v_cache;
+        fz.head_stride = fa.head_stride;
+        fz.new_key = fa.new_key;
+        pin_scalar(fz.q_proj);
+        pin_scalar(fz.k_proj);
+        pin_scalar(fz.v_proj);
+        pin_scalar(fz.q_norm);
+        pin_scalar(fz.k_norm);
+        pin_scalar(fz.rope);
+        pin_scalar(fz.pairs);
+        pin_scalar(fz.eps);
+        pin_scalar(fz.k_cache);
+        pin_scalar(fz.v_cache);
+        pin_scalar(fz.head_stride);
+        pin_scalar(fz.new_key);
+    }
+    if (nproblems != 1) {
+        pr = (const_ptr<Problem>)p.problems + find_problem_wave(p.problems, p.nproblems, blockIdx.x);
+        pv = decode_view(pr);
+    }
+    const uint32_t local = blockIdx.x - (uint32_t)pv.tile_base;
+    const int split = (int)(local % (uint32_t)pv.splits);
+    const int kvh = (int)(local / (uint32_t)pv.splits);
     const int G = p.group;
     const int Hq = p.query_heads;
-    const int nrows = pr->queries * G;
+    const int nrows = pv.queries * G;
 
     // This split's segment and logical key range [a, b): splits are laid out
     // segment by segment and never straddle a boundary, so the segment's base
     // pointers and strides are uniform for the workgroup.
-    int seg = 0, sidx = split;
-    if (sidx >= pr->seg_splits[0]) {
-        sidx -= pr->seg_splits[0];
-        seg = 1;
-        if (sidx >= pr->seg_splits[1]) {
-            sidx -= pr->seg_splits[1];
-            seg = 2;
+    int sidx = split;
+    DecodeSegment sg = pv.seg0;
+    if (sidx >= pv.seg_splits0) {
+        sidx -= pv.seg_splits0;
+        int which = 1;
+        if (sidx >= pv.seg_splits1) {
+            sidx -= pv.seg_splits1;
+            which = 2;
         }
+        sg = decode_segment(pr, which);
     }
-    const int64_t seg_lo = pr->seg[seg].start > pr->vis_lo ? pr->seg[seg].start : pr->vis_lo;
-    const int64_t seg_end = pr->seg[seg].start + pr->seg[seg].keys;
-    const int64_t seg_hi = seg_end < pr->vis_hi ? seg_end : pr->vis_hi;
-    const int64_t a = seg_lo + (int64_t)sidx * pr->split_keys;
-    int64_t b = a + pr->split_keys;
+    const int64_t seg_lo = sg.start > pv.vis_lo ? sg.start : pv.vis_lo;
+    const int64_t seg_end = sg.start + sg.keys;
+    const int64_t seg_hi = seg_end < pv.vis_hi ? seg_end : pv.vis_hi;
+    const int64_t a = seg_lo + (int64_t)sidx * pv.split_keys;
+    int64_t b = a + pv.split_keys;
     if (b > seg_hi) b = seg_hi;
     const int span = (int)(b - a);
     // Row r of key a + rel starts at kbase/vbase + rel * row_bytes.
-    const int64_t seg_first = (int64_t)kvh * pr->seg[seg].head_stride +
-                              (a - pr->seg[seg].start) * pr->seg[seg].row_stride;
-    const uint8_t *kseg = reinterpret_cast<const uint8_t *>(pr->seg[seg].k) + seg_first * ES + 16 * sub;
-    const uint8_t *vseg = reinterpret_cast<const uint8_t *>(pr->seg[seg].v) + seg_first * ES + 16 * sub;
-    const int64_t row_bytes = pr->seg[seg].row_stride * ES;
+    const int64_t seg_first = (int64_t)kvh * sg.head_stride + (a - sg.start) * sg.row_stride;
+    const uint8_t *kseg = reinterpret_cast<const uint8_t *>(sg.k) + seg_first * ES + 16 * sub;
+    const uint8_t *vseg = reinterpret_cast<const uint8_t *>(sg.v) + seg_first * ES + 16 * sub;
+    const int64_t row_bytes = sg.row_stride * ES;
 
     bool bad = false;
     // Rows: visible range relative to a, and the query chunks in registers.
     int rlo[R], rhi[R];
     u32x4 q[R][CPL];
-    const uint8_t *qbase = reinterpret_cast<const uint8_t *>(pr->q);
+    const uint8_t *qbase = reinterpret_cast<const uint8_t *>(pv.q);
     for (int r = 0; r < R; ++r) {
         rlo[r] = 0;
         rhi[r] = 0;
@@ -344,13 +451,13 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         if (r < nrows) {
             const int t = r / G, h = kvh * G + r % G;
             int64_t lo, hi;
-            visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + t, &lo, &hi);
+            visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + t, &lo, &hi);
             lo -= a;
             hi -= a;
             rlo[r] = (int)(lo < 0 ? 0 : (lo > span ? span : lo));
             rhi[r] = (int)(hi < 0 ? 0 : (hi > span ? span : hi));
             if constexpr (!FUSED) {
-                const uint8_t *qrow = qbase + ((int64_t)t * pr->q_row_stride + (int64_t)h * D) * ES;
+                const uint8_t *qrow = qbase + ((int64_t)t * pv.q_row_stride + (int64_t)h * D) * ES;
                 for (int c = 0; c < CPL; ++c) q[r][c] = load16(qrow + 128 * c + 16 * sub);
             }
         }
@@ -362,48 +469,45 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     int rel_new = -1;
     int stream_span = span;
     if constexpr (FUSED) {
-        const int64_t rn = p.fused.new_key - a;
+        const int64_t rn = fz.new_key - a;
         if (rn >= 0 && rn < span) {
             rel_new = (int)rn;
             stream_span = rel_new;  // keys after the new one: none (it is the last)
         }
     }
-    // The producer's work, after the first K/V block is in flight (below).
+    // The producer's work, after the first K/V block is in flight (below):
+    // one wave per row (the Q rows of this KV head and, in the workgroup
+    // holding the new key, its K and V rows), packed to the cache dtype in
+    // 16-byte chunks; Q rows go to LDS for every wave, the K/V rows to the
+    // cache and to LDS for the scoring of the new key after the stream.
     auto produce = [&]() {
         if constexpr (FUSED) {
-            // Every load first (Q rows, and for wave 0 of the workgroup holding
-            // the new key its K and V rows), then the arithmetic.
-            const FusedDecode &f = p.fused;
-            const bool make_kv = rel_new >= 0 && wave == 0;
-            float xq[R][EPL], wq[EPL], cs[ProduceLayout<DT, D>::CS], xk[EPL], wk[EPL], xv[EPL];
-            for (int r = 0; r < R; ++r)
-                if (r < nrows) produce_load<DT, D>(f.q_proj + (int64_t)(kvh * G + r % G) * D, sub, xq[r]);
-            if (f.q_norm) produce_load<DT, D>(f.q_norm, sub, wq);
-            if (f.rope) produce_load_rope<DT, D>(f.rope, sub, cs);
-            if (make_kv) {
-                produce_load<DT, D>(f.k_proj + (int64_t)kvh * D, sub, xk);
-                produce_load<DT, D>(f.v_proj + (int64_t)kvh * D, sub, xv);
-                if (f.k_norm) produce_load<DT, D>(f.k_norm, sub, wk);
-            }
-            const bool rot = f.rope != nullptr;
-            for (int r = 0; r < R; ++r)
-                if (r < nrows)
-                    produce_row<DT, D>(xq[r], f.q_norm != nullptr, wq, f.eps, rot, cs, f.pairs, sub,
-                                       q[r], bad);
-            if (make_kv) {
-                u32x4 knew[CPL], vnew[CPL];
-                produce_row<DT, D>(xk, f.k_norm != nullptr, wk, f.eps, rot, cs, f.pairs, sub, knew, bad);
-                produce_row<DT, D>(xv, false, wk, 0.0f, false, cs, 0, sub, vnew, bad);
-                if (kg == 0) {
-                    const int64_t row0 = ((int64_t)kvh * f.head_stride + f.new_key * D) * ES;
-                    for (int c = 0; c < CPL; ++c) {
-                        *gstore_ptr<u32x4>(reinterpret_cast<uint8_t *>(f.k_cache) + row0 + 128 * c + 16 * sub) = knew[c];
-                        *gstore_ptr<u32x4>(reinterpret_cast<uint8_t *>(f.v_cache) + row0 + 128 * c + 16 * sub) = vnew[c];
-                        lds_new[(0 * CPL + c) * 8 + sub] = knew[c];
-                        lds_new[(1 * CPL + c) * 8 + sub] = vnew[c];
+            const FusedDecode &f = fz;
+            const int jobs = nrows + (rel_new >= 0 ? 2 : 0);
+            float *row = lds_prow + wave * D;
+            for (int job = wave; job < jobs; job += nw) {
+                const bool is_q = job < nrows, is_k = job == nrows;
+                const float *src = is_q ? f.q_proj + (int64_t)(kvh * G + job % G) * D
+                                        : (is_k ? f.k_proj : f.v_proj) + (int64_t)kvh * D;
+                const float *wn = is_q ? f.q_norm : (is_k ? f.k_norm : nullptr);
+                wave_produce_row<D>(src, wn, f.eps, is_q || is_k ? f.rope : nullptr, f.pairs, row,
+                                    lane, bad);
+                if (lane < ROWB / 16) {
+                    const u32x4 chunk = pack_chunk<DT>(row + lane * EPC);
+                    if (is_q) {
+                        lds_q[job * CPL * 8 + lane] = chunk;
+                    } else {
+                        lds_new[(is_k ? 0 : CPL * 8) + lane] = chunk;
+                        void *cache = is_k ? f.k_cache : f.v_cache;
+                        const int64_t row0 = ((int64_t)kvh * f.head_stride + f.new_key * D) * ES;
+                        *gstore_ptr<u32x4>(reinterpret_cast<uint8_t *>(cache) + row0 + 16 * lane) = chunk;
                     }
                 }
             }
+            __syncthreads();
+            for (int r = 0; r < R; ++r)
+                for (int c = 0; c < CPL; ++c)
+                    q[r][c] = r < nrows ? lds_q[r * CPL * 8 + 8 * c + sub] : u32x4{0, 0, 0, 0};
         }
     };
 
@@ -586,8 +690,8 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     __syncthreads();
 
     // Merge the waves: one thread per (row, feature).
-    const bool single = pr->splits == 1;
-    const int64_t slot = pr->slot_base + (int64_t)kvh * pr->splits + split;
+    const bool single = pv.splits == 1;
+    const int64_t slot = pr->slot_base + (int64_t)kvh * pv.splits + split;
     bool bad_mass = false, bad_out = false;
     for (int i = threadIdx.x; i < R * D; i += blockDim.x) {
         const int r = i / D, d = i - r * D;
@@ -608,11 +712,17 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
             const float v = O / L;
             bad_out |= !is_finite_f(v);
             gstore_ptr<float>(pr->out)[((int64_t)t * Hq + h) * D + d] = v;
-        } else {
-            coherent_store(p.part_o + (slot * R + r) * D + d, O);
+        } else if (split == pv.splits - 1) {
+            lds_own[r * D + d] = O;
             if (d == 0) {
-                coherent_store(p.part_ml + (slot * R + r) * 2 + 0, M);
-                coherent_store(p.part_ml + (slot * R + r) * 2 + 1, L);
+                lds_own[R * D + 2 * r] = M;
+                lds_own[R * D + 2 * r + 1] = L;
+            }
+        } else {
+            split_store(p.part_o + (slot * R + r) * D + d, O);
+            if (d == 0) {
+                split_store(p.part_ml + (slot * R + r) * 2 + 0, M);
+                split_store(p.part_ml + (slot * R + r) * 2 + 1, L);
             }
         }
     }
@@ -623,117 +733,113 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         return;
     }
 
-    // Split-K: the last workgroup of this KV head to arrive merges the partials.
-    // The partials went out as device-coherent (write-through) stores; once
-    // they are acknowledged (vmcnt 0) and the workgroup has synchronised, one
-    // lane counts the arrival.  The merging workgroup reads them with
-    // device-coherent loads.  No L2-wide write-back/invalidate is needed.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    uint32_t *counter = p.counters + pr->group_base + kvh;
-    if (threadIdx.x == 0)
-        lds_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   (uint32_t)(pr->splits - 1);
-    __syncthreads();
-    if (!lds_last) return;
-    const int64_t slot0 = pr->slot_base + (int64_t)kvh * pr->splits;
-    const int S = pr->splits;
-    const int OUT = R * D;
-    const int nt = blockDim.x;
-    // Threads per output when the workgroup is wider than the output (P > 1,
-    // a power of two): thread (k, o) handles splits k, k + P, ...
-    const int P = nt >= OUT ? nt / OUT : 1;
-    const int o0 = threadIdx.x % OUT, k0 = nt >= OUT ? threadIdx.x / OUT : 0;
-    constexpr int VB = 32;  // partial loads per thread issued together
-    // One round trip: (max, mass) of every (split, row) into LDS, and this
-    // thread's first VB partial contexts into registers.
-    for (int i = threadIdx.x; i < S * R; i += nt) {
-        lds_w[i] = coherent_load(p.part_ml + (slot0 * R + i) * 2);
-        lds_l[i] = coherent_load(p.part_ml + (slot0 * R + i) * 2 + 1);
-    }
-    float v0[VB];
-    {
-        const int r = o0 / D;
-        for (int j = 0; j < VB; ++j) {
-            const int sp = k0 + j * P;
-            v0[j] = (nt >= OUT && r < nrows && sp < S)
-                        ? coherent_load(p.part_o + ((slot0 + sp) * R) * D + o0) : 0.0f;
-        }
-    }
-    __syncthreads();
-    // Per row (one wave each): global maximum, split weights 2^(m_s - M), total mass.
-    for (int r = wave; r < R; r += nw) {
-        float M = NEG_INF;
-        for (int sp = lane; sp < S; sp += 64) M = fmaxf(M, lds_w[sp * R + r]);
-        M = wave_max(M);
-        const float base = M == NEG_INF ? 0.0f : M;
-        float L = 0.0f;
-        for (int sp = lane; sp < S; sp += 64) {
-            const float w = __builtin_amdgcn_exp2f(lds_w[sp * R + r] - base);
-            lds_w[sp * R + r] = w;
-            L += w * lds_l[sp * R + r];
-        }
-        L = wave_sum(L);
-        if (lane == 0) lds_mass[r] = L;
-    }
-    __syncthreads();
-    if (nt >= OUT) {
-        // Weighted sum of this thread's splits, then the P shares through LDS.
-        const int r = o0 / D;
-        float O = 0.0f;
-        if (r < nrows) {
-            for (int j = 0; j < VB; ++j) {
-                const int sp = k0 + j * P;
-                if (sp < S) O = __builtin_fmaf(lds_w[sp * R + r], v0[j], O);
-            }
-            for (int base = VB * P; base < S; base += VB * P) {
-                float v[VB];
-                for (int j = 0; j < VB; ++j) {
-                    const int sp = base + k0 + j * P;
-                    v[j] = sp < S ? coherent_load(p.part_o + ((slot0 + sp) * R) * D + o0) : 0.0f;
-                }
-                for (int j = 0; j < VB; ++j) {
-                    const int sp = base + k0 + j * P;
-                    if (sp < S) O = __builtin_fmaf(lds_w[sp * R + r], v[j], O);
-                }
-            }
-        }
-        lds_o[k0 * OUT + o0] = O;
+    // Split-K completion without atomics: every split but the last stores its
+    // partial, waits until the stores are acknowledged, and then stores this
+    // launch's epoch into its flag.  The last split of the KV head (its block
+    // index is the head's highest, so every other split was dispatched before
+    // it) keeps its own partial in LDS, waits for the other flags (bounded)
+    // and merges.
+    const int S = pv.splits;
+    const uint32_t epoch = p.epoch;
+    if (split != S - 1) {
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (k0 == 0 && r < nrows) {
-            float total = 0.0f;
-            for (int k = 0; k < P; ++k) total += lds_o[k * OUT + o0];
-            const float L = lds_mass[r];
-            const int d = o0 - r * D;
-            const int t = r / G, h = kvh * G + r % G;
-            bad_mass |= !(L > 0.0f) || !is_finite_f(L);
-            const float v = total / L;
-            bad_out |= !is_finite_f(v);
-            gstore_ptr<float>(pr->out)[((int64_t)t * Hq + h) * D + d] = v;
-        }
-    } else {
-        // More outputs than threads: each thread loops over outputs.
-        for (int i = threadIdx.x; i < OUT; i += nt) {
-            const int r = i / D, d = i - r * D;
-            if (r >= nrows) continue;
-            float O = 0.0f;
-            int sp = 0;
-            for (; sp + VB <= S; sp += VB) {
-                float v[VB];
-                for (int j = 0; j < VB; ++j) v[j] = coherent_load(p.part_o + ((slot0 + sp + j) * R + r) * D + d);
-                for (int j = 0; j < VB; ++j) O = __builtin_fmaf(lds_w[(sp + j) * R + r], v[j], O);
+        if (threadIdx.x == 0) flag_store(p.flags + slot, epoch);
+        return;
+    }
+    const int64_t slot0 = pr->slot_base + (int64_t)kvh * S;
+    if (wave == 0) {
+        const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+        bool arrived = false;
+        for (;;) {
+            const uint32_t f = lane < S - 1 ? flag_load(p.flags + slot0 + lane) : epoch;
+            if (__ballot(f != epoch) == 0) {
+                arrived = true;
+                break;
             }
-            for (; sp < S; ++sp)
-                O = __builtin_fmaf(lds_w[sp * R + r], coherent_load(p.part_o + ((slot0 + sp) * R + r) * D + d), O);
-            const float L = lds_mass[r];
-            const int t = r / G, h = kvh * G + r % G;
-            bad_mass |= !(L > 0.0f) || !is_finite_f(L);
-            const float v = O / L;
-            bad_out |= !is_finite_f(v);
-            gstore_ptr<float>(pr->out)[((int64_t)t * Hq + h) * D + d] = v;
+            if (__builtin_amdgcn_s_memrealtime() - t_start > SPLIT_WAIT_TICKS) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane == 0) lds_own[R * D + 2 * R] = arrived ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+    const bool timed_out = lds_own[R * D + 2 * R] == 0.0f;
+    // One wave per 64 outputs of one row (D is a multiple of 64).  Lane
+    // (g4, q4) = (lane / 16, lane % 16) reads, for splits 4 g + g4, the four
+    // outputs d0 + 4 q4 .. + 3 (16-byte buffer loads, sc1) and the split's
+    // (max, mass); lanes past the other splits read out of the buffer's range,
+    // which returns zeros and touches no memory, so every load of the merge is
+    // issued in one straight run with no branches and no repeated address.
+    // Then: the row maximum, per-split weights, the weighted sums over the
+    // lane's splits, and lane swaps over the four split groups.
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(p.part_ml, 0, 0x7FFFFFFF, BUFFER_RSRC_WORD3);
+    const uint32_t o_base = (uint32_t)(reinterpret_cast<const char *>(p.part_o) -
+                                       reinterpret_cast<const char *>(p.part_ml));
+    const int g4 = lane >> 4, q4 = lane & 15;
+    const int ng = (S + 3) >> 2;
+    const int chunks = R * D / 64;
+    for (int c = wave; c < chunks && !timed_out; c += nw) {
+        const int r = c * 64 / D, d = c * 64 - r * D + 4 * q4;
+        if (r >= nrows) continue;  // uniform over the wave
+        const uint32_t ml0 = (uint32_t)((slot0 * R + r) * 2) * 4u, ml_step = (uint32_t)R * 8u;
+        const uint32_t o0 = o_base + (uint32_t)((slot0 * R + r) * D + d) * 4u, o_step = (uint32_t)(R * D) * 4u;
+        f32x4 ov[DECODE_MAX_SPLITS / 4];
+        f32x2 mv[DECODE_MAX_SPLITS / 4];
+        for (int g = 0; g < DECODE_MAX_SPLITS / 4; ++g) {
+            if (g < ng) {
+                const int sp = 4 * g + g4;
+                const bool theirs = sp < S - 1;
+                ov[g] = __builtin_amdgcn_raw_buffer_load_b128(prs, theirs ? o0 + (uint32_t)sp * o_step : OUT_OF_RANGE, 0, CPOL_SC1_NT);
+                mv[g] = __builtin_amdgcn_raw_buffer_load_b64(prs, theirs ? ml0 + (uint32_t)sp * ml_step : OUT_OF_RANGE, 0, CPOL_SC1_NT);
+            }
+        }
+        const f32x4 own_o = *reinterpret_cast<const f32x4 *>(lds_own + r * D + d);
+        const f32x2 own_ml = {lds_own[R * D + 2 * r], lds_own[R * D + 2 * r + 1]};
+        float mmax = NEG_INF;
+        for (int g = 0; g < DECODE_MAX_SPLITS / 4; ++g) {
+            if (g < ng) {
+                const int sp = 4 * g + g4;
+                if (sp == S - 1) {
+                    ov[g] = own_o;
+                    mv[g] = own_ml;
+                } else if (sp >= S) {
+                    mv[g][0] = NEG_INF;
+                }
+                mmax = fmaxf(mmax, mv[g][0]);
+            }
+        }
+        const float M = wave_max_regs(mmax);
+        const float base = M == NEG_INF ? 0.0f : M;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        float lsum = 0.0f;
+        for (int g = 0; g < DECODE_MAX_SPLITS / 4; ++g) {
+            if (g < ng) {
+                const float wgt = __builtin_amdgcn_exp2f(mv[g][0] - base);
+                for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(wgt, ov[g][k], acc[k]);
+                lsum = __builtin_fmaf(wgt, mv[g][1], lsum);
+            }
+        }
+        // Each split's mass was read by its 16 lanes: count it once.
+        const float L = wave_sum_regs(q4 == 0 ? lsum : 0.0f);
+        for (int k = 0; k < 4; ++k) {
+            float a, b;
+            lane_pair<16>(acc[k], a, b);
+            lane_pair<32>(a + b, a, b);
+            acc[k] = a + b;
+        }
+        const int t = r / G, h = kvh * G + r % G;
+        bad_mass |= !(L > 0.0f) || !is_finite_f(L);
+        if (g4 == 0) {
+            f32x4 v;
+            for (int k = 0; k < 4; ++k) {
+                v[k] = acc[k] / L;
+                bad_out |= !is_finite_f(v[k]);
+            }
+            *gstore_ptr<f32x4>(pr->out + ((int64_t)t * Hq + h) * D + d) = v;
         }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    raise_status(p, timed_out, ST_SPLIT_TIMEOUT);
     raise_status(p, bad_mass, ST_BAD_MASS);
     raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
 }

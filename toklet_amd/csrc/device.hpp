@@ -21,6 +21,7 @@ enum StatusBits : uint32_t {
     ST_NONFINITE_INPUT = 1u,   // a visible score, or a partial context, is not finite
     ST_BAD_MASS = 2u,          // softmax mass not finite or not positive
     ST_NONFINITE_OUTPUT = 4u,  // combined context not finite
+    ST_SPLIT_TIMEOUT = 8u,     // a decode merge gave up waiting for the other key splits
 };
 
 struct Segment {
@@ -120,7 +121,9 @@ struct Params {
     float *probs;
     int32_t diag_mode;      // 0 none, 1 full [Hq, queries, keys], 2 last row [keys]
     int32_t pad2;
-    uint32_t *counters;     // split-K arrival counters (zero between launches)
+    uint32_t *flags;        // decode split-K completion flags, one per partial slot
+    uint32_t epoch;         // decode split-K: this launch's flag value (never 0; flags start at 0)
+    int32_t pad3;
     FusedDecode fused;      // decode kernel built with FUSED only
     Problem single;         // the problem itself when nproblems == 1 (no descriptor upload)
 };
@@ -148,16 +151,35 @@ __device__ __forceinline__ int find_problem(const Params &p, int64_t tile) {
     return lo;
 }
 
+// The same search by a whole wave: each lane tests one candidate, a ballot
+// picks the interval, so up to 64 problems take one round trip of loads and up
+// to 4096 two (the scalar binary search above is a chain of log2(n) dependent
+// loads).  Every lane of the wave must be active.
+__device__ __forceinline__ int find_problem_wave(const Problem *problems, int n, int64_t tile) {
+    const int lane = threadIdx.x & 63;
+    int lo = 0, count = n;
+    while (count > 1) {
+        const int stride = (count + 63) >> 6;
+        const int off = lane * stride;
+        const bool le = off < count && gload_ptr<Problem>(problems + lo + off)->tile_base <= tile;
+        const uint64_t m = __ballot(le);  // bit 0 is set: problems[lo] starts at or before tile
+        const int k = 63 - __builtin_clzll(m);
+        lo += k * stride;
+        count = count - k * stride < stride ? count - k * stride : stride;
+    }
+    return __builtin_amdgcn_readfirstlane(lo);
+}
+
 // The problem owning global tile `tile`, as a constant-space pointer: either
 // the copy inside the kernel arguments (Params must be the kernel's first
 // argument) or an entry of the uploaded descriptor array.  Its fields are
-// uniform and load through the scalar cache.
+// uniform and load through the scalar cache.  Call with the whole wave active.
 __device__ __forceinline__ const_ptr<Problem> problem_ptr(const Params &p, int64_t tile) {
     if (p.nproblems == 1) {
         const_ptr<Params> args = (const_ptr<Params>)__builtin_amdgcn_kernarg_segment_ptr();
         return &args->single;
     }
-    return (const_ptr<Problem>)p.problems + find_problem(p, tile);
+    return (const_ptr<Problem>)p.problems + find_problem_wave(p.problems, p.nproblems, tile);
 }
 
 // Generic reference form used by the VALU and MFMA kernels.
@@ -240,6 +262,47 @@ constexpr float NEG_INF = -__builtin_inff();
 
 __device__ __forceinline__ float xor_max(float x, int mask) { return fmaxf(x, __shfl_xor(x, mask, 64)); }
 __device__ __forceinline__ float xor_sum(float x, int mask) { return x + __shfl_xor(x, mask, 64); }
+
+// Sum over the wave by the xor butterfly x + x[lane ^ m], m = 32, 16, ..., 1,
+// in FP64: every lane ends with the same, fixed association.  The partner
+// values move in registers (lane swaps for 32 and 16, a DPP row rotate for 8,
+// a swizzle for 4, DPP quad permutes for 2 and 1), not through LDS.
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    auto halves = [](double v, uint32_t &lo, uint32_t &hi) {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        lo = (uint32_t)u;
+        hi = (uint32_t)(u >> 32);
+    };
+    auto join = [](uint32_t lo, uint32_t hi) {
+        return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+    };
+    uint32_t lo, hi;
+    {
+        halves(x, lo, hi);
+        const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        x = join(l[0], h[0]) + join(l[1], h[1]);
+    }
+    {
+        halves(x, lo, hi);
+        const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        x = join(l[0], h[0]) + join(l[1], h[1]);
+    }
+    halves(x, lo, hi);
+    x += join((uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, 0x128, 0xF, 0xF, false),
+              (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, 0x128, 0xF, 0xF, false));
+    halves(x, lo, hi);
+    x += join((uint32_t)__builtin_amdgcn_ds_swizzle((int)lo, 0x101F),
+              (uint32_t)__builtin_amdgcn_ds_swizzle((int)hi, 0x101F));
+    halves(x, lo, hi);
+    x += join((uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, 0x4E, 0xF, 0xF, false),
+              (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, 0x4E, 0xF, 0xF, false));
+    halves(x, lo, hi);
+    x += join((uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, 0xB1, 0xF, 0xF, false),
+              (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, 0xB1, 0xF, 0xF, false));
+    return x;
+}
 
 __device__ __forceinline__ float wave_max(float x) {
     for (int m = 32; m >= 1; m >>= 1) x = xor_max(x, m);

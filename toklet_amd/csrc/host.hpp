@@ -16,9 +16,6 @@ namespace tkh_host {
 
 inline constexpr int kSlots = 16;
 inline constexpr int kSlotProblems = 1024;
-// Split-K arrival counters at the head of the workspace (decode kernel).
-inline constexpr size_t kCounters = 65536;
-inline constexpr size_t kCounterBytes = kCounters * sizeof(uint32_t);
 
 // ---------------------------------------------------------------- errors
 
@@ -118,6 +115,7 @@ struct tkh_context {
     int decode_groups = 256;     // target decode workgroups per launch
     int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
     int decode_disable = 0;
+    uint32_t epoch = 0;          // last decode split-K epoch handed out
     int prefill_groups = 512;    // below this many row-block workgroups, split the keys
     int prefill_max_splits = 16;
     int prefill_min_keys = 256;  // keys per split at least
@@ -129,6 +127,19 @@ struct tkh_context {
     uint64_t prof_launches = 0;
     double prof_attention_ms = 0, prof_combine_ms = 0;
 };
+
+// The workspace halves: split-K partials of the prefill and generic kernels
+// in the lower half, the decode kernel's tagged partials in the upper half
+// (kept apart so no other kernel's bits can pass for a decode tag).
+inline size_t split_region_bytes(const tkh_context *ctx) { return ctx->workspace_bytes / 2; }
+inline size_t decode_region_offset(const tkh_context *ctx) {
+    return (ctx->workspace_bytes / 2 + 255) / 256 * 256;
+}
+inline uint8_t *decode_region(const tkh_context *ctx) { return ctx->workspace + decode_region_offset(ctx); }
+inline size_t decode_region_bytes(const tkh_context *ctx) {
+    const size_t off = decode_region_offset(ctx);
+    return off < ctx->workspace_bytes ? (ctx->workspace_bytes - off) / 8 * 8 : 0;
+}
 
 struct tkh_kv {
     tkh_context *ctx = nullptr;

@@ -12,6 +12,8 @@
 //  * logit_softcap: cap * tanh(x / cap) in FP64, rounded once to FP32
 //    (src/cpu/softcap.rs:16-29).
 //  * convert: FP32 -> storage dtype rounding for callers that hold FP32 rows.
+#include <algorithm>
+
 #include "device.hpp"
 
 namespace tkh {
@@ -120,6 +122,11 @@ __global__ __launch_bounds__(256) void convert_from_f32(const float *src, void *
 
 __global__ void fill_u32(uint32_t *p, uint32_t v) { *p = v; }
 __global__ void fill_u64(uint64_t *p, uint64_t v) { *p = v; }
+__global__ __launch_bounds__(256) void zero_u64(uint64_t *p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
 
 }  // namespace tkh
 
@@ -193,6 +200,15 @@ extern "C" hipError_t tkh_launch_convert(int dtype, const float *src, void *dst,
 
 extern "C" hipError_t tkh_launch_fill_u64(uint64_t *p, uint64_t v, hipStream_t stream) {
     hipLaunchKernelGGL(fill_u64, dim3(1), dim3(1), 0, stream, p, v);
+    return hipGetLastError();
+}
+
+// Zero `words` 8-byte words (a kernel rather than a memset node, so the
+// clear also behaves inside a captured graph).
+extern "C" hipError_t tkh_launch_zero_u64(uint64_t *p, int64_t words, hipStream_t stream) {
+    if (words <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((words + 255) / 256, 4096);
+    hipLaunchKernelGGL(zero_u64, dim3((unsigned)blocks), dim3(256), 0, stream, p, words);
     return hipGetLastError();
 }
 

@@ -57,10 +57,6 @@ template <> __device__ __forceinline__ void store_out<BF16>(void *base, int64_t 
     reinterpret_cast<__bf16 *>(base)[i] = (__bf16)x;  // round to nearest even
 }
 
-__device__ __forceinline__ double wave_sum_f64(double x) {
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-    return x;
-}
 
 }  // namespace
 

@@ -296,9 +296,9 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
         return invalid("windowed layers need an explicit score scale", err);
     }
     s->history.reserve(o->capacity);
-    // Decode steps with the producer inside the decode kernel: head sizes of
-    // that kernel, GQA groups whose rows' producer inputs fit the registers
-    // (at most 1 KiB of cache-dtype rows per lane group), no softcap.
+    // Decode steps with the producer inside the decode kernel (one launch per
+    // step instead of two; TKH_FUSED_DECODE=0 turns it off): head sizes of
+    // that kernel, GQA groups of at most 1 KiB of cache-dtype rows, no softcap.
     {
         const uint64_t G = o->query_heads / o->kv_heads;
         const uint64_t rowb = o->head_dim * (uint64_t)esize(o->storage);
