@@ -227,11 +227,14 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
         max_span = std::max<int64_t>(max_span, p.vis_hi - p.vis_lo);
     }
     // Keys per split: about decode_groups workgroups in all, at most
-    // max_splits per KV head, in whole blocks; then as many waves (up to nw)
-    // as the split has blocks, so no wave starts without work.  Short spans
-    // thus spread over more, narrower workgroups.
+    // max_splits per KV head, in whole blocks, and at least one block for
+    // each wave a split launch needs (its merge reads 64 outputs per wave);
+    // then as many waves (up to nw) as the split has blocks, so no wave
+    // starts without work.
+    const int merge_waves = std::min(nw_max, (int)((R * D + 63) / 64));
     int64_t sk = (int64_t)std::ceil(work / ctx->decode_groups);
     sk = std::max<int64_t>(sk, (max_span + max_splits - 1) / max_splits);
+    if (sk < max_span) sk = std::max<int64_t>(sk, kpb * merge_waves);
     if (ctx->split_keys_override > 0) sk = ctx->split_keys_override;
     sk = std::max<int64_t>(kpb, (sk + kpb - 1) / kpb * kpb);
     if (sk > INT32_MAX) return fail(err, TKH_UNSUPPORTED, "keys", 0, 0, 0, "key range too large");
@@ -269,7 +272,7 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     // wave per 64 outputs (within the kernel's limit) makes the merge one pass.
     bool any_split = false;
     for (auto &p : group) any_split |= p.splits > 1;
-    if (any_split) nw = std::max(nw, std::min(nw_max, (int)((R * D + 63) / 64)));
+    if (any_split) nw = std::max(nw, merge_waves);
 
     // Decode partials: completion flags, then (max, mass) and contexts, in the
     // decode half of the workspace.
