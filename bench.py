@@ -12,8 +12,9 @@ Reported (one JSON line): decode attention GB/s over the decode phase as
 `value` (algorithmic bytes: visible keys x 2*Hkv*D*2 + Q/O bytes), prefill
 attention TFLOPS (4*Hq*D per visible (query, key) pair), the roofline of the
 decode attention kernel from HIP events on its stream, the north-star
-configurations (configs[2] batched decode, configs[4] batched prefill), and
-the CPU oracle timed on this host as the baseline.
+configurations (single-session and 16-session decode at 8192 keys,
+configs[2] batched decode, configs[3] Gemma local/global, configs[4] batched
+prefill), and the CPU oracle timed on this host as the baseline.
 """
 
 from __future__ import annotations
@@ -43,7 +44,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-north-star", action="store_true", help="skip configs[2]/[4]")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "d8k", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "d8k", "d8kb", "copy"], default=None,
                     help="run a single workload (for profiling); `copy` runs a plain 1 GiB "
                          "device copy that calibrates the FETCH_SIZE/WRITE_SIZE counters")
     return ap.parse_args()
@@ -464,6 +465,11 @@ def main():
                                  dtype=torch.bfloat16)
         log("single-session decode at 8192: " + json.dumps(d8k))
         result["decode_8k"] = d8k
+    if not args.no_north_star and args.only in (None, "d8kb"):
+        d8kb = bench_decode_batch(torch, ops, ctx, 20, 3, batch=16, lmin=8192, lmax=8192,
+                                  dtype=torch.bfloat16)
+        log("sustained decode at 8192, 16 sessions: " + json.dumps(d8kb))
+        result["decode_8k_batch16"] = d8kb
     if not args.no_north_star and args.only in (None, "c3"):
         c3 = bench_decode_batch(torch, ops, ctx, 20, 3, batch=64, lmin=512, lmax=8192,
                                 dtype=torch.float16)
@@ -523,7 +529,8 @@ def main():
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(c2["prefill_kernel_tflops"] / PEAK_BF16_TFLOPS, 5),
         },
-        "north_star": {k: result[k] for k in ("decode_8k", "c3", "c4", "c5") if k in result},
+        "north_star": {k: result[k] for k in ("decode_8k", "decode_8k_batch16", "c3", "c4", "c5")
+                       if k in result},
         "detail": c2,
     }
     if not args.no_cpu and w is not None:

@@ -214,11 +214,6 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
                        int rows, tkh_error *err) {
     const int64_t D = plan.head_dim, Hkv = plan.kv_heads;
     const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
-    const int nw_max = std::min(ctx->decode_waves, tkh_decode_max_waves((int)plan.dtype, (int)D, R));
-    int nw = nw_max;
-    const int u = tkh_decode_keys_per_lane((int)plan.dtype, (int)D, ctx->decode_keys_per_lane);
-    const int max_splits = std::min(ctx->decode_max_splits, tkh_decode_max_splits());
-    const int64_t kpb = (int64_t)8 * u;  // keys per wave block
     double work = 0;
     int64_t max_span = 0;
     for (auto &p : group) {
@@ -226,13 +221,32 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
         work += (double)Hkv * (double)(p.vis_hi - p.vis_lo);
         max_span = std::max<int64_t>(max_span, p.vis_hi - p.vis_lo);
     }
+    // Two regimes.  Little work (a few sessions): latency decides, so one
+    // round of wide workgroups (eight waves, one per CU).  Much work: the
+    // stream decides, so many narrower workgroups (two per CU), which keeps
+    // every CU streaming while others start or merge and evens out sessions
+    // of different lengths.
+    // With much work of even length (sessions of about the same span), one
+    // round of two workgroups per CU suffices and keeps the per-workgroup
+    // start and merge costs few; spans of mixed lengths take several rounds
+    // so the dispatcher can even them out.
+    const bool bulk = work >= (double)ctx->decode_bulk_keys * ctx->cus;
+    const bool even = work >= 0.9 * (double)Hkv * (double)max_span * (double)group.size();
+    const int nw_max = std::min(bulk ? ctx->decode_bulk_waves : ctx->decode_waves,
+                                tkh_decode_max_waves((int)plan.dtype, (int)D, R));
+    const double groups = !bulk ? ctx->decode_groups
+                                : (even ? ctx->decode_even_groups : ctx->decode_bulk_groups);
+    int nw = nw_max;
+    const int u = tkh_decode_keys_per_lane((int)plan.dtype, (int)D, ctx->decode_keys_per_lane);
+    const int max_splits = std::min(ctx->decode_max_splits, tkh_decode_max_splits());
+    const int64_t kpb = (int64_t)8 * u;  // keys per wave block
     // Keys per split: about decode_groups workgroups in all, at most
     // max_splits per KV head, in whole blocks, and at least one block for
     // each wave a split launch needs (its merge reads 64 outputs per wave);
     // then as many waves (up to nw) as the split has blocks, so no wave
     // starts without work.
     const int merge_waves = std::min(nw_max, (int)((R * D + 63) / 64));
-    int64_t sk = (int64_t)std::ceil(work / ctx->decode_groups);
+    int64_t sk = (int64_t)std::ceil(work / groups);
     sk = std::max<int64_t>(sk, (max_span + max_splits - 1) / max_splits);
     if (sk < max_span) sk = std::max<int64_t>(sk, kpb * merge_waves);
     if (ctx->split_keys_override > 0) sk = ctx->split_keys_override;
@@ -548,8 +562,13 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
         int cus = 256;
         if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
             cus = prop.multiProcessorCount;
+        ctx->cus = cus;
         ctx->decode_groups = std::max(1, env_int("TKH_DECODE_GROUPS", cus));
+        ctx->decode_bulk_groups = std::max(1, env_int("TKH_DECODE_BULK_GROUPS", 8 * cus));
+        ctx->decode_even_groups = std::max(1, env_int("TKH_DECODE_EVEN_GROUPS", 2 * cus));
     }
+    ctx->decode_bulk_waves = std::min(8, std::max(1, env_int("TKH_DECODE_BULK_WAVES", 4)));
+    ctx->decode_bulk_keys = std::max(1, env_int("TKH_DECODE_BULK_KEYS", 2048));
     ctx->decode_max_splits = std::max(1, env_int("TKH_DECODE_MAX_SPLITS", 64));
     ctx->decode_disable = env_int("TKH_DECODE_DISABLE", 0);
     ctx->prefill_groups = std::max(1, env_int("TKH_PREFILL_GROUPS", 512));

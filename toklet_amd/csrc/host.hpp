@@ -112,7 +112,12 @@ struct tkh_context {
     int force_generic = 0;
     int decode_waves = 8;        // waves per decode workgroup
     int decode_keys_per_lane = 4;  // keys each lane holds per streamed block
-    int decode_groups = 256;     // target decode workgroups per launch
+    int cus = 256;               // compute units of the device
+    int decode_groups = 256;     // target decode workgroups per launch (little work)
+    int decode_bulk_groups = 2048;  // ... when the launch has much work of mixed lengths
+    int decode_even_groups = 512;   // ... when the launch has much work of even length
+    int decode_bulk_waves = 4;   // waves per decode workgroup when the launch has much work
+    int decode_bulk_keys = 2048; // keys x KV heads per CU from which a launch has much work
     int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
     int decode_disable = 0;
     uint32_t epoch = 0;          // last decode split-K epoch handed out
