@@ -16,10 +16,12 @@
 //    Q stays in registers as the B operand for the whole key range.
 //  * O^T = V^T P^T on the same MFMA.  The V^T operand comes from LDS with
 //    ds_read_b64_tr_b16 (each 16-lane group reads 4 keys x 16 features and
-//    receives them transposed); P^T is already in B-operand layout.  For
-//    bf16 the probabilities are split into a bf16 head and a bf16 remainder
-//    (two MFMAs) because a single bf16 rounding of P can move the output by
-//    more than 2e-3; f16 probabilities are rounded once.
+//    receives them transposed); P^T is already in B-operand layout.  P is
+//    rounded once to f16 for both dtypes (a single bf16 rounding of P can
+//    move the output by more than 2e-3).  For bf16 the V tile is converted
+//    in LDS, once per workgroup, to f16 scaled by 2^-8 (exact for every bf16
+//    value from 2^-6 up; smaller ones lose at most 2^-17 absolute, and the
+//    f16 range then covers |v| < 2^24), and the context is scaled back by 2^8.
 //  * The online-softmax rescale of O is skipped for a tile unless some
 //    row's running maximum moved.
 //  * Workgroups are mapped XCD-major (dispatch slot b runs on XCD b % 8) so
@@ -129,6 +131,29 @@ template <int D> struct PrefillLds {
     __device__ static constexpr int at(int r, int c) { return r * row + ((c ^ swz(r)) << 4); }
 };
 
+// bf16 V tile (PF_KT keys x D, staged in LDS) to f16 scaled by 2^-8, in
+// place, by the whole workgroup: thread `tid` converts the 16-byte chunks
+// tid, tid + 256, ... (consecutive lanes, consecutive chunks).  Split in a
+// read half and a convert-and-write half so a caller can put MFMAs between.
+template <int D> struct VConvert {
+    static constexpr int chunks = PF_KT * D * 2 / 16 / (64 * PF_WAVES);  // per thread
+    u32x4 w[chunks];
+    __device__ void read(lds_ptr<uint8_t> vt, int tid) {
+        for (int c = 0; c < chunks; ++c) w[c] = ((lds_ptr<u32x4>)vt)[c * 64 * PF_WAVES + tid];
+    }
+    __device__ void write(lds_ptr<uint8_t> vt, int tid) {
+        for (int c = 0; c < chunks; ++c) {
+            u32x4 o;
+            for (int j = 0; j < 4; ++j) {
+                const f32x2 v = {__builtin_bit_cast(float, w[c][j] << 16) * 0x1p-8f,
+                                 __builtin_bit_cast(float, w[c][j] & 0xffff0000u) * 0x1p-8f};
+                o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+            }
+            ((lds_ptr<u32x4>)vt)[c * 64 * PF_WAVES + tid] = o;
+        }
+    }
+};
+
 // Wait until at most `ahead` later tiles' direct loads of this wave are in
 // flight, then synchronise the workgroup.  Direct global->LDS loads count in
 // vmcnt; the compiler neither tracks nor orders them, hence the explicit wait
@@ -161,7 +186,8 @@ template <int DT, int D, bool CAP>
 __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(Params p) {
     constexpr int KS = D / 16;        // QK k-steps (16 features each)
     constexpr int MB = D / 32;        // PV M-blocks (32 features each)
-    constexpr bool SPLIT_P = DT == BF16;
+    constexpr int PDT = F16;          // P and V^T operand type of the P.V MFMAs
+    constexpr bool VCONV = DT == BF16;  // V tiles converted to scaled f16 in LDS
     static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
     using L = PrefillLds<D>;
     constexpr int NS = L::stages;
@@ -341,22 +367,28 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     // position.  In iteration 0 step 1 multiplies zero operands, and after the
     // last tile step 3 scores stale LDS data (of a stage that holds an earlier
     // tile) that is never used.
-    constexpr int NPV = 2 * MB * (SPLIT_P ? 2 : 1);  // P.V MFMAs per tile
-    constexpr int W = SPLIT_P ? 2 : 1;
+    constexpr int NPV = 2 * MB;  // P.V MFMAs per tile
     for (int t = 0; t < NS - 1 && t < ntiles; ++t) issue(t);
     f32x16 st;
     for (int i = 0; i < 16; ++i) st[i] = 0.0f;
+    VConvert<D> vconv;
     if (ntiles > 0) {
         wait_tile(0);
         for (int ks = 0; ks < KS; ++ks) st = mfma32<DT>(*(lds_ptr<u32x4>)(lds + k_off[ks]), qb[ks], st);
+        if constexpr (VCONV) {
+            vconv.read(lds + L::tile, threadIdx.x);
+            vconv.write(lds + L::tile, threadIdx.x);
+            // Tile 0's V^T is read at the end of iteration 0, after the
+            // barrier of its step 2, which a single tile does not have.
+            if (ntiles == 1) __syncthreads();
+        }
     }
     u32x4 vop[2][MB];                  // V^T operands of the tile whose P.V is pending
-    uint32_t ph[8], pl[8];             // its probabilities (bf16: head and remainder)
+    uint32_t ph[8];                    // its probabilities (f16 pairs)
     for (int stp = 0; stp < 2; ++stp)
         for (int mb = 0; mb < MB; ++mb) vop[stp][mb] = u32x4{0, 0, 0, 0};
     for (int i = 0; i < 8; ++i) {
         ph[i] = 0u;
-        pl[i] = 0u;
     }
     int stage = 0;
     for (int t = 0; t < ntiles; ++t) {
@@ -370,14 +402,13 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         float tv[CAP ? 16 : 1];  // softcapped scores (the raw scores serve otherwise)
         float hi = NEG_INF, corr = 1.0f, nbase = 0.0f;
         bool rescale = false;
-        uint32_t nh[4], nl[4] = {0u, 0u, 0u, 0u};
+        uint32_t nh[4];
 #pragma unroll
         for (int k = 0; k < NPV; ++k) {
             {
-                const int stp = k / (MB * W), mb = (k / W) % MB, part = k % W;
-                const u32x4 bv = part ? u32x4{pl[4 * stp], pl[4 * stp + 1], pl[4 * stp + 2], pl[4 * stp + 3]}
-                                      : u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
-                acc[mb] = mfma32<DT>(vop[stp][mb], bv, acc[mb]);
+                const int stp = k / MB, mb = k % MB;
+                const u32x4 bv = u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
+                acc[mb] = mfma32<PDT>(vop[stp][mb], bv, acc[mb]);
             }
             __builtin_amdgcn_sched_barrier(0);
             if (k == 0) {
@@ -433,12 +464,11 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
                 if (k == (NPV > 2 ? 2 + (i * (NPV - 2)) / 4 : NPV - 1)) {
                     const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
                     const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
-                    nh[i] = pack2<DT>(e0, e1);
-                    if constexpr (SPLIT_P) nl[i] = pack2<DT>(e0 - lo_f<DT>(nh[i]), e1 - hi_f<DT>(nh[i]));
+                    nh[i] = pack2<PDT>(e0, e1);
                     l_run += e0 + e1;
                     // Pin the pair here: the compiler would otherwise sink it to
                     // its use after step 1, out of the MFMA shadow.
-                    asm volatile("" : "+v"(nh[i]), "+v"(nl[i]), "+v"(l_run));
+                    asm volatile("" : "+v"(nh[i]), "+v"(l_run));
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -448,7 +478,6 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
                 for (int i = 0; i < 16; ++i) acc[mb][i] *= corr;
         for (int i = 0; i < 4; ++i) {
             ph[i] = nh[i];
-            if constexpr (SPLIT_P) pl[i] = nl[i];
         }
 
         // ---- step 2: tile t + 1 resident; everyone is done with tile t - 1,
@@ -465,19 +494,26 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         for (int i = 0; i < 16; ++i) st_next[i] = 0.0f;
         u32x4 kq[KPRE];
         for (int i = 0; i < KPRE && i < KS; ++i) kq[i] = *(lds_ptr<u32x4>)(kn + k_off[i]);
+        // bf16: tile t + 1's V, resident since step 2, converted between these
+        // MFMAs; the barrier of the next step 2 precedes its V^T reads.
+        const bool conv_next = VCONV && t + 1 < ntiles;
+        lds_ptr<uint8_t> vn = kn + L::tile;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const u32x4 kcur = kq[ks % KPRE];
             if (ks + KPRE < KS) kq[ks % KPRE] = *(lds_ptr<u32x4>)(kn + k_off[ks + KPRE]);
             st_next = mfma32<DT>(kcur, qb[ks], st_next);
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (VCONV) {
+                if (ks == 0 && conv_next) vconv.read(vn, threadIdx.x);
+                if (ks == KS / 2 && conv_next) vconv.write(vn, threadIdx.x);
+            }
             for (int i = 4 + 4 * ks / KS; i < 4 + 4 * (ks + 1) / KS; ++i) {
                 const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
                 const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
-                ph[i] = pack2<DT>(e0, e1);
-                if constexpr (SPLIT_P) pl[i] = pack2<DT>(e0 - lo_f<DT>(ph[i]), e1 - hi_f<DT>(ph[i]));
+                ph[i] = pack2<PDT>(e0, e1);
                 l_run += e0 + e1;
-                asm volatile("" : "+v"(ph[i]), "+v"(pl[i]), "+v"(l_run));
+                asm volatile("" : "+v"(ph[i]), "+v"(l_run));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -499,10 +535,9 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     if (ntiles > 0) {
 #pragma unroll
         for (int k = 0; k < NPV; ++k) {
-            const int stp = k / (MB * W), mb = (k / W) % MB, part = k % W;
-            const u32x4 bv = part ? u32x4{pl[4 * stp], pl[4 * stp + 1], pl[4 * stp + 2], pl[4 * stp + 3]}
-                                  : u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
-            acc[mb] = mfma32<DT>(vop[stp][mb], bv, acc[mb]);
+            const int stp = k / MB, mb = k % MB;
+            const u32x4 bv = u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
+            acc[mb] = mfma32<PDT>(vop[stp][mb], bv, acc[mb]);
         }
     }
     // ---- the two key halves of each row (lanes j and j + 32) share m_run; add l.
@@ -518,9 +553,11 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     // O^T lane layout: row j, features 32 mb + 8 q + 4 h + r (register 4 q + r).
     const bool single = pr->splits == 1;
     bool bad_mass = false, bad_out = false;
+    // bf16: the P.V products used V scaled by 2^-8.
+    constexpr float oscale = VCONV ? 256.0f : 1.0f;
     if (single) {
         if (rvalid) {
-            const float inv = 1.0f / l_run;
+            const float inv = oscale / l_run;
             bad_mass |= !(l_run > 0.0f) || !is_finite_f(l_run);
             float *orow = pr->out + ((int64_t)t_row * Hq + h_row) * D;
             for (int mb = 0; mb < MB; ++mb)
@@ -547,7 +584,8 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     float *po = p.part_o + (slot * PF_ROWS + wave * 32 + j) * D;
     for (int mb = 0; mb < MB; ++mb)
         for (int q = 0; q < 4; ++q) {
-            const f32x4 v = {acc[mb][4 * q], acc[mb][4 * q + 1], acc[mb][4 * q + 2], acc[mb][4 * q + 3]};
+            const f32x4 v = {acc[mb][4 * q] * oscale, acc[mb][4 * q + 1] * oscale,
+                             acc[mb][4 * q + 2] * oscale, acc[mb][4 * q + 3] * oscale};
             *gstore_ptr<f32x4>(po + 32 * mb + 8 * q + 4 * h) = v;
         }
     if (h == 0) {
