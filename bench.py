@@ -67,9 +67,10 @@ def qk_producer(torch, x, weight, positions, theta):
 
 
 class C2:
-    """Qwen3-shaped single session driven through the native session:
-    per chunk and layer, the producer (per-head RMSNorm, rotary 1e6, bf16 rounding,
-    K/V append) and the attention kernel, issued by tkh_session_evaluate."""
+    """Qwen3-shaped single session driven through the native session
+    (tkh_session_evaluate): per prefill chunk and layer, the producer (per-head
+    RMSNorm, rotary 1e6, bf16 rounding, K/V append) and the attention kernel; per
+    decode step, one decode launch with the producer folded in."""
     hq, hkv, d = 16, 8, 128
     prefill, chunk, decode = 2048, 128, 256
 
@@ -513,7 +514,8 @@ def main():
         "decode_us_per_token": round(c2["decode_us_per_token"], 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_decode<bf16, D=128, 2 rows> (the 256 decode launches of configs[1])",
+            "kernel": "attn_decode<bf16, D=128, 2 rows, producer folded in> (the 256 decode "
+                      "launches of configs[1])",
             "achieved": round(c2["decode_kernel_gbs"], 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
