@@ -1,11 +1,14 @@
 """GPU parity of the streaming decode kernel (few query rows per KV head).
 
 Long contexts split the keys over many workgroups, so these cases exercise the
-split-K merge done by the last workgroup of each KV head, the arrival counters
-being reset between calls, per-row causal limits when a short chunk has
-several tokens, windows and the score softcap at head_dim 256, and ring spans.
-The checker is the CPU oracle on the same stored (rounded) values.
+split-K merge done by the last split of each KV head (completion flags with a
+new epoch per launch), per-row causal limits when a short chunk has several
+tokens, windows and the score softcap at head_dim 256, ring spans, both
+planner regimes for many sessions, and the merge's bounded wait (forced from
+the host).  The checker is the CPU oracle on the same stored (rounded) values.
 """
+
+import os
 
 import numpy as np
 import pytest
@@ -95,9 +98,9 @@ def test_gqa7_d64_and_fp32(torch_mod, ctx, ops, orc):
     assert err <= TOL_F32
 
 
-def test_repeated_calls_are_identical_and_counters_reset(torch_mod, ctx, ops, orc):
-    """The split-K arrival counters return to zero: the same call twice is bit-identical,
-    and a different split layout in between does not disturb it."""
+def test_repeated_calls_are_identical_across_epochs(torch_mod, ctx, ops, orc):
+    """Each launch waits for its own epoch: the same call twice is bit-identical, and a
+    different split layout in between (other flags, other slots) does not disturb it."""
     a1, ref = _cached_case(torch_mod, ctx, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
                            capacity=8192, offset=8191, tokens=1, seed=21)
     _cached_case(torch_mod, ctx, ops, orc, hq=16, hkv=8, D=128, dt="bf16", capacity=1000,
@@ -201,3 +204,55 @@ def test_decode_batch_many_sessions_lengths_to_8192(torch_mod, ctx, ops, orc):
         worst = max(worst, max_err(got[b], ref))
     log(f"decode batch of {B}: worst max abs error {worst:.3e}")
     assert worst <= TOL_HALF
+
+
+def test_decode_batch_even_lengths_one_round(torch_mod, ctx, ops, orc):
+    """8 bf16 sessions of 8192 keys: much work of even length, the planner's one-round
+    regime (four-wave workgroups, two per CU)."""
+    torch = torch_mod
+    rng = np.random.default_rng(53)
+    hq, hkv, D, B, L = 16, 8, 128, 8, 8192
+    n = hkv * L * D
+    kpool = stored(rng.standard_normal(B * n), "bf16")
+    vpool = stored(rng.standard_normal(B * n), "bf16")
+    q = stored(rng.standard_normal((B, hq, D)), "bf16")
+    out = torch.zeros(B * hq * D, dtype=torch.float32, device="cuda")
+    offsets = [b * n for b in range(B)]
+    ops.decode_batch(ctx, dev(q, "bf16"), dev(kpool, "bf16"), dev(vpool, "bf16"), offsets,
+                     [L * D] * B, [L] * B, out, query_heads=hq, kv_heads=hkv, head_dim=D,
+                     scale=1.0 / np.sqrt(D))
+    got = host(out).reshape(B, -1)
+    worst = 0.0
+    for b in range(B):
+        ref, _, _ = orc.attention_cached(q[b].reshape(-1), kpool[b * n:(b + 1) * n],
+                                         vpool[b * n:(b + 1) * n], 1, hq, hkv, D, L, L - 1)
+        worst = max(worst, max_err(got[b], ref))
+    log(f"decode batch of {B} x {L}: worst max abs error {worst:.3e}")
+    assert worst <= TOL_HALF
+
+
+def test_split_wait_is_bounded_and_reported(torch_mod, ops, orc):
+    """Forced from the host: a context whose decode merges wait for a flag value no split
+    stores, with a 20 us bound.  Every workgroup exits, the launch reports a device error
+    naming the splits, and a normal context afterwards computes correctly."""
+    saved = {k: os.environ.get(k) for k in ("TKH_TEST_SPLIT_WAIT_TICKS", "TKH_TEST_SPLIT_FLAG_SKEW")}
+    os.environ["TKH_TEST_SPLIT_WAIT_TICKS"] = "2000"
+    os.environ["TKH_TEST_SPLIT_FLAG_SKEW"] = "1"
+    try:
+        forced = ops.Context(0)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    with pytest.raises(ops.TkhError) as e:
+        _cached_case(torch_mod, forced, ops, orc, hq=16, hkv=8, D=128, dt="bf16", capacity=4100,
+                     offset=4095, tokens=1, seed=31)
+    assert e.value.name == "Device" and e.value.tensor == "decode splits"
+    assert "timed out" in e.value.message
+    forced.close()
+    clean = ops.Context(0)
+    got, ref = _cached_case(torch_mod, clean, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
+                            capacity=4100, offset=4095, tokens=1, seed=31)
+    assert max_err(got, ref) <= TOL_HALF

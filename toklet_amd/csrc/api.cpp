@@ -314,6 +314,10 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
         ctx->epoch = 1;
     }
     prm.epoch = ctx->epoch;
+    // The merging split waits for this launch's epoch; the test hook makes it
+    // wait for one that no split stores, to exercise the bounded wait.
+    prm.wait_epoch = ctx->epoch + (ctx->test_flag_skew ? 1u : 0u);
+    prm.split_wait_ticks = ctx->split_wait_ticks;
     prm.flags = reinterpret_cast<uint32_t *>(decode_region(ctx));
     float *ws = reinterpret_cast<float *>(decode_region(ctx) + flag_bytes);
     prm.part_ml = ws;
@@ -410,12 +414,6 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
     if (group.size() == 1) prm.single = group[0];
     prm.nproblems = (int32_t)group.size();
     prm.total_tiles = wgs;
-    bool split = false;
-    for (auto &p : group) split |= p.splits > 1;
-    if (split) {
-        if (++ctx->epoch == 0) ctx->epoch = 1;
-        prm.epoch = ctx->epoch;
-    }
     float *ws = reinterpret_cast<float *>(ctx->workspace);
     prm.part_ml = ws;
     prm.part_o = ws + (size_t)slots * rows_per * 2;
@@ -569,6 +567,10 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     }
     ctx->decode_bulk_waves = std::min(8, std::max(1, env_int("TKH_DECODE_BULK_WAVES", 4)));
     ctx->decode_bulk_keys = std::max(1, env_int("TKH_DECODE_BULK_KEYS", 2048));
+    // Test hooks for the decode merge's bounded wait (s_memrealtime ticks,
+    // 100 MHz; default half a second) and a flag value no split stores.
+    ctx->split_wait_ticks = (uint64_t)std::max(1, env_int("TKH_TEST_SPLIT_WAIT_TICKS", 50000000));
+    ctx->test_flag_skew = env_int("TKH_TEST_SPLIT_FLAG_SKEW", 0) != 0;
     ctx->decode_max_splits = std::max(1, env_int("TKH_DECODE_MAX_SPLITS", 64));
     ctx->decode_disable = env_int("TKH_DECODE_DISABLE", 0);
     ctx->prefill_groups = std::max(1, env_int("TKH_PREFILL_GROUPS", 512));

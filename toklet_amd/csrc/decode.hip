@@ -260,10 +260,6 @@ __device__ __forceinline__ float wave_sum_regs(float x) {
     return a + b;
 }
 
-// Longest wait of a merging workgroup for the other splits of its KV head
-// (s_memrealtime ticks, 100 MHz): half a second, far beyond any split's work,
-// after which the launch reports ST_SPLIT_TIMEOUT instead of waiting on.
-constexpr uint64_t SPLIT_WAIT_TICKS = 50000000ull;
 
 }  // namespace
 
@@ -752,12 +748,14 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
         bool arrived = false;
         for (;;) {
-            const uint32_t f = lane < S - 1 ? flag_load(p.flags + slot0 + lane) : epoch;
-            if (__ballot(f != epoch) == 0) {
+            const uint32_t f = lane < S - 1 ? flag_load(p.flags + slot0 + lane) : p.wait_epoch;
+            if (__ballot(f != p.wait_epoch) == 0) {
                 arrived = true;
                 break;
             }
-            if (__builtin_amdgcn_s_memrealtime() - t_start > SPLIT_WAIT_TICKS) break;
+            // Bounded (p.split_wait_ticks of the 100 MHz clock, half a second
+            // unless a test shortens it): then ST_SPLIT_TIMEOUT, not a hang.
+            if (__builtin_amdgcn_s_memrealtime() - t_start > p.split_wait_ticks) break;
             __builtin_amdgcn_s_sleep(1);
         }
         if (lane == 0) lds_own[R * D + 2 * R] = arrived ? 1.0f : 0.0f;

@@ -123,7 +123,8 @@ struct Params {
     int32_t pad2;
     uint32_t *flags;        // decode split-K completion flags, one per partial slot
     uint32_t epoch;         // decode split-K: this launch's flag value (never 0; flags start at 0)
-    int32_t pad3;
+    uint32_t wait_epoch;    // the flag value the merging split waits for (= epoch)
+    uint64_t split_wait_ticks;  // bound of that wait, s_memrealtime ticks
     FusedDecode fused;      // decode kernel built with FUSED only
     Problem single;         // the problem itself when nproblems == 1 (no descriptor upload)
 };

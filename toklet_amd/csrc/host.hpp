@@ -121,6 +121,8 @@ struct tkh_context {
     int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
     int decode_disable = 0;
     uint32_t epoch = 0;          // last decode split-K epoch handed out
+    uint64_t split_wait_ticks = 50000000;  // bound of a decode merge's wait for its splits
+    bool test_flag_skew = false; // test hook: merges wait for a flag value no split stores
     int prefill_groups = 512;    // below this many row-block workgroups, split the keys
     int prefill_max_splits = 16;
     int prefill_min_keys = 256;  // keys per split at least
