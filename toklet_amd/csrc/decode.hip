@@ -363,12 +363,16 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     // Segments past the first load only when the split lies in one (rings).
     const_ptr<Params> args = (const_ptr<Params>)__builtin_amdgcn_kernarg_segment_ptr();
     const_ptr<Problem> pr = &args->single;
+    // Every kernel-argument field the prologue and the stream need, read
+    // before the first use of any (the pins below then cost one wait): the
+    // problem view, the launch fields and the fused producer's descriptor.  A
+    // field first read after that wait is another round trip to L2.
     DecodeView pv = decode_view(pr);
     int nproblems = args->nproblems;
-    pin_scalar(nproblems);
-    pin_view(pv);
-    // The fused producer's descriptor, in the same batch (a kernel-argument
-    // line first touched later costs another memory round trip).
+    int G = args->group, Hq = args->query_heads, has_window = args->has_window;
+    int64_t window = args->window;
+    float scale_log2 = args->scale_log2, scale = args->scale;
+    float softcap = args->softcap, softcap_inv = args->softcap_inv;
     FusedDecode fz{};
     if constexpr (FUSED) {
         const auto &fa = args->fused;
@@ -384,6 +388,18 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         fz.v_cache = fa.v_cache;
         fz.head_stride = fa.head_stride;
         fz.new_key = fa.new_key;
+    }
+    pin_scalar(nproblems);
+    pin_view(pv);
+    pin_scalar(G);
+    pin_scalar(Hq);
+    pin_scalar(has_window);
+    pin_scalar(window);
+    pin_scalar(scale_log2);
+    pin_scalar(scale);
+    pin_scalar(softcap);
+    pin_scalar(softcap_inv);
+    if constexpr (FUSED) {
         pin_scalar(fz.q_proj);
         pin_scalar(fz.k_proj);
         pin_scalar(fz.v_proj);
@@ -404,8 +420,6 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     const uint32_t local = blockIdx.x - (uint32_t)pv.tile_base;
     const int split = (int)(local % (uint32_t)pv.splits);
     const int kvh = (int)(local / (uint32_t)pv.splits);
-    const int G = p.group;
-    const int Hq = p.query_heads;
     const int nrows = pv.queries * G;
 
     // This split's segment and logical key range [a, b): splits are laid out
@@ -447,7 +461,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         if (r < nrows) {
             const int t = r / G, h = kvh * G + r % G;
             int64_t lo, hi;
-            visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + t, &lo, &hi);
+            visible_range(has_window != 0, window, pv.k_pos0, pv.keys, pv.q_pos0 + t, &lo, &hi);
             lo -= a;
             hi -= a;
             rlo[r] = (int)(lo < 0 ? 0 : (lo > span ? span : lo));
@@ -513,9 +527,6 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         l[r] = 0.0f;
         for (int e = 0; e < EPL; ++e) acc[r][e] = 0.0f;
     }
-    const float scale_log2 = p.scale_log2;
-    const float scale = p.scale;
-    const float softcap = p.softcap, softcap_inv = p.softcap_inv;
 
     const int nblk = (stream_span + KPB - 1) / KPB;
 

@@ -344,16 +344,20 @@ __device__ __forceinline__ float softcap_fast(float x, float cap, float inv_cap)
 }
 
 // Visible key range [lo, hi) (logical indices) of a query at absolute `pos`.
-__device__ __forceinline__ void visible_range(const Params &p, int64_t k_pos0, int64_t keys,
-                                              int64_t pos, int64_t *lo, int64_t *hi) {
+__device__ __forceinline__ void visible_range(bool has_window, int64_t window, int64_t k_pos0,
+                                              int64_t keys, int64_t pos, int64_t *lo, int64_t *hi) {
     int64_t h = pos - k_pos0 + 1;
     *hi = h < keys ? h : keys;
     int64_t l = 0;
-    if (p.has_window) {
-        int64_t first = pos - (p.window - 1) - k_pos0;
+    if (has_window) {
+        int64_t first = pos - (window - 1) - k_pos0;
         l = first > 0 ? first : 0;
     }
     *lo = l;
+}
+__device__ __forceinline__ void visible_range(const Params &p, int64_t k_pos0, int64_t keys,
+                                              int64_t pos, int64_t *lo, int64_t *hi) {
+    visible_range(p.has_window != 0, p.window, k_pos0, keys, pos, lo, hi);
 }
 __device__ __forceinline__ void visible_range(const Params &p, const Problem &pr, int64_t pos,
                                               int64_t *lo, int64_t *hi) {
