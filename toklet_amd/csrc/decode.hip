@@ -156,50 +156,72 @@ template <> __device__ __forceinline__ u32x4 pack_chunk<F32>(const float *x) {
 }
 
 // The producer for one head row, by one whole wave, in produce_qkv's own
-// arithmetic and order (so both give the same bits): lane l takes elements
-// l, l + 64, ... into a per-wave LDS row; per-head RMSNorm with the squares
-// summed in FP64 per lane and then by the same xor butterfly (wave_sum_f64), the reciprocal
-// root in FP64 and value = f32(x * inv * w) in FP64; then the rotary of pair
-// j (elements j and j + D/2) with the row's (cos, sin) from the session's
-// table and FP32 products and sums rounded separately.  The caller packs the
-// row to the cache dtype.  A wave's LDS accesses complete in program order,
-// so the row needs no barrier between the steps.
+// arithmetic and order (so both give the same bits): lane l holds elements
+// l, l + 64, ...; per-head RMSNorm with the squares summed in FP64 per lane
+// and then by the same xor butterfly (wave_sum_f64), the reciprocal root in
+// FP64 and value = f32(x * inv * w) in FP64; then the rotary of pair j
+// (elements j and j + D/2) with the row's (cos, sin) from the session's table
+// and FP32 products and sums rounded separately.  Every load (the row, the
+// weights, the (cos, sin) pairs) is issued before any arithmetic, and the row
+// stays in registers: with D = 128 a lane holds both elements of its pair,
+// with D = 64 the partner comes by a lane swap.  Returns the lane's D/64
+// finished values.
 template <int D>
 __device__ __forceinline__ void wave_produce_row(const float *src, const float *w, float eps,
-                                                 const float *rope, int pairs, float *row, int lane,
-                                                 bool &bad) {
+                                                 const float *rope, int pairs, int lane,
+                                                 float (&y)[D / 64], bool &bad) {
 #pragma clang fp contract(off)
-    for (int i = lane; i < D; i += 64) {
-        const float x = src[i];
-        bad |= !is_finite_f(x);
-        row[i] = x;
+    static_assert(D == 64 || D == 128, "the fused producer covers head sizes 64 and 128");
+    constexpr int K = D / 64, half = D / 2;
+    float x[K], wv[K];
+    f32x2 cs = {1.0f, 0.0f};
+    const int j = lane % half;  // the pair this lane's first element belongs to
+    for (int k = 0; k < K; ++k) {
+        x[k] = src[lane + 64 * k];
+        wv[k] = w ? w[lane + 64 * k] : 1.0f;
     }
+    const bool rotated = rope && j < pairs;
+    if (rotated) cs = *gload_ptr<f32x2>(rope + 2 * j);
+    for (int k = 0; k < K; ++k) bad |= !is_finite_f(x[k]);
     if (w) {
         double ss = 0.0;
-        for (int i = lane; i < D; i += 64) {
-            const double x = (double)row[i];
-            ss += x * x;
-        }
+        for (int k = 0; k < K; ++k) ss += (double)x[k] * (double)x[k];
         ss = wave_sum_f64(ss);
         const double inv = 1.0 / sqrt(ss / (double)D + (double)eps);
-        for (int i = lane; i < D; i += 64) {
-            const float y = (float)((double)row[i] * inv * (double)w[i]);
-            bad |= !is_finite_f(y) || !is_finite_f(w[i]);
-            row[i] = y;
+        for (int k = 0; k < K; ++k) {
+            x[k] = (float)((double)x[k] * inv * (double)wv[k]);
+            bad |= !is_finite_f(x[k]) || !is_finite_f(wv[k]);
         }
     }
     if (rope) {
-        constexpr int half = D / 2;
-        for (int j = lane; j < half && j < pairs; j += 64) {
-            const float a = row[j], b = row[j + half];
-            const float c = rope[2 * j], sn = rope[2 * j + 1];
+        // a = element j, b = element j + half: with D = 128 x[0] and x[1] of this
+        // lane; with D = 64 this lane's x[0] and the one of lane ^ 32.
+        float a, b;
+        if constexpr (K == 2) {
+            a = x[0];
+            b = x[1];
+        } else {
+            float lo, hi;
+            lane_pair<32>(x[0], lo, hi);
+            a = lo;
+            b = hi;
+        }
+        if (rotated) {
+            const float c = cs[0], sn = cs[1];
             const float ac = a * c, bs = b * sn, bc = b * c, as = a * sn;
-            const float x = ac - bs, y = bc + as;
-            bad |= !is_finite_f(x) || !is_finite_f(y);
-            row[j] = x;
-            row[j + half] = y;
+            const float ra = ac - bs, rb = bc + as;
+            bad |= !is_finite_f(ra) || !is_finite_f(rb);
+            a = ra;
+            b = rb;
+        }
+        if constexpr (K == 2) {
+            x[0] = a;
+            x[1] = b;
+        } else {
+            x[0] = lane < half ? a : b;
         }
     }
+    for (int k = 0; k < K; ++k) y[k] = x[k];
 }
 
 // Split-K partials and completion flags: agent-scope accesses, which on
@@ -500,8 +522,11 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
                 const float *src = is_q ? f.q_proj + (int64_t)(kvh * G + job % G) * D
                                         : (is_k ? f.k_proj : f.v_proj) + (int64_t)kvh * D;
                 const float *wn = is_q ? f.q_norm : (is_k ? f.k_norm : nullptr);
-                wave_produce_row<D>(src, wn, f.eps, is_q || is_k ? f.rope : nullptr, f.pairs, row,
-                                    lane, bad);
+                float y[D / 64];
+                wave_produce_row<D>(src, wn, f.eps, is_q || is_k ? f.rope : nullptr, f.pairs, lane, y,
+                                    bad);
+                // Regroup into 16-byte chunks of the cache dtype through LDS.
+                for (int k = 0; k < D / 64; ++k) row[lane + 64 * k] = y[k];
                 if (lane < ROWB / 16) {
                     const u32x4 chunk = pack_chunk<DT>(row + lane * EPC);
                     if (is_q) {
