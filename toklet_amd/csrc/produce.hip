@@ -77,48 +77,71 @@ __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
     void *dst = kind == 0 ? p.q_out : (kind == 1 ? p.k_out : p.v_out);
     const int64_t dst0 = kind == 0 ? (t * p.hq + h) * D : h * p.out_head_stride + t * D;
 
-    bool bad = false;
-    for (int i = lane; i < D; i += 64) {
-        const float x = src[i];
-        bad |= !is_finite_f(x);
-        row[i] = x;
+    // Every load first (the row, the norm weights, the rotary pairs), then the
+    // arithmetic: one memory round trip per launch instead of three.
+    constexpr int KMAX = 8;  // elements per lane, D <= 512
+    const float *w = kind == 0 ? p.q_norm : (kind == 1 ? p.k_norm : nullptr);
+    const int half = D / 2;
+    const int pairs = kind == 2 ? 0 : rotary_pairs(p.rotary, D, p.rotated_dims);
+    float xv[KMAX], wv[KMAX], cv[KMAX / 2], sv[KMAX / 2];
+    for (int k = 0; k < KMAX; ++k) {
+        const int i = lane + 64 * k;
+        xv[k] = i < D ? src[i] : 0.0f;
+        wv[k] = w && i < D ? w[i] : 0.0f;
     }
+    for (int k = 0; k < KMAX / 2; ++k) {
+        const int j = lane + 64 * k;
+        cv[k] = 1.0f;
+        sv[k] = 0.0f;
+        if (j < half && j < pairs) {
+            if (p.rope) {
+                const float *cs = p.rope + 2 * ((p.position + t - p.rope_pos0) * pairs + j);
+                cv[k] = cs[0];
+                sv[k] = cs[1];
+            } else {
+                rotary_cos_sin(p.rotary, p.theta, p.factor, D, p.position + t, j, &cv[k], &sv[k]);
+            }
+        }
+    }
+
+    bool bad = false;
+    for (int k = 0; k < KMAX; ++k)
+        if (lane + 64 * k < D) bad |= !is_finite_f(xv[k]);
     if (kind == 2) {
-        for (int i = lane; i < D; i += 64) store_out<DT>(dst, dst0 + i, row[i]);
+        for (int k = 0; k < KMAX; ++k)
+            if (lane + 64 * k < D) store_out<DT>(dst, dst0 + lane + 64 * k, xv[k]);
         raise_status(p.status, bad, ST_NONFINITE_INPUT);
         return;
     }
-    const float *w = kind == 0 ? p.q_norm : p.k_norm;
     if (w) {
         double ss = 0.0;
-        for (int i = lane; i < D; i += 64) {
-            const double x = (double)row[i];
-            ss += x * x;
-        }
+        for (int k = 0; k < KMAX; ++k)
+            if (lane + 64 * k < D) {
+                const double x = (double)xv[k];
+                ss += x * x;
+            }
         ss = wave_sum_f64(ss);
         const double inv = 1.0 / sqrt(ss / (double)D + (double)p.eps);
-        for (int i = lane; i < D; i += 64) {
-            const float y = (float)((double)row[i] * inv * (double)w[i]);
-            bad |= !is_finite_f(y) || !is_finite_f(w[i]);
-            row[i] = y;
-        }
+        for (int k = 0; k < KMAX; ++k)
+            if (lane + 64 * k < D) {
+                const float y = (float)((double)xv[k] * inv * (double)wv[k]);
+                bad |= !is_finite_f(y) || !is_finite_f(wv[k]);
+                xv[k] = y;
+            }
     }
+    // The rotary pairs elements j and j + D/2, which may sit in other lanes:
+    // through LDS (one wave, whose LDS accesses complete in order).
+    for (int k = 0; k < KMAX; ++k)
+        if (lane + 64 * k < D) row[lane + 64 * k] = xv[k];
     __syncthreads();
-    const int half = D / 2;
-    const int pairs = rotary_pairs(p.rotary, D, p.rotated_dims);
-    for (int j = lane; j < half; j += 64) {
+    for (int k = 0; k < KMAX / 2; ++k) {
+        const int j = lane + 64 * k;
+        if (j >= half) break;
         const float a = row[j], b = row[j + half];
         float x = a, y = b;
         if (j < pairs) {
-            float c, s;
-            if (p.rope) {
-                const float *cs = p.rope + 2 * ((p.position + t - p.rope_pos0) * pairs + j);
-                c = cs[0];
-                s = cs[1];
-            } else {
-                rotary_cos_sin(p.rotary, p.theta, p.factor, D, p.position + t, j, &c, &s);
-            }
-            const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
+            const float c = cv[k], sn = sv[k];
+            const float ac = a * c, bs = b * sn, bc = b * c, as = a * sn;
             x = ac - bs;
             y = bc + as;
             bad |= !is_finite_f(x) || !is_finite_f(y);
