@@ -31,6 +31,7 @@
 //    and a second, fully parallel kernel (attn_prefill_merge) combines them,
 //    so no single workgroup reads a whole row block's partials.
 #include <type_traits>
+#include <utility>
 
 #include "device.hpp"
 
@@ -84,9 +85,20 @@ __device__ __forceinline__ u32x2 read_tr(lds_ptr<uint8_t> p) {
 // LDS address `l` + 16 i.  Issued as inline assembly so that the compiler,
 // which cannot prove these LDS writes apart from the tile being read, does not
 // put a full vmcnt(0) wait before every LDS read; ring_sync() orders them.
-__device__ __forceinline__ void dma16(const void *g, lds_ptr<uint8_t> l) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)l);  // wave-uniform
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+// The address is a scalar base plus this lane's 32-bit offset; `m` is the
+// wave-uniform LDS destination.
+__device__ __forceinline__ void dma16(const void *base, uint32_t off, uint32_t m) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m)
+                 : "memory", "m0");
+}
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F> __device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 __device__ __forceinline__ int64_t uniform64(int64_t x) {
@@ -293,6 +305,12 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
                               ((int64_t)t_row * pr->q_row_stride + (int64_t)h_row * D) * 2;
         for (int ks = 0; ks < KS; ++ks)
             qb[ks] = *gload_ptr<u32x4>(qrow + 32 * ks + 16 * h);
+        // Complete the Q loads before the first direct K/V load.  The compiler
+        // counts only the loads it sees (not the direct loads issued as inline
+        // assembly); with Q still pending on its books it would place
+        // vmcnt(7..3) waits before the QK MFMAs of every tile, which in
+        // hardware also wait for the K/V tiles just issued.
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
     }
 
     f32x16 acc[MB];
@@ -321,14 +339,23 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         off_last[i] = (rr < nlast ? rr : nlast - 1) * prow + cc;
     }
     int t_next = 0;
-    auto issue = [&](int st) {
-        const bool last = t_next == ntiles - 1;
-        lds_ptr<uint8_t> kt = lds + st * L::stage;
-        for (int i = 0; i < RPW; ++i) {
-            const int run = wave * RPW + i;
-            const uint32_t off = (uint32_t)(last ? off_last[i] : off_full[i]);
-            dma16(k_next + off, kt + run * 1024);
-            dma16(v_next + off, kt + L::tile + run * 1024);
+    // This wave's first 1 KiB run inside a tile, as a scalar.
+    const uint32_t run0 = (uint32_t)uniform32(wave) * (RPW * 1024);
+    // Issue the next tile into stage STG (a compile-time stage: the LDS
+    // destinations are scalar constants plus run0).
+    auto issue = [&](auto stg_tag) {
+        constexpr int STG = decltype(stg_tag)::value;
+        const uint32_t m = (uint32_t)(uintptr_t)(lds + STG * L::stage) + run0;
+        if (t_next == ntiles - 1) {
+            for (int i = 0; i < RPW; ++i) {
+                dma16(k_next, (uint32_t)off_last[i], m + i * 1024);
+                dma16(v_next, (uint32_t)off_last[i], m + L::tile + i * 1024);
+            }
+        } else {
+            for (int i = 0; i < RPW; ++i) {
+                dma16(k_next, (uint32_t)off_full[i], m + i * 1024);
+                dma16(v_next, (uint32_t)off_full[i], m + L::tile + i * 1024);
+            }
         }
         k_next += PF_KT * prow;
         v_next += PF_KT * prow;
@@ -368,7 +395,9 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     // last tile step 3 scores stale LDS data (of a stage that holds an earlier
     // tile) that is never used.
     constexpr int NPV = 2 * MB;  // P.V MFMAs per tile
-    for (int t = 0; t < NS - 1 && t < ntiles; ++t) issue(t);
+    static_for<NS - 1>([&](auto stg) {
+        if (decltype(stg)::value < ntiles) issue(stg);
+    });
     f32x16 st;
     for (int i = 0; i < 16; ++i) st[i] = 0.0f;
     VConvert<D> vconv;
@@ -390,11 +419,16 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     for (int i = 0; i < 8; ++i) {
         ph[i] = 0u;
     }
-    int stage = 0;
-    for (int t = 0; t < ntiles; ++t) {
-        const int stage_next = stage + 1 == NS ? 0 : stage + 1;
-        lds_ptr<uint8_t> vt = lds + stage * L::stage + L::tile;
-        lds_ptr<uint8_t> kn = lds + stage_next * L::stage;
+    // Tile t sits in stage t % NS.  The loop is unrolled by NS, so every
+    // stage, and with it every LDS offset, is a compile-time constant, and the
+    // two score registers swap roles (a copy per round only for an odd NS).
+    int t = 0;
+    f32x16 st_b;
+    auto body = [&](auto stg_tag, f32x16 &st, f32x16 &st_next) {
+        constexpr int STG = decltype(stg_tag)::value;
+        constexpr int STG_NEXT = (STG + 1) % NS;
+        lds_ptr<uint8_t> vt = lds + STG * L::stage + L::tile;
+        lds_ptr<uint8_t> kn = lds + STG_NEXT * L::stage;
 
         // ---- step 1.  t = raw dot (or, with the softcap, the capped score in
         // log2 units); p = 2^(t * tmul - m * tmul).  Both transforms are
@@ -484,13 +518,12 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         // whose stage takes the next load.
         if (t + 1 < ntiles) {
             wait_tile(t + 1);
-            if (t_next < ntiles) issue(stage == 0 ? NS - 1 : stage - 1);
+            if (t_next < ntiles) issue(std::integral_constant<int, (STG + NS - 1) % NS>{});
         }
 
         // ---- step 3: scores of tile t + 1 (K operands read KPRE steps ahead),
         // second half of tile t's probabilities.
         constexpr int KPRE = CAP ? 2 : 3;
-        f32x16 st_next;
         for (int i = 0; i < 16; ++i) st_next[i] = 0.0f;
         u32x4 kq[KPRE];
         for (int i = 0; i < KPRE && i < KS; ++i) kq[i] = *(lds_ptr<u32x4>)(kn + k_off[i]);
@@ -528,8 +561,20 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
                 const u32x2 r2 = read_tr(vt + v_off[stp][1][mb]);
                 vop[stp][mb] = u32x4{r1[0], r1[1], r2[0], r2[1]};
             }
-        st = st_next;
-        stage = stage_next;
+    };
+    for (bool go = true; go;) {
+        static_for<NS>([&](auto k) {
+            constexpr int K = decltype(k)::value;
+            if (!go || t >= ntiles) {
+                go = false;
+                return;
+            }
+            if constexpr (K % 2 == 0) body(std::integral_constant<int, K>{}, st, st_b);
+            else body(std::integral_constant<int, K>{}, st_b, st);
+            ++t;
+        });
+        // An odd ring leaves the next scores in st_b.
+        if constexpr (NS % 2 == 1) st = st_b;
     }
     // P.V of the last tile.
     if (ntiles > 0) {
