@@ -18,7 +18,8 @@
 //    ds_read_b64_tr_b16 (each 16-lane group reads 4 keys x 16 features and
 //    receives them transposed); P^T is already in B-operand layout.  P is
 //    rounded once to f16 for both dtypes (a single bf16 rounding of P can
-//    move the output by more than 2e-3).  For bf16 the V tile is converted
+//    move the output by more than 2e-3), and the row mass is summed from the
+//    same rounded values (one v_dot2 with (1, 1) per pair).  For bf16 the V tile is converted
 //    in LDS, once per workgroup, to f16 scaled by 2^-8 (exact for every bf16
 //    value from 2^-6 up; smaller ones lose at most 2^-17 absolute, and the
 //    f16 range then covers |v| < 2^24), and the context is scaled back by 2^8.
@@ -74,6 +75,13 @@ template <> __device__ __forceinline__ float lo_f<F16>(uint32_t w) {
 }
 template <> __device__ __forceinline__ float hi_f<F16>(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// l + a + b for the f16 pair (a, b) packed in `w`, in one instruction.  The
+// row mass is summed from the same rounded probabilities that weight V.
+__device__ __forceinline__ float add_pair(uint32_t w, float l) {
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), ones, l, false);
 }
 
 __device__ __forceinline__ u32x2 read_tr(lds_ptr<uint8_t> p) {
@@ -499,7 +507,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
                     const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
                     const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
                     nh[i] = pack2<PDT>(e0, e1);
-                    l_run += e0 + e1;
+                    l_run = add_pair(nh[i], l_run);
                     // Pin the pair here: the compiler would otherwise sink it to
                     // its use after step 1, out of the MFMA shadow.
                     asm volatile("" : "+v"(nh[i]), "+v"(l_run));
@@ -545,7 +553,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
                 const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
                 const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
                 ph[i] = pack2<PDT>(e0, e1);
-                l_run += e0 + e1;
+                l_run = add_pair(ph[i], l_run);
                 asm volatile("" : "+v"(ph[i]), "+v"(l_run));
             }
             __builtin_amdgcn_sched_barrier(0);
