@@ -5,6 +5,8 @@ frozen fixtures); bf16/f16 storage within 2e-3 max abs of the oracle run on the
 same stored (rounded) Q/K/V, with identical greedy tokens.
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -376,8 +378,45 @@ def test_decode_batch_varlen_f16(torch_mod, ctx, ops, orc):
         assert max_err(got[b], refs[b]) <= TOL_HALF
 
 
-def test_prefill_batch_bf16(torch_mod, ctx, ops, orc):
+def _context_with_env(ops, env):
+    """A context created under extra TKH_* settings (read once at creation)."""
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return ops.Context(0)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("waves", ["4", "8"])
+def test_prefill_workgroup_widths_chunked(torch_mod, ops, orc, waves):
+    """The prefill kernel with four- and eight-wave workgroups forced (the planner takes
+    eight only for launches whose 256-row blocks fill the device), on chunked prefill
+    with key splits and merges, then decode."""
+    log(f"qwen3 16/8/128 bf16 chunked prefill, {waves}-wave prefill workgroups")
+    c = _context_with_env(ops, {"TKH_PREFILL_WAVES": waves})
+    try:
+        worst, ctxs = _chunked_session(torch_mod, c, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
+                                       chunks=[256, 256, 128, 1, 1], capacity=700, seed=4)
+        rng = np.random.default_rng(98)
+        w = rng.standard_normal((4096, 16 * 128)).astype(np.float32)
+        for got, ref in ctxs:
+            assert_tokens_agree(got, ref, w)
+        log(f"  worst max abs error {worst:.3e}")
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("waves", ["0", "4", "8"])
+def test_prefill_batch_bf16(torch_mod, ops, orc, waves):
+    """Batched prefill over three sessions, with the planner's workgroup width and with
+    four and eight waves forced."""
     torch = torch_mod
+    ctx = _context_with_env(ops, {"TKH_PREFILL_WAVES": waves})
     rng = np.random.default_rng(7)
     hq, hkv, D, B, T = 32, 8, 128, 3, 128
     pos = rng.integers(50, 400, size=B)
@@ -403,6 +442,7 @@ def test_prefill_batch_bf16(torch_mod, ctx, ops, orc):
                       caps * D, pos, out, tokens=T, query_heads=hq, kv_heads=hkv, head_dim=D,
                       scale=float(1.0 / np.sqrt(np.float32(D))))
     got = host(out).reshape(B, -1)
+    ctx.close()
     for b in range(B):
         err = max_err(got[b], refs[b])
         assert err <= TOL_HALF, err

@@ -42,13 +42,13 @@ extern "C" hipError_t tkh_launch_softcap(float *x, int64_t n, float cap, uint32_
 extern "C" hipError_t tkh_launch_fill_u32(uint32_t *p, uint32_t v, hipStream_t stream);
 extern "C" hipError_t tkh_launch_zero_u64(uint64_t *p, int64_t words, hipStream_t stream);
 extern "C" int tkh_decode_max_rows(int dtype, int head_dim);
-extern "C" int tkh_prefill_rows_per_group(void);
+extern "C" int tkh_prefill_waves(int head_dim, int wide);
 extern "C" int tkh_prefill_max_splits(void);
 extern "C" int tkh_prefill_merge_rows_per_block(int head_dim);
-extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int64_t blocks,
-                                               hipStream_t stream, hipEvent_t start,
-                                               hipEvent_t stop);
-extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim,
+extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int rows,
+                                               int64_t blocks, hipStream_t stream,
+                                               hipEvent_t start, hipEvent_t stop);
+extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim, int waves,
                                          int64_t groups, hipStream_t stream, hipEvent_t start,
                                          hipEvent_t stop);
 extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int want);
@@ -337,7 +337,18 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
 uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
                         tkh_error *err) {
     const int64_t D = plan.head_dim, Hkv = plan.kv_heads, G = plan.query_heads / plan.kv_heads;
-    const int64_t rows_per = tkh_prefill_rows_per_group();
+    // Eight-wave (256-row) workgroups where the head_dim has them and their row
+    // blocks alone fill the device (the target is set in 128-row workgroups);
+    // four-wave ones otherwise.
+    int waves = tkh_prefill_waves((int)D, 0);
+    {
+        const int wide = tkh_prefill_waves((int)D, 1);
+        int64_t wide_groups = 0;
+        for (auto &p : group) wide_groups += Hkv * (((int64_t)p.queries * G + 32 * wide - 1) / (32 * wide));
+        if (wide != waves && wide_groups >= ctx->prefill_groups * 128 / (32 * wide)) waves = wide;
+        if (ctx->prefill_waves == 4 || ctx->prefill_waves == wide) waves = ctx->prefill_waves;
+    }
+    const int64_t rows_per = 32 * waves;
     int64_t base_groups = 0;
     int64_t max_span = 0;
     for (auto &p : group) {
@@ -346,10 +357,12 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
         base_groups += Hkv * p.row_blocks;
         max_span = std::max<int64_t>(max_span, p.vis_hi - p.vis_lo);
     }
-    // Too few row-block workgroups to fill the device: split the keys.
+    // Too few row-block workgroups to fill the device: split the keys.  The
+    // target is set in 128-row workgroups and scaled to this head_dim's size.
+    const int64_t target = std::max<int64_t>(1, ctx->prefill_groups * 128 / rows_per);
     int64_t splits = 1;
-    if (base_groups < ctx->prefill_groups) {
-        splits = (ctx->prefill_groups + base_groups - 1) / base_groups;
+    if (base_groups < target) {
+        splits = (target + base_groups - 1) / base_groups;
         splits = std::min<int64_t>(splits, ctx->prefill_max_splits);
         splits = std::min<int64_t>(splits, std::max<int64_t>(1, max_span / ctx->prefill_min_keys));
     }
@@ -420,12 +433,12 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
 
     hipEvent_t *ev = nullptr;
     if (ctx->profiling) TRY(profile_slot(ctx, &ev, merge_blocks > 0, err));
-    hipError_t e = tkh_launch_prefill(&prm, (int)plan.dtype, (int)D, wgs, ctx->stream,
+    hipError_t e = tkh_launch_prefill(&prm, (int)plan.dtype, (int)D, waves, wgs, ctx->stream,
                                       ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "prefill launch", err);
     if (merge_blocks > 0) {
-        e = tkh_launch_prefill_merge(&prm, (int)D, merge_blocks, ctx->stream, ev ? ev[2] : nullptr,
-                                     ev ? ev[3] : nullptr);
+        e = tkh_launch_prefill_merge(&prm, (int)D, (int)rows_per, merge_blocks, ctx->stream,
+                                     ev ? ev[2] : nullptr, ev ? ev[3] : nullptr);
         if (e != hipSuccess) return device_error(e, "prefill merge launch", err);
     }
     return TKH_OK;
@@ -577,6 +590,7 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     ctx->prefill_max_splits =
         std::min(tkh_prefill_max_splits(), std::max(1, env_int("TKH_PREFILL_MAX_SPLITS", 16)));
     ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 256));
+    ctx->prefill_waves = env_int("TKH_PREFILL_WAVES", 0);
     auto cleanup = [&](hipError_t e, const char *where) {
         tkh_context_destroy(ctx);
         return device_error(e, where, err);

@@ -4,11 +4,12 @@
 // (tokens x query heads of the GQA group, "packed rows") exceed what the
 // streaming decode kernel holds.  It is MFMA-bound:
 //
-//  * One workgroup = four waves = 128 packed rows of one (problem, KV head),
-//    optionally one key split of it.  Each wave owns 32 rows.
+//  * One workgroup = W waves of 32 packed rows each (W = 8 at head_dim 128
+//    when the row blocks fill the device, 4 otherwise) of one (problem, KV
+//    head), optionally one key split of it.
 //  * K and V tiles of 32 keys are copied once per workgroup into an LDS ring
 //    by direct global->LDS loads, two tiles ahead of the two in use, and read
-//    by all four waves.  The scores of tile t + 1 are formed while the
+//    by all waves.  The scores of tile t + 1 are formed while the
 //    softmax and P.V of tile t run (software pipeline).
 //  * Scores are formed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16: lane
 //    l holds query row l % 32 and sixteen keys of the tile, so the row's
@@ -124,8 +125,14 @@ __device__ __forceinline__ float coherent_load(const float *p) {
 
 }  // namespace
 
-constexpr int PF_WAVES = 4;
-constexpr int PF_ROWS = 32 * PF_WAVES;  // packed rows per workgroup
+// Waves per workgroup (32 packed rows each).  Four, or eight at head_dim 128,
+// where the registers still allow two waves per SIMD, so the V conversion and
+// the tile loads, which the workgroup shares, cost each wave half as much (a
+// head_dim 64 tile is only four 1 KiB load runs, and at head_dim 256 one wave
+// fills a SIMD's registers).  The host takes eight only for launches whose
+// row blocks fill the device: smaller ones want more, smaller workgroups.
+constexpr int PF_WAVES_NARROW = 4;
+__host__ __device__ constexpr int pf_wide_waves(int D) { return D == 128 ? 8 : PF_WAVES_NARROW; }
 constexpr int PF_KT = 32;               // keys per tile
 
 // LDS ring of K/V tiles.  Rows are unpadded (2D bytes) with the 16-byte
@@ -133,7 +140,7 @@ constexpr int PF_KT = 32;               // keys per tile
 // over the banks; direct global->LDS loads fill whole 1 KiB runs per wave
 // instruction.  Three tiles are in flight ahead of the one being consumed
 // (two for head_dim 256, where a stage is 32 KiB).
-template <int D> struct PrefillLds {
+template <int D, int W> struct PrefillLds {
     static constexpr int row = D * 2;                      // bytes per staged row
     static constexpr int chunks = row / 16;                // 16-byte chunks per row
     // Chunk swizzle of row r: XOR with (2r + r/4) mod 8.  Eight consecutive
@@ -145,8 +152,8 @@ template <int D> struct PrefillLds {
     static constexpr int stages = D >= 256 ? 3 : 4;
     static constexpr int bytes = stages * stage;
     static constexpr int runs = tile / 1024;               // 1 KiB runs per tile
-    static constexpr int runs_per_wave = runs / PF_WAVES;
-    static_assert(runs % PF_WAVES == 0, "tile runs must split evenly over the waves");
+    static constexpr int runs_per_wave = runs / W;
+    static_assert(runs % W == 0, "tile runs must split evenly over the waves");
     // Byte offset of chunk `c` of row `r` inside a tile.
     __device__ static constexpr int at(int r, int c) { return r * row + ((c ^ swz(r)) << 4); }
 };
@@ -155,11 +162,12 @@ template <int D> struct PrefillLds {
 // place, by the whole workgroup: thread `tid` converts the 16-byte chunks
 // tid, tid + 256, ... (consecutive lanes, consecutive chunks).  Split in a
 // read half and a convert-and-write half so a caller can put MFMAs between.
-template <int D> struct VConvert {
-    static constexpr int chunks = PF_KT * D * 2 / 16 / (64 * PF_WAVES);  // per thread
+template <int D, int W> struct VConvert {
+    static constexpr int threads = 64 * W;
+    static constexpr int chunks = PF_KT * D * 2 / 16 / threads;  // per thread
     u32x4 w[chunks];
     __device__ void read(lds_ptr<uint8_t> vt, int tid) {
-        for (int c = 0; c < chunks; ++c) w[c] = ((lds_ptr<u32x4>)vt)[c * 64 * PF_WAVES + tid];
+        for (int c = 0; c < chunks; ++c) w[c] = ((lds_ptr<u32x4>)vt)[c * threads + tid];
     }
     __device__ void write(lds_ptr<uint8_t> vt, int tid) {
         for (int c = 0; c < chunks; ++c) {
@@ -169,7 +177,7 @@ template <int D> struct VConvert {
                                  __builtin_bit_cast(float, w[c][j] & 0xffff0000u) * 0x1p-8f};
                 o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
             }
-            ((lds_ptr<u32x4>)vt)[c * 64 * PF_WAVES + tid] = o;
+            ((lds_ptr<u32x4>)vt)[c * threads + tid] = o;
         }
     }
 };
@@ -202,14 +210,15 @@ constexpr float RESCALE_SLACK = 8.0f;
 
 __device__ __forceinline__ int uniform32(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
-template <int DT, int D, bool CAP>
-__global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(Params p) {
+template <int DT, int D, bool CAP, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(Params p) {
+    constexpr int ROWS = 32 * W;  // packed rows per workgroup
     constexpr int KS = D / 16;        // QK k-steps (16 features each)
     constexpr int MB = D / 32;        // PV M-blocks (32 features each)
     constexpr int PDT = F16;          // P and V^T operand type of the P.V MFMAs
     constexpr bool VCONV = DT == BF16;  // V tiles converted to scaled f16 in LDS
     static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
-    using L = PrefillLds<D>;
+    using L = PrefillLds<D, W>;
     constexpr int NS = L::stages;
     constexpr int RPW = L::runs_per_wave;
     constexpr int LPT = 2 * RPW;      // direct loads per wave per tile (K + V)
@@ -262,7 +271,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     const int64_t s_hi = s_lo + pr->split_keys < seg_hi ? s_lo + pr->split_keys : seg_hi;
 
     // This lane's query row.
-    const int row = rb * PF_ROWS + wave * 32 + j;
+    const int row = rb * ROWS + wave * 32 + j;
     const bool rvalid = row < m_kv;
     const int rrow = rvalid ? row : m_kv - 1;
     const int t_row = rrow / G, h_row = kvh * G + rrow % G;
@@ -271,8 +280,8 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     if (!rvalid) r_hi = r_lo;  // no visible keys: never contributes, never stored
 
     // Key range of the workgroup: the union over its rows, clipped to the split.
-    const int wg_row_first = rb * PF_ROWS;
-    const int wg_row_last = min(wg_row_first + PF_ROWS, m_kv) - 1;
+    const int wg_row_first = rb * ROWS;
+    const int wg_row_last = min(wg_row_first + ROWS, m_kv) - 1;
     int64_t k_lo, k_hi, tmp;
     visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + wg_row_first / G, &k_lo, &tmp);
     visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + wg_row_last / G, &tmp, &k_hi);
@@ -408,7 +417,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     });
     f32x16 st;
     for (int i = 0; i < 16; ++i) st[i] = 0.0f;
-    VConvert<D> vconv;
+    VConvert<D, W> vconv;
     if (ntiles > 0) {
         wait_tile(0);
         for (int ks = 0; ks < KS; ++ks) st = mfma32<DT>(*(lds_ptr<u32x4>)(lds + k_off[ks]), qb[ks], st);
@@ -629,12 +638,12 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         return;
     }
 
-    // ---- split-K partial: slot (row block, split) holds PF_ROWS x (D + 2)
+    // ---- split-K partial: slot (row block, split) holds ROWS x (D + 2)
     // floats, merged by attn_prefill_merge after this kernel.
     raise_status(p, bad, ST_NONFINITE_INPUT);
     const int64_t group = (int64_t)kvh * pr->row_blocks + rb;
     const int64_t slot = pr->slot_base + group * pr->splits + split;
-    float *po = p.part_o + (slot * PF_ROWS + wave * 32 + j) * D;
+    float *po = p.part_o + (slot * ROWS + wave * 32 + j) * D;
     for (int mb = 0; mb < MB; ++mb)
         for (int q = 0; q < 4; ++q) {
             const f32x4 v = {acc[mb][4 * q] * oscale, acc[mb][4 * q + 1] * oscale,
@@ -643,7 +652,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         }
     if (h == 0) {
         const f32x2 ml = {m_run, l_run};
-        *gstore_ptr<f32x2>(p.part_ml + (slot * PF_ROWS + wave * 32 + j) * 2) = ml;
+        *gstore_ptr<f32x2>(p.part_ml + (slot * ROWS + wave * 32 + j) * 2) = ml;
     }
 }
 
@@ -652,7 +661,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(2
 // owns four features of one row and reads the S partials of its row at once
 // (one round trip): m and l of every split, then the weighted sum of the
 // unnormalised contexts.  Problem::part_base is the problem's first merge block.
-template <int D>
+template <int D, int ROWS>
 __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t blocks) {
     constexpr int TPR = D / 4;                  // threads per row
     constexpr int RPB = 256 / TPR;              // rows per merge block
@@ -674,12 +683,12 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t bloc
     const int G = p.group, Hq = p.query_heads;
     const int m_kv = pr->queries * G;
     const int64_t local = b - pr->part_base;
-    const int blocks_per_rb = PF_ROWS / RPB;
+    const int blocks_per_rb = ROWS / RPB;
     const int64_t group = local / blocks_per_rb;          // kvh * row_blocks + rb
     const int kvh = (int)(group / pr->row_blocks), rb = (int)(group % pr->row_blocks);
     const int r = (int)(local % blocks_per_rb) * RPB + (int)(threadIdx.x / TPR);
     const int f = (int)(threadIdx.x % TPR) * 4;
-    const int prow = rb * PF_ROWS + r;
+    const int prow = rb * ROWS + r;
     if (prow >= m_kv) return;
     const int S = pr->splits;
     const int64_t slot0 = pr->slot_base + group * S;
@@ -689,7 +698,7 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t bloc
 #pragma unroll
     for (int sp = 0; sp < MAXS; ++sp) {
         if (sp < S) {
-            const int64_t srow = (slot0 + sp) * PF_ROWS + r;
+            const int64_t srow = (slot0 + sp) * ROWS + r;
             ml[sp] = *gload_ptr<f32x2>(p.part_ml + srow * 2);
             po[sp] = *gload_ptr<f32x4>(p.part_o + srow * D + f);
         }
@@ -726,40 +735,43 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t bloc
 
 }  // namespace tkh
 
-extern "C" int tkh_prefill_rows_per_group(void) { return tkh::PF_ROWS; }
+extern "C" int tkh_prefill_waves(int head_dim, int wide) {
+    return wide ? tkh::pf_wide_waves(head_dim) : tkh::PF_WAVES_NARROW;
+}
 extern "C" int tkh_prefill_max_splits(void) { return 16; }
 extern "C" int tkh_prefill_merge_rows_per_block(int head_dim) { return 256 / (head_dim / 4); }
 
-extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int64_t blocks,
-                                               hipStream_t stream, hipEvent_t start,
-                                               hipEvent_t stop) {
+extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int rows,
+                                               int64_t blocks, hipStream_t stream,
+                                               hipEvent_t start, hipEvent_t stop) {
     using namespace tkh;
     dim3 grid((unsigned)blocks), block(256);
-    if (head_dim == 64)
-        hipExtLaunchKernelGGL((attn_prefill_merge<64>), grid, block, 0, stream, start, stop, 0, *p, blocks);
-    else if (head_dim == 128)
-        hipExtLaunchKernelGGL((attn_prefill_merge<128>), grid, block, 0, stream, start, stop, 0, *p, blocks);
-    else if (head_dim == 256)
-        hipExtLaunchKernelGGL((attn_prefill_merge<256>), grid, block, 0, stream, start, stop, 0, *p, blocks);
-    else return hipErrorInvalidValue;
-    return hipGetLastError();
+#define TKH_PM(DD, RR)                                                                           \
+    if (head_dim == DD && rows == RR) {                                                          \
+        hipExtLaunchKernelGGL((attn_prefill_merge<DD, RR>), grid, block, 0, stream, start, stop, 0, \
+                              *p, blocks);                                                       \
+        return hipGetLastError();                                                                \
+    }
+    TKH_PM(64, 128) TKH_PM(128, 128) TKH_PM(128, 256) TKH_PM(256, 128)
+#undef TKH_PM
+    return hipErrorInvalidValue;
 }
 
-extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim,
+extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim, int waves,
                                          int64_t groups, hipStream_t stream, hipEvent_t start,
                                          hipEvent_t stop) {
     using namespace tkh;
-    dim3 grid((unsigned)groups), block(64 * PF_WAVES);
-#define TKH_PF(DT, DD)                                                                  \
-    if (dtype == DT && head_dim == DD) {                                                \
+    dim3 grid((unsigned)groups), block(64 * waves);
+#define TKH_PF(DT, DD, WW)                                                              \
+    if (dtype == DT && head_dim == DD && waves == WW) {                                 \
         if (p->softcap != 0.0f)                                                         \
-            hipExtLaunchKernelGGL((attn_prefill<DT, DD, true>), grid, block, 0, stream, start, stop, 0, *p);  \
+            hipExtLaunchKernelGGL((attn_prefill<DT, DD, true, WW>), grid, block, 0, stream, start, stop, 0, *p);  \
         else                                                                            \
-            hipExtLaunchKernelGGL((attn_prefill<DT, DD, false>), grid, block, 0, stream, start, stop, 0, *p); \
+            hipExtLaunchKernelGGL((attn_prefill<DT, DD, false, WW>), grid, block, 0, stream, start, stop, 0, *p); \
         return hipGetLastError();                                                       \
     }
-    TKH_PF(BF16, 64) TKH_PF(BF16, 128) TKH_PF(BF16, 256)
-    TKH_PF(F16, 64) TKH_PF(F16, 128) TKH_PF(F16, 256)
+    TKH_PF(BF16, 64, 4) TKH_PF(BF16, 128, 4) TKH_PF(BF16, 128, 8) TKH_PF(BF16, 256, 4)
+    TKH_PF(F16, 64, 4) TKH_PF(F16, 128, 4) TKH_PF(F16, 128, 8) TKH_PF(F16, 256, 4)
 #undef TKH_PF
     return hipErrorInvalidValue;
 }
