@@ -138,8 +138,11 @@ constexpr int PF_KT = 32;               // keys per tile
 // LDS ring of K/V tiles.  Rows are unpadded (2D bytes) with the 16-byte
 // chunks XOR-swizzled by row, so the K-operand and transposed V reads spread
 // over the banks; direct global->LDS loads fill whole 1 KiB runs per wave
-// instruction.  Three tiles are in flight ahead of the one being consumed
-// (two for head_dim 256, where a stage is 32 KiB).
+// instruction.  The ring has NS stages: the tile being consumed, the next
+// one, and NS - 2 in flight; four (three for head_dim 256, where a stage is
+// 32 KiB).  Deeper rings measured slower on the 32-session 4096-key batch
+// (five stages 2%, six 3%, eight 6% with eight-wave workgroups): more tiles
+// in flight per CU only add L2 pressure.
 template <int D, int W> struct PrefillLds {
     static constexpr int row = D * 2;                      // bytes per staged row
     static constexpr int chunks = row / 16;                // 16-byte chunks per row
@@ -186,16 +189,17 @@ template <int D, int W> struct VConvert {
 // flight, then synchronise the workgroup.  Direct global->LDS loads count in
 // vmcnt; the compiler neither tracks nor orders them, hence the explicit wait
 // and the compiler fences around the barrier.
-template <int LPT> __device__ __forceinline__ void ring_sync(int ahead) {
-    static_assert(LPT * 2 < 64, "vmcnt field");
-    auto wait = [](auto n_tag) {
-        constexpr int n = decltype(n_tag)::value;
+template <int LPT, int MAXA> __device__ __forceinline__ void ring_sync(int ahead) {
+    static_assert(LPT * MAXA < 64, "vmcnt field");
+    // One exact wait per possible `ahead` (a wave-uniform value): the waits
+    // take immediates.
+    static_for<MAXA + 1>([&](auto a_tag) {
+        constexpr int a = decltype(a_tag)::value;
+        constexpr int n = a * LPT;
         // gfx9 s_waitcnt: vmcnt in [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
-        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-    };
-    if (ahead >= 2) wait(std::integral_constant<int, 2 * LPT>{});
-    else if (ahead == 1) wait(std::integral_constant<int, LPT>{});
-    else wait(std::integral_constant<int, 0>{});
+        if (ahead == a || (a == MAXA && ahead > MAXA))
+            __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+    });
     __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
@@ -381,7 +385,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // Wait for tile `t` (issued earlier) and synchronise the workgroup.
     auto wait_tile = [&](int t) {
         const int ahead = t_next - 1 - t;  // later tiles still allowed in flight
-        ring_sync<LPT>(ahead);
+        ring_sync<LPT, NS - 2>(ahead);
     };
 
     // LDS offsets of this lane's operand reads (tile-relative).
