@@ -15,13 +15,15 @@
 //    l holds query row l % 32 and sixteen keys of the tile, so the row's
 //    softmax state lives in one lane pair (one cross-lane step per tile).
 //    Q stays in registers as the B operand for the whole key range.
-//  * O^T = V^T P^T on the same MFMA.  The V^T operand comes from LDS with
-//    ds_read_b64_tr_b16 (each 16-lane group reads 4 keys x 16 features and
-//    receives them transposed); P^T is already in B-operand layout.  P is
+//  * O^T = V^T P^T on the same MFMA.  Each V tile is transposed once per
+//    workgroup (ds_read_b64_tr_b16: a 16-lane group reads 4 keys x 16
+//    features and receives them transposed) into a V^T buffer laid out in
+//    the A operand's key order, which every wave then reads with 16-byte
+//    loads; P^T is already in B-operand layout.  P is
 //    rounded once to f16 for both dtypes (a single bf16 rounding of P can
 //    move the output by more than 2e-3), and the row mass is summed from the
-//    same rounded values (one v_dot2 with (1, 1) per pair).  For bf16 the V tile is converted
-//    in LDS, once per workgroup, to f16 scaled by 2^-8 (exact for every bf16
+//    same rounded values (one v_dot2 with (1, 1) per pair).  For bf16 the
+//    transposing pass also converts V to f16 scaled by 2^-8 (exact for every bf16
 //    value from 2^-6 up; smaller ones lose at most 2^-17 absolute, and the
 //    f16 range then covers |v| < 2^24), and the context is scaled back by 2^8.
 //  * The online-softmax rescale of O is skipped for a tile unless some
@@ -153,7 +155,18 @@ template <int D, int W> struct PrefillLds {
     static constexpr int tile = PF_KT * row;               // one K or V tile
     static constexpr int stage = 2 * tile;                 // K + V
     static constexpr int stages = D >= 256 ? 3 : 4;
-    static constexpr int bytes = stages * stage;
+    // Transposed f16 V tiles, the A operand of the P.V MFMAs, in vt_bufs
+    // buffers after the ring (tile t in buffer t % vt_bufs).  Row f (a feature)
+    // holds the tile's 32 keys as four 16-byte chunks: chunk c = 2 stp + h holds
+    // keys 16 stp + 4 h + 0..3 and 16 stp + 8 + 4 h + 0..3, the key order of the
+    // MFMA's k slots, and sits at chunk c ^ ((f / 4) % 4), so 16 consecutive rows
+    // at one chunk (a 16-lane access) hit 16 distinct bank groups.
+    static constexpr int vt_row = PF_KT * 2;
+    static constexpr int vt_bytes = D * vt_row;
+    static constexpr int vt_bufs = stages % 2 == 0 ? 2 : stages;
+    static constexpr int vt_base = stages * stage;
+    static constexpr int bytes = vt_base + vt_bufs * vt_bytes;
+    __device__ static constexpr int vt_at(int f, int c) { return f * vt_row + ((c ^ ((f >> 2) & 3)) << 4); }
     static constexpr int runs = tile / 1024;               // 1 KiB runs per tile
     static constexpr int runs_per_wave = runs / W;
     static_assert(runs % W == 0, "tile runs must split evenly over the waves");
@@ -161,26 +174,49 @@ template <int D, int W> struct PrefillLds {
     __device__ static constexpr int at(int r, int c) { return r * row + ((c ^ swz(r)) << 4); }
 };
 
-// bf16 V tile (PF_KT keys x D, staged in LDS) to f16 scaled by 2^-8, in
-// place, by the whole workgroup: thread `tid` converts the 16-byte chunks
-// tid, tid + 256, ... (consecutive lanes, consecutive chunks).  Split in a
-// read half and a convert-and-write half so a caller can put MFMAs between.
-template <int D, int W> struct VConvert {
+// One V tile (PF_KT keys x D as staged by the direct loads) to its transposed
+// f16 form (PrefillLds::vt_at), by the whole workgroup: each thread builds
+// `per` 16-byte chunks.  A 16-lane group reads four keys x 16 features with
+// ds_read_b64_tr_b16 (lane j receives the four keys of feature fb + j), twice
+// for the chunk's two key quads; for bf16 each value is then converted to f16
+// scaled by 2^-8.  Split in a read half and a write half so a caller can put
+// MFMAs between.
+template <int D, int W, bool CONV> struct VTranspose {
+    using L = PrefillLds<D, W>;
     static constexpr int threads = 64 * W;
-    static constexpr int chunks = PF_KT * D * 2 / 16 / threads;  // per thread
-    u32x4 w[chunks];
-    __device__ void read(lds_ptr<uint8_t> vt, int tid) {
-        for (int c = 0; c < chunks; ++c) w[c] = ((lds_ptr<u32x4>)vt)[c * threads + tid];
+    static constexpr int per = D * 4 / threads;  // chunks per thread
+    static_assert(per >= 1 && D * 4 % threads == 0, "chunks must split evenly over the threads");
+    int src1[per], src2[per], dst[per];  // LDS offsets: the two key quads' reads, the write
+    u32x2 a[per], b[per];
+    __device__ explicit VTranspose(int tid) {
+        for (int n = 0; n < per; ++n) {
+            const int q = n * threads + tid;
+            const int g = q >> 4, jj = q & 15;  // 16-lane group, lane in it
+            const int c = g & 3, fb = 16 * (g >> 2);
+            const int row = 16 * (c >> 1) + 4 * (c & 1) + (jj >> 2);
+            const int fbyte = (fb + 4 * (jj & 3)) * 2;
+            src1[n] = L::at(row, fbyte >> 4) + (fbyte & 15);
+            src2[n] = L::at(row + 8, fbyte >> 4) + (fbyte & 15);
+            dst[n] = L::vt_at(fb + jj, c);
+        }
     }
-    __device__ void write(lds_ptr<uint8_t> vt, int tid) {
-        for (int c = 0; c < chunks; ++c) {
-            u32x4 o;
-            for (int j = 0; j < 4; ++j) {
-                const f32x2 v = {__builtin_bit_cast(float, w[c][j] << 16) * 0x1p-8f,
-                                 __builtin_bit_cast(float, w[c][j] & 0xffff0000u) * 0x1p-8f};
-                o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
-            }
-            ((lds_ptr<u32x4>)vt)[c * threads + tid] = o;
+    __device__ void read(lds_ptr<uint8_t> v) {
+        for (int n = 0; n < per; ++n) {
+            a[n] = read_tr(v + src1[n]);
+            b[n] = read_tr(v + src2[n]);
+        }
+    }
+    __device__ void write(lds_ptr<uint8_t> vt) {
+        for (int n = 0; n < per; ++n) {
+            u32x4 o = {a[n][0], a[n][1], b[n][0], b[n][1]};
+            if constexpr (CONV)
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t w = o[j];
+                    const f32x2 v = {__builtin_bit_cast(float, w << 16) * 0x1p-8f,
+                                     __builtin_bit_cast(float, w & 0xffff0000u) * 0x1p-8f};
+                    o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+                }
+            *(lds_ptr<u32x4>)(vt + dst[n]) = o;
         }
     }
 };
@@ -391,17 +427,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // LDS offsets of this lane's operand reads (tile-relative).
     int k_off[KS];
     for (int ks = 0; ks < KS; ++ks) k_off[ks] = L::at(j, 2 * ks + h);
-    const int gi = lane >> 4, si = lane & 15;
-    int v_off[2][2][MB];
-    for (int stp = 0; stp < 2; ++stp) {
-        const int kr1 = 16 * stp + 4 * (gi >> 1) + (si >> 2);
-        const int dsub = 16 * (gi & 1) + 4 * (si & 3);
-        for (int mb = 0; mb < MB; ++mb) {
-            const int db = (32 * mb + dsub) * 2;  // byte offset of the 4 features in a row
-            v_off[stp][0][mb] = L::at(kr1, db >> 4) + (db & 15);
-            v_off[stp][1][mb] = L::at(kr1 + 8, db >> 4) + (db & 15);
-        }
-    }
+    // V^T operand of M-block mb, key step stp: row 32 mb + j, chunk 2 stp + h
+    // (the swizzle depends on j only, so mb adds a constant).
+    int vt_off[2];
+    for (int stp = 0; stp < 2; ++stp) vt_off[stp] = L::vt_at(j, 2 * stp + h);
 
     // Software pipeline.  Iteration t:
     //   1. P.V of tile t - 1 on the matrix cores, with the statistics of tile
@@ -421,17 +450,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     });
     f32x16 st;
     for (int i = 0; i < 16; ++i) st[i] = 0.0f;
-    VConvert<D, W> vconv;
+    VTranspose<D, W, VCONV> vtr(threadIdx.x);
     if (ntiles > 0) {
         wait_tile(0);
         for (int ks = 0; ks < KS; ++ks) st = mfma32<DT>(*(lds_ptr<u32x4>)(lds + k_off[ks]), qb[ks], st);
-        if constexpr (VCONV) {
-            vconv.read(lds + L::tile, threadIdx.x);
-            vconv.write(lds + L::tile, threadIdx.x);
-            // Tile 0's V^T is read at the end of iteration 0, after the
-            // barrier of its step 2, which a single tile does not have.
-            if (ntiles == 1) __syncthreads();
-        }
+        vtr.read(lds + L::tile);
+        vtr.write(lds + L::vt_base);
+        // Tile 0's V^T is read at the end of iteration 0, after the barrier of
+        // its step 2, which a single tile does not have.
+        if (ntiles == 1) __syncthreads();
     }
     u32x4 vop[2][MB];                  // V^T operands of the tile whose P.V is pending
     uint32_t ph[8];                    // its probabilities (f16 pairs)
@@ -448,7 +475,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     auto body = [&](auto stg_tag, f32x16 &st, f32x16 &st_next) {
         constexpr int STG = decltype(stg_tag)::value;
         constexpr int STG_NEXT = (STG + 1) % NS;
-        lds_ptr<uint8_t> vt = lds + STG * L::stage + L::tile;
+        lds_ptr<uint8_t> vt = lds + L::vt_base + (STG % L::vt_bufs) * L::vt_bytes;
         lds_ptr<uint8_t> kn = lds + STG_NEXT * L::stage;
 
         // ---- step 1.  t = raw dot (or, with the softcap, the capped score in
@@ -540,6 +567,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         if (t + 1 < ntiles) {
             wait_tile(t + 1);
             if (t_next < ntiles) issue(std::integral_constant<int, (STG + NS - 1) % NS>{});
+        } else if (t > 0) {
+            // The last tile: its transposed V was written by the whole
+            // workgroup in the previous iteration's step 3, and no step-2
+            // barrier follows that here; step 4 reads it.
+            __syncthreads();
         }
 
         // ---- step 3: scores of tile t + 1 (K operands read KPRE steps ahead),
@@ -550,18 +582,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int i = 0; i < KPRE && i < KS; ++i) kq[i] = *(lds_ptr<u32x4>)(kn + k_off[i]);
         // bf16: tile t + 1's V, resident since step 2, converted between these
         // MFMAs; the barrier of the next step 2 precedes its V^T reads.
-        const bool conv_next = VCONV && t + 1 < ntiles;
+        const bool conv_next = t + 1 < ntiles;
         lds_ptr<uint8_t> vn = kn + L::tile;
+        lds_ptr<uint8_t> vtn = lds + L::vt_base + (STG_NEXT % L::vt_bufs) * L::vt_bytes;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const u32x4 kcur = kq[ks % KPRE];
             if (ks + KPRE < KS) kq[ks % KPRE] = *(lds_ptr<u32x4>)(kn + k_off[ks + KPRE]);
             st_next = mfma32<DT>(kcur, qb[ks], st_next);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (VCONV) {
-                if (ks == 0 && conv_next) vconv.read(vn, threadIdx.x);
-                if (ks == KS / 2 && conv_next) vconv.write(vn, threadIdx.x);
-            }
+            if (ks == 0 && conv_next) vtr.read(vn);
+            if (ks == KS / 2 && conv_next) vtr.write(vtn);
             for (int i = 4 + 4 * ks / KS; i < 4 + 4 * (ks + 1) / KS; ++i) {
                 const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
                 const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
@@ -572,16 +603,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        // ---- step 4: tile t's V^T operands.  Group gi of 16 lanes reads features
-        // 32 mb + 16 (gi & 1) + 0..15 of keys kb..kb+3; source lane si supplies row
-        // kb + si / 4, features + 4 (si % 4).  B slots 8h..8h+7 of step stp are
-        // keys {16 stp + 4h + 0..3, 16 stp + 8 + 4h + 0..3}.
+        // ---- step 4: tile t's V^T operands, one 16-byte read each.  B slots
+        // 8h..8h+7 of step stp are keys {16 stp + 4h + 0..3, 16 stp + 8 + 4h +
+        // 0..3}, the order in which the transposed tile stores them.
         for (int stp = 0; stp < 2; ++stp)
-            for (int mb = 0; mb < MB; ++mb) {
-                const u32x2 r1 = read_tr(vt + v_off[stp][0][mb]);
-                const u32x2 r2 = read_tr(vt + v_off[stp][1][mb]);
-                vop[stp][mb] = u32x4{r1[0], r1[1], r2[0], r2[1]};
-            }
+            for (int mb = 0; mb < MB; ++mb)
+                vop[stp][mb] = *(lds_ptr<u32x4>)(vt + vt_off[stp] + mb * 32 * L::vt_row);
     };
     for (bool go = true; go;) {
         static_for<NS>([&](auto k) {
