@@ -153,10 +153,14 @@ template <int D, int W> struct PrefillLds {
     // four rows of a transposed V read keep their two-chunk pairs disjoint.
     __device__ static constexpr int swz(int r) { return (2 * r + (r >> 2)) & 7; }
     static constexpr int tile = PF_KT * row;               // one K or V tile
-    static constexpr int stage = 2 * tile;                 // K + V
     static constexpr int stages = D >= 256 ? 3 : 4;
+    // Layout: the transposed V buffers, then the K tiles of the ring, then its
+    // raw V tiles.  The buffers every wave reads each tile (V^T and K) come
+    // first, so at head_dim 128 their offsets fit the 16-bit immediate of the
+    // LDS instructions; raw V is read only by the transposing pass.
+    //
     // Transposed f16 V tiles, the A operand of the P.V MFMAs, in vt_bufs
-    // buffers after the ring (tile t in buffer t % vt_bufs).  Row f (a feature)
+    // buffers (tile t in buffer t % vt_bufs).  Row f (a feature)
     // holds the tile's 32 keys as four 16-byte chunks: chunk c = 2 stp + h holds
     // keys 16 stp + 4 h + 0..3 and 16 stp + 8 + 4 h + 0..3, the key order of the
     // MFMA's k slots, and sits at chunk c ^ ((f / 4) % 4), so 16 consecutive rows
@@ -164,8 +168,12 @@ template <int D, int W> struct PrefillLds {
     static constexpr int vt_row = PF_KT * 2;
     static constexpr int vt_bytes = D * vt_row;
     static constexpr int vt_bufs = stages % 2 == 0 ? 2 : stages;
-    static constexpr int vt_base = stages * stage;
-    static constexpr int bytes = vt_base + vt_bufs * vt_bytes;
+    static constexpr int vt_base = 0;
+    static constexpr int k_base = vt_base + vt_bufs * vt_bytes;
+    static constexpr int v_base = k_base + stages * tile;
+    static constexpr int bytes = v_base + stages * tile;
+    static constexpr int k_at(int s) { return k_base + s * tile; }   // K tile of stage s
+    static constexpr int v_at(int s) { return v_base + s * tile; }   // raw V tile of stage s
     __device__ static constexpr int vt_at(int f, int c) { return f * vt_row + ((c ^ ((f >> 2) & 3)) << 4); }
     static constexpr int runs = tile / 1024;               // 1 KiB runs per tile
     static constexpr int runs_per_wave = runs / W;
@@ -402,16 +410,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // destinations are scalar constants plus run0).
     auto issue = [&](auto stg_tag) {
         constexpr int STG = decltype(stg_tag)::value;
-        const uint32_t m = (uint32_t)(uintptr_t)(lds + STG * L::stage) + run0;
+        const uint32_t mk = (uint32_t)(uintptr_t)(lds + L::k_at(STG)) + run0;
+        const uint32_t mv = (uint32_t)(uintptr_t)(lds + L::v_at(STG)) + run0;
         if (t_next == ntiles - 1) {
             for (int i = 0; i < RPW; ++i) {
-                dma16(k_next, (uint32_t)off_last[i], m + i * 1024);
-                dma16(v_next, (uint32_t)off_last[i], m + L::tile + i * 1024);
+                dma16(k_next, (uint32_t)off_last[i], mk + i * 1024);
+                dma16(v_next, (uint32_t)off_last[i], mv + i * 1024);
             }
         } else {
             for (int i = 0; i < RPW; ++i) {
-                dma16(k_next, (uint32_t)off_full[i], m + i * 1024);
-                dma16(v_next, (uint32_t)off_full[i], m + L::tile + i * 1024);
+                dma16(k_next, (uint32_t)off_full[i], mk + i * 1024);
+                dma16(v_next, (uint32_t)off_full[i], mv + i * 1024);
             }
         }
         k_next += PF_KT * prow;
@@ -453,8 +462,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     VTranspose<D, W, VCONV> vtr(threadIdx.x);
     if (ntiles > 0) {
         wait_tile(0);
-        for (int ks = 0; ks < KS; ++ks) st = mfma32<DT>(*(lds_ptr<u32x4>)(lds + k_off[ks]), qb[ks], st);
-        vtr.read(lds + L::tile);
+        for (int ks = 0; ks < KS; ++ks)
+            st = mfma32<DT>(*(lds_ptr<u32x4>)(lds + L::k_at(0) + k_off[ks]), qb[ks], st);
+        vtr.read(lds + L::v_at(0));
         vtr.write(lds + L::vt_base);
         // Tile 0's V^T is read at the end of iteration 0, after the barrier of
         // its step 2, which a single tile does not have.
@@ -476,7 +486,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         constexpr int STG = decltype(stg_tag)::value;
         constexpr int STG_NEXT = (STG + 1) % NS;
         lds_ptr<uint8_t> vt = lds + L::vt_base + (STG % L::vt_bufs) * L::vt_bytes;
-        lds_ptr<uint8_t> kn = lds + STG_NEXT * L::stage;
+        lds_ptr<uint8_t> kn = lds + L::k_at(STG_NEXT);
 
         // ---- step 1.  t = raw dot (or, with the softcap, the capped score in
         // log2 units); p = 2^(t * tmul - m * tmul).  Both transforms are
@@ -583,7 +593,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         // bf16: tile t + 1's V, resident since step 2, converted between these
         // MFMAs; the barrier of the next step 2 precedes its V^T reads.
         const bool conv_next = t + 1 < ntiles;
-        lds_ptr<uint8_t> vn = kn + L::tile;
+        lds_ptr<uint8_t> vn = lds + L::v_at(STG_NEXT);
         lds_ptr<uint8_t> vtn = lds + L::vt_base + (STG_NEXT % L::vt_bufs) * L::vt_bytes;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
