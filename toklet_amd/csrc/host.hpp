@@ -115,7 +115,7 @@ struct tkh_context {
     int cus = 256;               // compute units of the device
     int decode_groups = 256;     // target decode workgroups per launch (little work)
     int decode_bulk_groups = 2048;  // ... when the launch has much work of mixed lengths
-    int decode_even_groups = 512;   // ... when the launch has much work of even length
+    int decode_even_groups = 256;   // ... when the launch has much work of even length
     int decode_bulk_waves = 4;   // waves per decode workgroup when the launch has much work
     int decode_bulk_keys = 2048; // keys x KV heads per CU from which a launch has much work
     int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
