@@ -233,12 +233,19 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     // several rounds so the dispatcher can even them out.
     const bool bulk = work >= (double)ctx->decode_bulk_keys * ctx->cus;
     const bool even = work >= 0.9 * (double)Hkv * (double)max_span * (double)group.size();
-    const int nw_max = std::min(bulk ? ctx->decode_bulk_waves : ctx->decode_waves,
+    // Even spans at one workgroup per CU stream best with eight waves of two
+    // keys per lane (16 sessions at 8192 keys: 96 us against 98 us at four
+    // waves of four keys); mixed spans and latency-bound launches do not
+    // (configs[2] 199 -> 219 us, configs[1] steps 11.9 -> 13.0 us).
+    const int nw_max = std::min(!bulk ? ctx->decode_waves
+                                      : (even ? ctx->decode_even_waves : ctx->decode_bulk_waves),
                                 tkh_decode_max_waves((int)plan.dtype, (int)D, R));
     const double groups = !bulk ? ctx->decode_groups
                                 : (even ? ctx->decode_even_groups : ctx->decode_bulk_groups);
     int nw = nw_max;
-    const int u = tkh_decode_keys_per_lane((int)plan.dtype, (int)D, ctx->decode_keys_per_lane);
+    const int u = tkh_decode_keys_per_lane((int)plan.dtype, (int)D,
+                                           bulk && even ? ctx->decode_even_keys_per_lane
+                                                        : ctx->decode_keys_per_lane);
     const int max_splits = std::min(ctx->decode_max_splits, tkh_decode_max_splits());
     const int64_t kpb = (int64_t)8 * u;  // keys per wave block
     // Keys per split: about decode_groups workgroups in all, at most
@@ -580,6 +587,8 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
         ctx->decode_even_groups = std::max(1, env_int("TKH_DECODE_EVEN_GROUPS", cus));
     }
     ctx->decode_bulk_waves = std::min(8, std::max(1, env_int("TKH_DECODE_BULK_WAVES", 4)));
+    ctx->decode_even_waves = std::min(8, std::max(1, env_int("TKH_DECODE_EVEN_WAVES", 8)));
+    ctx->decode_even_keys_per_lane = std::max(1, env_int("TKH_DECODE_EVEN_KEYS_PER_LANE", 2));
     ctx->decode_bulk_keys = std::max(1, env_int("TKH_DECODE_BULK_KEYS", 2048));
     // Test hooks for the decode merge's bounded wait (s_memrealtime ticks,
     // 100 MHz; default half a second) and a flag value no split stores.

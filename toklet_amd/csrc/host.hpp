@@ -117,6 +117,8 @@ struct tkh_context {
     int decode_bulk_groups = 2048;  // ... when the launch has much work of mixed lengths
     int decode_even_groups = 256;   // ... when the launch has much work of even length
     int decode_bulk_waves = 4;   // waves per decode workgroup when the launch has much work
+    int decode_even_waves = 8;   // ... much work of even length
+    int decode_even_keys_per_lane = 2;  // keys per lane per block, much work of even length
     int decode_bulk_keys = 2048; // keys x KV heads per CU from which a launch has much work
     int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
     int decode_disable = 0;
