@@ -262,10 +262,11 @@ def test_mfma_qwen3_chunked_prefill_then_decode(torch_mod, ctx, ops, orc, dt):
     log(f"  worst max abs error {worst:.3e}")
 
 
-def test_mfma_qwen25_shape_d64_gqa7(torch_mod, ctx, ops, orc):
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_mfma_qwen25_shape_d64_gqa7(torch_mod, ctx, ops, orc, dt):
     torch = torch_mod
-    log("qwen2.5 14/2/64 bf16 chunks 37+91+1")
-    _chunked_session(torch, ctx, ops, orc, hq=14, hkv=2, D=64, dt="bf16",
+    log(f"qwen2.5 14/2/64 {dt} chunks 37+91+1")
+    _chunked_session(torch, ctx, ops, orc, hq=14, hkv=2, D=64, dt=dt,
                      chunks=[37, 91, 1, 1], capacity=140, seed=2)
 
 
