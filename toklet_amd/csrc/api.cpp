@@ -599,7 +599,9 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     ctx->prefill_groups = std::max(1, env_int("TKH_PREFILL_GROUPS", 512));
     ctx->prefill_max_splits =
         std::min(tkh_prefill_max_splits(), std::max(1, env_int("TKH_PREFILL_MAX_SPLITS", 16)));
-    ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 256));
+    // 64: configs[3] prefill 8.8 -> 7.5 ms and configs[1] chunks 17.9 -> 15.8 us
+    // against 256 (128: 7.6 ms, 16.1 us; 32: no better).
+    ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 64));
     ctx->prefill_waves = env_int("TKH_PREFILL_WAVES", 0);
     auto cleanup = [&](hipError_t e, const char *where) {
         tkh_context_destroy(ctx);

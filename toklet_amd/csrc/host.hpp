@@ -127,7 +127,7 @@ struct tkh_context {
     bool test_flag_skew = false; // test hook: merges wait for a flag value no split stores
     int prefill_groups = 512;    // below this many row-block workgroups, split the keys
     int prefill_max_splits = 16;
-    int prefill_min_keys = 256;  // keys per split at least
+    int prefill_min_keys = 64;   // keys per split at least
     int prefill_waves = 0;       // waves per prefill workgroup: 0 = chosen per launch, 4 or 8
     // profiling: per launch, start/stop of the attention kernel and of the combine kernel
     bool profiling = false;
