@@ -256,3 +256,52 @@ def test_split_wait_is_bounded_and_reported(torch_mod, ops, orc):
     got, ref = _cached_case(torch_mod, clean, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
                             capacity=4100, offset=4095, tokens=1, seed=31)
     assert max_err(got, ref) <= TOL_HALF
+
+
+def _context_with_env(ops, env):
+    """A context created under extra TKH_* settings (read once at creation)."""
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return ops.Context(0)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def test_stream_load_form_does_not_change_results(torch_mod, ops, orc):
+    """The K/V stream's load form (nontemporal for much work, plain for latency-bound
+    launches) is forced both ways in both regimes: the outputs are bit-identical and
+    match the oracle."""
+    torch = torch_mod
+    rng = np.random.default_rng(57)
+    hq, hkv, D, B, L = 16, 8, 128, 16, 4096
+    n = hkv * L * D
+    kpool = stored(rng.standard_normal(B * n), "bf16")
+    vpool = stored(rng.standard_normal(B * n), "bf16")
+    q = stored(rng.standard_normal((B, hq, D)), "bf16")
+    offsets = [b * n for b in range(B)]
+    results = {}
+    for nt in (0, 1):
+        c = _context_with_env(ops, {"TKH_DECODE_STREAM_NT": nt})
+        for batch in (1, B):  # one session: latency regime; sixteen: much work
+            log(f"stream loads nt={nt}, {batch} session(s) x {L} keys")
+            out = torch.zeros(batch * hq * D, dtype=torch.float32, device="cuda")
+            ops.decode_batch(c, dev(q[:batch], "bf16"), dev(kpool[:batch * n], "bf16"),
+                             dev(vpool[:batch * n], "bf16"), offsets[:batch], [L * D] * batch,
+                             [L] * batch, out, query_heads=hq, kv_heads=hkv, head_dim=D,
+                             scale=1.0 / np.sqrt(D))
+            results[(nt, batch)] = host(out).reshape(batch, -1)
+        c.close()
+    for batch in (1, B):
+        assert np.array_equal(results[(0, batch)], results[(1, batch)])
+    worst = 0.0
+    for b in (0, B - 1):
+        ref, _, _ = orc.attention_cached(q[b].reshape(-1), kpool[b * n:(b + 1) * n],
+                                         vpool[b * n:(b + 1) * n], 1, hq, hkv, D, L, L - 1)
+        worst = max(worst, max_err(results[(1, B)][b], ref))
+    log(f"  worst max abs error {worst:.3e}")
+    assert worst <= TOL_HALF

@@ -326,6 +326,11 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     // wait for one that no split stores, to exercise the bounded wait.
     prm.wait_epoch = ctx->epoch + (ctx->test_flag_skew ? 1u : 0u);
     prm.split_wait_ticks = ctx->split_wait_ticks;
+    // Much work streams at the HBM limit, where nontemporal loads raise the
+    // rate (configs[2] 200 -> 184 us, 16 sessions at 8192 keys 96 -> 86 us);
+    // a latency-bound launch is 0.4 us slower with them (one session at 8192
+    // keys 15.3 -> 15.7 us), so it keeps plain loads.
+    prm.stream_nt = ctx->decode_stream_nt < 0 ? (bulk ? 1 : 0) : ctx->decode_stream_nt;
     prm.flags = reinterpret_cast<uint32_t *>(decode_region(ctx));
     float *ws = reinterpret_cast<float *>(decode_region(ctx) + flag_bytes);
     prm.part_ml = ws;
@@ -590,6 +595,7 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     ctx->decode_even_waves = std::min(8, std::max(1, env_int("TKH_DECODE_EVEN_WAVES", 8)));
     ctx->decode_even_keys_per_lane = std::max(1, env_int("TKH_DECODE_EVEN_KEYS_PER_LANE", 2));
     ctx->decode_bulk_keys = std::max(1, env_int("TKH_DECODE_BULK_KEYS", 2048));
+    ctx->decode_stream_nt = std::min(1, std::max(-1, env_int("TKH_DECODE_STREAM_NT", -1)));
     // Test hooks for the decode merge's bounded wait (s_memrealtime ticks,
     // 100 MHz; default half a second) and a flag value no split stores.
     ctx->split_wait_ticks = (uint64_t)std::max(1, env_int("TKH_TEST_SPLIT_WAIT_TICKS", 50000000));

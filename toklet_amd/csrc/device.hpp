@@ -120,7 +120,7 @@ struct Params {
     float *scores;
     float *probs;
     int32_t diag_mode;      // 0 none, 1 full [Hq, queries, keys], 2 last row [keys]
-    int32_t pad2;
+    int32_t stream_nt;      // decode: K/V stream read with nontemporal loads (1) or plain (0)
     uint32_t *flags;        // decode split-K completion flags, one per partial slot
     uint32_t epoch;         // decode split-K: this launch's flag value (never 0; flags start at 0)
     uint32_t wait_epoch;    // the flag value the merging split waits for (= epoch)

@@ -120,6 +120,7 @@ struct tkh_context {
     int decode_even_waves = 8;   // ... much work of even length
     int decode_even_keys_per_lane = 2;  // keys per lane per block, much work of even length
     int decode_bulk_keys = 2048; // keys x KV heads per CU from which a launch has much work
+    int decode_stream_nt = -1;   // nontemporal K/V loads: -1 with much work only, 0 never, 1 always
     int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
     int decode_disable = 0;
     uint32_t epoch = 0;          // last decode split-K epoch handed out
