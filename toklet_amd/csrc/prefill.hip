@@ -599,7 +599,16 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int ks = 0; ks < KS; ++ks) {
             const u32x4 kcur = kq[ks % KPRE];
             if (ks + KPRE < KS) kq[ks % KPRE] = *(lds_ptr<u32x4>)(kn + k_off[ks + KPRE]);
+            // The two waves of a SIMD leave the step-2 barrier together and
+            // would contend for the matrix core and the vector unit in
+            // lockstep.  A raised priority over the first half of the Q.K
+            // chain lets whichever wave gets there first keep its MFMAs
+            // issuing while the other one's exp/pack work fills the gaps
+            // (configs[4]: 388 -> 377 us mean of three alternating runs;
+            // the whole chain or a quarter of it measured no gain).
             st_next = mfma32<DT>(kcur, qb[ks], st_next);
+            if (ks == 0) __builtin_amdgcn_s_setprio(1);
+            if (ks == KS / 2) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
             if (ks == 0 && conv_next) vtr.read(vn);
             if (ks == KS / 2 && conv_next) vtr.write(vtn);
