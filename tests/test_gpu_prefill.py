@@ -145,3 +145,38 @@ def test_split_results_do_not_depend_on_split_count(torch_mod, ctx, ops, orc):
         err = max_err(host(out), ref)
         log(f"max splits {max_splits}: max abs error {err:.3e}")
         assert err <= TOL_HALF
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("key", [40, 256 + 5])
+def test_minus_infinity_score_is_nonfinite(torch_mod, ctx, ops, orc, dt, key):
+    """A key with -inf in a feature where every query of its group is positive gives
+    exactly -inf scores (p = 0, nothing else non-finite): the prefill kernel still
+    reports NonFinite, as the reference rejects non-finite K (src/cpu/attention.rs:247-251).
+    Key 40 lies in a full tile of the cached prefix, key 261 in the causal diagonal
+    tile (visible to the chunk's tokens 5 and later)."""
+    torch = torch_mod
+    rng = np.random.default_rng(61)
+    hq, hkv, D, tokens, offset = 16, 8, 128, 128, 256
+    capacity = offset + tokens
+    k = rng.standard_normal((hkv, capacity, D)).astype(np.float32)
+    v = rng.standard_normal((hkv, capacity, D)).astype(np.float32)
+    q = rng.standard_normal((tokens, hq, D)).astype(np.float32)
+    g = hq // hkv
+    q[:, 3 * g:4 * g, 7] = np.abs(q[:, 3 * g:4 * g, 7]) + 0.25
+    bad_k = k.copy()
+    bad_k[3, key, 7] = -np.inf
+    log(f"prefill -inf score {dt} at key {key}")
+    out = torch.full((tokens * hq * D,), 123.0, dtype=torch.float32, device="cuda")
+    with pytest.raises(ops.TkhError) as e:
+        ops.attention_cached(ctx, dev(stored(q, dt), dt), dev(stored(bad_k, dt), dt),
+                             dev(stored(v, dt), dt), out, None, None,
+                             ops.CachedAttentionShape(tokens, hq, hkv, D, capacity, offset))
+    assert e.value.name == "NonFinite"
+    # The same call with the finite key computes correctly afterwards.
+    qs, ks, vs = stored(q, dt).reshape(-1), stored(k, dt), stored(v, dt)
+    out = torch.full((tokens * hq * D,), np.nan, dtype=torch.float32, device="cuda")
+    ops.attention_cached(ctx, dev(qs, dt), dev(ks, dt), dev(vs, dt), out, None, None,
+                         ops.CachedAttentionShape(tokens, hq, hkv, D, capacity, offset))
+    ref, _, _ = orc.attention_cached(qs, ks, vs, tokens, hq, hkv, D, capacity, offset)
+    assert max_err(host(out), ref) <= TOL_HALF
