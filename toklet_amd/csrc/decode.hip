@@ -257,39 +257,6 @@ constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
 constexpr int CPOL_SC1_NT = 16 | 2;
 constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
 
-// Maximum / sum over the whole wave in registers: DPP inside groups of eight,
-// then the lane swaps of lane_pair (no LDS round trips).
-__device__ __forceinline__ float dpp_max8(float x) {
-    int v = __builtin_bit_cast(int, x);
-    x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false)));
-    v = __builtin_bit_cast(int, x);
-    x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false)));
-    v = __builtin_bit_cast(int, x);
-    x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false)));
-    return x;
-}
-__device__ __forceinline__ float wave_max_regs(float x) {
-    float a, b;
-    x = dpp_max8(x);
-    lane_pair<8>(x, a, b);
-    x = fmaxf(a, b);
-    lane_pair<16>(x, a, b);
-    x = fmaxf(a, b);
-    lane_pair<32>(x, a, b);
-    return fmaxf(a, b);
-}
-__device__ __forceinline__ float wave_sum_regs(float x) {
-    float a, b;
-    x = dpp_sum8(x);
-    lane_pair<8>(x, a, b);
-    x = a + b;
-    lane_pair<16>(x, a, b);
-    x = a + b;
-    lane_pair<32>(x, a, b);
-    return a + b;
-}
-
-
 }  // namespace
 
 // A key segment's fields the decode kernel reads (Segment minus nothing it
@@ -880,7 +847,13 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
                 mmax = fmaxf(mmax, mv[g][0]);
             }
         }
-        const float M = wave_max_regs(mmax);
+        // The lanes of one split group (same g4) read the same (max, mass)
+        // words, so the row's maximum and mass need only the four groups:
+        // the lanes 16 and 32 apart.
+        float pa, pb;
+        lane_pair<16>(mmax, pa, pb);
+        lane_pair<32>(fmaxf(pa, pb), pa, pb);
+        const float M = fmaxf(pa, pb);
         const float base = M == NEG_INF ? 0.0f : M;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
         float lsum = 0.0f;
@@ -891,8 +864,9 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
                 lsum = __builtin_fmaf(wgt, mv[g][1], lsum);
             }
         }
-        // Each split's mass was read by its 16 lanes: count it once.
-        const float L = wave_sum_regs(q4 == 0 ? lsum : 0.0f);
+        lane_pair<16>(lsum, pa, pb);
+        lane_pair<32>(pa + pb, pa, pb);
+        const float L = pa + pb;
         for (int k = 0; k < 4; ++k) {
             float a, b;
             lane_pair<16>(acc[k], a, b);
