@@ -126,7 +126,8 @@ struct tkh_context {
     uint32_t epoch = 0;          // last decode split-K epoch handed out
     uint64_t split_wait_ticks = 50000000;  // bound of a decode merge's wait for its splits
     bool test_flag_skew = false; // test hook: merges wait for a flag value no split stores
-    int prefill_groups = 512;    // below this many row-block workgroups, split the keys
+    int prefill_groups = 128;    // below this many row-block workgroups (128-row units), split the keys
+    int prefill_fill_groups = 512;  // row-block workgroups (128-row units) from which eight-wave ones fill the device
     int prefill_max_splits = 16;
     int prefill_min_keys = 64;   // keys per split at least
     int prefill_waves = 0;       // waves per prefill workgroup: 0 = chosen per launch, 4 or 8
