@@ -313,7 +313,8 @@ typedef struct tkh_session tkh_session;
  * geometry the session's KV owners need.  layer_windows (per layer, 0 = full
  * retention) select ring caches for sliding layers (WindowKvCache).
  * score_scale 0 selects attention_cached semantics (dot / sqrt(D), no
- * softcap) for full layers; otherwise every layer uses window/span semantics
+ * softcap) for full layers, and a nonzero softcap with it is rejected
+ * (TKH_INVALID_CONFIG); otherwise every layer uses window/span semantics
  * with this scale and the optional score softcap. */
 typedef struct tkh_session_options {
     uint64_t capacity;

@@ -18,6 +18,13 @@ Fixture sets taken (all used by the reference's own attention tests):
   gemma-kv-v1                src/cpu/span_attention/tests.rs:212, src/model/window_cache/tests.rs:77
   gemma-softcap-v1           src/cpu/softcap/tests.rs:19
   qwen3-attention-inputs-v1  src/metal/compensated_attention.rs:465-561 (inputs only)
+  gemma-rotary-v1            src/cpu/proportional_rotary/tests.rs:34-71
+  tiny-v1 rmsnorm arrays     tests/cpu_reductions.rs:16-62, 140-175 (-> tiny_v1_norms)
+  gemma-reference-attention-v1
+                             tools/reference/test_gemma_reference_attention.py:17-42: the
+                             frozen outputs of both contracts; the inputs are rebuilt from the
+                             fixture's published rational recipe and checked against the
+                             manifest's SHA-256 (tests/goldens.py: reference_attention_inputs)
 """
 
 from __future__ import annotations
@@ -111,6 +118,54 @@ def qwen3_inputs(ref: str, out: str):
     json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
 
 
+def tiny_norms(ref: str, out: str):
+    """The arrays the reference's rmsnorm tests read from tiny-v1: each layer's
+    inputs (embedding / previous layer output, attention residual), weights and
+    expected outputs, the final norm, and the edge cases."""
+    root = os.path.join(ref, "tests", "fixtures", "tiny-v1")
+    manifest = json.load(open(os.path.join(root, "manifest.json")))
+    names = []
+    for case in manifest["cases"]:
+        names += [f"cases.{case}.tokens", f"cases.{case}.embedding", f"cases.{case}.final_norm"]
+        for layer in range(manifest["model"]["num_layers"]):
+            names += [f"cases.{case}.layers.{layer}.{k}" for k in
+                      ("input_norm", "post_attention_norm", "attention_residual", "output")]
+    for layer in range(manifest["model"]["num_layers"]):
+        names += [f"weights.layers.{layer}.input_layernorm",
+                  f"weights.layers.{layer}.post_attention_layernorm"]
+    names += ["weights.norm", "edge.rmsnorm.large_input", "edge.rmsnorm.large_output",
+              "edge.rmsnorm.zero_output"]
+    arrays = {n: read_array(root, manifest["arrays"][n]) for n in names}
+    meta = {"cases": manifest["cases"], "model": manifest["model"], "epsilon": 1e-6}
+    np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
+
+
+def reference_attention(ref: str, out: str):
+    """gemma-reference-attention-v1: the frozen scores, probabilities and contexts
+    of every case under both contracts (FP64 `math`, staged `staged_fp32`), each
+    checked against its SHA-256.  The inputs are not stored: they are the
+    fixture's rational recipe, rebuilt by tests/goldens.py and checked there
+    against the SHA-256 kept here."""
+    root = os.path.join(ref, "tests", "fixtures", "gemma-reference-attention-v1")
+    raw_meta = open(os.path.join(root, "manifest.json"), "rb").read()
+    manifest = json.loads(raw_meta)
+    raw = open(os.path.join(root, "arrays.bin"), "rb").read()
+    assert sha(raw) == manifest["binary"]["sha256"]
+    arrays = {}
+    for item in manifest["arrays"]:
+        body = raw[item["offset"]:item["offset"] + item["bytes"]]
+        assert sha(body) == item["sha256"], item["name"]
+        key = f"{item['case']}.{item['contract']}.{item['name']}"
+        arrays[key] = np.frombuffer(body, dtype=item["dtype"]).reshape(item["shape"]).copy()
+    inputs = [{k: item[k] for k in ("case", "contract", "name", "shape", "dtype", "sha256")}
+              for item in manifest["inputs"]]
+    meta = {"source_manifest_sha256": sha(raw_meta), "cases": manifest["cases"], "inputs": inputs,
+            "arithmetic": manifest["arithmetic"], "recipe": manifest["source_input_recipe"]}
+    np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
+
+
 def main(ref: str):
     attn = ["q_projection", "k_projection", "q_rotary", "k_rotary", "v_projection",
             "attention_scores", "attention_probabilities", "attention_context"]
@@ -120,6 +175,9 @@ def main(ref: str):
     math_json(ref, "gemma-kv-v1", "gemma_kv_v1")
     math_json(ref, "gemma-softcap-v1", "gemma_softcap_v1")
     qwen3_inputs(ref, "qwen3_attention_inputs_v1")
+    math_json(ref, "gemma-rotary-v1", "gemma_rotary_v1")
+    tiny_norms(ref, "tiny_v1_norms")
+    reference_attention(ref, "gemma_reference_attention_v1")
 
 
 if __name__ == "__main__":

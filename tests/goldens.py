@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import hashlib
 import json
 import os
 
@@ -37,3 +38,44 @@ def head_major_to_token_major(x, heads, tokens, dims):
 
 
 TINY_CASES = ["prompt", "future_changed", "offset", "single", "capacity"]
+
+
+# ---- gemma-reference-attention-v1 inputs ----
+
+# The fixture's published input recipe ("rational13-and-cancellation-near-ties-v1",
+# tools/reference/gemma_reference_attention_oracle.py:29-35): rationals n/13 from a
+# modular walk over (head, position, feature), and for `cancellation` mixed-sign
+# dyadic rows with near-tied keys.
+
+def _cancellation_value(kind: str, position: int, feature: int) -> float:
+    if kind == "q":
+        return (1024.0, 1.0, -1024.0, -1.0)[feature % 4]
+    if kind == "k":
+        return 1.0 + (position % 2) * 2.0 ** -20 + ((position % 7) * 2.0 ** -24 if feature % 4 == 1 else 0.0)
+    return (0.0 if position == 512 else (1024.0, 1.0, -1024.0, -1.0)[position % 4]) + (feature % 7) * 2.0 ** -8
+
+
+def reference_attention_inputs(golden: "Golden", case: dict, contract: str):
+    """q [1, heads, queries, D], k/v [1, 1, keys, D] of one case and contract
+    ("math": FP64, "staged_fp32": FP32), rebuilt from the recipe and checked
+    byte for byte against the SHA-256 the fixture's manifest records."""
+    out = []
+    for name in ("q", "k", "v"):
+        item = next(i for i in golden.meta["inputs"]
+                    if (i["case"], i["contract"], i["name"]) == (case["name"], contract, name))
+        origin = case["query_start"] if name == "q" else case["key_start"]
+        heads = case["heads"] if name == "q" else 1
+        n = case["queries"] if name == "q" else case["keys"]
+        d = case["head_dim"]
+        h, p, f = np.meshgrid(np.arange(heads), np.arange(n), np.arange(d), indexing="ij")
+        if case["name"] == "cancellation":
+            values = np.array([_cancellation_value(name, origin + pp, ff)
+                               for pp, ff in zip(p.ravel(), f.ravel())])
+        else:
+            shift = {"q": 3, "k": 11, "v": 23}[name]
+            values = (((h * 31 + (origin + p) * 17 + f * 7 + shift) % 53) - 26) / 13.0
+        values = np.asarray(values, dtype=item["dtype"]).reshape(item["shape"])
+        digest = hashlib.sha256(np.ascontiguousarray(values).tobytes()).hexdigest()
+        assert digest == item["sha256"], f"rebuilt {case['name']}/{contract}/{name} differs"
+        out.append(values)
+    return out

@@ -133,12 +133,17 @@ def test_gemma_window_decode_d256(torch_mod, ctx, ops, orc, softcap):
         assert err <= TOL_HALF
 
 
-def test_ring_span_decode_wraps(torch_mod, ctx, ops, orc):
-    """Decode over a W=1024 ring whose view is two old spans plus the new row."""
+@pytest.mark.parametrize("hq,hkv,D,W,offset", [
+    (8, 4, 128, 1024, 5000),   # slot 5000 % 1024 = 904: the old spans wrap around the ring
+    # One KV head, D=64: old spans of 1000 and 1047 rows plus the new one.  Rounded
+    # up per segment at 32 keys per split they would need 32 + 33 + 1 = 66 splits,
+    # two more than the merge reads; the planner must widen the splits instead.
+    (1, 1, 64, 2048, 3095),
+])
+def test_ring_span_decode_wraps(torch_mod, ctx, ops, orc, hq, hkv, D, W, offset):
+    """Decode over a ring whose view is two old spans plus the new row."""
     torch = torch_mod
     rng = np.random.default_rng(41)
-    hq, hkv, D, W = 8, 4, 128, 1024
-    offset = 5000  # slot 5000 % 1024 = 904: the old spans wrap around the ring
     ring_k = stored(rng.standard_normal((hkv, W, D)), "bf16")
     ring_v = stored(rng.standard_normal((hkv, W, D)), "bf16")
     nk = stored(rng.standard_normal((hkv, 1, D)), "bf16")
@@ -170,7 +175,7 @@ def test_ring_span_decode_wraps(torch_mod, ctx, ops, orc):
     ref, _, _ = orc.span_attention(q, segs_ref, 1, keys, hq, hkv, D, offset, key_start, W,
                                    np.float32(1.0 / np.sqrt(D)))
     err = max_err(host(out), ref)
-    log(f"ring decode: keys {keys}, max abs error {err:.3e}")
+    log(f"ring decode {hq}/{hkv}/{D} W={W}: keys {keys}, max abs error {err:.3e}")
     assert err <= TOL_HALF
 
 

@@ -310,6 +310,63 @@ def test_queued_ring_session_failure_rolls_back_to_last_ring_commit(torch_mod, o
     c.close()
 
 
+def test_queued_ring_sessions_sharing_a_context_see_commits_skipped_for_the_other(
+        torch_mod, ops, sess_mod, orc):
+    """Two queued ring sessions on one context.  B's fourth chunk holds a NaN, and A's
+    chunks are queued after it, so A's gated ring commits are all skipped.  B's
+    synchronize reports NonFinite and clears the context's status word; A's then
+    finds its committed length short of its evaluated length, reports a device
+    error and rolls back to position 0, and re-evaluating A matches the oracle."""
+    torch = torch_mod
+    rng = np.random.default_rng(17)
+    L, hq, hkv, D, total, W = 2, 4, 2, 64, 80, 32
+    c = ops.Context(0, synchronous=False)
+    opts = sess_mod.Options(capacity=total, prefill_chunk_size=16, vocab_size=10, layers=L,
+                            query_heads=hq, kv_heads=hkv, head_dim=D, storage="bf16",
+                            score_scale=0.125, layer_windows=[W, 0])
+    sess, ios, inputs, ctxs = [], [], [], []
+    for name in "AB":
+        qs, ks, vs, wq, wk = _session_inputs(rng, L, total, hq, hkv, D)
+        out = [torch.zeros((total, hq * D), dtype=torch.float32, device="cuda") for _ in range(L)]
+        kk = [k.copy() for k in ks]
+        if name == "B":
+            kk[0][55, 1, 3] = np.nan   # chunk [48, 64) of B
+        ios.append([sess_mod.LayerIo(_t(torch, qs[l]), _t(torch, kk[l]), _t(torch, vs[l]), out[l],
+                                     _t(torch, wq[l]), _t(torch, wk[l])) for l in range(L)])
+        inputs.append((qs, ks, vs, wq, wk))
+        ctxs.append(out)
+        sess.append(sess_mod.Session(c, opts))
+    a, b = sess
+    b.set_tokens([1] * total)
+    assert b.evaluate(ios[1]) == total
+    a.set_tokens([2] * total)
+    assert a.evaluate(ios[0]) == total
+    with pytest.raises(ops.TkhError) as e:
+        b.synchronize()
+    assert e.value.name == "NonFinite"
+    with pytest.raises(ops.TkhError) as e:
+        a.synchronize()
+    log(f"session A after B's failure: {e.value}")
+    assert e.value.name == "Device"
+    assert (a.evaluated_len(), a.pending_len()) == (0, total)
+    assert a.evaluate(ios[0]) == total
+    a.synchronize()
+    qs, ks, vs, wq, wk = inputs[0]
+    for l, window in enumerate([W, None]):
+        q = stored(_oracle_produce(orc, qs[l], wq[l], total, hq, D, 0), "bf16")
+        k = stored(_oracle_produce(orc, ks[l], wk[l], total, hkv, D, 0), "bf16")
+        v = stored(vs[l], "bf16")
+        ref, _, _ = orc.window_attention(q.reshape(-1), k.transpose(1, 0, 2).reshape(-1),
+                                         v.transpose(1, 0, 2).reshape(-1), total, total, total, hq,
+                                         hkv, D, 0, 0, window, 0.125)
+        err = max_err(host(ctxs[0][l]).reshape(-1), ref)
+        log(f"shared-context ring session A layer {l}: max abs error {err:.3e}")
+        assert err <= TOL_HALF
+    a.close()
+    b.close()
+    c.close()
+
+
 def test_queued_linear_session_failure_returns_to_checked_prefix(torch_mod, ops, sess_mod):
     torch = torch_mod
     rng = np.random.default_rng(8)

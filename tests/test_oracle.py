@@ -9,7 +9,8 @@ import math
 import numpy as np
 import pytest
 
-from goldens import TINY_CASES, Golden, close, head_major_to_token_major
+from goldens import (TINY_CASES, Golden, close, head_major_to_token_major,
+                     reference_attention_inputs)
 
 
 @pytest.fixture(scope="module")
@@ -468,6 +469,103 @@ def test_rmsnorm_closed_form(orc):
     out = orc.rmsnorm(x, [1.0, 2.0], 1, 2, 1e-6)
     rms = math.sqrt((9 + 16) / 2 + 1e-6)
     close(out, [3 / rms, 8 / rms], atol=1e-7, rtol=1e-7)
+
+
+# ---- tiny-v1 normalisations (tests/cpu_reductions.rs:16-62, 140-175) ----
+
+def test_rmsnorm_matches_every_tiny_normalization(orc):
+    """Every normalisation tiny-v1 freezes: per layer the input norm (of the
+    embedding or the previous layer's output) and the post-attention norm (of the
+    attention residual), then the final norm, hidden 32, epsilon 1e-6."""
+    g = Golden("tiny_v1_norms")
+    checked = 0
+    for case in TINY_CASES:
+        tokens = len(g.arrays[f"cases.{case}.tokens"])
+        for layer in range(2):
+            prefix = f"cases.{case}.layers.{layer}"
+            first = f"cases.{case}.embedding" if layer == 0 else f"cases.{case}.layers.0.output"
+            for src, weight, expected in (
+                    (first, f"weights.layers.{layer}.input_layernorm", f"{prefix}.input_norm"),
+                    (f"{prefix}.attention_residual", f"weights.layers.{layer}.post_attention_layernorm",
+                     f"{prefix}.post_attention_norm")):
+                out = orc.rmsnorm(g.arrays[src].reshape(-1), g.arrays[weight], tokens, 32, 1e-6)
+                close(out, g.arrays[expected])
+                checked += 1
+        out = orc.rmsnorm(g.arrays[f"cases.{case}.layers.1.output"].reshape(-1), g.arrays["weights.norm"],
+                          tokens, 32, 1e-6)
+        close(out, g.arrays[f"cases.{case}.final_norm"])
+        checked += 1
+    assert checked == 25
+
+
+def test_rmsnorm_edge_cases_and_epsilon(orc):
+    """Zero rows, FP32 overflow of the squares, and an epsilon that decides the
+    result (tests/cpu_reductions.rs:140-175)."""
+    g = Golden("tiny_v1_norms")
+    close(orc.rmsnorm(np.zeros(32), np.ones(32), 1, 32, 1e-6), g.arrays["edge.rmsnorm.zero_output"])
+    close(orc.rmsnorm(g.arrays["edge.rmsnorm.large_input"].reshape(-1), np.ones(4), 1, 4, 1e-6),
+          g.arrays["edge.rmsnorm.large_output"])
+    fmax = float(np.finfo(np.float32).max)
+    tiny = float(np.array([1], np.uint32).view(np.float32)[0])
+    r = 2.0 / math.sqrt(3.0)
+    close(orc.rmsnorm([fmax, -fmax, 0.0, fmax], np.ones(4), 1, 4, tiny), [r, -r, 0.0, r])
+    # Epsilon is added to the mean square: x = 1e-3 over a row of 4 with epsilon 3e-6 gives
+    # 1e-3 / sqrt(1e-6 + 3e-6) = 0.5, where an epsilon added to the root (or dropped) would not.
+    close(orc.rmsnorm(np.full(4, 1e-3), np.ones(4), 1, 4, 3e-6), np.full(4, 0.5), atol=1e-7, rtol=1e-6)
+
+
+# ---- gemma-rotary-v1 (src/cpu/proportional_rotary/tests.rs:34-71) ----
+
+def test_proportional_rotary_matches_gemma_rotary_fixture(orc):
+    """Every case of gemma-rotary-v1: factors 1, 2 and 2.5, rotated dims 0..128 of
+    8..512, positions up to 131071.  Outputs within 1e-5 + 1e-4|e|, and the pairs
+    past rotated_dims are copied bit for bit."""
+    g = Golden("gemma_rotary_v1")
+    checked = 0
+    for case in g.meta["cases"]:
+        if case["tokens"] == 0:
+            continue  # empty sequences make no operator calls
+        x = g[case["arrays"]["input"]].astype(np.float32).reshape(-1)
+        out = orc.proportional_rotary(x, case["tokens"], case["heads"], case["dims"],
+                                      case["rotated_dims"], case["offset"], case["base"], case["factor"])
+        close(out, g[case["arrays"]["output"]])
+        D, half = case["dims"], case["dims"] // 2
+        for first in range(0, x.size, D):
+            for pair in range(case["rotated_dims"] // 2, half):
+                for i in (first + pair, first + pair + half):
+                    assert out.view(np.uint32)[i] == x.view(np.uint32)[i]
+        checked += 1
+    assert checked == 7
+
+
+# ---- gemma-reference-attention-v1 (tools/reference/test_gemma_reference_attention.py:46-58) ----
+
+def _reference_attention_oracle(orc, case, q, k, v):
+    """window_attention over one case: q [1, H, Q, D] head-major, k/v [1, 1, K, D], scale 1."""
+    H, Q, K, D = case["heads"], case["queries"], case["keys"], case["head_dim"]
+    qt = head_major_to_token_major(q.astype(np.float32), H, Q, D)
+    return orc.window_attention(qt, k.astype(np.float32).reshape(-1), v.astype(np.float32).reshape(-1),
+                                Q, K, K, H, 1, D, case["query_start"], case["key_start"],
+                                case["window"], 1.0)
+
+
+def test_window_attention_matches_reference_attention_contracts(orc):
+    """The eight frozen cases (D up to 512, 1025 keys, windows 4 and 512, translated
+    origins, mixed-sign cancellation, near ties): the oracle's window_attention on
+    the staged FP32 inputs meets the staged contract's scores, probabilities and
+    contexts at the reference's gate, and the FP64 contract's contexts too."""
+    g = Golden("gemma_reference_attention_v1")
+    for case in g.meta["cases"]:
+        q, k, v = reference_attention_inputs(g, case, "staged_fp32")
+        ctx, sc, pr = _reference_attention_oracle(orc, case, q, k, v)
+        H, Q, D = case["heads"], case["queries"], case["head_dim"]
+        name = case["name"]
+        close(ctx, head_major_to_token_major(g.arrays[f"{name}.staged_fp32.context"], H, Q, D))
+        close(sc, g.arrays[f"{name}.staged_fp32.scores"])
+        close(pr, g.arrays[f"{name}.staged_fp32.probabilities"])
+        close(ctx, head_major_to_token_major(g.arrays[f"{name}.math.context"], H, Q, D))
+        mask = g.arrays[f"{name}.staged_fp32.probabilities"].reshape(-1) == 0
+        assert np.all(pr.reshape(-1)[mask].view(np.uint32) == 0)
 
 
 def test_proportional_rotary_reduces_to_rotary(orc):

@@ -175,3 +175,6 @@ def test_invalid_options_are_rejected():
     assert e.value.code == _lib.INVALID_PARAMETER
     with pytest.raises(TkhError):
         Session(None, Options(capacity=8, layers=2, layer_windows=[4, 0]))  # needs a score scale
+    with pytest.raises(TkhError) as e:  # attention_cached semantics have no softcap
+        Session(None, Options(capacity=8, softcap=50.0))
+    assert e.value.code == _lib.INVALID_CONFIG

@@ -259,6 +259,33 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     if (sk < max_span) sk = std::max<int64_t>(sk, kpb * merge_waves);
     if (ctx->split_keys_override > 0) sk = ctx->split_keys_override;
     sk = std::max<int64_t>(kpb, (sk + kpb - 1) / kpb * kpb);
+    // Splits never straddle a segment boundary, so a view of several segments
+    // rounds each one up: grow the split size (in whole blocks) until every
+    // problem fits the merge, which reads at most max_splits partials.
+    auto seg_split_counts = [&](tkh::Problem &p, int64_t keys_per_split) {
+        int64_t n_all = 0;
+        for (int s = 0; s < 3; ++s) {
+            int64_t n = 0;
+            if (s < p.nseg) {
+                const int64_t lo = std::max<int64_t>(p.vis_lo, p.seg[s].start);
+                const int64_t hi = std::min<int64_t>(p.vis_hi, p.seg[s].start + p.seg[s].keys);
+                if (hi > lo) n = (hi - lo + keys_per_split - 1) / keys_per_split;
+            }
+            p.seg_splits[s] = (int32_t)n;
+            n_all += n;
+        }
+        if (n_all == 0) {  // nothing visible: one empty split reports the bad mass
+            p.seg_splits[0] = 1;
+            n_all = 1;
+        }
+        return n_all;
+    };
+    for (;;) {
+        int64_t worst = 0;
+        for (auto &p : group) worst = std::max<int64_t>(worst, seg_split_counts(p, sk));
+        if (worst <= max_splits) break;
+        sk = (sk * 2 + kpb - 1) / kpb * kpb;
+    }
     if (sk > INT32_MAX) return fail(err, TKH_UNSUPPORTED, "keys", 0, 0, 0, "key range too large");
     nw = (int)std::min<int64_t>(nw, sk / kpb);
 
@@ -267,22 +294,7 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     for (size_t i = 0; i < group.size(); ++i) {
         auto &p = group[i];
         p.split_keys = (int32_t)sk;
-        int64_t splits = 0;
-        for (int s = 0; s < 3; ++s) {
-            int64_t n = 0;
-            if (s < p.nseg) {
-                const int64_t lo = std::max<int64_t>(p.vis_lo, p.seg[s].start);
-                const int64_t hi = std::min<int64_t>(p.vis_hi, p.seg[s].start + p.seg[s].keys);
-                if (hi > lo) n = (hi - lo + sk - 1) / sk;
-            }
-            p.seg_splits[s] = (int32_t)n;
-            splits += n;
-        }
-        if (splits == 0) {  // nothing visible: one empty split reports the bad mass
-            p.seg_splits[0] = 1;
-            splits = 1;
-        }
-        p.splits = (int32_t)splits;
+        p.splits = (int32_t)seg_split_counts(p, sk);
         p.row_blocks = 1;
         p.tile_base = wgs;
         p.slot_base = slots;
@@ -299,11 +311,17 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
     // Decode partials: completion flags, then (max, mass) and contexts, in the
     // decode half of the workspace.
     const size_t flag_bytes = ((size_t)slots * sizeof(uint32_t) + 255) / 256 * 256;
-    const size_t need = flag_bytes + (size_t)slots * R * (D + 2) * sizeof(float);
+    const size_t part_bytes = (size_t)slots * R * (D + 2) * sizeof(float);
+    const size_t need = flag_bytes + part_bytes;
     if (need > decode_region_bytes(ctx))
         return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, decode_region_bytes(ctx),
                     "decode needs %zu workspace bytes, context has %zu for it", need,
                     decode_region_bytes(ctx));
+    // The merge addresses every partial through one buffer resource based at
+    // the (max, mass) array, with 32-bit byte offsets below 2^31.
+    if (part_bytes > (size_t)INT32_MAX)
+        return fail(err, TKH_UNSUPPORTED, "workspace", 0, (size_t)INT32_MAX, part_bytes,
+                    "decode partials of %zu bytes exceed the merge's 2 GiB range", part_bytes);
 
     tkh::Problem *dev = nullptr;
     if (group.size() > 1) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));

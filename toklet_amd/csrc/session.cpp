@@ -217,25 +217,38 @@ void settle(tkh_session *s) {
 // Waits for queued work and checks the status word.  On failure the
 // provisional chunks are dropped: linear-cache sessions return to the last
 // checked prefix; ring sessions to the last chunk whose gated ring commit ran
-// (read back from the device), which is where their rings stand.
+// (read back from the device), which is where their rings stand.  The status
+// word belongs to the context, and whoever reads it first clears it (another
+// session, tkh_context_synchronize): a ring session therefore also reads back
+// its committed length when the status is clean, and a commit that was
+// skipped for a failure reported elsewhere is a failure here too.
 uint32_t synchronize(tkh_session *s, tkh_error *err) {
     if (!s->ctx) return ok(err);
     uint32_t rc = tkh_context_synchronize(s->ctx, err);
+    uint64_t back = s->checked;
+    bool valid = s->checked_valid;
+    const bool provisional = s->checked != s->evaluated;
+    if (s->rings && provisional) {
+        uint64_t c = s->checked;
+        const hipError_t e = hipMemcpy(&c, s->committed_dev, sizeof c, hipMemcpyDeviceToHost);
+        if (e == hipSuccess && c >= s->checked && c <= s->evaluated) {
+            valid = c > s->checked ? true : s->checked_valid;
+            back = c;
+        }
+        if (rc == TKH_OK && e != hipSuccess) rc = device_error(e, "session ring commit", err);
+        else if (rc == TKH_OK && back != s->evaluated)
+            rc = fail(err, TKH_DEVICE, "session ring commit", back, s->evaluated, back,
+                      "ring commits of queued chunks stopped at %llu of %llu: a failure on this "
+                      "context was reported to another caller",
+                      (unsigned long long)back, (unsigned long long)s->evaluated);
+    }
     if (rc == TKH_OK) {
         s->checked = s->evaluated;
         s->checked_valid = s->dist_valid;
         return rc;
     }
-    if (rc != TKH_NON_FINITE) return rc;
-    uint64_t back = s->checked;
-    bool valid = s->checked_valid;
+    if (!provisional) return rc;
     if (s->rings) {
-        uint64_t c = s->checked;
-        if (hipMemcpy(&c, s->committed_dev, sizeof c, hipMemcpyDeviceToHost) == hipSuccess &&
-            c >= s->checked && c <= s->evaluated) {
-            valid = c > s->checked ? true : s->checked_valid;
-            back = c;
-        }
         for (auto *kv : s->kv) {
             if (!kv->has_window) continue;
             kv->offset = back;
@@ -295,6 +308,13 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
         free_session(s);
         return invalid("windowed layers need an explicit score scale", err);
     }
+    // score_scale 0 selects attention_cached semantics, which have no softcap:
+    // a softcap there would be silently ignored.
+    if (o->softcap != 0.0f && o->score_scale == 0.0f) {
+        free_session(s);
+        return fail(err, TKH_INVALID_CONFIG, "session options", 0, 0, 0,
+                    "a score softcap needs an explicit score scale (window/span semantics)");
+    }
     s->history.reserve(o->capacity);
     // Decode steps with the producer inside the decode kernel (one launch per
     // step instead of two; TKH_FUSED_DECODE=0 turns it off): head sizes of
@@ -324,6 +344,7 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
             s->kv_bytes += s->kv[l]->allocated_bytes;
             s->rings |= ring;
         }
+        s->scratch_bytes = chunk * o->query_heads * D * es;
         hipError_t e = hipMalloc(&s->q_scratch, chunk * o->query_heads * D * es);
         if (e == hipSuccess) e = hipMalloc(&s->committed_dev, sizeof(uint64_t));
         if (e == hipSuccess) e = tkh_launch_fill_u64(s->committed_dev, 0, ctx->stream);
@@ -339,7 +360,6 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
             if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
             s->scratch_bytes += bytes;
         }
-        s->scratch_bytes = chunk * o->query_heads * D * es;
         for (uint64_t l = 0; e == hipSuccess && l < o->layers; ++l) {
             if (!s->kv[l]->has_window) continue;
             const size_t bytes = chunk * o->kv_heads * D * es;
