@@ -122,6 +122,31 @@ uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, t
                               uint64_t context_len, float *scores, uint64_t scores_len,
                               float *probabilities, uint64_t probabilities_len, tkh_error *err);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): tkh_attention_cached without a context and without the
+ * score/probability rows.  Its split-K partials, decode completion flags and
+ * (with status == NULL) its status word live in a fixed device array of
+ * TKH_STATIC_SCRATCH_BYTES per GPU, set up by the first call on each device
+ * and held until the process ends; no call allocates or frees memory.  A
+ * shape whose partials cannot fit the array returns TKH_UNSUPPORTED and
+ * computes nothing.  `stream` is the hipStream_t the work is queued on (NULL:
+ * the null stream).
+ *  - status != NULL: a device word owned by the caller; the kernels OR their
+ *    status bits into it and the call returns once the work is queued.  The
+ *    word is never cleared here.  Nonzero means the results are invalid:
+ *    bit 3 (8) a decode merge timed out (TKH_DEVICE), any other bit a
+ *    non-finite input or result (TKH_NON_FINITE).
+ *  - status == NULL: the call waits for the stream and reports as a
+ *    synchronous context does.
+ * Every call on one GPU shares that GPU's array and keeps its last contents:
+ * calls that overlap on a GPU (from other streams or threads) race. */
+#define TKH_STATIC_SCRATCH_BYTES (16u << 20)
+uint32_t tkh_attention_cached_static(int device, void *stream, const tkh_cached_shape *shape,
+                                     tkh_dtype dtype, const void *q, uint64_t q_len, const void *k,
+                                     uint64_t k_len, const void *v, uint64_t v_len, float *context,
+                                     uint64_t context_len, uint32_t *status, tkh_error *err);
+
 /* Shape of toklet::cpu::AttentionShape (src/cpu/attention.rs:67-72). */
 typedef struct tkh_attention_shape {
     uint64_t tokens, query_heads, kv_heads, head_dim;

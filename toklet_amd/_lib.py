@@ -109,6 +109,8 @@ SIGNATURES = {
     "tkh_context_profile_read": (u32, [vp, P(Profile), E]),
     "tkh_attention_cached": (u32, [vp, P(CachedShape), ctypes.c_int, vp, u64, vp, u64, vp, u64,
                                    fptr, u64, fptr, u64, fptr, u64, E]),
+    "tkh_attention_cached_static": (u32, [ctypes.c_int, vp, P(CachedShape), ctypes.c_int, vp, u64,
+                                          vp, u64, vp, u64, fptr, u64, P(u32), E]),
     "tkh_attention": (u32, [vp, P(AttentionShape), ctypes.c_int, vp, u64, vp, u64, vp, u64, fptr,
                             u64, fptr, u64, fptr, u64, E]),
     "tkh_window_attention": (u32, [vp, P(WindowShape), ctypes.c_int, vp, u64, vp, u64, vp, u64,

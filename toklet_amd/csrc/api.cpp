@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "../../include/tokhip.h"
@@ -62,6 +63,21 @@ using namespace tkh_host;
 
 namespace {
 
+// The error code of a nonzero device status word.
+uint32_t status_error(uint32_t st, tkh_error *err) {
+    if (st & tkh::ST_SPLIT_TIMEOUT)
+        return fail(err, TKH_DEVICE, "decode splits", 0, 0, 0,
+                    "a decode merge timed out waiting for its key splits (status 0x%x)", st);
+    if (st & tkh::ST_NONFINITE_INPUT)
+        return fail(err, TKH_NON_FINITE, "attention inputs", 0, 0, 0,
+                    "non-finite value in attention inputs or scores (status 0x%x)", st);
+    if (st & tkh::ST_BAD_MASS)
+        return fail(err, TKH_NON_FINITE, "attention probabilities", 0, 0, 0,
+                    "softmax mass is not finite and positive (status 0x%x)", st);
+    return fail(err, TKH_NON_FINITE, "attention context", 0, 0, 0,
+                "non-finite value in attention context (status 0x%x)", st);
+}
+
 // Completes queued work and turns the status word into an error code.
 uint32_t finish(tkh_context *ctx, tkh_error *err) {
     hipError_t e = hipMemcpyAsync(ctx->status_host, ctx->status_dev, sizeof(uint32_t),
@@ -74,17 +90,7 @@ uint32_t finish(tkh_context *ctx, tkh_error *err) {
     e = tkh_launch_fill_u32(ctx->status_dev, 0, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return device_error(e, "status reset", err);
-    if (st & tkh::ST_SPLIT_TIMEOUT)
-        return fail(err, TKH_DEVICE, "decode splits", 0, 0, 0,
-                    "a decode merge timed out waiting for its key splits (status 0x%x)", st);
-    if (st & tkh::ST_NONFINITE_INPUT)
-        return fail(err, TKH_NON_FINITE, "attention inputs", 0, 0, 0,
-                    "non-finite value in attention inputs or scores (status 0x%x)", st);
-    if (st & tkh::ST_BAD_MASS)
-        return fail(err, TKH_NON_FINITE, "attention probabilities", 0, 0, 0,
-                    "softmax mass is not finite and positive (status 0x%x)", st);
-    return fail(err, TKH_NON_FINITE, "attention context", 0, 0, 0,
-                "non-finite value in attention context (status 0x%x)", st);
+    return status_error(st, err);
 }
 
 uint32_t after_launch(tkh_context *ctx, tkh_error *err) {
@@ -105,6 +111,18 @@ struct Plan {
     float *scores = nullptr;
     float *probs = nullptr;
     const tkh::FusedDecode *fused = nullptr;  // decode with the producer folded in
+};
+
+// A run of problems launched together (a view into a Plan's problems, or a
+// problem held on the caller's stack).
+struct Problems {
+    tkh::Problem *p;
+    size_t n;
+    tkh::Problem *begin() const { return p; }
+    tkh::Problem *end() const { return p + n; }
+    tkh::Problem *data() const { return p; }
+    size_t size() const { return n; }
+    tkh::Problem &operator[](size_t i) const { return p[i]; }
 };
 
 tkh::Problem make_problem(const void *q, float *out, int64_t q_row_stride, int64_t q_pos0,
@@ -210,7 +228,7 @@ tkh::Params base_params(tkh_context *ctx, const Plan &plan) {
 }
 
 // Few query rows per KV head: the streaming decode kernel, one launch.
-uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
+uint32_t launch_decode(tkh_context *ctx, const Plan &plan, Problems group,
                        int rows, tkh_error *err) {
     const int64_t D = plan.head_dim, Hkv = plan.kv_heads;
     const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
@@ -365,7 +383,7 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, std::vector<tkh::Prob
 }
 
 // Many query rows per KV head (bf16/f16): the MFMA flash kernel, one launch.
-uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
+uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
                         tkh_error *err) {
     const int64_t D = plan.head_dim, Hkv = plan.kv_heads, G = plan.query_heads / plan.kv_heads;
     // Eight-wave (256-row) workgroups where the head_dim has them and their row
@@ -422,10 +440,21 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
         }
         return n_all;
     };
+    // The partials of a split launch must also fit the workspace: fewer, longer
+    // splits until they do (a launch without splits writes none).
+    auto partial_bytes = [&](int64_t keys_per_split) {
+        size_t n_slots = 0;
+        for (auto &p : group) {
+            const int64_t n = seg_split_counts(p, keys_per_split);
+            if (n > 1) n_slots += (size_t)(Hkv * p.row_blocks * n);
+        }
+        return n_slots * (size_t)rows_per * (size_t)(D + 2) * sizeof(float);
+    };
     for (;;) {
         int64_t worst = 0;
         for (auto &p : group) worst = std::max<int64_t>(worst, seg_split_counts(p, sk));
-        if (worst <= tkh_prefill_max_splits()) break;
+        const bool fits = worst == 1 || partial_bytes(sk) <= split_region_bytes(ctx);
+        if (worst <= tkh_prefill_max_splits() && (fits || sk >= max_span)) break;
         sk *= 2;
     }
     // Splits of one row block are combined by a second kernel, in merge blocks
@@ -476,7 +505,7 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, std::vector<tkh::Pro
 }
 
 // Launch one group of problems (<= kSlotProblems) through the workspace.
-uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Problem> &group,
+uint32_t launch_group(tkh_context *ctx, const Plan &plan, Problems group,
                       tkh_error *err) {
     const int64_t D = plan.head_dim, Hq = plan.query_heads, Hkv = plan.kv_heads;
     const int64_t G = Hq / Hkv;
@@ -504,9 +533,9 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
         size_t need = 0;
         for (auto &p : group) need += (size_t)p.queries * Hq * (D + 2);
         if (need > ws_floats)
-            return fail(err, TKH_UNSUPPORTED, "workspace", 0, need * 4, ctx->workspace_bytes,
-                        "attention needs %zu workspace bytes, context has %zu", need * 4,
-                        ctx->workspace_bytes);
+            return fail(err, TKH_UNSUPPORTED, "workspace", 0, need * 4, split_region_bytes(ctx),
+                        "attention needs %zu workspace bytes, context has %zu for it", need * 4,
+                        split_region_bytes(ctx));
     }
     int64_t tiles = 0, rows = 0, part_rows = 0;
     for (auto &p : group) {
@@ -555,44 +584,28 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, std::vector<tkh::Probl
     return TKH_OK;
 }
 
-uint32_t run(tkh_context *ctx, Plan &plan, tkh_error *err) {
+// Launch `count` problems in groups of at most kSlotProblems (their planning
+// fields are filled in place).
+uint32_t launch_all(tkh_context *ctx, const Plan &plan, tkh::Problem *probs, size_t count,
+                    tkh_error *err) {
     if (hipSetDevice(ctx->device) != hipSuccess)
         return fail(err, TKH_DEVICE, "device", 0, 0, 0, "hipSetDevice failed");
-    for (size_t i = 0; i < plan.problems.size(); i += kSlotProblems) {
-        size_t n = std::min<size_t>(kSlotProblems, plan.problems.size() - i);
-        std::vector<tkh::Problem> group(plan.problems.begin() + i, plan.problems.begin() + i + n);
-        TRY(launch_group(ctx, plan, group, err));
+    for (size_t i = 0; i < count; i += kSlotProblems) {
+        const size_t n = std::min<size_t>(kSlotProblems, count - i);
+        TRY(launch_group(ctx, plan, Problems{probs + i, n}, err));
     }
+    return TKH_OK;
+}
+
+uint32_t run(tkh_context *ctx, Plan &plan, tkh_error *err) {
+    TRY(launch_all(ctx, plan, plan.problems.data(), plan.problems.size(), err));
     return after_launch(ctx, err);
 }
 
 
-// First visible key (absolute) of a query at `position` (window_attention.rs:105-107).
-uint64_t first_visible(uint64_t key_start, uint64_t position, bool has_window, uint64_t window) {
-    if (!has_window) return key_start;
-    uint64_t lower = position >= window - 1 ? position - (window - 1) : 0;
-    return std::max(key_start, lower);
-}
-
-}  // namespace
-
-extern "C" {
-
-uint32_t tkh_abi_version(void) { return TKH_ABI_VERSION; }
-
-uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, int synchronous,
-                            tkh_context **out, tkh_error *err) {
-    if (!out) return invalid("context output", err);
-    *out = nullptr;
-    int count = 0;
-    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
-        return fail(err, TKH_DEVICE, "device", 0, 0, 0, "no HIP device is available");
-    if (device < 0 || device >= count) return invalid("device ordinal", err);
-    HIP_TRY(hipSetDevice(device), "hipSetDevice");
-    auto *ctx = new tkh_context();
-    ctx->device = device;
-    ctx->synchronous = synchronous != 0;
-    ctx->workspace_bytes = workspace_bytes ? workspace_bytes : (size_t)256 << 20;
+// The planner's settings of a context on `device`: the defaults, each
+// overridable by a TKH_* environment variable, and the device's CU count.
+void init_tuning(tkh_context *ctx, int device) {
     ctx->split_keys_override = env_int("TKH_SPLIT_KEYS", 0);
     ctx->force_generic = env_int("TKH_FORCE_GENERIC", 0);
     ctx->decode_waves = std::min(8, std::max(1, env_int("TKH_DECODE_WAVES", 8)));
@@ -632,6 +645,35 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     // against 256 (128: 7.6 ms, 16.1 us; 32: no better).
     ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 64));
     ctx->prefill_waves = env_int("TKH_PREFILL_WAVES", 0);
+}
+
+// First visible key (absolute) of a query at `position` (window_attention.rs:105-107).
+uint64_t first_visible(uint64_t key_start, uint64_t position, bool has_window, uint64_t window) {
+    if (!has_window) return key_start;
+    uint64_t lower = position >= window - 1 ? position - (window - 1) : 0;
+    return std::max(key_start, lower);
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t tkh_abi_version(void) { return TKH_ABI_VERSION; }
+
+uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, int synchronous,
+                            tkh_context **out, tkh_error *err) {
+    if (!out) return invalid("context output", err);
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(err, TKH_DEVICE, "device", 0, 0, 0, "no HIP device is available");
+    if (device < 0 || device >= count) return invalid("device ordinal", err);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    auto *ctx = new tkh_context();
+    ctx->device = device;
+    ctx->synchronous = synchronous != 0;
+    ctx->workspace_bytes = workspace_bytes ? workspace_bytes : (size_t)256 << 20;
+    init_tuning(ctx, device);
     auto cleanup = [&](hipError_t e, const char *where) {
         tkh_context_destroy(ctx);
         return device_error(e, where, err);
@@ -704,6 +746,49 @@ uint32_t tkh_context_profile_read(tkh_context *ctx, tkh_profile *out, tkh_error 
 
 // ---------------------------------------------------------------- operators
 
+}  // extern "C"
+
+namespace {
+
+// Sizes of an attention_cached call, checked in src/cpu/attention.rs:218-245's
+// order up to the context length.
+struct CachedDims {
+    uint64_t end, q_stride, head_stride;
+};
+uint32_t check_cached(const tkh_cached_shape &s, uint64_t q_len, uint64_t k_len, uint64_t v_len,
+                      uint64_t context_len, CachedDims *d, tkh_error *err) {
+    TRY(nonzero(s.tokens, "tokens", err));
+    TRY(nonzero(s.query_heads, "query_heads", err));
+    TRY(nonzero(s.kv_heads, "kv_heads", err));
+    TRY(nonzero(s.head_dim, "head_dim", err));
+    TRY(nonzero(s.capacity, "cache capacity", err));
+    if (s.query_heads % s.kv_heads != 0) return invalid("query_heads must be divisible by kv_heads", err);
+    TRY(add(s.offset, s.tokens, &d->end, err));
+    if (d->end > s.capacity) return invalid("cache capacity exceeded", err);
+    uint64_t q_count, kv_count;
+    TRY(product(s.query_heads, s.head_dim, &d->q_stride, err));
+    TRY(product(s.tokens, d->q_stride, &q_count, err));
+    TRY(product(s.capacity, s.head_dim, &d->head_stride, err));
+    TRY(product(s.kv_heads, d->head_stride, &kv_count, err));
+    TRY(length("q", q_len, q_count, err));
+    TRY(length("k cache", k_len, kv_count, err));
+    TRY(length("v cache", v_len, kv_count, err));
+    TRY(length("attention context", context_len, q_count, err));
+    return TKH_OK;
+}
+
+void cached_plan(const tkh_cached_shape &s, tkh_dtype dtype, Plan *plan) {
+    plan->dtype = dtype;
+    plan->query_heads = (int64_t)s.query_heads;
+    plan->kv_heads = (int64_t)s.kv_heads;
+    plan->head_dim = (int64_t)s.head_dim;
+    plan->scale = 1.0f / std::sqrt((float)s.head_dim);
+}
+
+}  // namespace
+
+extern "C" {
+
 uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, tkh_dtype dtype,
                               const void *q, uint64_t q_len, const void *k, uint64_t k_len,
                               const void *v, uint64_t v_len, float *context,
@@ -713,41 +798,117 @@ uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, t
     if (!shape) return invalid("shape", err);
     const tkh_cached_shape s = *shape;
     // src/cpu/attention.rs:218-251, in order.
-    TRY(nonzero(s.tokens, "tokens", err));
-    TRY(nonzero(s.query_heads, "query_heads", err));
-    TRY(nonzero(s.kv_heads, "kv_heads", err));
-    TRY(nonzero(s.head_dim, "head_dim", err));
-    TRY(nonzero(s.capacity, "cache capacity", err));
-    if (s.query_heads % s.kv_heads != 0) return invalid("query_heads must be divisible by kv_heads", err);
-    uint64_t end;
-    TRY(add(s.offset, s.tokens, &end, err));
-    if (end > s.capacity) return invalid("cache capacity exceeded", err);
-    uint64_t q_stride, q_count, head_stride, kv_count;
-    TRY(product(s.query_heads, s.head_dim, &q_stride, err));
-    TRY(product(s.tokens, q_stride, &q_count, err));
-    TRY(product(s.capacity, s.head_dim, &head_stride, err));
-    TRY(product(s.kv_heads, head_stride, &kv_count, err));
-    TRY(length("q", q_len, q_count, err));
-    TRY(length("k cache", k_len, kv_count, err));
-    TRY(length("v cache", v_len, kv_count, err));
-    TRY(length("attention context", context_len, q_count, err));
+    CachedDims d;
+    TRY(check_cached(s, q_len, k_len, v_len, context_len, &d, err));
     if (scores) TRY(length("attention scores", scores_len, s.capacity, err));
     if (probabilities) TRY(length("attention probabilities", probabilities_len, s.capacity, err));
     if (s.head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 0, 0, "head_dim above 512");
     if (!ctx) return invalid("context", err);
     Plan plan;
-    plan.dtype = dtype;
-    plan.query_heads = s.query_heads;
-    plan.kv_heads = s.kv_heads;
-    plan.head_dim = s.head_dim;
-    plan.scale = 1.0f / std::sqrt((float)s.head_dim);
+    cached_plan(s, dtype, &plan);
     plan.diag_mode = (scores || probabilities) ? 2 : 0;
     plan.scores = scores;
     plan.probs = probabilities;
-    tkh::Problem p = make_problem(q, context, q_stride, s.offset, 0, end, s.tokens);
-    add_segment(p, k, v, head_stride, s.head_dim, end, 0);
+    tkh::Problem p = make_problem(q, context, d.q_stride, s.offset, 0, d.end, s.tokens);
+    add_segment(p, k, v, d.head_stride, s.head_dim, d.end, 0);
     plan.problems.push_back(p);
     return run(ctx, plan, err);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- fixed scratch
+
+namespace {
+
+// The device memory of tkh_attention_cached_static: the status word (the first
+// 256 bytes), then a workspace laid out as a context's (split-K partials of
+// the prefill and generic kernels, then the decode kernel's completion flags
+// and partials).  Each GPU the library runs on holds its own copy, at its own
+// address, until the process ends.
+constexpr size_t kStaticStatusBytes = 256;
+__device__ __align__(256) uint8_t scratch[TKH_STATIC_SCRATCH_BYTES];
+
+constexpr int kStaticMaxDevices = 64;
+struct StaticDevice {
+    bool ready = false;
+    uint8_t *ptr = nullptr;  // this device's address of `scratch` (never the symbol itself)
+    tkh_context ctx;         // planner settings and decode epoch; views into ptr, owns nothing
+};
+std::mutex g_static_mutex;
+StaticDevice g_static[kStaticMaxDevices];
+
+// Once per device, with that device current: the array's address, the
+// planner settings, and a cleared array (status 0; decode flags 0, which no
+// launch epoch equals).
+uint32_t static_device(int device, hipStream_t stream, StaticDevice **out, tkh_error *err) {
+    if (device < 0 || device >= kStaticMaxDevices) return invalid("device ordinal", err);
+    StaticDevice &sd = g_static[device];
+    if (!sd.ready) {
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || device >= count)
+            return fail(err, TKH_DEVICE, "device", 0, 0, 0, "HIP device %d is not available", device);
+        HIP_TRY(hipSetDevice(device), "hipSetDevice");
+        void *ptr = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "scratch address");
+        sd.ptr = static_cast<uint8_t *>(ptr);
+        tkh_context &c = sd.ctx;
+        c.device = device;
+        c.synchronous = false;
+        c.workspace = sd.ptr + kStaticStatusBytes;
+        c.workspace_bytes = TKH_STATIC_SCRATCH_BYTES - kStaticStatusBytes;
+        init_tuning(&c, device);
+        HIP_TRY(tkh_launch_zero_u64(reinterpret_cast<uint64_t *>(sd.ptr),
+                                    (int64_t)(TKH_STATIC_SCRATCH_BYTES / sizeof(uint64_t)), stream),
+                "scratch clear");
+        sd.ready = true;
+    }
+    *out = &sd;
+    return TKH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t tkh_attention_cached_static(int device, void *stream, const tkh_cached_shape *shape,
+                                     tkh_dtype dtype, const void *q, uint64_t q_len, const void *k,
+                                     uint64_t k_len, const void *v, uint64_t v_len, float *context,
+                                     uint64_t context_len, uint32_t *status, tkh_error *err) {
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    if (!shape) return invalid("shape", err);
+    const tkh_cached_shape s = *shape;
+    CachedDims d;
+    TRY(check_cached(s, q_len, k_len, v_len, context_len, &d, err));
+    if (s.head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 0, 0, "head_dim above 512");
+    std::lock_guard<std::mutex> lock(g_static_mutex);
+    StaticDevice *sd = nullptr;
+    TRY(static_device(device, reinterpret_cast<hipStream_t>(stream), &sd, err));
+    tkh_context &c = sd->ctx;
+    c.stream = reinterpret_cast<hipStream_t>(stream);
+    c.status_dev = status ? status : reinterpret_cast<uint32_t *>(sd->ptr);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    if (!status) HIP_TRY(tkh_launch_fill_u32(c.status_dev, 0, c.stream), "status clear");
+    Plan plan;
+    cached_plan(s, dtype, &plan);
+    tkh::Problem p = make_problem(q, context, d.q_stride, s.offset, 0, d.end, s.tokens);
+    add_segment(p, k, v, d.head_stride, s.head_dim, d.end, 0);
+    tkh_error launch_err{};
+    const uint32_t rc = launch_all(&c, plan, &p, 1, &launch_err);
+    if (rc == TKH_UNSUPPORTED && std::strcmp(launch_err.tensor, "workspace") == 0)
+        return fail(err, TKH_UNSUPPORTED, "scratch", 0, launch_err.actual, launch_err.expected,
+                    "the call needs %llu bytes of split partials, the fixed scratch has %llu for them",
+                    (unsigned long long)launch_err.expected, (unsigned long long)launch_err.actual);
+    if (rc != TKH_OK) {
+        if (err) *err = launch_err;
+        return rc;
+    }
+    if (status) return ok(err);
+    uint32_t word = 0;
+    hipError_t e = hipMemcpyAsync(&word, c.status_dev, sizeof word, hipMemcpyDeviceToHost, c.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c.stream);
+    if (e != hipSuccess) return device_error(e, "synchronize", err);
+    return word ? status_error(word, err) : ok(err);
 }
 
 }  // extern "C"

@@ -199,6 +199,25 @@ def attention_cached(ctx: Context, q, k, v, context, scores, probabilities,
     _check(rc, err)
 
 
+def attention_cached_static(device: int, q, k, v, context, shape: CachedAttentionShape,
+                            stream: Optional[torch.cuda.Stream] = None,
+                            status: Optional[torch.Tensor] = None):
+    """attention_cached without a context or any allocation: split-K partials in
+    the library's fixed per-GPU scratch (tkh_attention_cached_static).  `status`:
+    an int32 device tensor of one element the kernels OR their status bits into
+    (the call then returns once queued), or None to wait and raise on failure."""
+    err = _lib.Error()
+    s = _lib.CachedShape(shape.tokens, shape.query_heads, shape.kv_heads, shape.head_dim,
+                         shape.capacity, shape.offset)
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    st = ctypes.cast(status.data_ptr(), ctypes.POINTER(ctypes.c_uint32)) if status is not None else None
+    rc = _lib.load().tkh_attention_cached_static(
+        device, ctypes.c_void_p(stream.cuda_stream), ctypes.byref(s), dtype_of(q, k, v), _ptr(q),
+        _n(q), _ptr(k), _n(k), _ptr(v), _n(v), _fptr(context), _n(context), st, ctypes.byref(err))
+    _check(rc, err)
+
+
 def attention(ctx: Context, q, k, v, context, scores, probabilities, shape: AttentionShape):
     """Full-prefix causal GQA with token-major K/V (reference: attention)."""
     err = _lib.Error()
