@@ -23,7 +23,12 @@
  *    unspecified and must be discarded, as the reference discards partial
  *    output after an arithmetic failure (src/cpu/mod.rs:5-7).  Shape and
  *    length errors are reported before any launch and leave every output
- *    untouched.
+ *    untouched.  One value-range limit is found the same way: the bf16/f16
+ *    chunk kernel takes bf16 V values as f16 scaled by 2^-8, so a finite bf16
+ *    V value of magnitude 2^24 or more that a chunk attends to is reported as
+ *    TKH_UNSUPPORTED (tensor "attention value"), with the context
+ *    unspecified; single-token decode and FP32 calls compute with any finite
+ *    value.
  *  - Tensors passed to operators are device pointers (HBM).  Q/context use
  *    [tokens, query_heads, head_dim]; K/V use the reference's head-major
  *    [kv_heads, capacity, head_dim] layout (strides [capacity*D, D, 1]).
@@ -135,8 +140,9 @@ uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, t
  *  - status != NULL: a device word owned by the caller; the kernels OR their
  *    status bits into it and the call returns once the work is queued.  The
  *    word is never cleared here.  Nonzero means the results are invalid:
- *    bit 3 (8) a decode merge timed out (TKH_DEVICE), any other bit a
- *    non-finite input or result (TKH_NON_FINITE).
+ *    bit 3 (8) a decode merge timed out (TKH_DEVICE), bit 4 (16) without
+ *    bit 0 a bf16 V value beyond the chunk kernel's range (TKH_UNSUPPORTED),
+ *    any other bit a non-finite input or result (TKH_NON_FINITE).
  *  - status == NULL: the call waits for the stream and reports as a
  *    synchronous context does.
  * Every call on one GPU shares that GPU's array and keeps its last contents:

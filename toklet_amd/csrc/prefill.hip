@@ -387,6 +387,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     const float tmul = CAP ? 1.0f : p.scale_log2;  // t units -> log2 units
     const float slack = RESCALE_SLACK / tmul;      // in t units
     float m_thr = NEG_INF;                         // rescale when a tile maximum exceeds this
+    // A row maximum of 2^10 or more in log2 units (natural-log logits above
+    // about 700) makes the rounding of m * tmul worth a large part of an
+    // exponent, so 2^(t * tmul - round(m * tmul)) would lose the mass.  A wave
+    // holding such a row subtracts the maximum in raw units first (wave-uniform,
+    // decided whenever a maximum moves).
+    bool huge = false;
 
     // ---- K/V tiles: PF_KT keys each, issued into an NS-stage LDS ring.
     const int prow = uniform32((int)(pr->seg[seg].row_stride * 2));  // bytes between keys
@@ -548,8 +554,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                         m_thr = m_new == NEG_INF ? NEG_INF : m_new + slack;
                     }
                     rescale = true;
+                    if constexpr (!CAP)
+                        huge = __ballot(m_run != NEG_INF && fabsf(m_run * tmul) >= 1024.0f) != 0;
                 }
                 nbase = m_run == NEG_INF ? 0.0f : -m_run * tmul;
+                if constexpr (!CAP) {
+                    if (huge) {
+                        const float mr = m_run == NEG_INF ? 0.0f : m_run;
+                        for (int i = 0; i < 16; ++i) st[i] -= mr;
+                        nbase = 0.0f;
+                    }
+                }
             }
             // First half of tile t's probabilities (tile t - 1's are still being read).
             for (int i = 0; i < 4; ++i) {
@@ -659,8 +674,40 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         const uint32_t a0 = pr32[0], a1 = pr32[1];
         l_run = __builtin_bit_cast(float, a0) + __builtin_bit_cast(float, a1);
     }
+    bool bad_acc = false;
     for (int mb = 0; mb < MB; ++mb)
-        for (int i = 0; i < 16; ++i) bad |= !is_finite_f(acc[mb][i]);
+        for (int i = 0; i < 16; ++i) bad_acc |= !is_finite_f(acc[mb][i]);
+    // bf16: the P.V products took V as f16 scaled by 2^-8, which overflows for
+    // finite values of magnitude 2^24 or more.  Only a wave whose context is
+    // not finite while its scores were reads the workgroup's V rows again, to
+    // tell a non-finite input (ST_NONFINITE_INPUT) from such a value, which is
+    // reported as out of this kernel's range (ST_V_RANGE) instead.
+    bool v_range = false;
+    if constexpr (VCONV) {
+        if (__ballot(bad_acc && !bad) != 0) {
+            constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
+            constexpr int RPI = 64 / CPR;    // rows per wave iteration
+            const uint8_t *vrows = reinterpret_cast<const uint8_t *>(pr->seg[seg].v) + first * 2;
+            bool nonfinite = false, big = false;
+            for (int r0 = 0; r0 < nkeys; r0 += RPI) {
+                const int r = r0 + lane / CPR;
+                if (r < nkeys) {
+                    const u32x4 w = *gload_ptr<u32x4>(vrows + (int64_t)r * prow + 16 * (lane % CPR));
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t x = w[e];
+                        const uint32_t lo = x & 0x7fffu, hi = (x >> 16) & 0x7fffu;
+                        nonfinite |= lo >= 0x7f80u || hi >= 0x7f80u;  // bf16 inf / NaN
+                        big |= lo >= 0x4b80u || hi >= 0x4b80u;        // |v| >= 2^24
+                    }
+                }
+            }
+            if (__ballot(nonfinite) == 0 && __ballot(big) != 0) {
+                v_range = true;
+                bad_acc = false;
+            }
+        }
+    }
+    bad |= bad_acc;
 
     // O^T lane layout: row j, features 32 mb + 8 q + 4 h + r (register 4 q + r).
     const bool single = pr->splits == 1;
@@ -684,13 +731,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
         raise_status(p, bad, ST_NONFINITE_INPUT);
         raise_status(p, bad_mass, ST_BAD_MASS);
-        raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
+        raise_status(p, bad_out && !v_range, ST_NONFINITE_OUTPUT);
+        raise_status(p, v_range, ST_V_RANGE);
         return;
     }
 
     // ---- split-K partial: slot (row block, split) holds ROWS x (D + 2)
     // floats, merged by attn_prefill_merge after this kernel.
     raise_status(p, bad, ST_NONFINITE_INPUT);
+    raise_status(p, v_range, ST_V_RANGE);
     const int64_t group = (int64_t)kvh * pr->row_blocks + rb;
     const int64_t slot = pr->slot_base + group * pr->splits + split;
     float *po = p.part_o + (slot * ROWS + wave * 32 + j) * D;
