@@ -215,14 +215,18 @@ def bench_decode_batch(torch, ops, ctx, steps, warmup, *, batch, lmin, lmax, dty
         offsets.append(acc)
         acc += hkv * c * d
     gd = torch.Generator(device="cuda").manual_seed(seed)
-    scales = torch.empty(batch, device="cuda").uniform_(0.5, 2.0, generator=gd)
+    # One scale per (session, KV head), applied to that head's K and V rows and
+    # to the query heads of its group.
+    scales = torch.empty(batch, hkv, device="cuda").uniform_(0.5, 2.0, generator=gd)
     kpool = torch.empty(acc, dtype=dtype, device="cuda")
     vpool = torch.empty(acc, dtype=dtype, device="cuda")
     for b in range(batch):
         n = hkv * caps[b] * d
-        kpool[offsets[b]:offsets[b] + n] = (torch.randn(n, generator=gd, device="cuda") * scales[b]).to(dtype)
-        vpool[offsets[b]:offsets[b] + n] = (torch.randn(n, generator=gd, device="cuda") * scales[b]).to(dtype)
-    q = (torch.randn(batch, hq, d, generator=gd, device="cuda") * scales[:, None, None]).to(dtype)
+        for pool in (kpool, vpool):
+            x = torch.randn(hkv, caps[b] * d, generator=gd, device="cuda") * scales[b][:, None]
+            pool[offsets[b]:offsets[b] + n] = x.reshape(-1).to(dtype)
+    q = (torch.randn(batch, hq, d, generator=gd, device="cuda") *
+         scales.repeat_interleave(hq // hkv, dim=1)[:, :, None]).to(dtype)
     out = torch.zeros(batch * hq * d, dtype=torch.float32, device="cuda")
     head_strides = [c * d for c in caps]
     scale = 1.0 / math.sqrt(d)
