@@ -215,6 +215,22 @@ uint32_t tkh_span_attention(tkh_context *ctx, const tkh_span_shape *shape, tkh_d
                             uint64_t scores_len, float *probabilities, uint64_t probabilities_len,
                             tkh_error *err);
 
+/* The step after attention, for token identity without host logits: the
+ * FP32 o-projection of cpu::matmul (src/cpu/mod.rs:140-247, no bias) followed
+ * by sampling::greedy (src/sampling.rs:5-18) on every row, in one call (no
+ * single reference call does both).  logits[r, v] = sum_d context[r, d] *
+ * weights[v, d], each product and each addition rounded in feature order as
+ * the reference's loop rounds them, so the logits are the reference's bit for
+ * bit; tokens[r] is the lowest id of row r's largest logit (+0 and -0 tie).
+ * context: [rows, hidden], weights: [vocab, hidden], logits: optional (NULL)
+ * [rows, vocab], all FP32; tokens: [rows] uint32; device pointers.  The
+ * checks follow matmul's order, then greedy's vocabulary bound; a non-finite
+ * logit (from any non-finite input) is TKH_NON_FINITE. */
+uint32_t tkh_project_greedy(tkh_context *ctx, uint64_t rows, uint64_t hidden, uint64_t vocab,
+                            const float *context, uint64_t context_len, const float *weights,
+                            uint64_t weights_len, float *logits, uint64_t logits_len,
+                            uint32_t *tokens, uint64_t tokens_len, tkh_error *err);
+
 /* Replaces cpu::logit_softcap (src/cpu/softcap.rs:16-29) on a device buffer. */
 uint32_t tkh_logit_softcap(tkh_context *ctx, float *logits, uint64_t len, float cap,
                            tkh_error *err);

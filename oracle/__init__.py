@@ -290,6 +290,21 @@ def copy_runs(capacity, offset, tokens, sliding):
     return [(out[0], out[1], out[2]), (out[3], out[4], out[5])]
 
 
+def matmul(x, weights, tokens, in_features, out_features, bias=None, out=None):
+    """FP32 projection [tokens, in] x [out, in]^T (+ bias) (src/cpu/mod.rs:183-247)."""
+    x, w = _f32(x), _f32(weights)
+    b = _f32(bias) if bias is not None else None
+    if out is None:
+        out = np.zeros(tokens * out_features, np.float32)
+    err = _Error()
+    rc = lib().orc_matmul(_ptr(x), _size(x.size), _ptr(w), _size(w.size),
+                          _ptr(b) if b is not None else None, _size(b.size if b is not None else 0),
+                          _ptr(out), _size(out.size), _size(tokens), _size(in_features),
+                          _size(out_features), ctypes.byref(err))
+    _check(rc, err)
+    return out
+
+
 def greedy(logits):
     x = _f32(logits)
     token = ctypes.c_uint32()

@@ -650,6 +650,42 @@ void orc_copy_runs(size_t capacity, size_t offset, size_t tokens, int sliding, s
 
 /* ---- greedy argmax: src/sampling.rs:5-18 ---- */
 
+/* ---- matmul: src/cpu/mod.rs:140-158, 183-247 (the FP32 path) ---- */
+
+uint32_t orc_matmul(const float *input, size_t input_len, const float *weights,
+                    size_t weights_len, const float *bias, size_t bias_len, float *output,
+                    size_t output_len, size_t tokens, size_t in_features, size_t out_features,
+                    orc_error *err) {
+    TRY(nonzero(tokens, "tokens", err));
+    TRY(nonzero(in_features, "in_features", err));
+    TRY(nonzero(out_features, "out_features", err));
+    size_t count;
+    TRY(product(tokens, in_features, &count, err));
+    TRY(length("input", input_len, count, err));
+    TRY(product(out_features, in_features, &count, err));
+    TRY(length("weights", weights_len, count, err));
+    TRY(product(tokens, out_features, &count, err));
+    TRY(length("output", output_len, count, err));
+    if (bias) {
+        TRY(length("bias", bias_len, out_features, err));
+        TRY(finite("bias", bias, bias_len, err));
+    }
+    TRY(finite("input", input, input_len, err));
+    TRY(finite("weights", weights, weights_len, err));
+    for (size_t token = 0; token < tokens; ++token) {
+        const float *row = input + token * in_features;
+        for (size_t feature = 0; feature < out_features; ++feature) {
+            const float *w = weights + feature * in_features;
+            float sum = 0.0f;
+            for (size_t i = 0; i < in_features; ++i) sum += row[i] * w[i];
+            if (bias) sum += bias[feature];
+            if (!isfinite(sum)) return non_finite("output", token * out_features + feature, err);
+            output[token * out_features + feature] = sum;
+        }
+    }
+    return ok(err);
+}
+
 uint32_t orc_greedy(const float *logits, size_t len, uint32_t *token, orc_error *err) {
     TRY(nonzero(len, "vocabulary", err));
     if (len - 1 > (size_t)UINT32_MAX) return invalid("vocabulary IDs must fit u32", err);

@@ -136,6 +136,10 @@ void orc_old_spans(size_t capacity, size_t offset, int has_window, size_t window
 void orc_copy_runs(size_t capacity, size_t offset, size_t tokens, int sliding, size_t out[6]);
 
 /* Greedy argmax with the lowest index on ties (src/sampling.rs:5-18). */
+uint32_t orc_matmul(const float *input, size_t input_len, const float *weights,
+                    size_t weights_len, const float *bias, size_t bias_len, float *output,
+                    size_t output_len, size_t tokens, size_t in_features, size_t out_features,
+                    orc_error *err);
 uint32_t orc_greedy(const float *logits, size_t len, uint32_t *token, orc_error *err);
 
 #ifdef __cplusplus

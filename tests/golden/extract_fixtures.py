@@ -20,6 +20,8 @@ Fixture sets taken (all used by the reference's own attention tests):
   qwen3-attention-inputs-v1  src/metal/compensated_attention.rs:465-561 (inputs only)
   gemma-rotary-v1            src/cpu/proportional_rotary/tests.rs:34-71
   tiny-v1 rmsnorm arrays     tests/cpu_reductions.rs:16-62, 140-175 (-> tiny_v1_norms)
+  tiny-v1 linear + greedy    tests/cpu_linear.rs:59-165, tests/cpu_decoder.rs:170-192
+                             (-> tiny_v1_linear)
   gemma-reference-attention-v1
                              tools/reference/test_gemma_reference_attention.py:17-42: the
                              frozen outputs of both contracts; the inputs are rebuilt from the
@@ -141,6 +143,33 @@ def tiny_norms(ref: str, out: str):
     json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
 
 
+def tiny_linear(ref: str, out: str):
+    """The arrays the reference's matmul and greedy tests read from tiny-v1: the
+    manual 2x3 projection, every layer's projections with their inputs and
+    weights (tests/cpu_linear.rs:59-165), and the four-step greedy trace's
+    logits and tokens (tests/cpu_decoder.rs:170-192)."""
+    root = os.path.join(ref, "tests", "fixtures", "tiny-v1")
+    manifest = json.load(open(os.path.join(root, "manifest.json")))
+    names = ["manual.inputs", "manual.weight", "manual.bias", "manual.output", "greedy.tokens"]
+    names += [f"greedy.step_{i}.logits" for i in range(4)]
+    for layer in range(manifest["model"]["num_layers"]):
+        for proj in ("q", "k", "v", "o", "gate", "up", "down"):
+            names.append(f"weights.layers.{layer}.{proj}_proj.weight")
+            if proj in ("q", "k", "v"):
+                names.append(f"weights.layers.{layer}.{proj}_proj.bias")
+    for case in manifest["cases"]:
+        names.append(f"cases.{case}.tokens")
+        for layer in range(manifest["model"]["num_layers"]):
+            names += [f"cases.{case}.layers.{layer}.{k}" for k in
+                      ("input_norm", "q_projection", "k_projection", "v_projection",
+                       "attention_context", "attention_projection", "post_attention_norm",
+                       "gate_projection", "up_projection", "gated", "down_projection")]
+    arrays = {n: read_array(root, manifest["arrays"][n]) for n in names}
+    meta = {"cases": manifest["cases"], "model": manifest["model"], "greedy": manifest["greedy"]}
+    np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
+
+
 def reference_attention(ref: str, out: str):
     """gemma-reference-attention-v1: the frozen scores, probabilities and contexts
     of every case under both contracts (FP64 `math`, staged `staged_fp32`), each
@@ -177,6 +206,7 @@ def main(ref: str):
     qwen3_inputs(ref, "qwen3_attention_inputs_v1")
     math_json(ref, "gemma-rotary-v1", "gemma_rotary_v1")
     tiny_norms(ref, "tiny_v1_norms")
+    tiny_linear(ref, "tiny_v1_linear")
     reference_attention(ref, "gemma_reference_attention_v1")
 
 

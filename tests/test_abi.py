@@ -136,6 +136,30 @@ def test_softcap_validation(lib):
         assert lib.tkh_logit_softcap(None, None, 4, cap, ctypes.byref(err)) == _lib.INVALID_PARAMETER
 
 
+def test_project_greedy_validation_order(lib):
+    """matmul's checks in order (src/cpu/mod.rs:192-201), then greedy's vocabulary
+    bound (src/sampling.rs:7-9), all before any launch."""
+    from toklet_amd import _lib
+
+    err = _lib.Error()
+
+    def call(rows, hidden, vocab, ctx_len, w_len, logits_len, tok_len, logits=False):
+        lg = ctypes.cast(1, _lib.fptr) if logits else None
+        return lib.tkh_project_greedy(None, rows, hidden, vocab, None, ctx_len, None, w_len, lg,
+                                      logits_len, None, tok_len, ctypes.byref(err))
+
+    assert call(0, 4, 8, 0, 32, 0, 0) == _lib.ZERO_DIMENSION and err.tensor == b"tokens"
+    assert call(2, 0, 8, 0, 0, 0, 2) == _lib.ZERO_DIMENSION and err.tensor == b"in_features"
+    assert call(2, 4, 0, 8, 0, 0, 2) == _lib.ZERO_DIMENSION and err.tensor == b"out_features"
+    assert call(2, 4, 8, 7, 32, 0, 2) == _lib.LENGTH and err.tensor == b"input"
+    assert call(2, 4, 8, 8, 31, 0, 2) == _lib.LENGTH and err.tensor == b"weights"
+    assert call(2, 4, 8, 8, 32, 15, 2, logits=True) == _lib.LENGTH and err.tensor == b"output"
+    assert call(2, 4, 8, 8, 32, 0, 3) == _lib.LENGTH and err.tensor == b"tokens"
+    assert call(1, 1, 2 ** 33, 1, 2 ** 33, 0, 1) == _lib.INVALID_PARAMETER
+    assert call(2 ** 40, 2 ** 30, 8, 0, 0, 0, 0) == _lib.SIZE_OVERFLOW
+    assert call(2, 4, 8, 8, 32, 16, 2, logits=True) == _lib.INVALID_PARAMETER  # no context
+
+
 def test_kv_planned_bytes_mirror_kv_owner(lib):
     """capacity::KvOwner::at_capacity (src/capacity.rs:49-80) with a bf16 storage kind."""
     from toklet_amd import _lib

@@ -20,7 +20,7 @@ import math
 import numpy as np
 import pytest
 
-from gpu_util import TOL_HALF, assert_tokens_agree, dev, host, log, max_err, stored
+from gpu_util import TOL_F32, TOL_HALF, assert_tokens_agree, dev, host, log, max_err, stored
 
 pytestmark = pytest.mark.gpu
 
@@ -55,6 +55,72 @@ def _produce(orc, x, w, rows, heads, D, position, theta, dt):
     """Oracle producer (rmsnorm when w is given, split-half rotary), rounded to the cache dtype."""
     y = orc.rmsnorm(x.reshape(-1), w, rows * heads, D, 1e-6) if w is not None else x.reshape(-1)
     return stored(orc.rotary(y, rows, heads, D, position, theta), dt).reshape(rows, heads, D)
+
+
+def _projection_weights(torch, vocab, hidden, seed):
+    """A seeded N(0, 1) FP32 output projection [vocab, hidden], on the device and the host."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randn(vocab, hidden, generator=g, device="cuda")
+    return w, w.cpu().numpy()
+
+
+def _check_projection(torch, ops, orc, ctx, got_rows, ref_rows, w_dev, w_host, label):
+    """Device o-projection + greedy of the device contexts: logits bit-exact with the
+    oracle's FP32 matmul and tokens equal to its greedy pick; against the tokens of
+    the oracle's own contexts, identical except where the two contexts' difference
+    can reach a tie."""
+    rows, hidden = got_rows.shape
+    vocab = w_host.shape[0]
+    c = torch.from_numpy(np.ascontiguousarray(got_rows)).cuda()
+    tokens = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    logits = torch.full((rows, vocab), np.nan, dtype=torch.float32, device="cuda")
+    ops.project_greedy(ctx, c, w_dev, tokens, logits)
+    tok = tokens.cpu().numpy().view(np.uint32)
+    lg = host(logits)
+    for r in range(rows):
+        ref = orc.matmul(got_rows[r], w_host, 1, hidden, vocab)
+        assert np.array_equal(lg[r].view(np.uint32), ref.view(np.uint32)), f"{label} row {r} logits"
+        assert tok[r] == orc.greedy(ref), f"{label} row {r} token"
+    ties = assert_tokens_agree(got_rows, ref_rows, w_host)
+    log(f"{label}: {rows} rows projected onto {vocab} ids on the device, logits bit-exact, "
+        f"tokens identical; against the oracle's contexts {ties} ties")
+
+
+def test_configs0_fp32_session_and_projection_full_size(torch_mod, ops, sess_mod, orc):
+    """Qwen2.5-0.5B-shaped FP32 attention (14/2/64, rotary 1e6, scale 1/8),
+    a 128-token prompt then 32 decode steps, and the greedy token of every row over a
+    seeded 896 x 151936 projection on the device."""
+    torch = torch_mod
+    rng = np.random.default_rng(100)
+    hq, hkv, D, prompt, steps = 14, 2, 64, 128, 32
+    total = prompt + steps
+    qp = rng.standard_normal((total, hq, D)).astype(np.float32)
+    kp = rng.standard_normal((total, hkv, D)).astype(np.float32)
+    vp = rng.standard_normal((total, hkv, D)).astype(np.float32)
+    ctx = ops.Context(0)
+    out = torch.full((total, hq * D), np.nan, dtype=torch.float32, device="cuda")
+    s = sess_mod.Session(ctx, sess_mod.Options(capacity=total, prefill_chunk_size=128,
+                                               vocab_size=151936, layers=1, query_heads=hq,
+                                               kv_heads=hkv, head_dim=D, storage="f32", theta=1e6))
+    io = [sess_mod.LayerIo(_t(torch, qp), _t(torch, kp), _t(torch, vp), out)]
+    s.set_tokens([5] * prompt)
+    assert s.evaluate(io) == prompt
+    s.append([6] * steps)
+    assert s.evaluate(io, chunk_limit=1) == steps
+    got = host(out)
+    q = _produce(orc, qp, None, total, hq, D, 0, 1e6, "f32")
+    k = _produce(orc, kp, None, total, hkv, D, 0, 1e6, "f32")
+    ref, _, _ = orc.attention(q.reshape(-1), k.reshape(-1), vp.reshape(-1), total, hq, hkv, D)
+    ref = ref.reshape(total, hq * D)
+    err = max_err(got, ref)
+    log(f"configs[0] FP32 session: {total} rows, max abs error {err:.3e}")
+    assert err <= TOL_F32
+    w_dev, w_host = _projection_weights(torch, 151936, hq * D, 100)
+    sample = [0, 63, 127] + list(range(prompt, total))
+    _check_projection(torch, ops, orc, ctx, got[sample], ref[sample], w_dev, w_host,
+                      "configs[0] prompt rows 0/63/127 and all 32 decode steps")
+    s.close()
+    ctx.close()
 
 
 def test_configs1_qwen3_session_full_size(torch_mod, ops, sess_mod, orc):
@@ -96,6 +162,11 @@ def test_configs1_qwen3_session_full_size(torch_mod, ops, sess_mod, orc):
     log(f"configs[1] session: {len(rows)} rows (every chunk's first, middle and last, decode "
         f"steps 1, 2, 128, 256), max abs error {worst:.3e}, greedy ties {ties}")
     assert worst <= TOL_HALF
+    del w
+    w_dev, w_host = _projection_weights(torch, 151936, hq * D, 101)
+    decode = [i for i, p in enumerate(rows) if p >= prompt]
+    _check_projection(torch, ops, orc, ctx, np.stack(gots)[decode], np.stack(refs)[decode], w_dev,
+                      w_host, "configs[1] decode steps 1, 2, 128, 256")
     s.close()
     ctx.close()
 

@@ -460,8 +460,62 @@ def test_attention_on_half_storage_matches_fp16_fixture(orc):
 def test_greedy_lowest_index_on_ties(orc):
     assert orc.greedy([1.0, 3.0, 3.0, 2.0]) == 1
     assert orc.greedy([-1.0]) == 0
+    assert orc.greedy([-0.0, 0.0]) == 0 and orc.greedy([-1.0, 0.0, -0.0]) == 1  # zeros tie
     with pytest.raises(orc.OracleError):
         orc.greedy([1.0, float("nan")])
+    with pytest.raises(orc.OracleError):
+        orc.greedy([])
+
+
+# ---- tiny-v1 linear projections and greedy trace (tests/cpu_linear.rs, tests/cpu_decoder.rs) ----
+
+def test_matmul_manual_known_answers(orc):
+    """tests/cpu_linear.rs:59-72: the 2x3 manual projection with and without bias."""
+    g = Golden("tiny_v1_linear")
+    x, w, b = g.arrays["manual.inputs"], g.arrays["manual.weight"], g.arrays["manual.bias"]
+    assert orc.matmul(x, w, 2, 3, 2, bias=b).tolist() == [-3.75, 14.5, -2.75, 5.0]
+    assert g.arrays["manual.output"].reshape(-1).tolist() == [-3.75, 14.5, -2.75, 5.0]
+    assert orc.matmul(x[:1], w, 1, 3, 2).tolist() == [-4.0, 15.0]
+    with pytest.raises(orc.OracleError) as e:
+        orc.matmul([1.0, 1.0, 1.0], [1.0, np.nan, 1.0], 1, 3, 1)
+    assert e.value.code == orc.NON_FINITE
+    with pytest.raises(orc.OracleError) as e:
+        orc.matmul([np.finfo(np.float32).max], [2.0], 1, 1, 1)
+    assert (e.value.code, e.value.tensor) == (orc.NON_FINITE, "output")
+
+
+def test_matmul_matches_every_tiny_projection(orc):
+    """tests/cpu_linear.rs:75-165: q/k/v (with bias), o (the attention context's
+    projection), gate, up and down of every case and layer."""
+    g = Golden("tiny_v1_linear")
+    checked = 0
+    for case in TINY_CASES:
+        tokens = len(g.arrays[f"cases.{case}.tokens"])
+        for layer in range(2):
+            pre, wp = f"cases.{case}.layers.{layer}", f"weights.layers.{layer}"
+            for name, src, dst, bias in (("q", "input_norm", "q_projection", True),
+                                         ("k", "input_norm", "k_projection", True),
+                                         ("v", "input_norm", "v_projection", True),
+                                         ("o", "attention_context", "attention_projection", False),
+                                         ("gate", "post_attention_norm", "gate_projection", False),
+                                         ("up", "post_attention_norm", "up_projection", False),
+                                         ("down", "gated", "down_projection", False)):
+                w = g.arrays[f"{wp}.{name}_proj.weight"]
+                b = g.arrays[f"{wp}.{name}_proj.bias"] if bias else None
+                out = orc.matmul(g.arrays[f"{pre}.{src}"].reshape(-1), w, tokens, w.shape[1],
+                                 w.shape[0], bias=b)
+                close(out, g.arrays[f"{pre}.{dst}"])
+                checked += 1
+    assert checked == 70
+
+
+def test_greedy_matches_tiny_trace(orc):
+    """tests/cpu_decoder.rs:170-192: each step's frozen logits choose the frozen token."""
+    g = Golden("tiny_v1_linear")
+    expected = g.meta["greedy"]["generated_tokens"]
+    assert g.arrays["greedy.tokens"].tolist() == expected
+    for step, token in enumerate(expected):
+        assert orc.greedy(g.arrays[f"greedy.step_{step}.logits"]) == token
 
 
 def test_rmsnorm_closed_form(orc):

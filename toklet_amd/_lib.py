@@ -117,6 +117,8 @@ SIGNATURES = {
                                    fptr, u64, fptr, u64, fptr, u64, E]),
     "tkh_span_attention": (u32, [vp, P(SpanShape), ctypes.c_int, vp, u64, P(Segment), fptr, u64,
                                  fptr, u64, fptr, u64, E]),
+    "tkh_project_greedy": (u32, [vp, u64, u64, u64, fptr, u64, fptr, u64, fptr, u64, P(u32), u64,
+                                 E]),
     "tkh_logit_softcap": (u32, [vp, fptr, u64, f32, E]),
     "tkh_decode_batch": (u32, [vp, u64, u64, u64, u64, ctypes.c_int, vp, vp, vp, P(u64), P(u64),
                                P(u64), f32, fptr, E]),

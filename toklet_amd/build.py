@@ -23,7 +23,7 @@ LIB = os.path.join(HERE, "libtokhip.so")
 # they compile in parallel; the largest units are listed first.
 DECODE_UNITS = [f"decode_{dt}_{d}.hip" for dt in ("bf16", "f16", "f32") for d in (128, 64, 256)]
 SOURCES = DECODE_UNITS + ["prefill.hip", "decode.hip", "api.cpp", "session.cpp", "attention.hip",
-                          "kv.hip", "produce.hip"]
+                          "kv.hip", "produce.hip", "project.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

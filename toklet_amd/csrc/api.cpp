@@ -55,6 +55,9 @@ extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int he
 extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int want);
 extern "C" int tkh_decode_max_waves(int dtype, int head_dim, int rows);
 extern "C" int tkh_decode_max_splits(void);
+extern "C" int tkh_project_vocab_per_block(void);
+extern "C" hipError_t tkh_launch_project(const tkh::ProjectParams *p, hipStream_t stream,
+                                         hipEvent_t start, hipEvent_t stop);
 extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int head_dim, int rows,
                                         int keys_per_lane, int waves, int64_t groups, int fused,
                                         hipStream_t stream, hipEvent_t start, hipEvent_t stop);
@@ -78,6 +81,9 @@ uint32_t status_error(uint32_t st, tkh_error *err) {
     if (st & tkh::ST_NONFINITE_INPUT)
         return fail(err, TKH_NON_FINITE, "attention inputs", 0, 0, 0,
                     "non-finite value in attention inputs or scores (status 0x%x)", st);
+    if (st & tkh::ST_NONFINITE_LOGIT)
+        return fail(err, TKH_NON_FINITE, "output", 0, 0, 0,
+                    "non-finite projected logit (status 0x%x)", st);
     if (st & tkh::ST_BAD_MASS)
         return fail(err, TKH_NON_FINITE, "attention probabilities", 0, 0, 0,
                     "softmax mass is not finite and positive (status 0x%x)", st);
@@ -1147,6 +1153,54 @@ uint32_t tkh_span_attention(tkh_context *ctx, const tkh_span_shape *shape, tkh_d
     }
     plan.problems.push_back(p);
     return run(ctx, plan, err);
+}
+
+uint32_t tkh_project_greedy(tkh_context *ctx, uint64_t rows, uint64_t hidden, uint64_t vocab,
+                            const float *context, uint64_t context_len, const float *weights,
+                            uint64_t weights_len, float *logits, uint64_t logits_len,
+                            uint32_t *tokens, uint64_t tokens_len, tkh_error *err) {
+    // src/cpu/mod.rs:192-201 in order, then src/sampling.rs:6-9.
+    TRY(nonzero(rows, "tokens", err));
+    TRY(nonzero(hidden, "in_features", err));
+    TRY(nonzero(vocab, "out_features", err));
+    uint64_t n;
+    TRY(product(rows, hidden, &n, err));
+    TRY(length("input", context_len, n, err));
+    TRY(product(vocab, hidden, &n, err));
+    TRY(length("weights", weights_len, n, err));
+    TRY(product(rows, vocab, &n, err));
+    if (logits) TRY(length("output", logits_len, n, err));
+    TRY(length("tokens", tokens_len, rows, err));
+    if (vocab - 1 > (uint64_t)UINT32_MAX) return invalid("vocabulary IDs must fit u32", err);
+    if (!ctx) return invalid("context", err);
+    if (!context || !weights || !tokens) return invalid("projection buffers", err);
+    const int64_t per = tkh_project_vocab_per_block();
+    const uint64_t vblocks = (vocab + per - 1) / per;
+    if (vblocks > (uint64_t)INT32_MAX || rows > (uint64_t)UINT32_MAX || rows / 16 >= 65535)
+        return fail(err, TKH_UNSUPPORTED, "projection", 0, 0, 0, "projection grid too large");
+    uint64_t need;
+    TRY(product(rows, vblocks * sizeof(uint64_t), &need, err));
+    if (need > split_region_bytes(ctx))
+        return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, split_region_bytes(ctx),
+                    "projection needs %llu workspace bytes, context has %zu for it",
+                    (unsigned long long)need, split_region_bytes(ctx));
+    tkh::ProjectParams p{};
+    p.context = context;
+    p.weights = weights;
+    p.logits = logits;
+    p.pairs = reinterpret_cast<uint64_t *>(ctx->workspace);
+    p.tokens = tokens;
+    p.rows = (int64_t)rows;
+    p.hidden = (int64_t)hidden;
+    p.vocab = (int64_t)vocab;
+    p.vblocks = (int32_t)vblocks;
+    p.status = ctx->status_dev;
+    HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    hipEvent_t *ev = nullptr;
+    if (ctx->profiling) TRY(profile_slot(ctx, &ev, false, err));
+    HIP_TRY(tkh_launch_project(&p, ctx->stream, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr),
+            "projection launch");
+    return after_launch(ctx, err);
 }
 
 uint32_t tkh_logit_softcap(tkh_context *ctx, float *logits, uint64_t len, float cap,

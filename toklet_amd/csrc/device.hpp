@@ -24,6 +24,19 @@ enum StatusBits : uint32_t {
     ST_SPLIT_TIMEOUT = 8u,     // a decode merge gave up waiting for the other key splits
     ST_V_RANGE = 16u,          // a finite bf16 V value of magnitude 2^24 or more met the chunk
                                // kernel, whose P.V products take V as f16 scaled by 2^-8
+    ST_NONFINITE_LOGIT = 32u,  // a projected logit is not finite (project.hip)
+};
+
+// The o-projection and greedy pick (project.hip).
+struct ProjectParams {
+    const float *context;  // [rows, hidden] FP32
+    const float *weights;  // [vocab, hidden] FP32
+    float *logits;         // [rows, vocab] or null
+    uint64_t *pairs;       // [rows, vblocks]: each workgroup's best (key << 32 | ~id)
+    uint32_t *tokens;      // [rows]
+    int64_t rows, hidden, vocab;
+    int32_t vblocks;       // workgroups along the vocabulary
+    uint32_t *status;
 };
 
 struct Segment {

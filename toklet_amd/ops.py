@@ -264,6 +264,24 @@ def span_attention(ctx: Context, q, segments: Sequence[AttentionKvSegment], cont
     _check(rc, err)
 
 
+def project_greedy(ctx: Context, context: torch.Tensor, weights: torch.Tensor,
+                   tokens: torch.Tensor, logits: Optional[torch.Tensor] = None):
+    """The o-projection of FP32 context rows [rows, hidden] by weights [vocab, hidden]
+    in the reference matmul's FP32 order, then the greedy token of each row
+    (reference: cpu::matmul + sampling::greedy).  tokens: int32 device tensor
+    [rows] (holding the uint32 ids); logits: optional FP32 [rows, vocab]."""
+    err = _lib.Error()
+    rows, hidden = context.shape[0], context.shape[-1]
+    vocab = weights.shape[0]
+    if tokens.dtype != torch.int32:
+        raise TypeError("tokens is an int32 tensor (uint32 ids)")
+    tok = ctypes.cast(tokens.data_ptr(), ctypes.POINTER(ctypes.c_uint32))
+    rc = _lib.load().tkh_project_greedy(
+        ctx.handle, rows, hidden, vocab, _fptr(context), _n(context), _fptr(weights), _n(weights),
+        _fptr(logits), _n(logits), tok, _n(tokens), ctypes.byref(err))
+    _check(rc, err)
+
+
 def logit_softcap(ctx: Context, logits: torch.Tensor, cap: float):
     """In-place cap*tanh(x/cap) in FP64 rounded to FP32 (reference: logit_softcap)."""
     err = _lib.Error()
