@@ -1,20 +1,20 @@
 """Benchmark of the session attention path on one MI355X.
 
-Default workload (Qwen3-shaped single session):
-16 query heads, 8 KV heads, head_dim 128, bf16 KV (and Q stored as bf16),
-per-head RMSNorm (weights N(1, 0.02)) and RoPE (theta 1e6) on seeded N(0,1)
-Q/K, causal prefill of 2048 tokens in 128-token chunks, then 256 decode
-steps at context 2049..2304.  One step = that whole job for one layer:
-16 x (KV append + chunk attention) + 256 x (KV append + decode attention),
-every call through the C ABI.  Inputs are resident in HBM before timing.
+The line's workload is the metric's decode configuration, configs[2] of
+64 independent sessions at Qwen3 shape (16 query heads, 8 KV
+heads, head_dim 128), f16 KV, lengths drawn U[512, 8192], one query token per
+session per step (one batched decode launch).  A step is one such launch over
+all 64 sessions; inputs are resident in HBM before timing.  `value` is decode
+attention GB/s over the timed steps (algorithmic bytes: visible keys x
+2*Hkv*D*2 + Q/O bytes), `roofline` the decode kernel's rate from HIP events on
+its stream, with HBM traffic from the committed rocprofv3 counter passes.
 
-Reported (one JSON line): decode attention GB/s over the decode phase as
-`value` (algorithmic bytes: visible keys x 2*Hkv*D*2 + Q/O bytes), prefill
-attention TFLOPS (4*Hq*D per visible (query, key) pair), the roofline of the
-decode attention kernel from HIP events on its stream, the north-star
-configurations (single-session and 16-session decode at 8192 keys,
-configs[2] batched decode, configs[3] Gemma local/global, configs[4] batched
-prefill), and the CPU oracle timed on this host as the baseline.
+Also on the line: `prefill_roofline` on configs[4] (32 sessions x (4096 cached
++ 128 new), the MFMA-bound prefill), the CPU baselines of both on BASELINE.md's
+subsets (the oracle on one host core), configs[0] (FP32 session, GPU and CPU
+tokens/s, and the device o-projection + greedy pick), configs[1] (Qwen3
+session job), configs[3] (Gemma local/global session), decode at 8192 keys for
+one and 16 sessions, and the host CPU model.
 """
 
 from __future__ import annotations
@@ -40,11 +40,12 @@ def log(msg):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--no-north-star", action="store_true", help="skip configs[2]/[4]")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "d8k", "d8kb", "copy"], default=None,
+    ap.add_argument("--no-north-star", action="store_true",
+                    help="run only the headline configs[2] and configs[4]")
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "d8k", "d8kb", "copy"], default=None,
                     help="run a single workload (for profiling); `copy` runs a plain 1 GiB "
                          "device copy that calibrates the FETCH_SIZE/WRITE_SIZE counters")
     return ap.parse_args()
@@ -249,7 +250,7 @@ def bench_decode_batch(torch, ops, ctx, steps, warmup, *, batch, lmin, lmax, dty
     # Kernel durations over the same lengths, in a pass of their own.
     cur[:] = start_lengths
     prof = profiled(torch, ctx, step, steps)
-    return {
+    res = {
         "batch": batch, "sum_keys": sum(start_lengths), "dtype": str(dtype).replace("torch.", ""),
         "ms_per_step": s / steps * 1e3,
         "gbs": total_bytes / s / 1e9,
@@ -257,7 +258,11 @@ def bench_decode_batch(torch, ops, ctx, steps, warmup, *, batch, lmin, lmax, dty
         "combine_us": prof["combine_ms"] / max(1, prof["launches"]) * 1e3,
         "kernel_gbs": total_bytes / (prof["attention_ms"] / 1e3) / 1e9,
         "kernel_frac_hbm": total_bytes / (prof["attention_ms"] / 1e3) / 1e9 / PEAK_HBM_GBS,
+        "bytes_per_step": total_bytes / steps,
     }
+    state = {"q": q, "k": kpool, "v": vpool, "offsets": offsets, "caps": caps,
+             "lengths": start_lengths, "hq": hq, "hkv": hkv, "d": d, "bytes_of": bytes_of}
+    return res, state
 
 
 def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096, tokens=128,
@@ -290,7 +295,7 @@ def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096
     s, _ = time_region(torch, step, steps, 0)
     prof = profiled(torch, ctx, step, steps)
     kernel_s = (prof["attention_ms"] + prof["combine_ms"]) / 1e3
-    return {
+    res = {
         "sessions": batch, "cached": cached, "new": tokens,
         "ms_per_step": s / steps * 1e3,
         "tflops": flops * steps / s / 1e12,
@@ -300,6 +305,9 @@ def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096
         "kernel_frac_mfma": flops * steps / kernel_s / 1e12 / PEAK_BF16_TFLOPS,
         "gflop_per_step": flops / 1e9,
     }
+    state = {"q": q, "k": k, "v": v, "per": per, "cap": cap, "cached": cached, "tokens": tokens,
+             "hq": hq, "hkv": hkv, "d": d, "flops_per_session": flops / batch}
+    return res, state
 
 
 def bench_c4(torch, ops, sessmod, ctx, steps, warmup, softcap=50.0, seed=5):
@@ -397,57 +405,159 @@ def measured_traffic(key):
     return entry.get("bytes_per_launch"), entry
 
 
-def cpu_baseline(w, torch, seconds=10.0, max_passes=20):
-    """The reference's CPU path for configs[1]'s decode steps, restated by the oracle
-    (single thread): per step rmsnorm + rotary of the new Q/K rows (FP64), append into
-    FP32 head-major caches (the reference's CPU storage), attention_cached (FP32 dot,
-    FP64 softmax).  All 256 steps after an untimed 2048-token prefix, run as repeated
-    passes (each pass rewrites the same rows with the same values) until at least
-    `seconds` of CPU time have been measured, so the sample is about 10 s of work."""
+def host_info():
+    """The host CPU the baselines ran on: model name and visible CPUs."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "cpus_visible": os.cpu_count()}
+
+
+def cpu_baseline_decode_batch(state, seconds=10.0, steps=2):
+    """The reference's CPU path for configs[2] on BASELINE.md's subset (2 decode steps
+    of all 64 sessions), restated by the oracle on one thread: attention_cached per
+    session (FP32 dot, FP64 softmax) over FP32 copies of the stored f16 K/V, repeated
+    in passes until `seconds` have been measured.  Reported as GB/s of the same
+    algorithmic bytes the GPU line counts (f16 K/V bytes + Q/O)."""
     import numpy as np
 
     import oracle
 
     oracle.lib()
-    hq, hkv, d, cap, pre = w.hq, w.hkv, w.d, w.total, w.prefill
-    qp = w.q_proj.cpu().numpy()
-    kp = w.k_proj.cpu().numpy()
-    vp = w.v_proj.cpu().numpy()
-    wq = w.wq.cpu().numpy()
-    wk = w.wk.cpu().numpy()
-
-    def produce(x, wt, t0, n, heads):
-        y = oracle.rmsnorm(x[t0:t0 + n].reshape(-1), wt, n * heads, d, 1e-6)
-        return oracle.rotary(y, n, heads, d, t0, 1e6).reshape(n, heads, d)
-
-    kc = np.zeros((hkv, cap, d), np.float32)
-    vc = np.zeros((hkv, cap, d), np.float32)
-    kc[:, :pre] = produce(kp, wk, 0, pre, hkv).transpose(1, 0, 2)
-    vc[:, :pre] = vp[:pre].transpose(1, 0, 2)
-    positions = list(range(pre, cap))
-    passes = 0
-    t0 = time.perf_counter()
+    hq, hkv, d = state["hq"], state["hkv"], state["d"]
+    kh = state["k"].float().cpu().numpy()
+    vh = state["v"].float().cpu().numpy()
+    qh = state["q"].float().cpu().numpy()
+    offsets, lengths = state["offsets"], state["lengths"]
+    nbytes_pass = sum(state["bytes_of"]([l + i + 1 for l in lengths]) for i in range(steps))
+    passes, t0 = 0, time.perf_counter()
     while True:
-        for p in positions:
-            q = produce(qp, wq, p, 1, hq)
-            kc[:, p] = produce(kp, wk, p, 1, hkv)[0]
-            vc[:, p] = vp[p]
-            oracle.attention_cached(q.reshape(-1), kc, vc, 1, hq, hkv, d, cap, p)
+        for i in range(steps):
+            for b, l0 in enumerate(lengths):
+                L = l0 + i + 1
+                cap = state["caps"][b]  # rows per head of the session's cache; [0, L) are keys
+                kb = kh[offsets[b]:offsets[b] + hkv * cap * d]
+                vb = vh[offsets[b]:offsets[b] + hkv * cap * d]
+                oracle.attention_cached(qh[b].reshape(-1), kb, vb, 1, hq, hkv, d, cap, L - 1)
         passes += 1
         dt = time.perf_counter() - t0
-        if dt >= seconds or passes >= max_passes:
+        if dt >= seconds:
             break
-    steps = passes * len(positions)
-    nbytes = passes * sum(w.decode_bytes_per_step(p + 1) for p in positions)
     return {
-        "value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": f"configs[1] decode, 1 layer, all {len(positions)} steps (context {positions[0] + 1}.."
-                  f"{positions[-1] + 1}) x {passes} passes: oracle rmsnorm + rotary + append + "
-                  f"attention_cached (FP32 KV, FP64 softmax), {dt:.2f} s; bytes counted as the "
-                  f"GPU's bf16 bytes",
+        "value": nbytes_pass * passes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"configs[2] subset: {steps} decode steps of all {len(lengths)} sessions "
+                  f"(sum of lengths {sum(lengths)}), oracle attention_cached (FP32 dot, FP64 "
+                  f"softmax) on FP32 copies of the f16 K/V, x {passes} passes, {dt:.2f} s; bytes "
+                  f"counted as the GPU's f16 bytes",
         "seconds": dt,
-        "us_per_token": dt / steps * 1e6,
-        "host_cpus": os.cpu_count(),
+    }
+
+
+def cpu_baseline_prefill_batch(state, seconds=10.0):
+    """The reference's CPU path for configs[4] on BASELINE.md's subset (1 of 32
+    sessions: 128 new rows over 4224 keys, all 32 heads), restated by the oracle on
+    one thread, in passes until `seconds` have been measured; TFLOP/s of the same
+    algorithmic FLOPs (4 Hq D per visible pair) as the GPU line."""
+    import oracle
+
+    oracle.lib()
+    hq, hkv, d, per, cap = state["hq"], state["hkv"], state["d"], state["per"], state["cap"]
+    kb = state["k"][:per].float().cpu().numpy()
+    vb = state["v"][:per].float().cpu().numpy()
+    qb = state["q"][0].float().cpu().numpy().reshape(-1)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        oracle.attention_cached(qb, kb, vb, state["tokens"], hq, hkv, d, cap, state["cached"])
+        passes += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    return {
+        "value": state["flops_per_session"] * passes / dt / 1e12, "unit": "TFLOP/s", "cores": 1,
+        "kind": "port",
+        "sample": f"configs[4] subset: session 0 of 32 (128 new rows x {hq} heads over {cap} keys), "
+                  f"oracle attention_cached on FP32 copies of the bf16 K/V, x {passes} passes, "
+                  f"{dt:.2f} s",
+        "seconds": dt,
+    }
+
+
+def bench_c1(torch, ops, sessmod, ctx, steps, warmup, seed=3):
+    """Qwen2.5-0.5B-shaped attention on the FP32 path (14/2/64, rotary 1e6,
+    scale 1/8), one session: a 128-token prompt then 32 decode steps, through the
+    native session (producer + attention per chunk or step).  One step = that whole
+    job.  The greedy token of every row over a seeded 896 x 151936 projection runs
+    after the timed region, on the device, and is reported separately.  The CPU line
+    runs the oracle's rotary + attention for the same job on one thread."""
+    import numpy as np
+
+    import oracle
+
+    hq, hkv, d, prompt, dec = 14, 2, 64, 128, 32
+    total = prompt + dec
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    qp = torch.randn(total, hq, d, generator=g, device="cuda")
+    kp = torch.randn(total, hkv, d, generator=g, device="cuda")
+    vp = torch.randn(total, hkv, d, generator=g, device="cuda")
+    out = torch.zeros(total, hq * d, dtype=torch.float32, device="cuda")
+    sess = sessmod.Session(ctx, sessmod.Options(
+        capacity=total, prefill_chunk_size=128, vocab_size=151936, layers=1, query_heads=hq,
+        kv_heads=hkv, head_dim=d, storage="f32", theta=1e6))
+    io = [sessmod.LayerIo(qp, kp, vp, out)]
+
+    def step():
+        sess.reset()
+        sess.set_tokens([1] * prompt)
+        sess.evaluate(io)
+        sess.append([2] * dec)
+        sess.evaluate(io, chunk_limit=1)
+        sess.synchronize()
+
+    s, _ = time_region(torch, step, steps, warmup)
+    # The step after: o-projection + greedy pick of every row (untimed above).
+    w = torch.randn(151936, hq * d, generator=g, device="cuda")
+    tokens = torch.zeros(total, dtype=torch.int32, device="cuda")
+    ops.project_greedy(ctx, out, w, tokens)
+    torch.cuda.synchronize()
+    t_rows, _ = time_region(torch, lambda: ops.project_greedy(ctx, out, w, tokens), 5, 1)
+    one = torch.zeros(1, dtype=torch.int32, device="cuda")
+    t_one, _ = time_region(torch, lambda: ops.project_greedy(ctx, out[-1:], w, one), 20, 2)
+    # CPU: the oracle's producer (rotary) and attention for the same job, one thread.
+    oracle.lib()
+    qh, kh, vh = qp.cpu().numpy(), kp.cpu().numpy(), vp.cpu().numpy()
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        q = oracle.rotary(qh.reshape(-1), total, hq, d, 0, 1e6)
+        k = oracle.rotary(kh.reshape(-1), total, hkv, d, 0, 1e6).reshape(total, hkv, d)
+        kc = np.zeros((hkv, total, d), np.float32)
+        vc = np.zeros((hkv, total, d), np.float32)
+        kc[:, :prompt] = k[:prompt].transpose(1, 0, 2)
+        vc[:, :prompt] = vh[:prompt].transpose(1, 0, 2)
+        oracle.attention_cached(q[:prompt * hq * d], kc, vc, prompt, hq, hkv, d, total, 0)
+        for p in range(prompt, total):
+            kc[:, p] = k[p]
+            vc[:, p] = vh[p]
+            oracle.attention_cached(q[p * hq * d:(p + 1) * hq * d], kc, vc, 1, hq, hkv, d, total, p)
+        passes += 1
+        dt = time.perf_counter() - t0
+        if dt >= 2.0:
+            break
+    sess.close()
+    return {
+        "tokens_per_s": total * steps / s,
+        "ms_per_job": s / steps * 1e3,
+        "projection_greedy_us_160_rows": t_rows / 5 * 1e6,
+        "projection_greedy_us_1_row": t_one / 20 * 1e6,
+        "projection_1_row_gbs": 151936 * hq * d * 4 / (t_one / 20) / 1e9,
+        "cpu_baseline": {"value": total * passes / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                         "sample": f"the same job (rotary + 128-token prefill + 32 decode steps) x "
+                                   f"{passes} passes, {dt:.2f} s"},
     }
 
 
@@ -467,89 +577,107 @@ def main():
         print(json.dumps(copy_calibration(torch)))
         return
     ctx = ops.Context(0, synchronous=False)
-    result = {}
-    w = None
-    if args.only in (None, "c2"):
-        c2, w = bench_c2(torch, ops, sessmod, ctx, args.steps, args.warmup)
-        log(json.dumps(c2))
+    run = lambda name: args.only in (None, name) and (args.only == name or not args.no_north_star
+                                                      or name in ("c3", "c5"))
+    result, states = {}, {}
+    if run("c3"):
+        c3, states["c3"] = bench_decode_batch(torch, ops, ctx, args.steps, args.warmup, batch=64,
+                                              lmin=512, lmax=8192, dtype=torch.float16)
+        log("c3 (configs[2] batched decode): " + json.dumps(c3))
+        result["c3"] = c3
+    if run("c5"):
+        c5, states["c5"] = bench_prefill_batch(torch, ops, ctx, 10, 2)
+        log("c5 (configs[4] batched prefill): " + json.dumps(c5))
+        result["c5"] = c5
+    if run("c1"):
+        c1 = bench_c1(torch, ops, sessmod, ctx, 10, 2)
+        log("c1 (configs[0] FP32 session): " + json.dumps(c1))
+        result["c1"] = c1
+    if run("c2"):
+        c2, _ = bench_c2(torch, ops, sessmod, ctx, 5, 1)
+        log("c2 (configs[1] session job): " + json.dumps(c2))
         result["c2"] = c2
-    if not args.no_north_star and args.only in (None, "d8k"):
-        d8k = bench_decode_batch(torch, ops, ctx, 50, 5, batch=1, lmin=8192, lmax=8192,
-                                 dtype=torch.bfloat16)
+    if run("c4"):
+        c4 = bench_c4(torch, ops, sessmod, ctx, 2, 1)
+        log("c4 (configs[3] Gemma session): " + json.dumps(c4))
+        result["c4"] = c4
+    if run("d8k"):
+        d8k, _ = bench_decode_batch(torch, ops, ctx, 50, 5, batch=1, lmin=8192, lmax=8192,
+                                    dtype=torch.bfloat16)
         log("single-session decode at 8192: " + json.dumps(d8k))
         result["decode_8k"] = d8k
-    if not args.no_north_star and args.only in (None, "d8kb"):
-        d8kb = bench_decode_batch(torch, ops, ctx, 20, 3, batch=16, lmin=8192, lmax=8192,
-                                  dtype=torch.bfloat16)
+    if run("d8kb"):
+        d8kb, _ = bench_decode_batch(torch, ops, ctx, 20, 3, batch=16, lmin=8192, lmax=8192,
+                                     dtype=torch.bfloat16)
         log("sustained decode at 8192, 16 sessions: " + json.dumps(d8kb))
         result["decode_8k_batch16"] = d8kb
-    if not args.no_north_star and args.only in (None, "c3"):
-        c3 = bench_decode_batch(torch, ops, ctx, 20, 3, batch=64, lmin=512, lmax=8192,
-                                dtype=torch.float16)
-        log("c3: " + json.dumps(c3))
-        result["c3"] = c3
-    if not args.no_north_star and args.only in (None, "c4"):
-        c4 = bench_c4(torch, ops, sessmod, ctx, 2, 1)
-        log("c4: " + json.dumps(c4))
-        result["c4"] = c4
-    if not args.no_north_star and args.only in (None, "c5"):
-        c5 = bench_prefill_batch(torch, ops, ctx, 10, 2)
-        log("c5: " + json.dumps(c5))
-        result["c5"] = c5
-    if args.only is not None and args.only != "c2":
+    if args.only is not None and args.only not in ("c3",):
         print(json.dumps(result))
         return
 
-    c2 = result["c2"]
-    traffic, traffic_entry = measured_traffic("c2_decode")
+    c3 = result["c3"]
+    traffic, traffic_entry = measured_traffic("c3_decode")
     line = {
         "metric": "decode attn GB/s (% HBM peak); prefill attn TFLOPS (% MFMA peak)",
-        "value": round(c2["decode_gbs"], 2),
+        "value": round(c3["gbs"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(c2["job_ms_per_step"], 4),
+        "ms_per_step": round(c3["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) Q/K/V, per-head RMSNorm N(1,0.02) weights, RoPE 1e6)",
-        "config": {"workload": "configs[1] Qwen3 16q/8kv/d128 bf16 KV, prefill 2048 in 128-token "
-                               "chunks + 256 decode steps, 1 layer per step",
-                   "query_heads": 16, "kv_heads": 8, "head_dim": 128, "prefill": 2048, "chunk": 128,
-                   "decode_steps": 256},
-        "prefill_tflops": round(c2["prefill_tflops"], 3),
-        "prefill_frac_mfma": round(c2["prefill_tflops"] / PEAK_BF16_TFLOPS, 5),
-        "decode_frac_hbm": round(c2["decode_gbs"] / PEAK_HBM_GBS, 5),
-        "tokens_per_s": round(c2["tokens_per_s"], 1),
-        "decode_us_per_token": round(c2["decode_us_per_token"], 3),
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) Q/K/V times a U[0.5, 2] scale per (session, KV head))",
+        "config": {"workload": "configs[2] batched decode: 64 independent sessions, L ~ U[512, 8192] "
+                               "(seeded), one query token per session per step, Qwen3 16q/8kv/d128, "
+                               "f16 KV, FP32 accumulation",
+                   "sessions": 64, "query_heads": 16, "kv_heads": 8, "head_dim": 128,
+                   "sum_keys_first_step": c3["sum_keys"]},
+        "decode_frac_hbm": round(c3["gbs"] / PEAK_HBM_GBS, 5),
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_decode<bf16, D=128, 2 rows, producer folded in> (the 256 decode "
-                      "launches of configs[1])",
-            "achieved": round(c2["decode_kernel_gbs"], 2),
+            "kernel": "attn_decode<f16, D=128, 2 rows, 4 keys per lane> (configs[2], one launch "
+                      "per step)",
+            "achieved": round(c3["kernel_gbs"], 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
-            "frac": round(c2["decode_kernel_gbs"] / PEAK_HBM_GBS, 5),
+            "frac": round(c3["kernel_gbs"] / PEAK_HBM_GBS, 5),
             "traffic": traffic,
             "traffic_source": (traffic_entry or {}).get("source"),
-            "avg_kernel_us": round(c2["decode_kernel_us"], 3),
-            "algorithmic_bytes_per_launch": round(c2["decode_bytes_per_step_avg"]),
+            "avg_kernel_us": round(c3["kernel_us"], 3),
+            "algorithmic_bytes_per_launch": round(c3["bytes_per_step"]),
             "timing": "hipExtLaunchKernelGGL start/stop events on the library's stream",
         },
-        "prefill_roofline": {
-            "bound": "mfma", "achieved": round(c2["prefill_kernel_tflops"], 3),
-            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(c2["prefill_kernel_tflops"] / PEAK_BF16_TFLOPS, 5),
-        },
-        "north_star": {k: result[k] for k in ("decode_8k", "decode_8k_batch16", "c3", "c4", "c5")
-                       if k in result},
-        "detail": c2,
     }
-    if not args.no_cpu and w is not None:
-        log("cpu baseline: oracle on the host cores")
-        line["cpu_baseline"] = cpu_baseline(w, torch)
+    if "c5" in result:
+        c5 = result["c5"]
+        ptraffic, ptraffic_entry = measured_traffic("c5_prefill")
+        line["prefill_tflops"] = round(c5["tflops"], 2)
+        line["prefill_roofline"] = {
+            "bound": "mfma",
+            "kernel": "attn_prefill<bf16, D=128, 8 waves> (configs[4]: 32 sessions x (4096 cached "
+                      "+ 128 new), 32q/8kv/d128)",
+            "achieved": round(c5["kernel_tflops"], 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(c5["kernel_frac_mfma"], 5),
+            "traffic": ptraffic,
+            "traffic_source": (ptraffic_entry or {}).get("source"),
+            "avg_kernel_us": round(c5["kernel_us"], 3),
+            "algorithmic_flops_per_launch": round(c5["gflop_per_step"] * 1e9),
+            "timing": "hipExtLaunchKernelGGL start/stop events on the library's stream",
+        }
+    line["configs"] = {k: result[k] for k in ("c1", "c2", "c4", "decode_8k", "decode_8k_batch16", "c5")
+                       if k in result}
+    line["configs"]["c3"] = c3
+    line["host"] = host_info()
+    if not args.no_cpu:
+        log("cpu baselines: the oracle on one host core")
+        line["cpu_baseline"] = cpu_baseline_decode_batch(states["c3"])
+        if "c5" in states:
+            line["prefill_cpu_baseline"] = cpu_baseline_prefill_batch(states["c5"])
     print(json.dumps(line))
 
 
