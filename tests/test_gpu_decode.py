@@ -179,11 +179,14 @@ def test_ring_span_decode_wraps(torch_mod, ctx, ops, orc, hq, hkv, D, W, offset)
     assert err <= TOL_HALF
 
 
-def test_decode_batch_many_sessions_lengths_to_8192(torch_mod, ctx, ops, orc):
-    """configs[2] in miniature: 24 f16 sessions, lengths 1..8192, one query token each."""
+@pytest.mark.parametrize("B", [24, 80])
+def test_decode_batch_many_sessions_lengths_to_8192(torch_mod, ctx, ops, orc, B):
+    """configs[2] in miniature: f16 sessions, lengths 1..8192, one query token each.
+    Up to 64 sessions travel in the decode kernel's arguments; 80 upload their
+    descriptors."""
     torch = torch_mod
     rng = np.random.default_rng(51)
-    hq, hkv, D, B = 16, 8, 128, 24
+    hq, hkv, D = 16, 8, 128
     lengths = np.concatenate([[1, 2, 8192, 513], rng.integers(1, 8193, B - 4)])
     scales = rng.uniform(0.5, 2.0, B)
     offsets, pool_k, pool_v, total = [], [], [], 0

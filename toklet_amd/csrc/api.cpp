@@ -58,7 +58,7 @@ extern "C" int tkh_decode_max_splits(void);
 extern "C" int tkh_project_vocab_per_block(void);
 extern "C" hipError_t tkh_launch_project(const tkh::ProjectParams *p, hipStream_t stream,
                                          hipEvent_t start, hipEvent_t stop);
-extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int head_dim, int rows,
+extern "C" hipError_t tkh_launch_decode(const tkh::DecodeArgs *p, int dtype, int head_dim, int rows,
                                         int keys_per_lane, int waves, int64_t groups, int fused,
                                         hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
@@ -354,9 +354,49 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, Problems group,
         return fail(err, TKH_UNSUPPORTED, "workspace", 0, (size_t)INT32_MAX, part_bytes,
                     "decode partials of %zu bytes exceed the merge's 2 GiB range", part_bytes);
 
+    // Up to DECODE_BATCH_MAX single-token sessions laid out as tkh_decode_batch
+    // lays them out (Q/context rows consecutive, K and V at one offset from
+    // common bases) travel in the kernel arguments; other launches of several
+    // problems upload their descriptors.
+    tkh::DecodeArgs args{};
+    tkh::DecodeBatch &cb = args.b;
+    if (group.size() > 1 && group.size() <= (size_t)tkh::DECODE_BATCH_MAX && !plan.fused) {
+        const tkh::Problem &p0 = group[0];
+        const int64_t es = esize(plan.dtype), row = plan.query_heads * D;
+        bool compact = true;
+        for (size_t i = 0; i < group.size() && compact; ++i) {
+            const tkh::Problem &p = group[i];
+            const int64_t dk = (const uint8_t *)p.seg[0].k - (const uint8_t *)p0.seg[0].k;
+            const int64_t dv = (const uint8_t *)p.seg[0].v - (const uint8_t *)p0.seg[0].v;
+            compact = p.nseg == 1 && p.queries == 1 && p.k_pos0 == 0 && p.seg[0].start == 0 &&
+                      p.seg[0].row_stride == D && p.keys == p.seg[0].keys &&
+                      p.q_pos0 == p.keys - 1 && p.vis_lo == 0 && p.vis_hi == p.keys &&
+                      p.keys <= UINT32_MAX && p.seg[0].head_stride <= UINT32_MAX &&
+                      p.tile_base <= UINT32_MAX && p.slot_base == p.tile_base &&
+                      (const uint8_t *)p.q == (const uint8_t *)p0.q + (int64_t)i * row * es &&
+                      p.out == p0.out + (int64_t)i * row && dk == dv && dk % es == 0;
+            if (compact) {
+                tkh::DecodeBatchEntry &e = cb.e[i];
+                e.kv_offset = dk / es;
+                e.head_stride = (uint32_t)p.seg[0].head_stride;
+                e.keys = (uint32_t)p.keys;
+                e.tile_base = (uint32_t)p.tile_base;
+                e.splits = (uint32_t)p.splits;
+            }
+        }
+        if (compact) {
+            cb.q = p0.q;
+            cb.out = p0.out;
+            cb.k = p0.seg[0].k;
+            cb.v = p0.seg[0].v;
+            cb.count = (int32_t)group.size();
+            cb.split_keys = (int32_t)sk;
+        }
+    }
     tkh::Problem *dev = nullptr;
-    if (group.size() > 1) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
-    tkh::Params prm = base_params(ctx, plan);
+    if (group.size() > 1 && cb.count == 0) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
+    tkh::Params &prm = args.p;
+    prm = base_params(ctx, plan);
     prm.problems = dev;
     if (group.size() == 1) prm.single = group[0];
     prm.nproblems = (int32_t)group.size();
@@ -388,7 +428,7 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, Problems group,
     hipEvent_t *ev = nullptr;
     if (ctx->profiling) TRY(profile_slot(ctx, &ev, false, err));
     if (plan.fused) prm.fused = *plan.fused;
-    hipError_t e = tkh_launch_decode(&prm, (int)plan.dtype, (int)D, R, u, nw, wgs,
+    hipError_t e = tkh_launch_decode(&args, (int)plan.dtype, (int)D, R, u, nw, wgs,
                                      plan.fused ? 1 : 0, ctx->stream, ev ? ev[0] : nullptr,
                                      ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "decode launch", err);

@@ -2,15 +2,15 @@
 // kernel (decode_kernel.hpp); the kernel builds live in decode_<dtype>_<D>.hip.
 #include "decode_kernel.hpp"
 
-hipError_t tkh_decode_launch_bf16_64(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
-hipError_t tkh_decode_launch_bf16_128(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
-hipError_t tkh_decode_launch_bf16_256(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
-hipError_t tkh_decode_launch_f16_64(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
-hipError_t tkh_decode_launch_f16_128(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
-hipError_t tkh_decode_launch_f16_256(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
-hipError_t tkh_decode_launch_f32_64(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
-hipError_t tkh_decode_launch_f32_128(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
-hipError_t tkh_decode_launch_f32_256(const tkh::Params *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_bf16_64(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_bf16_128(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_bf16_256(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_f16_64(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_f16_128(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_f16_256(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_f32_64(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_f32_128(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
+hipError_t tkh_decode_launch_f32_256(const tkh::DecodeArgs *, int, int, int, dim3, dim3, hipStream_t, hipEvent_t, hipEvent_t);
 
 // Rows per KV head the decode kernel handles for a head_dim / dtype (0: none).
 extern "C" int tkh_decode_max_rows(int dtype, int head_dim) {
@@ -34,7 +34,7 @@ extern "C" int tkh_decode_max_waves(int dtype, int head_dim, int rows) {
 }
 extern "C" int tkh_decode_max_splits(void) { return tkh::DECODE_MAX_SPLITS; }
 
-extern "C" hipError_t tkh_launch_decode(const tkh::Params *p, int dtype, int head_dim, int rows,
+extern "C" hipError_t tkh_launch_decode(const tkh::DecodeArgs *p, int dtype, int head_dim, int rows,
                                         int keys_per_lane, int waves, int64_t groups, int fused,
                                         hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     if (waves < 1 || waves > tkh_decode_max_waves(dtype, head_dim, rows)) return hipErrorInvalidValue;

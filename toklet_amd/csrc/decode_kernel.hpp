@@ -326,8 +326,19 @@ constexpr int DECODE_MAX_SPLITS = 64;  // key splits per KV head (bounds the mer
 // row size leave room in the register file (256 VGPRs per lane), else four.
 constexpr int decode_waves_for(int row_bytes, int rows) { return rows <= 2 && row_bytes <= 512 ? 8 : 4; }
 
+// The session of global workgroup `tile` in a compact batch, by the whole
+// wave: lane i tests entry i, a ballot picks the last entry that starts at or
+// before the tile.
+__device__ __forceinline__ int find_batch_entry(const_ptr<DecodeBatch> b, int count, uint32_t tile) {
+    const int lane = threadIdx.x & 63;
+    const bool le = lane < count && b->e[lane].tile_base <= tile;
+    const uint64_t m = __ballot(le);  // bit 0 is set: entry 0 starts at tile 0
+    return __builtin_amdgcn_readfirstlane(63 - __builtin_clzll(m));
+}
+
 template <int DT, int D, int R, int U, bool CAP, bool FUSED>
-__global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void attn_decode(Params p) {
+__global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void attn_decode(DecodeArgs kargs) {
+    const Params &p = kargs.p;
     constexpr int ES = Elem<DT>::size;
     constexpr int NWMAX = decode_waves_for(D * ES, R);
     constexpr int ROWB = D * ES;            // bytes per K/V row
@@ -359,14 +370,19 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     // count (a single-problem launch needs nothing else), and a batched launch
     // then finds its problem by a wave-parallel search and reads it again.
     // Segments past the first load only when the split lies in one (rings).
-    const_ptr<Params> args = (const_ptr<Params>)__builtin_amdgcn_kernarg_segment_ptr();
+    const_ptr<DecodeArgs> dargs = (const_ptr<DecodeArgs>)__builtin_amdgcn_kernarg_segment_ptr();
+    const_ptr<Params> args = &dargs->p;
+    const_ptr<DecodeBatch> batch = &dargs->b;
     const_ptr<Problem> pr = &args->single;
     // Every kernel-argument field the prologue and the stream need, read
     // before the first use of any (the pins below then cost one wait): the
     // problem view, the launch fields and the fused producer's descriptor.  A
     // field first read after that wait is another round trip to L2.
     DecodeView pv = decode_view(pr);
+    int64_t slot_base = pr->slot_base;
+    float *out = pr->out;
     int nproblems = args->nproblems;
+    int bcount = batch->count;
     int G = args->group, Hq = args->query_heads, has_window = args->has_window;
     int64_t window = args->window;
     float scale_log2 = args->scale_log2, scale = args->scale;
@@ -389,6 +405,9 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         fz.new_key = fa.new_key;
     }
     pin_scalar(nproblems);
+    pin_scalar(bcount);
+    pin_scalar(slot_base);
+    pin_scalar(out);
     pin_view(pv);
     pin_scalar(G);
     pin_scalar(Hq);
@@ -413,9 +432,37 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         pin_scalar(fz.head_stride);
         pin_scalar(fz.new_key);
     }
-    if (nproblems != 1) {
+    if (bcount > 0) {
+        // A compact batch: one segment, one query token at the last key.
+        const int i = find_batch_entry(batch, bcount, blockIdx.x);
+        const auto &e = batch->e[i];
+        const int64_t kv_offset = e.kv_offset;
+        const uint32_t keys = e.keys, tile_base = e.tile_base, splits = e.splits;
+        const uint32_t head_stride = e.head_stride;
+        const int64_t row = (int64_t)Hq * D;
+        pv.tile_base = tile_base;
+        pv.vis_lo = 0;
+        pv.vis_hi = keys;
+        pv.k_pos0 = 0;
+        pv.keys = keys;
+        pv.q_pos0 = (int64_t)keys - 1;
+        pv.q_row_stride = row;
+        pv.q = reinterpret_cast<const uint8_t *>(batch->q) + (int64_t)i * row * ES;
+        pv.splits = (int32_t)splits;
+        pv.split_keys = batch->split_keys;
+        pv.seg_splits0 = (int32_t)splits;
+        pv.seg_splits1 = 0;
+        pv.queries = 1;
+        pv.seg0 = DecodeSegment{reinterpret_cast<const uint8_t *>(batch->k) + kv_offset * ES,
+                                reinterpret_cast<const uint8_t *>(batch->v) + kv_offset * ES,
+                                (int64_t)head_stride, D, (int64_t)keys, 0};
+        slot_base = tile_base;
+        out = batch->out + (int64_t)i * row;
+    } else if (nproblems != 1) {
         pr = (const_ptr<Problem>)p.problems + find_problem_wave(p.problems, p.nproblems, blockIdx.x);
         pv = decode_view(pr);
+        slot_base = pr->slot_base;
+        out = pr->out;
     }
     const uint32_t local = blockIdx.x - (uint32_t)pv.tile_base;
     const int split = (int)(local % (uint32_t)pv.splits);
@@ -729,7 +776,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
 
     // Merge the waves: one thread per (row, feature).
     const bool single = pv.splits == 1;
-    const int64_t slot = pr->slot_base + (int64_t)kvh * pv.splits + split;
+    const int64_t slot = slot_base + (int64_t)kvh * pv.splits + split;
     bool bad_mass = false, bad_out = false;
     for (int i = threadIdx.x; i < R * D; i += blockDim.x) {
         const int r = i / D, d = i - r * D;
@@ -749,7 +796,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
             bad_mass |= !(L > 0.0f) || !is_finite_f(L);
             const float v = O / L;
             bad_out |= !is_finite_f(v);
-            gstore_ptr<float>(pr->out)[((int64_t)t * Hq + h) * D + d] = v;
+            gstore_ptr<float>(out)[((int64_t)t * Hq + h) * D + d] = v;
         } else if (split == pv.splits - 1) {
             lds_own[r * D + d] = O;
             if (d == 0) {
@@ -785,7 +832,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         if (threadIdx.x == 0) flag_store(p.flags + slot, epoch);
         return;
     }
-    const int64_t slot0 = pr->slot_base + (int64_t)kvh * S;
+    const int64_t slot0 = slot_base + (int64_t)kvh * S;
     if (wave == 0) {
         const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
         bool arrived = false;
@@ -883,7 +930,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
                 v[k] = acc[k] / L;
                 bad_out |= !is_finite_f(v[k]);
             }
-            *gstore_ptr<f32x4>(pr->out + ((int64_t)t * Hq + h) * D + d) = v;
+            *gstore_ptr<f32x4>(out + ((int64_t)t * Hq + h) * D + d) = v;
         }
     }
     raise_status(p, timed_out, ST_SPLIT_TIMEOUT);
@@ -899,24 +946,24 @@ namespace tkh {
 // The producer is folded in only for rows of at most 256 bytes (its per-lane
 // row copy fits the register budget there).
 template <int DT, int DD, int RR, int UU>
-hipError_t decode_launch_variant(const Params *p, int fused, dim3 grid, dim3 block,
+hipError_t decode_launch_variant(const DecodeArgs *a, int fused, dim3 grid, dim3 block,
                                  hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     if (fused) {
         if constexpr (DD * Elem<DT>::size <= 256) {
-            if (p->softcap != 0.0f) return hipErrorInvalidValue;
+            if (a->p.softcap != 0.0f) return hipErrorInvalidValue;
             hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false, true>), grid, block, 0, stream,
-                                  start, stop, 0, *p);
+                                  start, stop, 0, *a);
             return hipGetLastError();
         } else {
             return hipErrorInvalidValue;
         }
     }
-    if (p->softcap != 0.0f)
+    if (a->p.softcap != 0.0f)
         hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, true, false>), grid, block, 0, stream,
-                              start, stop, 0, *p);
+                              start, stop, 0, *a);
     else
         hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false, false>), grid, block, 0, stream,
-                              start, stop, 0, *p);
+                              start, stop, 0, *a);
     return hipGetLastError();
 }
 
@@ -924,7 +971,7 @@ hipError_t decode_launch_variant(const Params *p, int fused, dim3 grid, dim3 blo
 // with 2 or 4 keys per lane for rows of at most 256 bytes, up to 4 with 1 or
 // 2 keys for 512-byte rows, up to 2 with 1 key for 1024-byte rows.
 template <int DT, int DD>
-hipError_t decode_launch_unit(const Params *p, int rows, int keys_per_lane, int fused, dim3 grid,
+hipError_t decode_launch_unit(const DecodeArgs *p, int rows, int keys_per_lane, int fused, dim3 grid,
                               dim3 block, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     constexpr int ROWB = DD * Elem<DT>::size;
     constexpr int UMAX = ROWB <= 256 ? 4 : (ROWB <= 512 ? 2 : 1);
@@ -957,7 +1004,7 @@ hipError_t decode_launch_unit(const Params *p, int rows, int keys_per_lane, int 
 // One translation unit per (dtype, head_dim) instantiates its builds (they
 // compile in parallel); decode.hip dispatches to them.
 #define TKH_DECODE_UNIT(DT, DD, NAME)                                                          \
-    hipError_t tkh_decode_launch_##NAME(const tkh::Params *p, int rows, int keys_per_lane,    \
+    hipError_t tkh_decode_launch_##NAME(const tkh::DecodeArgs *p, int rows, int keys_per_lane, \
                                         int fused, dim3 grid, dim3 block, hipStream_t stream,   \
                                         hipEvent_t start, hipEvent_t stop) {                    \
         return tkh::decode_launch_unit<tkh::DT, DD>(p, rows, keys_per_lane, fused, grid, block, \

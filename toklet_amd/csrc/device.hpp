@@ -144,6 +144,36 @@ struct Params {
     Problem single;         // the problem itself when nproblems == 1 (no descriptor upload)
 };
 
+// A batch of single-segment, single-token decode problems (tkh_decode_batch of
+// at most DECODE_BATCH_MAX sessions) carried in the decode kernel's own
+// arguments, so the launch needs no descriptor upload: the upload is a copy
+// ordered after the previous kernel on the stream, about 20 us of idle device
+// time per launch.  Session i reads Q row i and writes context row i; its K/V
+// cache starts kv_offset elements from k/v.
+constexpr int DECODE_BATCH_MAX = 64;
+struct DecodeBatchEntry {
+    int64_t kv_offset;     // elements from k / v to the session's cache
+    uint32_t head_stride;  // elements between its KV heads
+    uint32_t keys;         // its keys (the query sits at position keys - 1)
+    uint32_t tile_base;    // its first workgroup, which is also its first partial slot
+    uint32_t splits;       // its key splits per KV head
+};
+struct DecodeBatch {
+    const void *q;         // [count, Hq, D] in the cache dtype
+    float *out;            // [count, Hq, D]
+    const void *k, *v;
+    int32_t count;         // 0: the launch describes its problems in Params
+    int32_t split_keys;
+    DecodeBatchEntry e[DECODE_BATCH_MAX];
+};
+
+// The decode kernel's one argument: the launch parameters, then the compact
+// batch (count 0 when unused).
+struct DecodeArgs {
+    Params p;
+    DecodeBatch b;
+};
+
 // Address-space qualified views: the problem descriptors are read-only for a
 // launch (scalar loads through the constant space), tensors are global.
 template <class T> using const_ptr = const __attribute__((address_space(4))) T *;
