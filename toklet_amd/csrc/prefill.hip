@@ -256,6 +256,15 @@ template <int LPT, int MAXA> __device__ __forceinline__ void ring_sync(int ahead
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
 }
+// ring_sync for a compile-time `ahead`: one wait, no selection.
+template <int LPT, int A> __device__ __forceinline__ void ring_sync_fixed() {
+    constexpr int n = A * LPT;
+    static_assert(n < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
 
 // The running maximum of a row is moved (and O and l rescaled) only when a
 // tile's maximum exceeds it by more than 2^RESCALE_SLACK in probability: until
@@ -422,11 +431,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     const uint32_t run0 = (uint32_t)uniform32(wave) * (RPW * 1024);
     // Issue the next tile into stage STG (a compile-time stage: the LDS
     // destinations are scalar constants plus run0).
-    auto issue = [&](auto stg_tag) {
+    // FULL: the caller knows this is not the last tile.
+    auto issue = [&](auto stg_tag, auto full_tag) {
         constexpr int STG = decltype(stg_tag)::value;
+        constexpr bool FULL = decltype(full_tag)::value;
         const uint32_t mk = (uint32_t)(uintptr_t)(lds + L::k_at(STG)) + run0;
         const uint32_t mv = (uint32_t)(uintptr_t)(lds + L::v_at(STG)) + run0;
-        if (t_next == ntiles - 1) {
+        if (!FULL && t_next == ntiles - 1) {
             for (int i = 0; i < RPW; ++i) {
                 dma16(k_next, (uint32_t)off_last[i], mk + i * 1024);
                 dma16(v_next, (uint32_t)off_last[i], mv + i * 1024);
@@ -461,15 +472,16 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     //      its probabilities on the vector unit between those MFMAs;
     //   2. wait for tile t + 1 and hand the stage of tile t - 1 to a new load;
     //   3. the scores of tile t + 1 (QK MFMAs) with the second half of tile t's
-    //      probabilities between them;
-    //   4. read tile t's V^T operands for step 1 of the next iteration.
+    //      probabilities and the reads of tile t's V^T operands (for step 1 of
+    //      the next iteration) between them.
     // Scheduling fences keep that interleave; every MFMA slot is a compile-time
     // position.  In iteration 0 step 1 multiplies zero operands, and after the
     // last tile step 3 scores stale LDS data (of a stage that holds an earlier
     // tile) that is never used.
     constexpr int NPV = 2 * MB;  // P.V MFMAs per tile
+    static_assert(NPV == KS, "one V^T operand read per Q.K k-step");
     static_for<NS - 1>([&](auto stg) {
-        if (decltype(stg)::value < ntiles) issue(stg);
+        if (decltype(stg)::value < ntiles) issue(stg, std::false_type{});
     });
     f32x16 st;
     for (int i = 0; i < 16; ++i) st[i] = 0.0f;
@@ -491,14 +503,21 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     for (int i = 0; i < 8; ++i) {
         ph[i] = 0u;
     }
+    int t = 0;
     // Tile t sits in stage t % NS.  The loop is unrolled by NS, so every
     // stage, and with it every LDS offset, is a compile-time constant, and the
     // two score registers swap roles (a copy per round only for an odd NS).
-    int t = 0;
     f32x16 st_b;
+    // bulk: the round of NS iterations starting at t is steady-state: every
+    // tile t' of it is visible to all rows of the wave, tile t' + 1 and the
+    // tile it issues (t' + NS - 1) come before the last.  Such an iteration
+    // skips the visibility test, takes a fixed ring wait and issues and
+    // converts unconditionally.
+    bool bulk = false;
     auto body = [&](auto stg_tag, f32x16 &st, f32x16 &st_next) {
         constexpr int STG = decltype(stg_tag)::value;
         constexpr int STG_NEXT = (STG + 1) % NS;
+        __builtin_amdgcn_sched_barrier(0);
         lds_ptr<uint8_t> vt = lds + L::vt_base + (STG % L::vt_bufs) * L::vt_bytes;
         lds_ptr<uint8_t> kn = lds + L::k_at(STG_NEXT);
 
@@ -518,7 +537,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             }
             __builtin_amdgcn_sched_barrier(0);
             if (k == 0) {
-                if (t >= tf_lo && t < tf_hi) {
+                if (bulk || (t >= tf_lo && t < tf_hi)) {
                     hi = fmaxf(fmaxf(st[0], st[1]), st[2]);
                     float lo = fminf(fminf(st[0], st[1]), st[2]);
                     for (int i = 3; i < 16; ++i) {
@@ -597,13 +616,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 
         // ---- step 2: tile t + 1 resident; everyone is done with tile t - 1,
         // whose stage takes the next load.
-        if (t + 1 < ntiles) {
+        if (bulk) {
+            // t_next == t + NS - 1: NS - 3 later tiles may stay in flight.
+            ring_sync_fixed<LPT, NS - 3>();
+            issue(std::integral_constant<int, (STG + NS - 1) % NS>{}, std::true_type{});
+        } else if (t + 1 < ntiles) {
             wait_tile(t + 1);
-            if (t_next < ntiles) issue(std::integral_constant<int, (STG + NS - 1) % NS>{});
+            if (t_next < ntiles) issue(std::integral_constant<int, (STG + NS - 1) % NS>{}, std::false_type{});
         } else if (t > 0) {
             // The last tile: its transposed V was written by the whole
             // workgroup in the previous iteration's step 3, and no step-2
-            // barrier follows that here; step 4 reads it.
+            // barrier follows that here; step 3 reads it.
             __syncthreads();
         }
 
@@ -615,13 +638,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int i = 0; i < KPRE && i < KS; ++i) kq[i] = *(lds_ptr<u32x4>)(kn + k_off[i]);
         // bf16: tile t + 1's V, resident since step 2, converted between these
         // MFMAs; the barrier of the next step 2 precedes its V^T reads.
-        const bool conv_next = t + 1 < ntiles;
+        const bool conv_next = bulk || t + 1 < ntiles;
         lds_ptr<uint8_t> vn = lds + L::v_at(STG_NEXT);
         lds_ptr<uint8_t> vtn = lds + L::vt_base + (STG_NEXT % L::vt_bufs) * L::vt_bytes;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const u32x4 kcur = kq[ks % KPRE];
             if (ks + KPRE < KS) kq[ks % KPRE] = *(lds_ptr<u32x4>)(kn + k_off[ks + KPRE]);
+            // Tile t's V^T operands (for step 1 of the next iteration), one
+            // per k-step: resident since the step-2 barrier, and a whole Q.K
+            // chain ahead of their use.  B slots 8h..8h+7 of step stp are keys
+            // {16 stp + 4h + 0..3, 16 stp + 8 + 4h + 0..3}, the order in which
+            // the transposed tile stores them.  (2 MB == KS.)
+            vop[ks / MB][ks % MB] = *(lds_ptr<u32x4>)(vt + vt_off[ks / MB] + (ks % MB) * 32 * L::vt_row);
             // The two waves of a SIMD leave the step-2 barrier together and
             // would contend for the matrix core and the vector unit in
             // lockstep.  A raised priority over the first half of the Q.K
@@ -645,14 +674,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        // ---- step 4: tile t's V^T operands, one 16-byte read each.  B slots
-        // 8h..8h+7 of step stp are keys {16 stp + 4h + 0..3, 16 stp + 8 + 4h +
-        // 0..3}, the order in which the transposed tile stores them.
-        for (int stp = 0; stp < 2; ++stp)
-            for (int mb = 0; mb < MB; ++mb)
-                vop[stp][mb] = *(lds_ptr<u32x4>)(vt + vt_off[stp] + mb * 32 * L::vt_row);
+        __builtin_amdgcn_sched_barrier(0);
     };
     for (bool go = true; go;) {
+        // A round of NS steady-state iterations when all of them qualify
+        // (t is a multiple of NS here, so stage K is tile t + K's).
+        bulk = t >= tf_lo && t + NS <= tf_hi && t + 2 * NS - 1 < ntiles && t_next == t + NS - 1;
         static_for<NS>([&](auto k) {
             constexpr int K = decltype(k)::value;
             if (!go || t >= ntiles) {
