@@ -44,6 +44,7 @@ extern "C" hipError_t tkh_launch_fill_u32(uint32_t *p, uint32_t v, hipStream_t s
 extern "C" hipError_t tkh_launch_zero_u64(uint64_t *p, int64_t words, hipStream_t stream);
 extern "C" int tkh_decode_max_rows(int dtype, int head_dim);
 extern "C" int tkh_prefill_waves(int head_dim, int wide);
+extern "C" hipError_t tkh_launch_copy_batch(const tkh::CopyBatch *b, hipStream_t stream);
 extern "C" int tkh_prefill_max_splits(void);
 extern "C" int tkh_prefill_merge_rows_per_block(int head_dim);
 extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int rows,
@@ -52,7 +53,7 @@ extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_di
 extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim, int waves,
                                          int64_t groups, hipStream_t stream, hipEvent_t start,
                                          hipEvent_t stop);
-extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int want);
+extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int rows, int want);
 extern "C" int tkh_decode_max_waves(int dtype, int head_dim, int rows);
 extern "C" int tkh_decode_max_splits(void);
 extern "C" int tkh_project_vocab_per_block(void);
@@ -274,7 +275,7 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, Problems group,
     const double groups = !bulk ? ctx->decode_groups
                                 : (even ? ctx->decode_even_groups : ctx->decode_bulk_groups);
     int nw = nw_max;
-    const int u = tkh_decode_keys_per_lane((int)plan.dtype, (int)D,
+    const int u = tkh_decode_keys_per_lane((int)plan.dtype, (int)D, R,
                                            bulk && even ? ctx->decode_even_keys_per_lane
                                                         : ctx->decode_keys_per_lane);
     const int max_splits = std::min(ctx->decode_max_splits, tkh_decode_max_splits());
@@ -567,7 +568,9 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, Problems group,
         for (auto &p : group) max_rows = std::max<int64_t>(max_rows, (int64_t)p.queries * G);
         const int limit = tkh_decode_max_rows((int)plan.dtype, (int)D);
         if (plan.fused) {
-            if (limit <= 0 || max_rows > limit || plan.diag_mode != 0 || plan.softcap != 0.0f)
+            // The softcap build of the fused decode exists at head_dim 256.
+            if (limit <= 0 || max_rows > limit || plan.diag_mode != 0 ||
+                (plan.softcap != 0.0f && D != 256))
                 return fail(err, TKH_UNSUPPORTED, "fused decode", 0, limit, max_rows,
                             "fused producer decode needs the streaming decode kernel");
             return launch_decode(ctx, plan, group, (int)max_rows, err);
@@ -995,6 +998,51 @@ uint32_t tkh_host::attention_cached_fused(tkh_context *ctx, const tkh_cached_sha
     plan.fused = &fused;
     tkh::Problem p = make_problem(nullptr, context, s.query_heads * s.head_dim, s.offset, 0, end, 1);
     add_segment(p, k, v, s.capacity * s.head_dim, s.head_dim, end, 0);
+    plan.problems.push_back(p);
+    return run(ctx, plan, err);
+}
+
+uint32_t tkh_host::span_attention_fused(tkh_context *ctx, const tkh_span_shape *shape,
+                                        tkh_dtype dtype, const tkh_segment segments[3],
+                                        float *context, const tkh::FusedDecode &fused,
+                                        tkh_error *err) {
+    if (!valid_dtype(dtype)) return invalid("dtype", err);
+    if (!ctx || !shape || !segments) return invalid("shape", err);
+    const tkh_span_shape s = *shape;
+    if (s.queries != 1) return invalid("fused decode takes one token", err);
+    TRY(nonzero(s.keys, "keys", err));
+    TRY(nonzero(s.query_heads, "query_heads", err));
+    TRY(nonzero(s.kv_heads, "kv_heads", err));
+    TRY(nonzero(s.head_dim, "head_dim", err));
+    if (s.query_heads % s.kv_heads != 0 || (s.has_window && s.window == 0) ||
+        !std::isfinite(s.scale) || s.scale <= 0.0f)
+        return invalid("segmented attention heads/window/scale", err);
+    if (s.softcap != 0.0f && (!std::isfinite(s.softcap) || s.softcap < 0.0f))
+        return invalid("attention score softcap", err);
+    // The new key is the view's last (fused.new_key counts from the view's
+    // first key, as its segments do), at the query's position.
+    if (fused.new_key != (int64_t)(s.keys - 1) || s.query_start + 1 != s.key_start + s.keys)
+        return invalid("fused decode: the new key must end the view", err);
+    Plan plan;
+    plan.dtype = dtype;
+    plan.query_heads = s.query_heads;
+    plan.kv_heads = s.kv_heads;
+    plan.head_dim = s.head_dim;
+    plan.has_window = s.has_window != 0;
+    plan.window = (int64_t)s.window;
+    plan.scale = s.scale;
+    plan.softcap = s.softcap;
+    plan.fused = &fused;
+    tkh::Problem p = make_problem(nullptr, context, s.query_heads * s.head_dim, s.query_start,
+                                  s.key_start, s.keys, 1);
+    uint64_t logical = 0;
+    for (int i = 0; i < 3; ++i) {
+        const tkh_segment &seg = segments[i];
+        if (seg.keys == 0) continue;
+        add_segment(p, seg.k, seg.v, seg.head_stride, s.head_dim, seg.keys, logical);
+        logical += seg.keys;
+    }
+    if (logical != s.keys) return invalid("attention segment keys", err);
     plan.problems.push_back(p);
     return run(ctx, plan, err);
 }
@@ -1606,24 +1654,48 @@ uint32_t tkh_host::commit_frames(tkh_kv *const *kvs, const tkh_kv_frame *frames,
             if (kvs[i] == kvs[j])
                 return fail(err, TKH_INVALID_CONFIG, "KV frame", 0, 0, 0, "duplicate KV owner in commit");
     // No fallible arithmetic remains: copy only the final min(tokens, W) rows.
+    // Consecutive rings of one context and stream go out in one launch (up to
+    // COPY_BATCH_MAX each); the last launch records the committed length.
+    // A ring's offset and generation advance once its copy is queued.
+    tkh::CopyBatch batch{};
+    tkh_context *batch_ctx = nullptr;
+    std::pair<tkh_kv *, uint64_t> pending[tkh::COPY_BATCH_MAX];
+    auto flush = [&](bool last) -> uint32_t {
+        if (batch.count == 0) return TKH_OK;
+        batch.gate = gate;
+        batch.committed = last ? committed : nullptr;
+        batch.committed_value = committed_value;
+        HIP_TRY(hipSetDevice(batch_ctx->device), "hipSetDevice");
+        HIP_TRY(tkh_launch_copy_batch(&batch, batch_ctx->stream), "KV commit");
+        for (int j = 0; j < batch.count; ++j) {
+            pending[j].first->offset += pending[j].second;
+            pending[j].first->generation += 1;
+        }
+        batch.count = 0;
+        return TKH_OK;
+    };
     for (uint64_t i = 0; i < count; ++i) {
         tkh_kv *kv = kvs[i];
         const tkh_kv_frame &f = frames[i];
+        if (batch.count == tkh::COPY_BATCH_MAX || (batch_ctx && (kv->ctx->device != batch_ctx->device ||
+                                                                  kv->ctx->stream != batch_ctx->stream)))
+            TRY(flush(false));
+        batch_ctx = kv->ctx;
         uint64_t runs[6];
         copy_runs(kv->capacity, kv->offset, f.tokens, kv->has_window, runs);
-        int64_t r[6];
-        for (int j = 0; j < 6; ++j) r[j] = (int64_t)runs[j];
-        tkh_context *ctx = kv->ctx;
-        HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
-        HIP_TRY(tkh_launch_copy_runs(f.k, f.v, kv->k, kv->v, (int64_t)f.tokens, (int)kv->heads,
-                                     (int64_t)(kv->dims * esize(kv->storage)),
-                                     (int64_t)kv->capacity, r, gate,
-                                     i + 1 == count ? committed : nullptr, committed_value,
-                                     ctx->stream),
-                "KV commit");
-        kv->offset += f.tokens;
-        kv->generation += 1;
+        tkh::CopyRunsEntry &e = batch.e[batch.count++];
+        e.src_k = static_cast<const uint8_t *>(f.k);
+        e.src_v = static_cast<const uint8_t *>(f.v);
+        e.dst_k = static_cast<uint8_t *>(kv->k);
+        e.dst_v = static_cast<uint8_t *>(kv->v);
+        e.tokens = (int64_t)f.tokens;
+        e.row_bytes = (int64_t)(kv->dims * esize(kv->storage));
+        e.capacity = (int64_t)kv->capacity;
+        for (int j = 0; j < 6; ++j) e.runs[j] = (int64_t)runs[j];
+        e.heads = (int32_t)kv->heads;
+        pending[batch.count - 1] = {kv, f.tokens};
     }
+    TRY(flush(true));
     for (uint64_t i = 0; i < count; ++i)
         if (kvs[i]->ctx->synchronous) HIP_TRY(hipStreamSynchronize(kvs[i]->ctx->stream), "KV commit");
     return ok(err);

@@ -167,30 +167,36 @@ template <> __device__ __forceinline__ u32x4 pack_chunk<F32>(const float *x) {
 // The producer for one head row, by one whole wave, in produce_qkv's own
 // arithmetic and order (so both give the same bits): lane l holds elements
 // l, l + 64, ...; per-head RMSNorm with the squares summed in FP64 per lane
-// and then by the same xor butterfly (wave_sum_f64), the reciprocal root in
-// FP64 and value = f32(x * inv * w) in FP64; then the rotary of pair j
-// (elements j and j + D/2) with the row's (cos, sin) from the session's table
-// and FP32 products and sums rounded separately.  Every load (the row, the
-// weights, the (cos, sin) pairs) is issued before any arithmetic, and the row
-// stays in registers: with D = 128 a lane holds both elements of its pair,
-// with D = 64 the partner comes by a lane swap.  Returns the lane's D/64
-// finished values.
+// (in element order) and then by the same xor butterfly (wave_sum_f64), the
+// reciprocal root in FP64 and value = f32(x * inv * w) in FP64; then the
+// rotary of pair j (elements j and j + D/2) with the row's (cos, sin) from the
+// session's table and FP32 products and sums rounded separately.  Every load
+// (the row, the weights, the (cos, sin) pairs) is issued before any
+// arithmetic, and the row stays in registers: with D = 128 a lane holds both
+// elements of its pair, with D = 256 both elements of two pairs (j = l and
+// l + 64), with D = 64 the partner comes by a lane swap.  Returns the lane's
+// D/64 finished values.
 template <int D>
 __device__ __forceinline__ void wave_produce_row(const float *src, const float *w, float eps,
                                                  const float *rope, int pairs, int lane,
                                                  float (&y)[D / 64], bool &bad) {
 #pragma clang fp contract(off)
-    static_assert(D == 64 || D == 128, "the fused producer covers head sizes 64 and 128");
+    static_assert(D == 64 || D == 128 || D == 256, "the fused producer covers head sizes 64, 128, 256");
     constexpr int K = D / 64, half = D / 2;
+    constexpr int NP = K >= 2 ? K / 2 : 1;  // rotary pairs a lane computes
     float x[K], wv[K];
-    f32x2 cs = {1.0f, 0.0f};
-    const int j = lane % half;  // the pair this lane's first element belongs to
+    f32x2 cs[NP];
+    bool rotated[NP];
     for (int k = 0; k < K; ++k) {
         x[k] = src[lane + 64 * k];
         wv[k] = w ? w[lane + 64 * k] : 1.0f;
     }
-    const bool rotated = rope && j < pairs;
-    if (rotated) cs = *gload_ptr<f32x2>(rope + 2 * j);
+    for (int q = 0; q < NP; ++q) {
+        const int j = K >= 2 ? lane + 64 * q : lane % half;  // the pair of element x[q]
+        cs[q] = f32x2{1.0f, 0.0f};
+        rotated[q] = rope && j < pairs;
+        if (rotated[q]) cs[q] = *gload_ptr<f32x2>(rope + 2 * j);
+    }
     for (int k = 0; k < K; ++k) bad |= !is_finite_f(x[k]);
     if (w) {
         double ss = 0.0;
@@ -203,31 +209,34 @@ __device__ __forceinline__ void wave_produce_row(const float *src, const float *
         }
     }
     if (rope) {
-        // a = element j, b = element j + half: with D = 128 x[0] and x[1] of this
-        // lane; with D = 64 this lane's x[0] and the one of lane ^ 32.
-        float a, b;
-        if constexpr (K == 2) {
-            a = x[0];
-            b = x[1];
-        } else {
-            float lo, hi;
-            lane_pair<32>(x[0], lo, hi);
-            a = lo;
-            b = hi;
-        }
-        if (rotated) {
-            const float c = cs[0], sn = cs[1];
-            const float ac = a * c, bs = b * sn, bc = b * c, as = a * sn;
-            const float ra = ac - bs, rb = bc + as;
-            bad |= !is_finite_f(ra) || !is_finite_f(rb);
-            a = ra;
-            b = rb;
-        }
-        if constexpr (K == 2) {
-            x[0] = a;
-            x[1] = b;
-        } else {
-            x[0] = lane < half ? a : b;
+        for (int q = 0; q < NP; ++q) {
+            // a = element j, b = element j + half: with D >= 128 x[q] and
+            // x[q + K/2] of this lane; with D = 64 this lane's x[0] and the
+            // one of lane ^ 32.
+            float a, b;
+            if constexpr (K >= 2) {
+                a = x[q];
+                b = x[q + K / 2];
+            } else {
+                float lo, hi;
+                lane_pair<32>(x[0], lo, hi);
+                a = lo;
+                b = hi;
+            }
+            if (rotated[q]) {
+                const float c = cs[q][0], sn = cs[q][1];
+                const float ac = a * c, bs = b * sn, bc = b * c, as = a * sn;
+                const float ra = ac - bs, rb = bc + as;
+                bad |= !is_finite_f(ra) || !is_finite_f(rb);
+                a = ra;
+                b = rb;
+            }
+            if constexpr (K >= 2) {
+                x[q] = a;
+                x[q + K / 2] = b;
+            } else {
+                x[0] = lane < half ? a : b;
+            }
         }
     }
     for (int k = 0; k < K; ++k) y[k] = x[k];
@@ -403,6 +412,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         fz.v_cache = fa.v_cache;
         fz.head_stride = fa.head_stride;
         fz.new_key = fa.new_key;
+        fz.new_row = fa.new_row;
     }
     pin_scalar(nproblems);
     pin_scalar(bcount);
@@ -431,6 +441,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         pin_scalar(fz.v_cache);
         pin_scalar(fz.head_stride);
         pin_scalar(fz.new_key);
+        pin_scalar(fz.new_row);
     }
     if (bcount > 0) {
         // A compact batch: one segment, one query token at the last key.
@@ -559,7 +570,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
                     } else {
                         lds_new[(is_k ? 0 : CPL * 8) + lane] = chunk;
                         void *cache = is_k ? f.k_cache : f.v_cache;
-                        const int64_t row0 = ((int64_t)kvh * f.head_stride + f.new_key * D) * ES;
+                        const int64_t row0 = ((int64_t)kvh * f.head_stride + f.new_row * D) * ES;
                         *gstore_ptr<u32x4>(reinterpret_cast<uint8_t *>(cache) + row0 + 16 * lane) = chunk;
                     }
                 }
@@ -943,14 +954,21 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
 namespace tkh {
 
 // Launch of one attn_decode geometry: the softcap and fused-producer variants.
-// The producer is folded in only for rows of at most 256 bytes (its per-lane
-// row copy fits the register budget there).
+// The producer is folded in for bf16/f16 rows (head_dim 64 to 256) and, with
+// the score softcap, for head_dim 256 (Gemma's sliding and global layers).
 template <int DT, int DD, int RR, int UU>
 hipError_t decode_launch_variant(const DecodeArgs *a, int fused, dim3 grid, dim3 block,
                                  hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     if (fused) {
-        if constexpr (DD * Elem<DT>::size <= 256) {
-            if (a->p.softcap != 0.0f) return hipErrorInvalidValue;
+        if constexpr (DT != F32 && DD * Elem<DT>::size <= 512) {
+            if (a->p.softcap != 0.0f) {
+                if constexpr (DD == 256) {
+                    hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, true, true>), grid, block, 0,
+                                          stream, start, stop, 0, *a);
+                    return hipGetLastError();
+                }
+                return hipErrorInvalidValue;
+            }
             hipExtLaunchKernelGGL((attn_decode<DT, DD, RR, UU, false, true>), grid, block, 0, stream,
                                   start, stop, 0, *a);
             return hipGetLastError();

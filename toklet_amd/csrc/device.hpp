@@ -96,8 +96,9 @@ struct ProduceParams {
 // Decode steps of a session with the producer folded in: one new token whose
 // Q/K/V projections are normalised, rotated and rounded inside the decode
 // kernel (every workgroup makes the Q rows it needs; the workgroup whose key
-// split holds the new key makes that K/V row, uses it, and stores it into the
-// cache row `new_key`).
+// split holds the new key makes that K/V row, uses it, and stores it into
+// cache row `new_row`: the row of key `new_key` in a linear cache, or a ring
+// layer's staging row, which the gated commit copies into the ring).
 struct FusedDecode {
     const float *q_proj;   // [Hq, D] FP32
     const float *k_proj;   // [Hkv, D]
@@ -111,6 +112,7 @@ struct FusedDecode {
     void *v_cache;
     int64_t head_stride;
     int64_t new_key;       // logical key index of the new token
+    int64_t new_row;       // cache row its K/V go to (new_key for a linear cache, 0 for a ring's stage)
 };
 
 struct Params {
@@ -142,6 +144,25 @@ struct Params {
     uint64_t split_wait_ticks;  // bound of that wait, s_memrealtime ticks
     FusedDecode fused;      // decode kernel built with FUSED only
     Problem single;         // the problem itself when nproblems == 1 (no descriptor upload)
+};
+
+// The ring commits of one chunk (one per sliding layer) in a single launch:
+// entry i copies its staged rows [heads, tokens, row_bytes] into up to two
+// runs of ring slots, runs {source row, slot, rows} (kv_copy_batch).
+constexpr int COPY_BATCH_MAX = 16;
+struct CopyRunsEntry {
+    const uint8_t *src_k, *src_v;
+    uint8_t *dst_k, *dst_v;
+    int64_t tokens, row_bytes, capacity;
+    int64_t runs[6];
+    int32_t heads;
+};
+struct CopyBatch {
+    CopyRunsEntry e[COPY_BATCH_MAX];
+    int32_t count;
+    const uint32_t *gate;
+    uint64_t *committed;
+    uint64_t committed_value;
 };
 
 // A batch of single-segment, single-token decode problems (tkh_decode_batch of

@@ -172,6 +172,13 @@ namespace tkh_host {
 uint32_t attention_cached_fused(tkh_context *ctx, const tkh_cached_shape *shape, tkh_dtype dtype,
                                 const void *k, const void *v, float *context,
                                 const tkh::FusedDecode &fused, tkh_error *err);
+// span_attention of one token (the last key of the view) with the producer
+// folded into the decode kernel: the session's decode steps of layers with a
+// score scale, softcap or window, and of ring caches (the new K/V row goes to
+// the layer's staging row, fused.new_row 0).
+uint32_t span_attention_fused(tkh_context *ctx, const tkh_span_shape *shape, tkh_dtype dtype,
+                              const tkh_segment segments[3], float *context,
+                              const tkh::FusedDecode &fused, tkh_error *err);
 // tkh_kv_commit_batch with an optional device gate (api.cpp).
 uint32_t commit_frames(tkh_kv *const *kvs, const tkh_kv_frame *frames, uint64_t count,
                        const uint32_t *gate, uint64_t *committed, uint64_t committed_value,

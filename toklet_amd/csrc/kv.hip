@@ -87,6 +87,31 @@ __global__ __launch_bounds__(256) void kv_copy_runs(const uint8_t *src_k, const 
     }
 }
 
+// kv_copy_runs for several rings at once: blockIdx.y is the entry.  The gate
+// is read once per workgroup before any copy, so either every entry is
+// copied or none is, as with one launch per ring in a row.
+__global__ __launch_bounds__(256) void kv_copy_batch(CopyBatch b) {
+    if (b.gate && *(volatile const uint32_t *)b.gate != 0) return;
+    if (b.committed && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+        *b.committed = b.committed_value;
+    const CopyRunsEntry &e = b.e[blockIdx.y];
+    const int64_t words = e.row_bytes / 2;
+    const int64_t r0_rows = e.runs[2], rows = e.runs[2] + e.runs[5];
+    const int64_t total = (int64_t)e.heads * rows * words;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t w = i % words;
+        const int64_t r = (i / words) % rows;
+        const int64_t h = i / (words * rows);
+        const int64_t srow = r < r0_rows ? e.runs[0] + r : e.runs[3] + (r - r0_rows);
+        const int64_t slot = r < r0_rows ? e.runs[1] + r : e.runs[4] + (r - r0_rows);
+        const int64_t sidx = ((h * e.tokens + srow) * e.row_bytes) / 2 + w;
+        const int64_t didx = ((h * e.capacity + slot) * e.row_bytes) / 2 + w;
+        reinterpret_cast<uint16_t *>(e.dst_k)[didx] = reinterpret_cast<const uint16_t *>(e.src_k)[sidx];
+        reinterpret_cast<uint16_t *>(e.dst_v)[didx] = reinterpret_cast<const uint16_t *>(e.src_v)[sidx];
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void check_finite(const void *a, const void *b, int64_t n,
                                                     uint32_t *status) {
@@ -169,6 +194,19 @@ extern "C" hipError_t tkh_launch_copy_runs(const void *src_k, const void *src_v,
                        (const uint8_t *)src_v, (uint8_t *)dst_k, (uint8_t *)dst_v, tokens, heads,
                        row_bytes, capacity, runs[0], runs[1], runs[2], runs[3], runs[4], runs[5],
                        gate, committed, committed_value);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t tkh_launch_copy_batch(const tkh::CopyBatch *b, hipStream_t stream) {
+    using namespace tkh;
+    if (b->count < 1 || b->count > COPY_BATCH_MAX) return hipErrorInvalidValue;
+    int64_t most = 1;
+    for (int i = 0; i < b->count; ++i) {
+        const auto &e = b->e[i];
+        most = std::max<int64_t>(most, (int64_t)e.heads * (e.runs[2] + e.runs[5]) * (e.row_bytes / 2));
+    }
+    dim3 grid(grid_for(most), (unsigned)b->count), block(256);
+    hipLaunchKernelGGL(kv_copy_batch, grid, block, 0, stream, *b);
     return hipGetLastError();
 }
 

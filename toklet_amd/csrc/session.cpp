@@ -317,14 +317,18 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
     }
     s->history.reserve(o->capacity);
     // Decode steps with the producer inside the decode kernel (one launch per
-    // step instead of two; TKH_FUSED_DECODE=0 turns it off): head sizes of
-    // that kernel, GQA groups of at most 1 KiB of cache-dtype rows, no softcap.
+    // step and layer instead of two; TKH_FUSED_DECODE=0 turns it off): the
+    // kernel's bf16/f16 builds of head_dim 64, 128 and 256 (256: with or
+    // without the score softcap; 64 and 128: without), GQA groups of at most
+    // 1 KiB of cache-dtype rows.
     {
         const uint64_t G = o->query_heads / o->kv_heads;
         const uint64_t rowb = o->head_dim * (uint64_t)esize(o->storage);
         const uint64_t limit = rowb <= 256 ? 8 : (rowb <= 512 ? 4 : 2);
-        s->fused_decode = (o->head_dim == 64 || o->head_dim == 128) && rowb <= 256 &&
-                          G <= limit && G * rowb <= 1024 && env_int("TKH_FUSED_DECODE", 1) != 0;
+        const bool dims = o->head_dim == 64 || o->head_dim == 128 || o->head_dim == 256;
+        s->fused_decode = dims && o->storage != TKH_F32 && G <= limit && G * rowb <= 1024 &&
+                          (o->softcap == 0.0f || o->head_dim == 256) &&
+                          env_int("TKH_FUSED_DECODE", 1) != 0;
     }
     if (ctx) {
         const uint64_t D = o->head_dim, es = (uint64_t)esize(o->storage);
@@ -513,8 +517,11 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
         tkh_kv *kv = s->kv[l];
         const bool ring = kv->has_window;
         const uint64_t window = s->windows[l];
-        if (!ring && count == 1 && o.score_scale == 0.0f && s->fused_decode) {
-            // A decode step: the producer runs inside the decode kernel.
+        // A decode step folds the producer into the decode kernel: its Q/K/V
+        // projections are normalised, rotated and rounded there, and the new
+        // K/V row goes to the cache (linear) or the staging rows (ring).
+        auto fused_desc = [&](void *kc, void *vc, int64_t head_stride, int64_t new_key,
+                              int64_t new_row) {
             tkh::FusedDecode f{};
             f.q_proj = q;
             f.k_proj = k;
@@ -524,10 +531,43 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
             f.pairs = tkh_rotary_pairs((int)o.rotary, (int)D, (int)o.rotated_dims);
             f.rope = f.pairs > 0 ? s->rope + 2 * start * (uint64_t)f.pairs : nullptr;
             f.eps = o.norm_epsilon;
-            f.k_cache = kv->k;
-            f.v_cache = kv->v;
-            f.head_stride = (int64_t)(kv->capacity * D);
-            f.new_key = (int64_t)start;
+            f.k_cache = kc;
+            f.v_cache = vc;
+            f.head_stride = head_stride;
+            f.new_key = new_key;
+            f.new_row = new_row;
+            return f;
+        };
+        const bool fused_step = count == 1 && s->fused_decode;
+        if (!ring && fused_step && o.score_scale != 0.0f) {
+            // Window/score-scale layer with a linear cache: the span form over
+            // keys [first visible, start] of the cache.
+            tkh_span_shape span{};
+            const uint64_t first = window != 0 && start + 1 > window ? start + 1 - window : 0;
+            span.queries = 1;
+            span.keys = start + 1 - first;
+            span.query_heads = Hq;
+            span.kv_heads = Hkv;
+            span.head_dim = D;
+            span.query_start = start;
+            span.key_start = first;
+            span.has_window = window != 0;
+            span.window = window;
+            span.scale = o.score_scale;
+            span.softcap = o.softcap;
+            const uint64_t stride = kv->capacity * D;
+            tkh_segment segs[3]{};
+            segs[0] = tkh_segment{(const uint8_t *)kv->k + first * D * es, (Hkv - 1) * stride + span.keys * D,
+                                  (const uint8_t *)kv->v + first * D * es, (Hkv - 1) * stride + span.keys * D,
+                                  span.keys, stride, first};
+            segs[1].key_start = segs[2].key_start = start + 1;
+            const tkh::FusedDecode f = fused_desc(kv->k, kv->v, (int64_t)stride,
+                                                  (int64_t)(span.keys - 1), (int64_t)start);
+            TRY(span_attention_fused(ctx, &span, o.storage, segs, context, f, err));
+        } else if (!ring && fused_step) {
+            // attention_cached form: every key up to the new one.
+            const tkh::FusedDecode f = fused_desc(kv->k, kv->v, (int64_t)(kv->capacity * D),
+                                                  (int64_t)start, (int64_t)start);
             tkh_cached_shape cs{1, Hq, Hkv, D, kv->capacity, start};
             TRY(attention_cached_fused(ctx, &cs, o.storage, kv->k, kv->v, context, f, err));
         } else if (!ring) {
@@ -566,9 +606,10 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
                             "ring cache of layer %llu is at %llu, chunk starts at %llu",
                             (unsigned long long)l, (unsigned long long)kv->offset,
                             (unsigned long long)start);
-            TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
-                                s->stage_k[l], s->stage_v[l], count * D, err, s->rope,
-                                o.position_offset));
+            if (!fused_step)
+                TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
+                                    s->stage_k[l], s->stage_v[l], count * D, err, s->rope,
+                                    o.position_offset));
             tkh_kv_frame f{};
             f.k = s->stage_k[l];
             f.v = s->stage_v[l];
@@ -580,8 +621,15 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
             tkh_span_shape span{};
             TRY(tkh_kv_view(kv, &f, Hq, o.score_scale, segs, &span, err));
             span.softcap = o.softcap;
-            TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
-                                   context, count * Hq * D, nullptr, 0, nullptr, 0, err));
+            if (fused_step) {
+                // The new row is the view's last key; its K/V go to staging row 0.
+                const tkh::FusedDecode fd = fused_desc(s->stage_k[l], s->stage_v[l], (int64_t)D,
+                                                       (int64_t)(span.keys - 1), 0);
+                TRY(span_attention_fused(ctx, &span, o.storage, segs, context, fd, err));
+            } else {
+                TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
+                                       context, count * Hq * D, nullptr, 0, nullptr, 0, err));
+            }
             ring_kv.push_back(kv);
             frames.push_back(f);
         }
