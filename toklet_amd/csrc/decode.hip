@@ -54,3 +54,96 @@ extern "C" hipError_t tkh_launch_decode(const tkh::DecodeArgs *p, int dtype, int
     if (dtype == tkh::F32 && head_dim == 256) return tkh_decode_launch_f32_256(p, rows, keys_per_lane, fused, grid, block, stream, start, stop);
     return hipErrorInvalidValue;
 }
+
+namespace tkh {
+// Split-K combine of a single-problem decode launch, as a second kernel: one
+// wave per 64 outputs of one row of one KV head.  Lane (g4, q4) = (lane / 16,
+// lane % 16) reads, for splits 4 g + g4, the four outputs d0 + 4 q4 .. + 3
+// (16-byte buffer loads) and the split's (max, mass); lanes past the last
+// split read beyond the buffer range, which returns zeros, so every load is
+// issued in one straight run.  The partial slot of split s is slot_base +
+// kvh * S + s with `rows` rows (the decode build's R).  Weights 2^(m_s - M)
+// in the kernel's log2 units; the context is divided by the mass.
+template <int D>
+__global__ __launch_bounds__(64) void attn_decode_merge(Params p, int rows) {
+    constexpr int CH = D / 64;  // 64-output chunks per row
+    const Problem &pr = p.single;
+    const int S = pr.splits, G = p.group, Hq = p.query_heads;
+    const int nrows = pr.queries * G;
+    const int b = blockIdx.x;
+    const int c = b % CH, r = (b / CH) % nrows, kvh = b / (CH * nrows);
+    const int lane = threadIdx.x, g4 = lane >> 4, q4 = lane & 15;
+    const int d = 64 * c + 4 * q4;
+    const int64_t slot0 = pr.slot_base + (int64_t)kvh * S;
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(p.part_ml, 0, 0x7FFFFFFF, BUFFER_RSRC_WORD3);
+    const uint32_t o_base = (uint32_t)(reinterpret_cast<const char *>(p.part_o) -
+                                       reinterpret_cast<const char *>(p.part_ml));
+    const uint32_t ml0 = (uint32_t)((slot0 * rows + r) * 2) * 4u, ml_step = (uint32_t)rows * 8u;
+    const uint32_t o0 = o_base + (uint32_t)((slot0 * rows + r) * D + d) * 4u,
+                   o_step = (uint32_t)(rows * D) * 4u;
+    constexpr int NG = DECODE_MAX_SPLITS / 4;
+    f32x4 ov[NG];
+    f32x2 mv[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int sp = 4 * g + g4;
+        const bool in = sp < S;
+        ov[g] = __builtin_amdgcn_raw_buffer_load_b128(prs, in ? o0 + (uint32_t)sp * o_step : OUT_OF_RANGE, 0, 0);
+        mv[g] = __builtin_amdgcn_raw_buffer_load_b64(prs, in ? ml0 + (uint32_t)sp * ml_step : OUT_OF_RANGE, 0, 0);
+    }
+    float mmax = NEG_INF;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        if (4 * g + g4 >= S) mv[g][0] = NEG_INF;
+        mmax = fmaxf(mmax, mv[g][0]);
+    }
+    float pa, pb;
+    lane_pair<16>(mmax, pa, pb);
+    lane_pair<32>(fmaxf(pa, pb), pa, pb);
+    const float M = fmaxf(pa, pb);
+    const float base = M == NEG_INF ? 0.0f : M;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float lsum = 0.0f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const float w = __builtin_amdgcn_exp2f(mv[g][0] - base);
+        for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(w, ov[g][k], acc[k]);
+        lsum = __builtin_fmaf(w, mv[g][1], lsum);
+    }
+    lane_pair<16>(lsum, pa, pb);
+    lane_pair<32>(pa + pb, pa, pb);
+    const float L = pa + pb;
+    for (int k = 0; k < 4; ++k) {
+        float x, y;
+        lane_pair<16>(acc[k], x, y);
+        lane_pair<32>(x + y, x, y);
+        acc[k] = x + y;
+    }
+    const bool bad_mass = !(L > 0.0f) || !is_finite_f(L);
+    bool bad_out = false;
+    if (g4 == 0) {
+        f32x4 v;
+        for (int k = 0; k < 4; ++k) {
+            v[k] = acc[k] / L;
+            bad_out |= !is_finite_f(v[k]);
+        }
+        const int t = r / G, h = kvh * G + r % G;
+        *gstore_ptr<f32x4>(pr.out + ((int64_t)t * Hq + h) * D + d) = v;
+    }
+    raise_status(p, bad_mass, ST_BAD_MASS);
+    raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
+}
+}  // namespace tkh
+
+extern "C" hipError_t tkh_launch_decode_merge(const tkh::Params *p, int head_dim, int rows, int kv_heads,
+                                               hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+    using namespace tkh;
+    const int nrows = p->single.queries * p->group;
+    const dim3 grid((unsigned)(kv_heads * nrows * (head_dim / 64))), block(64);
+    if (head_dim == 64) hipExtLaunchKernelGGL(attn_decode_merge<64>, grid, block, 0, stream, start, stop, 0, *p, rows);
+    else if (head_dim == 128) hipExtLaunchKernelGGL(attn_decode_merge<128>, grid, block, 0, stream, start, stop, 0, *p, rows);
+    else if (head_dim == 256) hipExtLaunchKernelGGL(attn_decode_merge<256>, grid, block, 0, stream, start, stop, 0, *p, rows);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}

@@ -808,6 +808,14 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
             const float v = O / L;
             bad_out |= !is_finite_f(v);
             gstore_ptr<float>(out)[((int64_t)t * Hq + h) * D + d] = v;
+        } else if (p.merge_launch) {
+            // Combined by attn_decode_merge after this kernel: the kernel
+            // boundary orders the stores, so they are plain.
+            p.part_o[(slot * R + r) * D + d] = O;
+            if (d == 0) {
+                p.part_ml[(slot * R + r) * 2 + 0] = M;
+                p.part_ml[(slot * R + r) * 2 + 1] = L;
+            }
         } else if (split == pv.splits - 1) {
             lds_own[r * D + d] = O;
             if (d == 0) {
@@ -828,6 +836,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
         return;
     }
+    if (p.merge_launch) return;
 
     // Split-K completion without atomics: every split but the last stores its
     // partial, waits until the stores are acknowledged, and then stores this

@@ -142,6 +142,7 @@ struct Params {
     uint32_t epoch;         // decode split-K: this launch's flag value (never 0; flags start at 0)
     uint32_t wait_epoch;    // the flag value the merging split waits for (= epoch)
     uint64_t split_wait_ticks;  // bound of that wait, s_memrealtime ticks
+    int32_t merge_launch;   // decode split-K: every split stores its partial; attn_decode_merge combines
     FusedDecode fused;      // decode kernel built with FUSED only
     Problem single;         // the problem itself when nproblems == 1 (no descriptor upload)
 };
