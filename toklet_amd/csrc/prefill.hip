@@ -87,6 +87,26 @@ __device__ __forceinline__ float add_pair(uint32_t w, float l) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), ones, l, false);
 }
 
+// Maximum and minimum of three (two) floats in one instruction, maxNum /
+// minNum semantics (a NaN operand is ignored; NaN scores reach the context
+// through their probabilities).  Written out because fmaxf/fminf chains
+// compile with a canonicalising v_max per operand.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float min3f(float a, float b, float c) {
+    float r;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float max2f(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 __device__ __forceinline__ u32x2 read_tr(lds_ptr<uint8_t> p) {
     const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)p);
     return __builtin_bit_cast(u32x2, r);
@@ -399,6 +419,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     for (int mb = 0; mb < MB; ++mb)
         for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
     float m_run = NEG_INF, l_run = 0.0f;
+    // The smallest visible score of fully visible tiles (a -inf one is a
+    // non-finite score) and the exp base -m_run * tmul, updated with m_run.
+    float lo_run = -NEG_INF, nbase_run = 0.0f;
     bool bad = false;  // an infinite visible score (NaN reaches the mass and the context)
     const float scale = p.scale, softcap = p.softcap, softcap_inv = p.softcap_inv;
     const float tmul = CAP ? 1.0f : p.scale_log2;  // t units -> log2 units
@@ -538,13 +561,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             __builtin_amdgcn_sched_barrier(0);
             if (k == 0) {
                 if (bulk || (t >= tf_lo && t < tf_hi)) {
-                    hi = fmaxf(fmaxf(st[0], st[1]), st[2]);
-                    float lo = fminf(fminf(st[0], st[1]), st[2]);
-                    for (int i = 3; i < 16; ++i) {
-                        hi = fmaxf(hi, st[i]);
-                        lo = fminf(lo, st[i]);
-                    }
-                    bad |= lo == NEG_INF;
+                    hi = max3f(st[0], st[1], st[2]);
+                    float lo = min3f(lo_run, st[0], st[1]);
+                    for (int i = 3; i < 15; i += 2) hi = max3f(hi, st[i], st[i + 1]);
+                    hi = max2f(hi, st[15]);
+                    for (int i = 2; i < 16; i += 2) lo = min3f(lo, st[i], st[i + 1]);
+                    lo_run = lo;
                     if constexpr (CAP)
                         for (int i = 0; i < 16; ++i) tv[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
                 } else {
@@ -562,14 +584,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                 }
             }
             if (k == (NPV > 1 ? 1 : 0)) {
-                bad |= hi == -NEG_INF;
+                // A +inf score: checked here under the softcap (which maps it
+                // to the cap); otherwise it becomes the running maximum, which
+                // is checked once after the loop.
+                if constexpr (CAP) bad |= hi == -NEG_INF;
                 float mt;
                 if constexpr (CAP) mt = hi == NEG_INF ? NEG_INF : softcap_fast(hi * scale, softcap, softcap_inv) * LOG2E;
                 else mt = hi;
                 const uint32_t u = __builtin_bit_cast(uint32_t, mt);
                 const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
                 const uint32_t a0 = pr32[0], a1 = pr32[1];
-                mt = fmaxf(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+                mt = max2f(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
                 // Rare: a maximum moved past the slack.  l and the maximum change
                 // now; O, which still receives tile t - 1's P.V, after step 1.
                 if (__ballot(mt > m_thr) != 0) {
@@ -579,12 +604,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                         l_run *= corr;
                         m_run = m_new;
                         m_thr = m_new == NEG_INF ? NEG_INF : m_new + slack;
+                        nbase_run = m_new == NEG_INF ? 0.0f : -m_new * tmul;
                     }
                     rescale = true;
                     if constexpr (!CAP)
                         huge = __ballot(m_run != NEG_INF && fabsf(m_run * tmul) >= 1024.0f) != 0;
                 }
-                nbase = m_run == NEG_INF ? 0.0f : -m_run * tmul;
+                nbase = nbase_run;
                 if constexpr (!CAP) {
                     if (huge) {
                         const float mr = m_run == NEG_INF ? 0.0f : m_run;
@@ -702,6 +728,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             acc[mb] = mfma32<PDT>(vop[stp][mb], bv, acc[mb]);
         }
     }
+    bad |= lo_run == NEG_INF;
+    if constexpr (!CAP) bad |= m_run == -NEG_INF;
     // ---- the two key halves of each row (lanes j and j + 32) share m_run; add l.
     {
         const uint32_t u = __builtin_bit_cast(uint32_t, l_run);
