@@ -17,7 +17,8 @@
 //    LDS with coalesced 16-byte loads (rows padded to 68 floats, so a lane's
 //    16-byte reads of its own row hit distinct bank groups within each
 //    16-lane phase) while the context tile is read by every lane at once (a
-//    broadcast).  At the end the workgroup reduces, per row, the best
+//    broadcast); the next tile's loads are in flight while a tile is
+//    multiplied.  At the end the workgroup reduces, per row, the best
 //    (key, id) pair of its 256 candidates and stores it.
 //  * project_pick: one wave per row reduces those pairs to the token.
 //
@@ -68,33 +69,10 @@ __global__ __launch_bounds__(256) void project_logits(ProjectParams p) {
     float acc[R];
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-    for (int64_t d0 = 0; d0 < H; d0 += PJ_D) {
-        const int dn = (int)(H - d0 < PJ_D ? H - d0 : PJ_D);
-        __syncthreads();
-        if constexpr (VEC) {
-            // 16 chunks of 4 features per row; thread t covers row i >> 4.
-            for (int i = t; i < PJ_V * (PJ_D / 4); i += 256) {
-                const int row = i >> 4, c = i & 15;
-                const int64_t v = v0 + row;
-                f32x4 x = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (v < p.vocab && 4 * c < dn) x = *gload_ptr<f32x4>(p.weights + v * H + d0 + 4 * c);
-                *reinterpret_cast<f32x4 *>(wt + row * PJ_PAD + 4 * c) = x;
-            }
-        } else {
-            for (int i = t; i < PJ_V * PJ_D; i += 256) {
-                const int row = i / PJ_D, c = i % PJ_D;
-                const int64_t v = v0 + row;
-                wt[row * PJ_PAD + c] = v < p.vocab && c < dn ? p.weights[v * H + d0 + c] : 0.0f;
-            }
-        }
-        for (int i = t; i < R * PJ_D; i += 256) {
-            const int r = i / PJ_D, c = i % PJ_D;
-            ct[i] = r < nr && c < dn ? p.context[(r0 + r) * H + d0 + c] : 0.0f;
-        }
-        __syncthreads();
-        // Features past the end of the range are zeros in both tiles: adding
-        // their +-0 products leaves every sum unchanged (a sum that starts at
-        // +0 is never -0).
+    // Features past the end of the range are zeros in both tiles: adding
+    // their +-0 products leaves every sum unchanged (a sum that starts at +0
+    // is never -0).
+    auto compute = [&]() {
         for (int q = 0; q < PJ_D / 4; ++q) {
             const f32x4 w = *reinterpret_cast<const f32x4 *>(wt + t * PJ_PAD + 4 * q);
             for (int r = 0; r < R; ++r) {
@@ -106,6 +84,67 @@ __global__ __launch_bounds__(256) void project_logits(ProjectParams p) {
                 s = s + c[3] * w[3];
                 acc[r] = s;
             }
+        }
+    };
+
+    if constexpr (VEC) {
+        // Thread t stages chunks i = t + 256 n (n < 16) of the tile: row i / 16,
+        // features 4 (i % 16) ..+3; the context tile's R x 16 chunks likewise.
+        // A tile's loads are all issued at once, and the next tile's go out
+        // before the current one is multiplied, so every thread keeps a whole
+        // tile in flight instead of one load at a time.
+        constexpr int NW = PJ_V * (PJ_D / 4) / 256;            // weight chunks per thread
+        constexpr int NC = (R * (PJ_D / 4) + 255) / 256;       // context chunks per thread
+        f32x4 wb[NW], cb[NC];
+        auto load = [&](int64_t d0) {
+            const int dn = (int)(H - d0 < PJ_D ? H - d0 : PJ_D);
+#pragma unroll
+            for (int n = 0; n < NW; ++n) {
+                const int i = t + 256 * n, row = i >> 4, c = i & 15;
+                const int64_t v = v0 + row;
+                wb[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (v < p.vocab && 4 * c < dn) wb[n] = *gload_ptr<f32x4>(p.weights + v * H + d0 + 4 * c);
+            }
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                const int i = t + 256 * n, r = i >> 4, c = i & 15;
+                cb[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (i < R * (PJ_D / 4) && r < nr && 4 * c < dn)
+                    cb[n] = *gload_ptr<f32x4>(p.context + (r0 + r) * H + d0 + 4 * c);
+            }
+        };
+        load(0);
+        for (int64_t d0 = 0; d0 < H; d0 += PJ_D) {
+            __syncthreads();  // the previous tile is no longer read
+#pragma unroll
+            for (int n = 0; n < NW; ++n) {
+                const int i = t + 256 * n;
+                *reinterpret_cast<f32x4 *>(wt + (i >> 4) * PJ_PAD + 4 * (i & 15)) = wb[n];
+            }
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                const int i = t + 256 * n;
+                if (i < R * (PJ_D / 4)) *reinterpret_cast<f32x4 *>(ct + (i >> 4) * PJ_D + 4 * (i & 15)) = cb[n];
+            }
+            __syncthreads();
+            if (d0 + PJ_D < H) load(d0 + PJ_D);
+            compute();
+        }
+    } else {
+        for (int64_t d0 = 0; d0 < H; d0 += PJ_D) {
+            const int dn = (int)(H - d0 < PJ_D ? H - d0 : PJ_D);
+            __syncthreads();
+            for (int i = t; i < PJ_V * PJ_D; i += 256) {
+                const int row = i / PJ_D, c = i % PJ_D;
+                const int64_t v = v0 + row;
+                wt[row * PJ_PAD + c] = v < p.vocab && c < dn ? p.weights[v * H + d0 + c] : 0.0f;
+            }
+            for (int i = t; i < R * PJ_D; i += 256) {
+                const int r = i / PJ_D, c = i % PJ_D;
+                ct[i] = r < nr && c < dn ? p.context[(r0 + r) * H + d0 + c] : 0.0f;
+            }
+            __syncthreads();
+            compute();
         }
     }
 
