@@ -46,6 +46,8 @@ extern "C" int tkh_decode_max_rows(int dtype, int head_dim);
 extern "C" int tkh_prefill_waves(int head_dim, int wide);
 extern "C" hipError_t tkh_launch_decode_merge(const tkh::Params *p, int head_dim, int rows, int kv_heads,
                                               hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+extern "C" hipError_t tkh_launch_decode_merge_batch(const tkh::DecodeArgs *a, int head_dim, int rows,
+                                                    hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 extern "C" hipError_t tkh_launch_copy_batch(const tkh::CopyBatch *b, hipStream_t stream);
 extern "C" int tkh_prefill_max_splits(void);
 extern "C" int tkh_prefill_merge_rows_per_block(int head_dim);
@@ -433,8 +435,9 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, Problems group,
     // exits, and the kernel boundary orders the stores, instead of the
     // in-kernel merge's three memory round trips between workgroups.
     // (The bounded-wait test hook exercises the in-kernel merge.)
-    const bool merge_launch = split && group.size() == 1 && !bulk && ctx->decode_merge_launch &&
-                              !ctx->test_flag_skew;
+    const bool merge_batch = split && cb.count > 0 && ctx->decode_merge_batch && !ctx->test_flag_skew;
+    const bool merge_launch = merge_batch || (split && group.size() == 1 && !bulk &&
+                                              ctx->decode_merge_launch && !ctx->test_flag_skew);
     prm.merge_launch = merge_launch ? 1 : 0;
     hipEvent_t *ev = nullptr;
     if (ctx->profiling) TRY(profile_slot(ctx, &ev, merge_launch, err));
@@ -443,7 +446,11 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, Problems group,
                                      plan.fused ? 1 : 0, ctx->stream, ev ? ev[0] : nullptr,
                                      ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "decode launch", err);
-    if (merge_launch) {
+    if (merge_batch) {
+        e = tkh_launch_decode_merge_batch(&args, (int)D, R, ctx->stream, ev ? ev[2] : nullptr,
+                                          ev ? ev[3] : nullptr);
+        if (e != hipSuccess) return device_error(e, "decode merge launch", err);
+    } else if (merge_launch) {
         e = tkh_launch_decode_merge(&prm, (int)D, R, (int)Hkv, ctx->stream, ev ? ev[2] : nullptr,
                                     ev ? ev[3] : nullptr);
         if (e != hipSuccess) return device_error(e, "decode merge launch", err);
@@ -705,6 +712,7 @@ void init_tuning(tkh_context *ctx, int device) {
     ctx->decode_max_splits = std::max(1, env_int("TKH_DECODE_MAX_SPLITS", 64));
     ctx->decode_disable = env_int("TKH_DECODE_DISABLE", 0);
     ctx->decode_merge_launch = env_int("TKH_DECODE_MERGE_LAUNCH", 1) != 0;
+    ctx->decode_merge_batch = env_int("TKH_DECODE_MERGE_BATCH", 0) != 0;
     // Split target: 128 workgroups.  At configs[1] chunk sizes (16 row blocks)
     // that is 8 key splits instead of the 16 a 512 target gave: half the
     // partials to write and merge, 21.7 -> 21.0 us per chunk for the two

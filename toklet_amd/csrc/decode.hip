@@ -64,17 +64,15 @@ namespace tkh {
 // issued in one straight run.  The partial slot of split s is slot_base +
 // kvh * S + s with `rows` rows (the decode build's R).  Weights 2^(m_s - M)
 // in the kernel's log2 units; the context is divided by the mass.
+// One wave's share of the combine: 64 outputs of row r of KV head kvh of a
+// problem with S splits whose partials start at slot_base.
 template <int D>
-__global__ __launch_bounds__(64) void attn_decode_merge(Params p, int rows) {
-    constexpr int CH = D / 64;  // 64-output chunks per row
-    const Problem &pr = p.single;
-    const int S = pr.splits, G = p.group, Hq = p.query_heads;
-    const int nrows = pr.queries * G;
-    const int b = blockIdx.x;
-    const int c = b % CH, r = (b / CH) % nrows, kvh = b / (CH * nrows);
+__device__ __forceinline__ void merge_chunk(const Params &p, int rows, int S, int64_t slot_base,
+                                            float *out, int kvh, int r, int c) {
+    const int G = p.group, Hq = p.query_heads;
     const int lane = threadIdx.x, g4 = lane >> 4, q4 = lane & 15;
     const int d = 64 * c + 4 * q4;
-    const int64_t slot0 = pr.slot_base + (int64_t)kvh * S;
+    const int64_t slot0 = slot_base + (int64_t)kvh * S;
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc(p.part_ml, 0, 0x7FFFFFFF, BUFFER_RSRC_WORD3);
     const uint32_t o_base = (uint32_t)(reinterpret_cast<const char *>(p.part_o) -
@@ -129,12 +127,57 @@ __global__ __launch_bounds__(64) void attn_decode_merge(Params p, int rows) {
             bad_out |= !is_finite_f(v[k]);
         }
         const int t = r / G, h = kvh * G + r % G;
-        *gstore_ptr<f32x4>(pr.out + ((int64_t)t * Hq + h) * D + d) = v;
+        *gstore_ptr<f32x4>(out + ((int64_t)t * Hq + h) * D + d) = v;
     }
     raise_status(p, bad_mass, ST_BAD_MASS);
     raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
 }
+
+// Split-K combine of a single-problem decode launch, as a second kernel: one
+// wave per 64 outputs of one row of one KV head.  Lane (g4, q4) = (lane / 16,
+// lane % 16) reads, for splits 4 g + g4, the four outputs d0 + 4 q4 .. + 3
+// (16-byte buffer loads) and the split's (max, mass); lanes past the last
+// split read beyond the buffer range, which returns zeros, so every load is
+// issued in one straight run.  The partial slot of split s is slot_base +
+// kvh * S + s with `rows` rows (the decode build's R).  Weights 2^(m_s - M)
+// in the kernel's log2 units; the context is divided by the mass.
+template <int D>
+__global__ __launch_bounds__(64) void attn_decode_merge(Params p, int rows) {
+    constexpr int CH = D / 64;  // 64-output chunks per row
+    const Problem &pr = p.single;
+    const int nrows = pr.queries * p.group;
+    const int b = blockIdx.x;
+    const int c = b % CH, r = (b / CH) % nrows, kvh = b / (CH * nrows);
+    merge_chunk<D>(p, rows, pr.splits, pr.slot_base, pr.out, kvh, r, c);
+}
+
+// The same for a compact batch (one query token per session): the sessions
+// share Hkv, the GQA group and D, so wave b serves session b / (Hkv G D/64);
+// sessions with one split wrote their context themselves.
+template <int D>
+__global__ __launch_bounds__(64) void attn_decode_merge_batch(Params p, DecodeBatch bt, int rows) {
+    constexpr int CH = D / 64;
+    const int G = p.group;
+    const int per = p.kv_heads * G * CH;
+    const int i = blockIdx.x / per, b = blockIdx.x % per;
+    const DecodeBatchEntry &e = bt.e[i];
+    const int S = (int)e.splits;
+    if (S <= 1) return;
+    const int c = b % CH, r = (b / CH) % G, kvh = b / (CH * G);
+    merge_chunk<D>(p, rows, S, (int64_t)e.tile_base, bt.out + (int64_t)i * p.query_heads * D, kvh, r, c);
+}
 }  // namespace tkh
+
+extern "C" hipError_t tkh_launch_decode_merge_batch(const tkh::DecodeArgs *a, int head_dim, int rows,
+                                                     hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+    using namespace tkh;
+    const dim3 grid((unsigned)(a->b.count * a->p.kv_heads * a->p.group * (head_dim / 64))), block(64);
+    if (head_dim == 64) hipExtLaunchKernelGGL(attn_decode_merge_batch<64>, grid, block, 0, stream, start, stop, 0, a->p, a->b, rows);
+    else if (head_dim == 128) hipExtLaunchKernelGGL(attn_decode_merge_batch<128>, grid, block, 0, stream, start, stop, 0, a->p, a->b, rows);
+    else if (head_dim == 256) hipExtLaunchKernelGGL(attn_decode_merge_batch<256>, grid, block, 0, stream, start, stop, 0, a->p, a->b, rows);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
 
 extern "C" hipError_t tkh_launch_decode_merge(const tkh::Params *p, int head_dim, int rows, int kv_heads,
                                                hipStream_t stream, hipEvent_t start, hipEvent_t stop) {

@@ -124,6 +124,7 @@ struct tkh_context {
     int decode_max_splits = 64;  // cap on key splits per KV head (bounds the merge)
     int decode_disable = 0;
     bool decode_merge_launch = true;  // single-problem, latency-bound decode: combine in a second launch
+    bool decode_merge_batch = false;  // compact-batch decode: combine in a second launch
     uint32_t epoch = 0;          // last decode split-K epoch handed out
     uint64_t split_wait_ticks = 50000000;  // bound of a decode merge's wait for its splits
     bool test_flag_skew = false; // test hook: merges wait for a flag value no split stores
