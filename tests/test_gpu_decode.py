@@ -179,12 +179,15 @@ def test_ring_span_decode_wraps(torch_mod, ctx, ops, orc, hq, hkv, D, W, offset)
     assert err <= TOL_HALF
 
 
-@pytest.mark.parametrize("B", [24, 80])
-def test_decode_batch_many_sessions_lengths_to_8192(torch_mod, ctx, ops, orc, B):
+@pytest.mark.parametrize("B,merge_batch", [(24, 0), (80, 0), (24, 1), (64, 1)])
+def test_decode_batch_many_sessions_lengths_to_8192(torch_mod, ctx, ops, orc, B, merge_batch):
     """configs[2] in miniature: f16 sessions, lengths 1..8192, one query token each.
     Up to 64 sessions travel in the decode kernel's arguments; 80 upload their
-    descriptors."""
+    descriptors.  merge_batch: the compact batch's splits combined by a second
+    launch (TKH_DECODE_MERGE_BATCH)."""
     torch = torch_mod
+    if merge_batch:
+        ctx = _context_with_env(ops, {"TKH_DECODE_MERGE_BATCH": 1})
     rng = np.random.default_rng(51)
     hq, hkv, D = 16, 8, 128
     lengths = np.concatenate([[1, 2, 8192, 513], rng.integers(1, 8193, B - 4)])
@@ -210,7 +213,7 @@ def test_decode_batch_many_sessions_lengths_to_8192(torch_mod, ctx, ops, orc, B)
         vb = vpool[offsets[b]:offsets[b] + hkv * L * D]
         ref, _, _ = orc.attention_cached(q[b].reshape(-1), kb, vb, 1, hq, hkv, D, L, L - 1)
         worst = max(worst, max_err(got[b], ref))
-    log(f"decode batch of {B}: worst max abs error {worst:.3e}")
+    log(f"decode batch of {B} (merge launch {merge_batch}): worst max abs error {worst:.3e}")
     assert worst <= TOL_HALF
 
 

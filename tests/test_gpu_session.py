@@ -177,9 +177,14 @@ def test_session_qwen3_prefill_chunks_then_decode_steps(torch_mod, ctx, ops, ses
         assert err <= TOL_HALF
 
 
-def test_session_sliding_and_global_layers_gemma_shape(torch_mod, ctx, ops, sess_mod, orc):
+@pytest.mark.parametrize("fused", ["1", "0"])
+def test_session_sliding_and_global_layers_gemma_shape(torch_mod, ctx, ops, sess_mod, orc, fused):
     """A sliding (W=64, ring cache) and a global layer at 8/4/256, scale 1/16, score
-    softcap 50, proportional rotary: 200 prompt tokens in 64-token chunks, 5 decode steps."""
+    softcap 50, proportional rotary: 200 prompt tokens in 64-token chunks, 5 decode steps.
+    fused "1": the decode steps fold the producer into the decode launch (new K/V row
+    to the ring's staging row, then the batched ring commit); "0": separate launches."""
+    import os
+
     torch = torch_mod
     rng = np.random.default_rng(4)
     L, hq, hkv, D, prompt, steps, W = 2, 8, 4, 256, 200, 5, 64
@@ -189,7 +194,15 @@ def test_session_sliding_and_global_layers_gemma_shape(torch_mod, ctx, ops, sess
                             query_heads=hq, kv_heads=hkv, head_dim=D, storage="bf16",
                             score_scale=1.0 / 16.0, softcap=50.0, rotary=2, theta=1e6,
                             rotated_dims=128, factor=8.0, layer_windows=[W, 0])
-    s = sess_mod.Session(ctx, opts)
+    saved = os.environ.get("TKH_FUSED_DECODE")
+    os.environ["TKH_FUSED_DECODE"] = fused
+    try:
+        s = sess_mod.Session(ctx, opts)
+    finally:
+        if saved is None:
+            os.environ.pop("TKH_FUSED_DECODE", None)
+        else:
+            os.environ["TKH_FUSED_DECODE"] = saved
     ctxs = [torch.full((total, hq * D), np.nan, dtype=torch.float32, device="cuda") for _ in range(L)]
     io = [sess_mod.LayerIo(_t(torch, qs[l]), _t(torch, ks[l]), _t(torch, vs[l]), ctxs[l],
                            _t(torch, wq[l]), _t(torch, wk[l])) for l in range(L)]
@@ -207,7 +220,7 @@ def test_session_sliding_and_global_layers_gemma_shape(torch_mod, ctx, ops, sess
         ref, _, _ = orc.window_attention(q.reshape(-1), kh.reshape(-1), vh.reshape(-1), total, total,
                                          total, hq, hkv, D, 0, 0, window, 1.0 / 16.0, softcap=50.0)
         err = max_err(host(ctxs[l]).reshape(-1), ref)
-        log(f"layer {l} window {window}: max abs error {err:.3e}")
+        log(f"fused {fused} layer {l} window {window}: max abs error {err:.3e}")
         assert err <= TOL_HALF
 
 
