@@ -87,25 +87,15 @@ __device__ __forceinline__ float add_pair(uint32_t w, float l) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), ones, l, false);
 }
 
-// Maximum and minimum of three (two) floats in one instruction, maxNum /
-// minNum semantics (a NaN operand is ignored; NaN scores reach the context
-// through their probabilities).  Written out because fmaxf/fminf chains
-// compile with a canonicalising v_max per operand.
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-__device__ __forceinline__ float min3f(float a, float b, float c) {
-    float r;
-    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-__device__ __forceinline__ float max2f(float a, float b) {
-    float r;
-    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
+// Maximum and minimum with IEEE 754-2019 maximum/minimum semantics: a NaN
+// operand gives NaN.  A NaN score makes its row's probabilities, and with
+// them the context, NaN, which is reported as a non-finite input whatever the
+// row maximum became.  Chains of these compile to v_maximum3_f32 /
+// v_minimum3_f32 (two operands per instruction) with no canonicalising moves,
+// which fmaxf/fminf chains need, and no hazard padding, which the same chains
+// written as inline assembly get.
+__device__ __forceinline__ float maxn(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float minn(float a, float b) { return __builtin_elementwise_minimum(a, b); }
 
 __device__ __forceinline__ u32x2 read_tr(lds_ptr<uint8_t> p) {
     const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr<i16x4>)p);
@@ -561,11 +551,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             __builtin_amdgcn_sched_barrier(0);
             if (k == 0) {
                 if (bulk || (t >= tf_lo && t < tf_hi)) {
-                    hi = max3f(st[0], st[1], st[2]);
-                    float lo = min3f(lo_run, st[0], st[1]);
-                    for (int i = 3; i < 15; i += 2) hi = max3f(hi, st[i], st[i + 1]);
-                    hi = max2f(hi, st[15]);
-                    for (int i = 2; i < 16; i += 2) lo = min3f(lo, st[i], st[i + 1]);
+                    hi = maxn(st[0], st[1]);
+                    float lo = minn(lo_run, st[0]);
+                    for (int i = 2; i < 16; ++i) hi = maxn(hi, st[i]);
+                    for (int i = 1; i < 16; ++i) lo = minn(lo, st[i]);
                     lo_run = lo;
                     if constexpr (CAP)
                         for (int i = 0; i < 16; ++i) tv[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
@@ -577,10 +566,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                         const int kk = 8 * (i >> 2) + 4 * h + (i & 3);
                         const bool vis = kk >= lo_rel && kk < hi_rel;
                         bad |= vis && st[i] == NEG_INF;
-                        hi = fmaxf(hi, vis ? st[i] : NEG_INF);
                         if constexpr (CAP) tv[i] = vis ? softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E : NEG_INF;
-                        else st[i] = vis ? st[i] : NEG_INF;  // masked in place: no copy of the scores
+                        st[i] = vis ? st[i] : NEG_INF;  // masked in place: no copy of the scores
                     }
+                    hi = maxn(st[0], st[1]);
+                    for (int i = 2; i < 16; ++i) hi = maxn(hi, st[i]);
                 }
             }
             if (k == (NPV > 1 ? 1 : 0)) {
@@ -594,7 +584,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const uint32_t u = __builtin_bit_cast(uint32_t, mt);
                 const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
                 const uint32_t a0 = pr32[0], a1 = pr32[1];
-                mt = max2f(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+                mt = maxn(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
                 // Rare: a maximum moved past the slack.  l and the maximum change
                 // now; O, which still receives tile t - 1's P.V, after step 1.
                 if (__ballot(mt > m_thr) != 0) {
