@@ -591,27 +591,22 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
 
     const int nblk = (stream_span + KPB - 1) / KPB;
 
+    // Every load of a block is issued, with no branch: a key past the stream
+    // (in the block's tail) reads the stream's last row instead, which is in
+    // bounds and which consume() masks (its rel lies past every rhi).  The
+    // compiler then knows how many loads follow a block's, so consuming it
+    // waits for that block only, not for the next one issued just before
+    // (with loads under per-key branches it had to wait for all of them).
     auto load_block_as = [&](auto nt_tag, int blk, u32x4 (&kb)[U][CPL], u32x4 (&vb)[U][CPL]) {
         constexpr bool NT = decltype(nt_tag)::value;
         for (int u = 0; u < U; ++u) {
             const int rel = blk * KPB + kg + 8 * u;
-            if (rel < stream_span) {
-                const uint8_t *kp = kseg + rel * row_bytes;
-                const uint8_t *vp = vseg + rel * row_bytes;
-                for (int c = 0; c < CPL; ++c) kb[u][c] = NT ? load16_stream(kp + 128 * c) : load16(kp + 128 * c);
-                for (int c = 0; c < CPL; ++c) vb[u][c] = NT ? load16_stream(vp + 128 * c) : load16(vp + 128 * c);
-            } else {
-                for (int c = 0; c < CPL; ++c) {
-                    kb[u][c] = u32x4{0, 0, 0, 0};
-                    vb[u][c] = u32x4{0, 0, 0, 0};
-                }
-            }
+            const int row = rel < stream_span ? rel : stream_span - 1;
+            const uint8_t *kp = kseg + row * row_bytes;
+            const uint8_t *vp = vseg + row * row_bytes;
+            for (int c = 0; c < CPL; ++c) kb[u][c] = NT ? load16_stream(kp + 128 * c) : load16(kp + 128 * c);
+            for (int c = 0; c < CPL; ++c) vb[u][c] = NT ? load16_stream(vp + 128 * c) : load16(vp + 128 * c);
         }
-    };
-    // The load form is uniform per launch (a scalar branch per block).
-    auto load_block = [&](int blk, u32x4 (&kb)[U][CPL], u32x4 (&vb)[U][CPL]) {
-        if (stream_nt) load_block_as(std::true_type{}, blk, kb, vb);
-        else load_block_as(std::false_type{}, blk, kb, vb);
     };
 
     auto consume = [&](int blk, const u32x4 (&kb)[U][CPL], const u32x4 (&vb)[U][CPL]) {
@@ -672,26 +667,31 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         if (rhi[r] > stream_span) rhi[r] = stream_span;
     }
 
-    // Block blk + nw streams in while block blk is consumed.
-    int blk = wave;
-    u32x4 kc[U][CPL], vc[U][CPL];
-    if (blk < nblk) load_block(blk, kc, vc);
-    produce();
-    if (blk < nblk) {
-        for (;;) {
-            const bool more = blk + nw < nblk;
+    // Block blk + nw streams in while block blk is consumed; the last block
+    // is consumed after the loop, so inside it the next block's loads are
+    // always issued.  The load form (nontemporal or not) is uniform per
+    // launch, so the whole stream is built once per form rather than
+    // branching per block.
+    auto stream = [&](auto nt_tag) {
+        int blk = wave;
+        u32x4 kc[U][CPL], vc[U][CPL];
+        if (blk < nblk) load_block_as(nt_tag, blk, kc, vc);
+        produce();
+        if (blk >= nblk) return;
+        for (; blk + nw < nblk; blk += nw) {
             u32x4 kn[U][CPL], vn[U][CPL];
-            if (more) load_block(blk + nw, kn, vn);
+            load_block_as(nt_tag, blk + nw, kn, vn);
             consume(blk, kc, vc);
-            if (!more) break;
             for (int u = 0; u < U; ++u)
                 for (int c = 0; c < CPL; ++c) {
                     kc[u][c] = kn[u][c];
                     vc[u][c] = vn[u][c];
                 }
-            blk += nw;
         }
-    }
+        consume(blk, kc, vc);
+    };
+    if (stream_nt) stream(std::true_type{});
+    else stream(std::false_type{});
 
     // Fused producer: wave 0 of the workgroup holding the new key scores it
     // (lanes kg == 0 hold its chunks; the other key lanes add nothing).
