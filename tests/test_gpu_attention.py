@@ -449,6 +449,47 @@ def test_prefill_batch_bf16(torch_mod, ops, orc, waves):
         assert err <= TOL_HALF, err
 
 
+@pytest.mark.parametrize("D,hq,hkv", [(128, 32, 8), (64, 14, 2), (256, 8, 4)])
+def test_prefill_batch_compact_arguments(torch_mod, ops, orc, D, hq, hkv):
+    """Batched prefill whose chunks travel in the kernel's own arguments (one
+    shape, no key splits: the split target is forced to one workgroup) against
+    the same launch with its descriptors uploaded (bit for bit) and the oracle;
+    ragged positions, a zero-length cached prefix, one-token chunks."""
+    torch = torch_mod
+    rng = np.random.default_rng(31 + D)
+    for B, T in ((5, 128), (3, 1)):
+        pos = rng.integers(0, 300, size=B)
+        pos[0] = 0
+        caps = pos + T + rng.integers(0, 9, size=B)  # spare cache rows past the chunk
+        offsets = np.concatenate([[0], np.cumsum(hkv * caps * D)[:-1]])
+        total = int((hkv * caps * D).sum())
+        kpool = np.zeros(total, np.float32)
+        vpool = np.zeros(total, np.float32)
+        q = stored(rng.standard_normal((B, T, hq, D)), "bf16")
+        refs = []
+        for b in range(B):
+            k = head_major_cache(stored(rng.standard_normal((caps[b], hkv, D)), "bf16"), hkv, caps[b], D)
+            v = head_major_cache(stored(rng.standard_normal((caps[b], hkv, D)), "bf16"), hkv, caps[b], D)
+            kpool[offsets[b]:offsets[b] + k.size] = k.reshape(-1)
+            vpool[offsets[b]:offsets[b] + v.size] = v.reshape(-1)
+            ref, _, _ = orc.attention_cached(q[b].reshape(-1), k, v, T, hq, hkv, D, int(caps[b]), int(pos[b]))
+            refs.append(ref)
+        log(f"compact prefill batch D={D} B={B} T={T} positions {pos.tolist()}")
+        outs = {}
+        for compact in ("1", "0"):
+            ctx = _context_with_env(ops, {"TKH_PREFILL_COMPACT": compact, "TKH_PREFILL_GROUPS": "1"})
+            out = _zeros(torch, B * T * hq * D)
+            ops.prefill_batch(ctx, dev(q, "bf16"), dev(kpool, "bf16"), dev(vpool, "bf16"), offsets,
+                              caps * D, pos, out, tokens=T, query_heads=hq, kv_heads=hkv, head_dim=D,
+                              scale=float(1.0 / np.sqrt(np.float32(D))))
+            outs[compact] = host(out).reshape(B, -1)
+            ctx.close()
+        assert np.array_equal(outs["1"], outs["0"])
+        for b in range(B):
+            err = max_err(outs["1"][b], refs[b])
+            assert err <= TOL_HALF, err
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
 def test_nonfinite_visible_input_reports_nonfinite(torch_mod, ctx, ops, dt):
     """A NaN in visible Q/K/V is NonFinite (src/cpu/attention.rs:247-251); the context

@@ -54,7 +54,7 @@ extern "C" int tkh_prefill_merge_rows_per_block(int head_dim);
 extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int rows,
                                                int64_t blocks, hipStream_t stream,
                                                hipEvent_t start, hipEvent_t stop);
-extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim, int waves,
+extern "C" hipError_t tkh_launch_prefill(const tkh::PrefillArgs *p, int dtype, int head_dim, int waves,
                                          int64_t groups, hipStream_t stream, hipEvent_t start,
                                          hipEvent_t stop);
 extern "C" int tkh_decode_keys_per_lane(int dtype, int head_dim, int rows, int want);
@@ -458,6 +458,45 @@ uint32_t launch_decode(tkh_context *ctx, const Plan &plan, Problems group,
     return TKH_OK;
 }
 
+// Planned chunks of one shape (equal query counts, one segment from key 0
+// ending at the chunk, no key splits, Q and contexts at one stride, K and V at
+// the same offset from the first chunk's) as a compact batch in the kernel's
+// arguments; false when the group does not have that shape.
+bool compact_prefill(const Plan &plan, const Problems &group, tkh::PrefillBatch *b) {
+    if (group.size() < 2 || group.size() > (size_t)tkh::PREFILL_BATCH_MAX) return false;
+    const int64_t D = plan.head_dim, es = esize(plan.dtype), row = plan.query_heads * D;
+    const tkh::Problem &p0 = group[0];
+    const int64_t step = (int64_t)p0.queries * row;
+    const uint8_t *k0 = static_cast<const uint8_t *>(p0.seg[0].k);
+    const uint8_t *v0 = static_cast<const uint8_t *>(p0.seg[0].v);
+    for (size_t i = 0; i < group.size(); ++i) {
+        const tkh::Problem &p = group[i];
+        const tkh::Segment &sg = p.seg[0];
+        if (p.nseg != 1 || p.splits != 1 || p.queries != p0.queries || p.row_blocks != p0.row_blocks ||
+            p.k_pos0 != 0 || sg.start != 0 || sg.keys != p.keys || sg.row_stride != D ||
+            p.q_row_stride != row || p.q_pos0 + p.queries != p.keys || p.vis_lo != 0 ||
+            p.vis_hi != p.keys)
+            return false;
+        if (static_cast<const uint8_t *>(p.q) != static_cast<const uint8_t *>(p0.q) + (int64_t)i * step * es ||
+            p.out != p0.out + (int64_t)i * step)
+            return false;
+        const int64_t dk = static_cast<const uint8_t *>(sg.k) - k0;
+        const int64_t dv = static_cast<const uint8_t *>(sg.v) - v0;
+        if (dk != dv || dk % es != 0) return false;
+        b->e[i] = tkh::PrefillBatchEntry{dk / es, sg.head_stride, p.q_pos0, p.tile_base};
+    }
+    b->q = p0.q;
+    b->out = p0.out;
+    b->k = k0;
+    b->v = v0;
+    b->q_step = step;
+    b->count = (int32_t)group.size();
+    b->tokens = p0.queries;
+    b->row_blocks = p0.row_blocks;
+    b->split_keys = p0.split_keys;
+    return true;
+}
+
 // Many query rows per KV head (bf16/f16): the MFMA flash kernel, one launch.
 uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
                         tkh_error *err) {
@@ -556,9 +595,12 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
         return fail(err, TKH_UNSUPPORTED, "workspace", 0, need, split_region_bytes(ctx),
                     "attention needs %zu workspace bytes, context has %zu for it", need,
                     split_region_bytes(ctx));
+    tkh::PrefillArgs args{};
     tkh::Problem *dev = nullptr;
-    if (group.size() > 1) TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
-    tkh::Params prm = base_params(ctx, plan);
+    if (group.size() > 1 && !(ctx->prefill_compact && compact_prefill(plan, group, &args.b)))
+        TRY(upload(ctx, group.data(), (int)group.size(), &dev, err));
+    tkh::Params &prm = args.p;
+    prm = base_params(ctx, plan);
     prm.problems = dev;
     if (group.size() == 1) prm.single = group[0];
     prm.nproblems = (int32_t)group.size();
@@ -569,7 +611,7 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
 
     hipEvent_t *ev = nullptr;
     if (ctx->profiling) TRY(profile_slot(ctx, &ev, merge_blocks > 0, err));
-    hipError_t e = tkh_launch_prefill(&prm, (int)plan.dtype, (int)D, waves, wgs, ctx->stream,
+    hipError_t e = tkh_launch_prefill(&args, (int)plan.dtype, (int)D, waves, wgs, ctx->stream,
                                       ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "prefill launch", err);
     if (merge_blocks > 0) {
@@ -725,6 +767,7 @@ void init_tuning(tkh_context *ctx, int device) {
     // against 256 (128: 7.6 ms, 16.1 us; 32: no better).
     ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 64));
     ctx->prefill_waves = env_int("TKH_PREFILL_WAVES", 0);
+    ctx->prefill_compact = env_int("TKH_PREFILL_COMPACT", 1) != 0;
 }
 
 // First visible key (absolute) of a query at `position` (window_attention.rs:105-107).

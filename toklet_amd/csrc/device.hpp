@@ -196,6 +196,38 @@ struct DecodeArgs {
     DecodeBatch b;
 };
 
+// Chunks of one shape (tkh_prefill_batch: equal query counts, one K/V segment
+// from key 0 each, no window, no key splits; at most PREFILL_BATCH_MAX) carried
+// in the prefill kernel's own arguments, so the launch needs no descriptor
+// upload (a copy ordered after the previous kernel: about 4 us plus the gaps
+// around it per launch).  Chunk i reads Q and writes context from q_step * i
+// elements past q / out; its K/V cache starts kv_offset elements from k / v
+// (the same offset for both), and its first query sits at key `position`.
+constexpr int PREFILL_BATCH_MAX = 64;
+struct PrefillBatchEntry {
+    int64_t kv_offset;
+    int64_t head_stride;  // elements between its KV heads
+    int64_t position;
+    int64_t tile_base;    // its first workgroup
+};
+struct PrefillBatch {
+    const void *q;        // chunk 0's Q in the cache dtype, [tokens, Hq, D]
+    float *out;           // chunk 0's context
+    const void *k, *v;
+    int64_t q_step;       // elements between consecutive chunks' Q (and contexts)
+    int32_t count;        // 0: the launch describes its problems in Params
+    int32_t tokens;       // query tokens per chunk
+    int32_t row_blocks;   // row blocks per KV head
+    int32_t split_keys;
+    PrefillBatchEntry e[PREFILL_BATCH_MAX];
+};
+struct PrefillArgs {
+    Params p;             // first: the single-problem path reads it at the kernel-argument base
+    PrefillBatch b;
+};
+static_assert(sizeof(PrefillArgs) <= 4096, "kernel arguments");
+static_assert(sizeof(DecodeArgs) <= 4096, "kernel arguments");
+
 // Address-space qualified views: the problem descriptors are read-only for a
 // launch (scalar loads through the constant space), tensors are global.
 template <class T> using const_ptr = const __attribute__((address_space(4))) T *;

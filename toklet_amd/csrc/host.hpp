@@ -133,6 +133,7 @@ struct tkh_context {
     int prefill_max_splits = 16;
     int prefill_min_keys = 64;   // keys per split at least
     int prefill_waves = 0;       // waves per prefill workgroup: 0 = chosen per launch, 4 or 8
+    bool prefill_compact = true; // chunks of one shape carried in the kernel arguments (no upload)
     // profiling: per launch, start/stop of the attention kernel and of the combine kernel
     bool profiling = false;
     std::vector<hipEvent_t> prof_events;

@@ -285,8 +285,30 @@ constexpr float RESCALE_SLACK = 8.0f;
 
 __device__ __forceinline__ int uniform32(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// The fields of a problem the prefill kernel reads, with the segment of the
+// workgroup's split: from the problem descriptors, or built from a compact
+// batch entry (one segment from key 0, causal, no splits).
+struct PfView {
+    const void *q;
+    float *out;
+    int64_t q_row_stride, q_pos0, k_pos0, keys, vis_lo, vis_hi, tile_base, slot_base;
+    int32_t queries, row_blocks, splits, split_keys;
+    Segment sg;
+};
+
+// The entry of a compact prefill batch that holds global workgroup `tile`, by
+// the whole wave: lane i tests entry i, a ballot picks the last entry that
+// starts at or before the tile.
+__device__ __forceinline__ int find_prefill_entry(const_ptr<PrefillBatch> b, int count, int64_t tile) {
+    const int lane = threadIdx.x & 63;
+    const bool le = lane < count && b->e[lane].tile_base <= tile;
+    const uint64_t m = __ballot(le);  // bit 0 is set: entry 0 starts at tile 0
+    return __builtin_amdgcn_readfirstlane(63 - __builtin_clzll(m));
+}
+
 template <int DT, int D, bool CAP, int W>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(Params p) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(PrefillArgs a) {
+    const Params &p = a.p;
     constexpr int ROWS = 32 * W;  // packed rows per workgroup
     constexpr int KS = D / 16;        // QK k-steps (16 features each)
     constexpr int MB = D / 32;        // PV M-blocks (32 features each)
@@ -316,34 +338,87 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         const int64_t full = nb % 8 == 0 ? 8 : nb % 8;  // XCDs that receive `per` blocks
         tile = x < full ? x * per + k : full * per + (x - full) * (per - 1) + k;
     }
-    const_ptr<Problem> pr = problem_ptr(p, tile);
-    int64_t local = tile - pr->tile_base;
-    const int rb = (int)(local % pr->row_blocks);
-    local /= pr->row_blocks;
-    const int split = (int)(local % pr->splits);
-    const int kvh = (int)(local / pr->splits);
     const int G = p.group;
     const int Hq = p.query_heads;
-    const int m_kv = pr->queries * G;
-
-    // This split's segment: splits are laid out segment by segment over the
-    // visible range and never straddle a boundary, so one base pointer and
-    // row stride serve every tile of the workgroup.
-    int seg = 0, sidx = split;
-    if (sidx >= pr->seg_splits[0]) {
-        sidx -= pr->seg_splits[0];
-        seg = 1;
-        if (sidx >= pr->seg_splits[1]) {
-            sidx -= pr->seg_splits[1];
-            seg = 2;
+    PfView pv;
+    int rb, split, kvh, sidx;
+    {
+        const_ptr<PrefillArgs> args = (const_ptr<PrefillArgs>)__builtin_amdgcn_kernarg_segment_ptr();
+        const_ptr<PrefillBatch> batch = &args->b;
+        const int bcount = batch->count;
+        if (bcount > 0) {
+            // A compact batch: one segment from key 0, no key splits.
+            const int i = find_prefill_entry(batch, bcount, tile);
+            const auto &e = batch->e[i];
+            const int64_t tokens = batch->tokens, position = e.position;
+            const int64_t step = batch->q_step * i;
+            pv.q = reinterpret_cast<const uint8_t *>(batch->q) + step * 2;
+            pv.out = batch->out + step;
+            pv.q_row_stride = (int64_t)Hq * D;
+            pv.q_pos0 = position;
+            pv.k_pos0 = 0;
+            pv.keys = position + tokens;
+            pv.vis_lo = 0;
+            pv.vis_hi = position + tokens;
+            pv.tile_base = e.tile_base;
+            pv.slot_base = 0;
+            pv.queries = (int32_t)tokens;
+            pv.row_blocks = batch->row_blocks;
+            pv.splits = 1;
+            pv.split_keys = batch->split_keys;
+            pv.sg = Segment{reinterpret_cast<const uint8_t *>(batch->k) + e.kv_offset * 2,
+                            reinterpret_cast<const uint8_t *>(batch->v) + e.kv_offset * 2,
+                            e.head_stride, D, position + tokens, 0};
+            int64_t local = tile - pv.tile_base;
+            rb = (int)(local % pv.row_blocks);
+            kvh = (int)(local / pv.row_blocks);
+            split = 0;
+            sidx = 0;
+        } else {
+            const_ptr<Problem> pr = problem_ptr(p, tile);
+            pv.q = pr->q;
+            pv.out = pr->out;
+            pv.q_row_stride = pr->q_row_stride;
+            pv.q_pos0 = pr->q_pos0;
+            pv.k_pos0 = pr->k_pos0;
+            pv.keys = pr->keys;
+            pv.vis_lo = pr->vis_lo;
+            pv.vis_hi = pr->vis_hi;
+            pv.tile_base = pr->tile_base;
+            pv.slot_base = pr->slot_base;
+            pv.queries = pr->queries;
+            pv.row_blocks = pr->row_blocks;
+            pv.splits = pr->splits;
+            pv.split_keys = pr->split_keys;
+            int64_t local = tile - pv.tile_base;
+            rb = (int)(local % pv.row_blocks);
+            local /= pv.row_blocks;
+            split = (int)(local % pv.splits);
+            kvh = (int)(local / pv.splits);
+            // This split's segment: splits are laid out segment by segment over
+            // the visible range and never straddle a boundary, so one base
+            // pointer and row stride serve every tile of the workgroup.
+            int seg = 0;
+            sidx = split;
+            if (sidx >= pr->seg_splits[0]) {
+                sidx -= pr->seg_splits[0];
+                seg = 1;
+                if (sidx >= pr->seg_splits[1]) {
+                    sidx -= pr->seg_splits[1];
+                    seg = 2;
+                }
+            }
+            const auto &sgp = pr->seg[seg];
+            pv.sg = Segment{sgp.k, sgp.v, sgp.head_stride, sgp.row_stride, sgp.keys, sgp.start};
         }
     }
-    const int64_t seg_start = pr->seg[seg].start;
-    const int64_t seg_end = seg_start + pr->seg[seg].keys;
-    const int64_t seg_lo = seg_start > pr->vis_lo ? seg_start : pr->vis_lo;
-    const int64_t seg_hi = seg_end < pr->vis_hi ? seg_end : pr->vis_hi;
-    const int64_t s_lo = seg_lo + (int64_t)sidx * pr->split_keys;
-    const int64_t s_hi = s_lo + pr->split_keys < seg_hi ? s_lo + pr->split_keys : seg_hi;
+    const int m_kv = pv.queries * G;
+    const int64_t seg_start = pv.sg.start;
+    const int64_t seg_end = seg_start + pv.sg.keys;
+    const int64_t seg_lo = seg_start > pv.vis_lo ? seg_start : pv.vis_lo;
+    const int64_t seg_hi = seg_end < pv.vis_hi ? seg_end : pv.vis_hi;
+    const int64_t s_lo = seg_lo + (int64_t)sidx * pv.split_keys;
+    const int64_t s_hi = s_lo + pv.split_keys < seg_hi ? s_lo + pv.split_keys : seg_hi;
 
     // This lane's query row.
     const int row = rb * ROWS + wave * 32 + j;
@@ -351,15 +426,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     const int rrow = rvalid ? row : m_kv - 1;
     const int t_row = rrow / G, h_row = kvh * G + rrow % G;
     int64_t r_lo, r_hi;
-    visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + t_row, &r_lo, &r_hi);
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + t_row, &r_lo, &r_hi);
     if (!rvalid) r_hi = r_lo;  // no visible keys: never contributes, never stored
 
     // Key range of the workgroup: the union over its rows, clipped to the split.
     const int wg_row_first = rb * ROWS;
     const int wg_row_last = min(wg_row_first + ROWS, m_kv) - 1;
     int64_t k_lo, k_hi, tmp;
-    visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + wg_row_first / G, &k_lo, &tmp);
-    visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + wg_row_last / G, &tmp, &k_hi);
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + wg_row_first / G, &k_lo, &tmp);
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + wg_row_last / G, &tmp, &k_hi);
     if (k_lo < s_lo) k_lo = s_lo;
     if (k_hi > s_hi) k_hi = s_hi;
     if (k_hi < k_lo) k_hi = k_lo;
@@ -372,8 +447,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         const int w_first = min(wg_row_first + wave * 32, m_kv - 1);
         const int w_last = min(wg_row_first + wave * 32 + 31, m_kv - 1);
         int64_t a, b, full_lo, full_hi;
-        visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + w_first / G, &a, &full_hi);
-        visible_range(p, pr->k_pos0, pr->keys, pr->q_pos0 + w_last / G, &full_lo, &b);
+        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + w_first / G, &a, &full_hi);
+        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + w_last / G, &full_lo, &b);
         int64_t lo_t = full_lo - k_lo;
         lo_t = lo_t <= 0 ? 0 : (lo_t + PF_KT - 1) / PF_KT;
         int64_t hi_t = full_hi - k_lo;
@@ -393,8 +468,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // Q^T B operands: lane holds row j, features 16 ks + 8 h .. + 7.
     u32x4 qb[KS];
     {
-        const uint8_t *qrow = reinterpret_cast<const uint8_t *>(pr->q) +
-                              ((int64_t)t_row * pr->q_row_stride + (int64_t)h_row * D) * 2;
+        const uint8_t *qrow = reinterpret_cast<const uint8_t *>(pv.q) +
+                              ((int64_t)t_row * pv.q_row_stride + (int64_t)h_row * D) * 2;
         for (int ks = 0; ks < KS; ++ks)
             qb[ks] = *gload_ptr<u32x4>(qrow + 32 * ks + 16 * h);
         // Complete the Q loads before the first direct K/V load.  The compiler
@@ -425,10 +500,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     bool huge = false;
 
     // ---- K/V tiles: PF_KT keys each, issued into an NS-stage LDS ring.
-    const int prow = uniform32((int)(pr->seg[seg].row_stride * 2));  // bytes between keys
-    const int64_t first = (int64_t)kvh * pr->seg[seg].head_stride + (k_lo - seg_start) * pr->seg[seg].row_stride;
-    const uint8_t *k_next = reinterpret_cast<const uint8_t *>(pr->seg[seg].k) + uniform64(first * 2);
-    const uint8_t *v_next = reinterpret_cast<const uint8_t *>(pr->seg[seg].v) + uniform64(first * 2);
+    const int prow = uniform32((int)(pv.sg.row_stride * 2));  // bytes between keys
+    const int64_t first = (int64_t)kvh * pv.sg.head_stride + (k_lo - seg_start) * pv.sg.row_stride;
+    const uint8_t *k_next = reinterpret_cast<const uint8_t *>(pv.sg.k) + uniform64(first * 2);
+    const uint8_t *v_next = reinterpret_cast<const uint8_t *>(pv.sg.v) + uniform64(first * 2);
     // Per-lane offsets of the direct loads (row in the tile, swizzled chunk);
     // rows past the last tile's keys repeat a valid row.
     int off_full[RPW], off_last[RPW];
@@ -740,7 +815,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         if (__ballot(bad_acc && !bad) != 0) {
             constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
             constexpr int RPI = 64 / CPR;    // rows per wave iteration
-            const uint8_t *vrows = reinterpret_cast<const uint8_t *>(pr->seg[seg].v) + first * 2;
+            const uint8_t *vrows = reinterpret_cast<const uint8_t *>(pv.sg.v) + first * 2;
             bool nonfinite = false, big = false;
             for (int r0 = 0; r0 < nkeys; r0 += RPI) {
                 const int r = r0 + lane / CPR;
@@ -763,7 +838,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     bad |= bad_acc;
 
     // O^T lane layout: row j, features 32 mb + 8 q + 4 h + r (register 4 q + r).
-    const bool single = pr->splits == 1;
+    const bool single = pv.splits == 1;
     bool bad_mass = false, bad_out = false;
     // bf16: the P.V products used V scaled by 2^-8.
     constexpr float oscale = VCONV ? 256.0f : 1.0f;
@@ -771,7 +846,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         if (rvalid) {
             const float inv = oscale / l_run;
             bad_mass |= !(l_run > 0.0f) || !is_finite_f(l_run);
-            float *orow = pr->out + ((int64_t)t_row * Hq + h_row) * D;
+            float *orow = pv.out + ((int64_t)t_row * Hq + h_row) * D;
             for (int mb = 0; mb < MB; ++mb)
                 for (int q = 0; q < 4; ++q) {
                     f32x4 v;
@@ -793,8 +868,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // floats, merged by attn_prefill_merge after this kernel.
     raise_status(p, bad, ST_NONFINITE_INPUT);
     raise_status(p, v_range, ST_V_RANGE);
-    const int64_t group = (int64_t)kvh * pr->row_blocks + rb;
-    const int64_t slot = pr->slot_base + group * pr->splits + split;
+    const int64_t group = (int64_t)kvh * pv.row_blocks + rb;
+    const int64_t slot = pv.slot_base + group * pv.splits + split;
     float *po = p.part_o + (slot * ROWS + wave * 32 + j) * D;
     for (int mb = 0; mb < MB; ++mb)
         for (int q = 0; q < 4; ++q) {
@@ -909,14 +984,14 @@ extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_di
     return hipErrorInvalidValue;
 }
 
-extern "C" hipError_t tkh_launch_prefill(const tkh::Params *p, int dtype, int head_dim, int waves,
+extern "C" hipError_t tkh_launch_prefill(const tkh::PrefillArgs *p, int dtype, int head_dim, int waves,
                                          int64_t groups, hipStream_t stream, hipEvent_t start,
                                          hipEvent_t stop) {
     using namespace tkh;
     dim3 grid((unsigned)groups), block(64 * waves);
 #define TKH_PF(DT, DD, WW)                                                              \
     if (dtype == DT && head_dim == DD && waves == WW) {                                 \
-        if (p->softcap != 0.0f)                                                         \
+        if (p->p.softcap != 0.0f)                                                       \
             hipExtLaunchKernelGGL((attn_prefill<DT, DD, true, WW>), grid, block, 0, stream, start, stop, 0, *p);  \
         else                                                                            \
             hipExtLaunchKernelGGL((attn_prefill<DT, DD, false, WW>), grid, block, 0, stream, start, stop, 0, *p); \
