@@ -459,6 +459,56 @@ def cpu_baseline_decode_batch(state, seconds=10.0, steps=2):
     }
 
 
+def cpu_threads():
+    """Host threads for the all-core CPU baselines: the job's CPU share
+    (OMP_NUM_THREADS when the launcher sets it, else the affinity mask), at most 16."""
+    n = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    return max(1, min(16, n))
+
+
+def cpu_baseline_decode_batch_threads(state, seconds=8.0, steps=2):
+    """cpu_baseline_decode_batch with the same calls spread over cpu_threads() host
+    threads (one session's attention_cached per task; the oracle's C calls run
+    without the interpreter lock)."""
+    import numpy as np  # noqa: F401
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle
+
+    oracle.lib()
+    hq, hkv, d = state["hq"], state["hkv"], state["d"]
+    kh = state["k"].float().cpu().numpy()
+    vh = state["v"].float().cpu().numpy()
+    qh = state["q"].float().cpu().numpy()
+    offsets, lengths = state["offsets"], state["lengths"]
+    nbytes_pass = sum(state["bytes_of"]([l + i + 1 for l in lengths]) for i in range(steps))
+    tasks = [(i, b) for i in range(steps) for b in range(len(lengths))]
+
+    def one(task):
+        i, b = task
+        cap = state["caps"][b]
+        kb = kh[offsets[b]:offsets[b] + hkv * cap * d]
+        vb = vh[offsets[b]:offsets[b] + hkv * cap * d]
+        oracle.attention_cached(qh[b].reshape(-1), kb, vb, 1, hq, hkv, d, cap, lengths[b] + i)
+
+    n = cpu_threads()
+    passes, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(max_workers=n) as pool:
+        while True:
+            list(pool.map(one, tasks))
+            passes += 1
+            dt = time.perf_counter() - t0
+            if dt >= seconds:
+                break
+    return {
+        "value": nbytes_pass * passes / dt / 1e9, "unit": "GB/s", "cores": n, "kind": "port",
+        "sample": f"the single-thread line's subset and calls ({steps} decode steps of all "
+                  f"{len(lengths)} sessions), one session per task over {n} host threads, x {passes} "
+                  f"passes, {dt:.2f} s",
+        "seconds": dt,
+    }
+
+
 def cpu_baseline_prefill_batch(state, seconds=10.0):
     """The reference's CPU path for configs[4] on BASELINE.md's subset (1 of 32
     sessions: 128 new rows over 4224 keys, all 32 heads), restated by the oracle on
@@ -484,6 +534,48 @@ def cpu_baseline_prefill_batch(state, seconds=10.0):
         "sample": f"configs[4] subset: session 0 of 32 (128 new rows x {hq} heads over {cap} keys), "
                   f"oracle attention_cached on FP32 copies of the bf16 K/V, x {passes} passes, "
                   f"{dt:.2f} s",
+        "seconds": dt,
+    }
+
+
+def cpu_baseline_prefill_batch_threads(state, seconds=8.0, sessions=4):
+    """cpu_baseline_prefill_batch over cpu_threads() host threads: the first
+    `sessions` sessions, each split by KV head (its query-head group against its K/V
+    rows) into one oracle call per task."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle
+
+    oracle.lib()
+    hq, hkv, d, per, cap = state["hq"], state["hkv"], state["d"], state["per"], state["cap"]
+    T, G = state["tokens"], hq // hkv
+    work = []
+    for b in range(sessions):
+        kb = state["k"][b * per:(b + 1) * per].float().cpu().numpy().reshape(hkv, cap * d)
+        vb = state["v"][b * per:(b + 1) * per].float().cpu().numpy().reshape(hkv, cap * d)
+        qb = state["q"][b].float().cpu().numpy().reshape(T, hq, d)
+        for h in range(hkv):
+            work.append((qb[:, h * G:(h + 1) * G, :].copy().reshape(-1), kb[h].copy(), vb[h].copy()))
+
+    def one(item):
+        q, k, v = item
+        oracle.attention_cached(q, k, v, T, G, 1, d, cap, state["cached"])
+
+    n = cpu_threads()
+    passes, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(max_workers=n) as pool:
+        while True:
+            list(pool.map(one, work))
+            passes += 1
+            dt = time.perf_counter() - t0
+            if dt >= seconds:
+                break
+    return {
+        "value": state["flops_per_session"] * sessions * passes / dt / 1e12, "unit": "TFLOP/s",
+        "cores": n, "kind": "port",
+        "sample": f"configs[4] subset: sessions 0-{sessions - 1} of 32, one (session, KV head) per "
+                  f"task over {n} host threads, oracle attention_cached on FP32 copies of the bf16 "
+                  f"K/V, x {passes} passes, {dt:.2f} s",
         "seconds": dt,
     }
 
@@ -674,10 +766,12 @@ def main():
     line["configs"]["c3"] = c3
     line["host"] = host_info()
     if not args.no_cpu:
-        log("cpu baselines: the oracle on one host core")
+        log("cpu baselines: the oracle on one host core, then on the job's host threads")
         line["cpu_baseline"] = cpu_baseline_decode_batch(states["c3"])
+        line["cpu_baseline_all_cores"] = cpu_baseline_decode_batch_threads(states["c3"])
         if "c5" in states:
             line["prefill_cpu_baseline"] = cpu_baseline_prefill_batch(states["c5"])
+            line["prefill_cpu_baseline_all_cores"] = cpu_baseline_prefill_batch_threads(states["c5"])
     print(json.dumps(line))
 
 
