@@ -316,3 +316,34 @@ def test_stream_load_form_does_not_change_results(torch_mod, ops, orc):
         worst = max(worst, max_err(results[(1, B)][b], ref))
     log(f"  worst max abs error {worst:.3e}")
     assert worst <= TOL_HALF
+
+
+@pytest.mark.parametrize("context", [300, 2049, 8192])
+def test_stream_tail_reads_only_visible_rows(torch_mod, ctx, ops, orc, context):
+    """A wave block past a split's last key reads the split's last row again (its
+    loads are unconditional) and masks it.  Infinities in the cache rows past the
+    query position are never read, so the result still matches the oracle; an
+    infinity in V of the last visible row is reported as a non-finite input, as the
+    reference's visible-prefix check reports it (src/cpu/attention.rs:247-251)."""
+    torch = torch_mod
+    rng = np.random.default_rng(71 + context)
+    hq, hkv, D, capacity = 16, 8, 128, context + 40
+    k = stored(rng.standard_normal((hkv, capacity, D)), "bf16")
+    v = stored(rng.standard_normal((hkv, capacity, D)), "bf16")
+    q = stored(rng.standard_normal((1, hq, D)), "bf16").reshape(-1)
+    k[:, context:, :] = np.inf  # rows past the query position: never visible
+    v[:, context:, :] = -np.inf
+    shape = ops.CachedAttentionShape(1, hq, hkv, D, capacity, context - 1)
+    log(f"stream tail: context {context}, infinities past it")
+    out = torch.full((hq * D,), np.nan, dtype=torch.float32, device="cuda")
+    ops.attention_cached(ctx, dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), out, None, None, shape)
+    ref, _, _ = orc.attention_cached(q, np.where(np.isfinite(k), k, 0), np.where(np.isfinite(v), v, 0),
+                                     1, hq, hkv, D, capacity, context - 1)
+    assert max_err(host(out), ref) <= TOL_HALF
+    v2 = v.copy()
+    v2[3, context - 1, 5] = np.inf  # the last visible key of KV head 3
+    log(f"stream tail: context {context}, infinity in the last visible V row")
+    with pytest.raises(ops.TkhError) as e:
+        ops.attention_cached(ctx, dev(q, "bf16"), dev(k, "bf16"), dev(v2, "bf16"), out, None, None,
+                             shape)
+    assert e.value.name == "NonFinite"
