@@ -50,7 +50,9 @@
 extern "C" {
 #endif
 
-#define TKH_ABI_VERSION 1u
+/* 2: tkh_producer_shape and tkh_session_options end with the Llama 3 rotary
+ * parameters (low/high frequency factors, original context length). */
+#define TKH_ABI_VERSION 2u
 
 typedef enum tkh_status {
     TKH_OK = 0,
@@ -322,9 +324,16 @@ uint32_t tkh_kv_reset_batch(tkh_kv *const *kvs, uint64_t count, tkh_error *err);
 
 /* ---------------- producer (the step before attention) ---------------- */
 
-/* Rotary variants: none, Qwen split-half (src/cpu/attention.rs:10-64) and
- * proportional (src/cpu/proportional_rotary.rs:32-91). */
-typedef enum tkh_rotary { TKH_ROTARY_NONE = 0, TKH_ROTARY_SPLIT_HALF = 1, TKH_ROTARY_PROPORTIONAL = 2 } tkh_rotary;
+/* Rotary variants: none, Qwen split-half (src/cpu/attention.rs:10-64),
+ * proportional (src/cpu/proportional_rotary.rs:32-91) and Llama 3
+ * wavelength-band scaling (src/cpu/llama3_rotary.rs:13-146, selected by
+ * PositionPlan::Llama3, src/model/position.rs:7-45). */
+typedef enum tkh_rotary {
+    TKH_ROTARY_NONE = 0,
+    TKH_ROTARY_SPLIT_HALF = 1,
+    TKH_ROTARY_PROPORTIONAL = 2,
+    TKH_ROTARY_LLAMA3 = 3
+} tkh_rotary;
 
 /* Per-layer producer of Model::run (src/model/mod.rs:611-662): optional
  * per-head RMSNorm of Q and K (cpu::rmsnorm, src/cpu/reductions.rs:8-49,
@@ -334,9 +343,12 @@ typedef struct tkh_producer_shape {
     uint64_t position;
     float norm_epsilon;  /* used when norm weights are given */
     uint32_t rotary;     /* tkh_rotary */
-    float theta;         /* split-half theta, or proportional base */
+    float theta;         /* split-half / Llama 3 theta, or proportional base */
     uint64_t rotated_dims; /* proportional only */
-    float factor;          /* proportional only */
+    float factor;          /* proportional and Llama 3 (Llama3Scaling::new: >= 1) */
+    float low_freq_factor;           /* Llama 3 only: > 0 */
+    float high_freq_factor;          /* Llama 3 only: > low_freq_factor */
+    uint64_t original_max_positions; /* Llama 3 only: 1..2^53 */
 } tkh_producer_shape;
 
 /* Replaces the rmsnorm -> rotary -> LayerKv::append sequence of Model::run
@@ -377,6 +389,9 @@ typedef struct tkh_session_options {
     float theta;
     uint64_t rotated_dims;
     float factor;
+    float low_freq_factor;    /* Llama 3 parameters, as in tkh_producer_shape */
+    float high_freq_factor;
+    uint64_t original_max_positions;
 } tkh_session_options;
 
 /* Session::new (src/session.rs:205-245): validates, then allocates every

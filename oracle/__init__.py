@@ -131,6 +131,41 @@ def proportional_rotary(x, tokens, heads, head_dim, rotated_dims, offset, base, 
     return out
 
 
+class _Llama3(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in ("factor", "low", "high", "original")]
+
+
+def llama3_scaling(factor, low, high, original):
+    """Llama3Scaling::new (src/cpu/llama3_rotary.rs:14-37)."""
+    s, err = _Llama3(), _Error()
+    rc = lib().orc_llama3_scaling(ctypes.c_float(factor), ctypes.c_float(low), ctypes.c_float(high),
+                                  _size(original), ctypes.byref(s), ctypes.byref(err))
+    _check(rc, err)
+    return s
+
+
+def llama3_inverse_frequency(scaling, ordinary):
+    """Llama3Scaling::inverse_frequency (src/cpu/llama3_rotary.rs:44-61), FP64."""
+    out, err = ctypes.c_double(), _Error()
+    rc = lib().orc_llama3_inverse_frequency(ctypes.byref(scaling), ctypes.c_double(ordinary),
+                                            ctypes.byref(out), ctypes.byref(err))
+    _check(rc, err)
+    return out.value
+
+
+def llama3_rotary(x, tokens, heads, head_dim, offset, theta, factor, low, high, original):
+    """llama3_rotary (src/cpu/llama3_rotary.rs:87-146)."""
+    s = llama3_scaling(factor, low, high, original)
+    x = _f32(x)
+    out = np.zeros_like(x)
+    err = _Error()
+    rc = lib().orc_llama3_rotary(
+        _ptr(x), _size(x.size), _ptr(out), _size(out.size), _size(tokens), _size(heads),
+        _size(head_dim), _size(offset), ctypes.c_float(theta), ctypes.byref(s), ctypes.byref(err))
+    _check(rc, err)
+    return out
+
+
 def rmsnorm(x, weight, tokens, hidden, epsilon):
     x, weight = _f32(x), _f32(weight)
     out = np.zeros_like(x)

@@ -165,6 +165,90 @@ uint32_t orc_proportional_rotary(const float *input, size_t input_len, float *ou
     return ok(err);
 }
 
+/* ---- Llama 3 rotary: src/cpu/llama3_rotary.rs:13-146 ---- */
+
+/* Llama3Scaling::new (src/cpu/llama3_rotary.rs:14-37): the FP32 parameters are
+ * widened to FP64 once. */
+uint32_t orc_llama3_scaling(float factor, float low, float high, size_t original,
+                            orc_llama3 *out, orc_error *err) {
+    if (!isfinite(factor) || factor < 1.0f || !isfinite(low) || low <= 0.0f ||
+        !isfinite(high) || high <= low || original == 0 ||
+        (unsigned __int128)original > ((unsigned __int128)1 << 53))
+        return invalid("Llama3 rotary scaling", err);
+    out->factor = (double)factor;
+    out->low = (double)low;
+    out->high = (double)high;
+    out->original = (double)original;
+    return ok(err);
+}
+
+/* Llama3Scaling::inverse_frequency (src/cpu/llama3_rotary.rs:44-61), in FP64:
+ * wavelengths below original/high keep the ordinary frequency, those above
+ * original/low divide it by factor, and the closed band between blends the two
+ * linearly in original/wavelength. */
+uint32_t orc_llama3_inverse_frequency(const orc_llama3 *s, double ordinary, double *out,
+                                      orc_error *err) {
+    if (!isfinite(ordinary) || ordinary <= 0.0) return invalid("Llama3 inverse frequency", err);
+    const double wavelength = 6.283185307179586 / ordinary;  /* 2*pi in FP64 */
+    double result;
+    if (s->factor == 1.0 || wavelength < s->original / s->high) {
+        result = ordinary;
+    } else if (wavelength > s->original / s->low) {
+        result = ordinary / s->factor;
+    } else {
+        const double smooth = (s->original / wavelength - s->low) / (s->high - s->low);
+        result = (1.0 - smooth) * ordinary / s->factor + smooth * ordinary;
+    }
+    if (!isfinite(result) || result <= 0.0)
+        return invalid("Llama3 scaled frequency underflow", err);
+    *out = result;
+    return ok(err);
+}
+
+/* llama3_rotary (src/cpu/llama3_rotary.rs:87-146): split-half pairs over the
+ * whole head, frequency theta^(-2j/D) scaled as above, angle and sine/cosine
+ * in FP64, rounded to FP32, FP32 rotation. */
+uint32_t orc_llama3_rotary(const float *input, size_t input_len, float *output,
+                           size_t output_len, size_t tokens, size_t heads, size_t head_dim,
+                           size_t offset, float theta, const orc_llama3 *scaling,
+                           orc_error *err) {
+    TRY(nonzero(tokens, "tokens", err));
+    TRY(nonzero(heads, "heads", err));
+    TRY(nonzero(head_dim, "head_dim", err));
+    if (head_dim % 2 != 0) return invalid("Llama3 rotary head_dim must be even", err);
+    if (!isfinite(theta) || theta <= 0.0f) return invalid("theta must be finite and positive", err);
+    size_t last;
+    TRY(checked_add(offset, tokens - 1, &last, err));
+    if ((unsigned __int128)last > ((unsigned __int128)1 << 53))
+        return invalid("rotary positions must be at most 2^53", err);
+    size_t stride, count;
+    TRY(product(heads, head_dim, &stride, err));
+    TRY(product(tokens, stride, &count, err));
+    TRY(length("Llama3 rotary input", input_len, count, err));
+    TRY(length("Llama3 rotary output", output_len, count, err));
+    TRY(finite("Llama3 rotary input", input, input_len, err));
+    for (size_t pair = 0; pair < head_dim / 2; ++pair) {
+        const double ordinary = pow((double)theta, -(2.0 * (double)pair) / (double)head_dim);
+        double inverse;
+        TRY(orc_llama3_inverse_frequency(scaling, ordinary, &inverse, err));
+        for (size_t token = 0; token < tokens; ++token) {
+            const double angle = (double)(offset + token) * inverse;
+            const float s = (float)sin(angle), c = (float)cos(angle);
+            for (size_t head = 0; head < heads; ++head) {
+                const size_t first = token * stride + head * head_dim + pair;
+                const size_t second = first + head_dim / 2;
+                const float a = input[first] * c - input[second] * s;
+                const float b = input[second] * c + input[first] * s;
+                if (!isfinite(a) || !isfinite(b))
+                    return non_finite("Llama3 rotary output", !isfinite(a) ? first : second, err);
+                output[first] = a;
+                output[second] = b;
+            }
+        }
+    }
+    return ok(err);
+}
+
 /* ---- rmsnorm: src/cpu/reductions.rs:8-49 ---- */
 
 uint32_t orc_rmsnorm(const float *input, size_t input_len, const float *weight,

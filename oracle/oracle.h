@@ -94,6 +94,22 @@ uint32_t orc_proportional_rotary(const float *input, size_t input_len, float *ou
                                  size_t head_dim, size_t rotated_dims, size_t offset,
                                  float base, float factor, orc_error *err);
 
+/* Llama3Scaling (src/cpu/llama3_rotary.rs:6-11): parameters widened to FP64. */
+typedef struct orc_llama3 {
+    double factor, low, high, original;
+} orc_llama3;
+
+uint32_t orc_llama3_scaling(float factor, float low, float high, size_t original,
+                            orc_llama3 *out, orc_error *err);
+
+uint32_t orc_llama3_inverse_frequency(const orc_llama3 *s, double ordinary, double *out,
+                                      orc_error *err);
+
+uint32_t orc_llama3_rotary(const float *input, size_t input_len, float *output,
+                           size_t output_len, size_t tokens, size_t heads, size_t head_dim,
+                           size_t offset, float theta, const orc_llama3 *scaling,
+                           orc_error *err);
+
 uint32_t orc_rmsnorm(const float *input, size_t input_len, const float *weight,
                      size_t weight_len, float *output, size_t output_len, size_t tokens,
                      size_t hidden, float epsilon, orc_error *err);

@@ -19,6 +19,7 @@ Fixture sets taken (all used by the reference's own attention tests):
   gemma-softcap-v1           src/cpu/softcap/tests.rs:19
   qwen3-attention-inputs-v1  src/metal/compensated_attention.rs:465-561 (inputs only)
   gemma-rotary-v1            src/cpu/proportional_rotary/tests.rs:34-71
+  llama3-rotary-v1           src/cpu/llama3_rotary/tests.rs:33-127 (-> llama3_rotary_v1)
   tiny-v1 rmsnorm arrays     tests/cpu_reductions.rs:16-62, 140-175 (-> tiny_v1_norms)
   tiny-v1 linear + greedy    tests/cpu_linear.rs:59-165, tests/cpu_decoder.rs:170-192
                              (-> tiny_v1_linear)
@@ -102,6 +103,28 @@ def math_json(ref: str, name: str, out: str):
     arrays = {}
     cases = json_arrays(data["cases"], "cases", arrays)
     meta = {"source_sha256": sha(raw), "format": data.get("format"), "cases": cases}
+    np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
+
+
+def llama3_rotary(ref: str, out: str):
+    """llama3-rotary-v1: every case's FP32 input, its FP64 inverse frequencies and
+    outputs, and the scaling controls (src/cpu/llama3_rotary/tests.rs:33-127).  The
+    input decimals become FP32 through FP64, as the reference's JSON reader does."""
+    path = os.path.join(ref, "tests", "fixtures", "llama3-rotary-v1", "math.json")
+    raw = open(path, "rb").read()
+    assert sha(raw) == "980c8835bc5485c7d064b77e868dab44891a55c2bbff8365ea3b30c96d4c1692"
+    data = json.loads(raw)
+    arrays, cases = {}, []
+    for case in data["cases"]:
+        name = case["name"]
+        arrays[f"{name}.input"] = np.array(case["input"], dtype=np.float64).astype(np.float32)
+        arrays[f"{name}.inverse_frequencies"] = np.array(case["inverse_frequencies"], dtype=np.float64)
+        arrays[f"{name}.output"] = np.array(case["output"], dtype=np.float64)
+        cases.append({k: v for k, v in case.items()
+                      if k not in ("input", "inverse_frequencies", "output")})
+    meta = {"source_sha256": sha(raw), "format": data.get("format"), "cases": cases,
+            "controls": data["controls"]}
     np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
     json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
 
@@ -205,6 +228,7 @@ def main(ref: str):
     math_json(ref, "gemma-softcap-v1", "gemma_softcap_v1")
     qwen3_inputs(ref, "qwen3_attention_inputs_v1")
     math_json(ref, "gemma-rotary-v1", "gemma_rotary_v1")
+    llama3_rotary(ref, "llama3_rotary_v1")
     tiny_norms(ref, "tiny_v1_norms")
     tiny_linear(ref, "tiny_v1_linear")
     reference_attention(ref, "gemma_reference_attention_v1")

@@ -41,7 +41,31 @@ def test_bindings_cover_the_header():
 
 
 def test_abi_version(lib):
-    assert lib.tkh_abi_version() == 1
+    from toklet_amd import _lib
+
+    text = open(HEADER).read()
+    assert lib.tkh_abi_version() == _lib.ABI_VERSION == 2
+    assert re.search(r"#define TKH_ABI_VERSION 2u", text)
+
+
+def test_struct_layouts_match_header():
+    """The ctypes mirrors' sizes equal the C structures' (gcc on the header)."""
+    import subprocess
+    import tempfile
+
+    from toklet_amd import _lib
+
+    names = {"tkh_producer_shape": _lib.ProducerShape, "tkh_session_options": _lib.SessionOptions}
+    src = '#include <stdio.h>\n#include "tokhip.h"\nint main(void){' + "".join(
+        f'printf("%zu\\n", sizeof({n}));' for n in names) + "return 0;}"
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "s.c"), os.path.join(d, "s")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        sizes = [int(x) for x in subprocess.run([exe], check=True, capture_output=True,
+                                                text=True).stdout.split()]
+    for (n, cls), size in zip(names.items(), sizes):
+        assert ctypes.sizeof(cls) == size, n
 
 
 def _cached(lib, shape, q_len, kv_len, ctx_len, scores_len=0):

@@ -48,12 +48,14 @@ def _t(torch, a, dtype=None):
 
 
 def _oracle_produce(orc, x, w, tokens, heads, D, position, *, eps=1e-6, rotary="split",
-                    theta=1e6, rotated=0, factor=1.0):
+                    theta=1e6, rotated=0, factor=1.0, low=1.0, high=4.0, original=8192):
     y = orc.rmsnorm(x.reshape(-1), w, tokens * heads, D, eps) if w is not None else x.reshape(-1)
     if rotary == "split":
         y = orc.rotary(y, tokens, heads, D, position, theta)
     elif rotary == "proportional":
         y = orc.proportional_rotary(y, tokens, heads, D, rotated, position, theta, factor)
+    elif rotary == "llama3":
+        y = orc.llama3_rotary(y, tokens, heads, D, position, theta, factor, low, high, original)
     return y.reshape(tokens, heads, D)
 
 
@@ -120,6 +122,80 @@ def test_producer_proportional_partial_bf16(torch_mod, ctx, ops, orc):
         assert np.mean(d == 0) > 0.999
         assert np.all(d <= np.abs(r) * 2.0 ** -7 + 1e-30)
     assert np.array_equal(host(vo).reshape(hkv, T, D).transpose(1, 0, 2), stored(v, "bf16"))
+
+
+def _llama3_shape(ops, T, hq, hkv, D, pos, theta, factor, low, high, original):
+    return ops.ProducerShape(T, hq, hkv, D, pos, 1e-6, ops.ROTARY_LLAMA3, theta, 0, factor, low,
+                             high, original)
+
+
+def test_producer_llama3_matches_llama3_rotary_fixture(torch_mod, ctx, ops, orc):
+    """Every case of llama3-rotary-v1 through the producer (Q heads, no norm, FP32):
+    within the reference's gate 1e-5 + 1e-4|e| of the frozen outputs
+    (src/cpu/llama3_rotary/tests.rs:63-95), and within 1 ulp of the oracle."""
+    from goldens import Golden, close
+
+    torch = torch_mod
+    g = Golden("llama3_rotary_v1")
+    for case in g.meta["cases"]:
+        name, T, H, D = case["name"], case["tokens"], case["heads"], case["head_dim"]
+        x = g.arrays[f"{name}.input"].reshape(T, H, D)
+        zeros = np.zeros((T, 1, D), np.float32)
+        qo = torch.full((T * H * D,), np.nan, dtype=torch.float32, device="cuda")
+        ko = torch.zeros(T * D, dtype=torch.float32, device="cuda")
+        vo = torch.zeros(T * D, dtype=torch.float32, device="cuda")
+        shape = _llama3_shape(ops, T, H, 1, D, case["offset"], case["theta"], case["factor"],
+                              case["low"], case["high"], case["original"])
+        ops.produce_qkv(ctx, shape, _t(torch, x), _t(torch, zeros), _t(torch, zeros), None, None,
+                        qo, ko, vo, T * D)
+        got = host(qo)
+        close(got, g.arrays[f"{name}.output"])
+        ref = orc.llama3_rotary(x.reshape(-1), T, H, D, case["offset"], case["theta"],
+                                case["factor"], case["low"], case["high"], case["original"])
+        u = _ulp_diff_f32(got, ref)
+        log(f"{name}: max ulp {u.max()}")
+        assert u.max() <= 1
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_producer_llama3_across_original_context_edge(torch_mod, ctx, ops, orc, dtype):
+    """Llama 3.1 8B geometry (32/8/128, theta 500000, factor 8, bands 1/4 over 8192)
+    at positions 8160..8223, across the original context length: FP32 within 1 ulp
+    of the oracle (device pow/sin/cos may move a rounding tie), bf16 equal to the
+    oracle rounded once up to a bf16 ulp at ties; V copied."""
+    torch = torch_mod
+    rng = np.random.default_rng(11)
+    T, hq, hkv, D, pos = 64, 32, 8, 128, 8160
+    q = rng.standard_normal((T, hq, D)).astype(np.float32) * 2
+    k = rng.standard_normal((T, hkv, D)).astype(np.float32) * 2
+    v = rng.standard_normal((T, hkv, D)).astype(np.float32)
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    qo = torch.zeros(T * hq * D, dtype=tdt, device="cuda")
+    ko = torch.zeros(hkv * T * D, dtype=tdt, device="cuda")
+    vo = torch.zeros(hkv * T * D, dtype=tdt, device="cuda")
+    shape = _llama3_shape(ops, T, hq, hkv, D, pos, 500000.0, 8.0, 1.0, 4.0, 8192)
+    ops.produce_qkv(ctx, shape, _t(torch, q), _t(torch, k), _t(torch, v), None, None, qo, ko, vo,
+                    T * D)
+    kw = dict(rotary="llama3", theta=500000.0, factor=8.0, low=1.0, high=4.0, original=8192)
+    rq = _oracle_produce(orc, q, None, T, hq, D, pos, **kw)
+    rk = _oracle_produce(orc, k, None, T, hkv, D, pos, **kw)
+    gq = host(qo).reshape(T, hq, D)
+    gk = host(ko).reshape(hkv, T, D).transpose(1, 0, 2)
+    gv = host(vo).reshape(hkv, T, D).transpose(1, 0, 2)
+    for name, gg, r in (("q", gq, rq), ("k", gk, rk)):
+        if dtype == "f32":
+            u = _ulp_diff_f32(gg, r)
+            log(f"{name}: exact {np.mean(u == 0):.6f}, max ulp {u.max()}")
+            assert u.max() <= 1 and np.mean(u == 0) > 0.999
+        else:
+            r = stored(r, "bf16")
+            d = np.abs(gg - r)
+            assert np.mean(d == 0) > 0.999
+            assert np.all(d <= np.abs(r) * 2.0 ** -7 + 1e-30)
+    assert np.array_equal(gv, v if dtype == "f32" else stored(v, "bf16"))
+    # The scaling matters here: the ordinary rotary differs from both.
+    plain = _oracle_produce(orc, q, None, T, hq, D, pos, rotary="split", theta=500000.0)
+    assert not np.allclose(plain, rq, atol=1e-3)
 
 
 def test_producer_nonfinite_input_reports(torch_mod, ctx, ops):
@@ -222,6 +298,50 @@ def test_session_sliding_and_global_layers_gemma_shape(torch_mod, ctx, ops, sess
         err = max_err(host(ctxs[l]).reshape(-1), ref)
         log(f"fused {fused} layer {l} window {window}: max abs error {err:.3e}")
         assert err <= TOL_HALF
+
+
+@pytest.mark.parametrize("fused", ["1", "0"])
+def test_session_llama3_rotary_prefill_then_decode(torch_mod, ctx, ops, sess_mod, orc, fused):
+    """Llama 3.2 1B attention geometry (32/8/64, theta 500000, factor 32, bands 1/4
+    over 8192), bf16 KV, no QK-norm, position offset 8100: 200 prompt tokens in
+    64-token chunks, then 4 decode steps, crossing the original context length.
+    Each context equals full-prefix attention over the oracle's Llama 3 rotary
+    (PositionPlan::Llama3, src/model/position.rs:32-43)."""
+    import os
+
+    torch = torch_mod
+    rng = np.random.default_rng(12)
+    L, hq, hkv, D, prompt, steps, off = 1, 32, 8, 64, 200, 4, 8100
+    total = prompt + steps
+    qs, ks, vs, _, _ = _session_inputs(rng, L, total, hq, hkv, D)
+    opts = sess_mod.Options(capacity=total, prefill_chunk_size=64, position_offset=off,
+                            vocab_size=100, layers=L, query_heads=hq, kv_heads=hkv, head_dim=D,
+                            storage="bf16", rotary=ops.ROTARY_LLAMA3, theta=500000.0, factor=32.0,
+                            low_freq_factor=1.0, high_freq_factor=4.0, original_max_positions=8192)
+    saved = os.environ.get("TKH_FUSED_DECODE")
+    os.environ["TKH_FUSED_DECODE"] = fused
+    try:
+        s = sess_mod.Session(ctx, opts)
+    finally:
+        if saved is None:
+            os.environ.pop("TKH_FUSED_DECODE", None)
+        else:
+            os.environ["TKH_FUSED_DECODE"] = saved
+    out = torch.full((total, hq * D), np.nan, dtype=torch.float32, device="cuda")
+    io = [sess_mod.LayerIo(_t(torch, qs[0]), _t(torch, ks[0]), _t(torch, vs[0]), out, None, None)]
+    s.set_tokens([3] * prompt)
+    assert s.evaluate(io) == prompt
+    s.append([4] * steps)
+    assert s.evaluate(io, chunk_limit=1) == steps
+    kw = dict(rotary="llama3", theta=500000.0, factor=32.0, low=1.0, high=4.0, original=8192)
+    q = stored(_oracle_produce(orc, qs[0], None, total, hq, D, off, **kw), "bf16")
+    k = stored(_oracle_produce(orc, ks[0], None, total, hkv, D, off, **kw), "bf16")
+    v = stored(vs[0], "bf16")
+    ref, _, _ = orc.attention(q.reshape(-1), k.reshape(-1), v.reshape(-1), total, hq, hkv, D)
+    err = max_err(host(out).reshape(-1), ref)
+    log(f"fused {fused}: max abs error {err:.3e}")
+    assert err <= TOL_HALF
+    s.close()
 
 
 def test_session_failed_chunk_commits_nothing_and_retry_succeeds(torch_mod, ctx, ops, sess_mod, orc):

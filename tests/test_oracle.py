@@ -592,6 +592,130 @@ def test_proportional_rotary_matches_gemma_rotary_fixture(orc):
     assert checked == 7
 
 
+# ---- llama3-rotary-v1 (src/cpu/llama3_rotary/tests.rs:63-302) ----
+
+def _llama3_ordinary(theta, pair, head_dim):
+    return float(np.float32(theta)) ** (-(2.0 * pair) / head_dim)
+
+
+def test_llama3_rotary_matches_llama3_rotary_fixture(orc):
+    """Every case of llama3-rotary-v1 (position 0, short inputs, the original
+    context edge, the declared 131072 end, position 2^20, factor 1, other band
+    parameters): FP64 inverse frequencies within 1e-15 + 1e-13|e| and outputs
+    within 1e-5 + 1e-4|e|, the reference's own gates."""
+    g = Golden("llama3_rotary_v1")
+    for case in g.meta["cases"]:
+        name, D = case["name"], case["head_dim"]
+        s = orc.llama3_scaling(case["factor"], case["low"], case["high"], case["original"])
+        want = g.arrays[f"{name}.inverse_frequencies"]
+        assert want.size == D // 2
+        for pair, e in enumerate(want):
+            a = orc.llama3_inverse_frequency(s, _llama3_ordinary(case["theta"], pair, D))
+            assert abs(a - e) <= 1e-15 + 1e-13 * abs(e), (name, pair, a, e)
+        out = orc.llama3_rotary(g.arrays[f"{name}.input"], case["tokens"], case["heads"], D,
+                                case["offset"], case["theta"], case["factor"], case["low"],
+                                case["high"], case["original"])
+        close(out, g.arrays[f"{name}.output"])
+    assert len(g.meta["cases"]) == 7
+
+
+def test_llama3_scaling_bands_and_edges(orc):
+    """The fixture's controls, the band edges (wavelength original/high keeps the
+    ordinary frequency, original/low divides it by factor exactly), continuity one
+    ulp either side of each edge, and the 15/3/14 split of theta 500000, D 64 over
+    the three bands (src/cpu/llama3_rotary/tests.rs:97-127)."""
+    g = Golden("llama3_rotary_v1")
+    s = orc.llama3_scaling(32.0, 1.0, 4.0, 8192)
+    assert len(g.meta["controls"]) == 5
+    for c in g.meta["controls"]:
+        a = orc.llama3_inverse_frequency(s, c["ordinary"])
+        assert abs(a - c["scaled"]) <= 1e-17 + 1e-13 * abs(c["scaled"])
+    high = 2.0 * math.pi * 4.0 / 8192.0
+    low = 2.0 * math.pi / 8192.0
+    assert orc.llama3_inverse_frequency(s, high) == high
+    assert orc.llama3_inverse_frequency(s, low) == low / 32.0
+    for edge in (low, high):
+        at = orc.llama3_inverse_frequency(s, edge)
+        for x in (np.nextafter(edge, 0.0), np.nextafter(edge, 1.0)):
+            assert abs(orc.llama3_inverse_frequency(s, float(x)) - at) < 1e-17
+    # Inside the band the result is the linear blend of ordinary/factor and
+    # ordinary in original/wavelength: at the band's middle (wavelength 4096,
+    # original/wavelength 2 = low + (high - low) / 3) one third of the ordinary
+    # frequency is kept.
+    mid = 2.0 * math.pi / 4096.0
+    want = (2.0 / 3.0) * mid / 32.0 + (1.0 / 3.0) * mid
+    assert abs(orc.llama3_inverse_frequency(s, mid) - want) <= 1e-15 * want
+    bands = [0, 0, 0]
+    for pair in range(32):
+        wavelength = 2.0 * math.pi / _llama3_ordinary(500000.0, pair, 64)
+        assert wavelength not in (2048.0, 8192.0)
+        bands[0 if wavelength < 2048.0 else (2 if wavelength > 8192.0 else 1)] += 1
+    assert bands == [15, 3, 14]
+
+
+def test_llama3_rotary_reduces_to_ordinary_rotary(orc):
+    """Factor 1, and a theta whose every wavelength sits below original/high, give
+    the split-half rotary bit for bit; at short positions the scaled pairs differ
+    (scaling applies before the position, even for short inputs); chunks at
+    absolute offsets join to the whole (src/cpu/llama3_rotary/tests.rs:130-204)."""
+    x = np.array([((i * 7 % 31) - 15) * 0.125 for i in range(96)], np.float32)
+    for theta, factor in ((500000.0, 1.0), (2.0, 32.0)):
+        a = orc.llama3_rotary(x, 3, 2, 16, 131069, theta, factor, 1.0, 4.0, 8192)
+        b = orc.rotary(x, 3, 2, 16, 131069, theta)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    x = np.array([((i * 7 % 31) - 15) * 0.125 for i in range(384)], np.float32)
+    whole = orc.llama3_rotary(x, 3, 2, 64, 131069, 500000.0, 32.0, 1.0, 4.0, 8192)
+    for chunk in (1, 2):
+        parts = []
+        for first in range(0, 3, chunk):
+            n = min(chunk, 3 - first)
+            parts.append(orc.llama3_rotary(x[first * 128:(first + n) * 128], n, 2, 64,
+                                           131069 + first, 500000.0, 32.0, 1.0, 4.0, 8192))
+        assert np.array_equal(np.concatenate(parts), whole)
+    short = orc.llama3_rotary(x, 3, 2, 64, 1, 500000.0, 32.0, 1.0, 4.0, 8192)
+    ordinary = orc.rotary(x, 3, 2, 64, 1, 500000.0)
+    assert not np.array_equal(short.view(np.uint32), ordinary.view(np.uint32))
+    # The pairs below original/high (the first 15 of 32) keep the ordinary rotation.
+    sr, orr = short.reshape(3, 2, 64), ordinary.reshape(3, 2, 64)
+    assert np.array_equal(sr[..., :15], orr[..., :15]) and np.array_equal(sr[..., 32:47], orr[..., 32:47])
+
+
+def test_llama3_rotary_rejects_invalid_parameters(orc):
+    """Llama3Scaling::new and llama3_rotary refuse what the reference refuses
+    (src/cpu/llama3_rotary/tests.rs:207-302); position 2^53 is accepted."""
+    bad = [(v, 1.0, 4.0, 8192) for v in (0.0, -1.0, 0.5, math.nan, math.inf)]
+    bad += [(32.0, v, 4.0, 8192) for v in (0.0, -1.0, math.nan, math.inf)]
+    bad += [(32.0, 1.0, v, 8192) for v in (0.0, -1.0, math.nan, math.inf)]
+    bad += [(32.0, 4.0, 4.0, 8192), (32.0, 5.0, 4.0, 8192), (32.0, 1.0, 4.0, 0),
+            (32.0, 1.0, 4.0, (1 << 53) + 1)]
+    for args in bad:
+        with pytest.raises(orc.OracleError) as e:
+            orc.llama3_scaling(*args)
+        assert e.value.name == "InvalidParameter"
+    s = orc.llama3_scaling(32.0, 1.0, 4.0, 8192)
+    for v in (0.0, -1.0, math.nan, math.inf, 5e-324):
+        with pytest.raises(orc.OracleError):
+            orc.llama3_inverse_frequency(s, v)
+    ones = np.ones(16, np.float32)
+    geometry = [(0, 1, 16, 1, 500000.0), (1, 0, 16, 1, 500000.0), (1, 1, 3, 1, 500000.0),
+                (1, 1, 16, (1 << 53) + 1, 500000.0), (1, 1, 16, 1, 0.0), (1, 1, 16, 1, math.nan)]
+    for tokens, heads, d, offset, theta in geometry:
+        with pytest.raises(orc.OracleError):
+            orc.llama3_rotary(ones, tokens, heads, d, offset, theta, 32.0, 1.0, 4.0, 8192)
+    for value in (math.nan, math.inf, -math.inf):
+        x = ones.copy()
+        x[15] = value
+        with pytest.raises(orc.OracleError) as e:
+            orc.llama3_rotary(x, 1, 1, 16, 1, 500000.0, 32.0, 1.0, 4.0, 8192)
+        assert e.value.name == "NonFinite"
+    fmax = float(np.finfo(np.float32).max)
+    with pytest.raises(orc.OracleError) as e:
+        orc.llama3_rotary(np.array([fmax, -fmax], np.float32), 1, 1, 2, 1, 500000.0, 32.0, 1.0,
+                          4.0, 8192)
+    assert e.value.name == "NonFinite"
+    orc.llama3_rotary(ones, 1, 1, 16, 1 << 53, 500000.0, 32.0, 1.0, 4.0, 8192)
+
+
 # ---- gemma-reference-attention-v1 (tools/reference/test_gemma_reference_attention.py:46-58) ----
 
 def _reference_attention_oracle(orc, case, q, k, v):

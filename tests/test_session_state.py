@@ -178,3 +178,33 @@ def test_invalid_options_are_rejected():
     with pytest.raises(TkhError) as e:  # attention_cached semantics have no softcap
         Session(None, Options(capacity=8, softcap=50.0))
     assert e.value.code == _lib.INVALID_CONFIG
+
+
+def test_llama3_rotary_options_are_validated():
+    """Llama3Scaling::new's rules (src/cpu/llama3_rotary.rs:14-37, tests.rs:207-221)
+    hold for the session's rotary options: factor >= 1, low > 0, high > low, the
+    original context length in 1..2^53, theta finite and positive."""
+    from toklet_amd.ops import ROTARY_LLAMA3
+
+    def opts(**kw):
+        base = dict(capacity=8, query_heads=4, kv_heads=2, head_dim=8, rotary=ROTARY_LLAMA3,
+                    theta=500000.0, factor=32.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                    original_max_positions=8192)
+        base.update(kw)
+        return Options(**base)
+
+    Session(None, opts()).close()
+    Session(None, opts(factor=1.0)).close()
+    nan, inf = float("nan"), float("inf")
+    bad = [dict(factor=v) for v in (0.0, -1.0, 0.5, nan, inf)]
+    bad += [dict(low_freq_factor=v) for v in (0.0, -1.0, nan, inf)]
+    bad += [dict(high_freq_factor=v) for v in (0.0, -1.0, nan, inf)]
+    bad += [dict(low_freq_factor=4.0), dict(low_freq_factor=5.0), dict(original_max_positions=0),
+            dict(original_max_positions=(1 << 53) + 1), dict(theta=0.0), dict(theta=nan)]
+    for kw in bad:
+        with pytest.raises(TkhError) as e:
+            Session(None, opts(**kw))
+        assert e.value.code == _lib.INVALID_PARAMETER, kw
+    with pytest.raises(TkhError) as e:
+        Session(None, opts(rotary=4))
+    assert e.value.code == _lib.INVALID_PARAMETER

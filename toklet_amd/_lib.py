@@ -73,10 +73,15 @@ class KvFrame(ctypes.Structure):
                 ("tokens", u64)]
 
 
+# TKH_ABI_VERSION of include/tokhip.h that the structures below mirror.
+ABI_VERSION = 2
+
+
 class ProducerShape(ctypes.Structure):
     _fields_ = [(n, u64) for n in ("tokens", "query_heads", "kv_heads", "head_dim", "position")] + [
         ("norm_epsilon", f32), ("rotary", u32), ("theta", f32), ("rotated_dims", u64),
-        ("factor", f32)]
+        ("factor", f32), ("low_freq_factor", f32), ("high_freq_factor", f32),
+        ("original_max_positions", u64)]
 
 
 class SessionOptions(ctypes.Structure):
@@ -84,7 +89,8 @@ class SessionOptions(ctypes.Structure):
                                    "vocab_size", "layers", "query_heads", "kv_heads",
                                    "head_dim")] + [
         ("storage", ctypes.c_int), ("score_scale", f32), ("softcap", f32), ("norm_epsilon", f32),
-        ("rotary", u32), ("theta", f32), ("rotated_dims", u64), ("factor", f32)]
+        ("rotary", u32), ("theta", f32), ("rotated_dims", u64), ("factor", f32),
+        ("low_freq_factor", f32), ("high_freq_factor", f32), ("original_max_positions", u64)]
 
 
 class SessionState(ctypes.Structure):
@@ -165,6 +171,9 @@ def load():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        if lib.tkh_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {lib.tkh_abi_version()}, these "
+                               f"bindings expect {ABI_VERSION}: rebuild it")
         _lib = lib
     return _lib
 

@@ -72,6 +72,17 @@ struct Problem {
 };
 
 // Producer launch (produce.hip): per-head RMSNorm, rotary, cache rounding.
+// Rotary position embedding of the producer: kind 0 none, 1 split-half
+// (theta), 2 proportional (base in theta, rotated_dims, factor), 3 Llama 3
+// wavelength bands (theta, factor, low/high frequency factors, original
+// context length).
+struct RotarySpec {
+    int32_t kind;
+    int32_t rotated_dims;
+    float theta, factor, low, high;
+    double original;
+};
+
 struct ProduceParams {
     const float *q, *k, *v;   // [T, Hq, D], [T, Hkv, D], [T, Hkv, D] FP32, token-major
     const float *q_norm;      // [D] or null (no norm)
@@ -82,9 +93,8 @@ struct ProduceParams {
     int64_t tokens;
     int64_t position;         // absolute rotary position of token 0
     int32_t hq, hkv, d;
-    int32_t rotary;           // 0 none, 1 split-half, 2 proportional
-    int32_t rotated_dims;     // proportional: rotated features (even, <= D)
-    float eps, theta, factor; // theta: split-half theta or proportional base
+    RotarySpec rot;
+    float eps;
     uint32_t *status;
     // Optional precomputed (cos, sin) per (position, pair), rows from absolute
     // position rope_pos0, `pairs` entries per row (the same FP64 formulas,

@@ -13,6 +13,10 @@
 //  * proportional rotary (src/cpu/proportional_rotary.rs:32-91): inverse
 //    frequency base^(-2j/D) / factor for pairs j < rotated_dims / 2, other
 //    features copied;
+//  * Llama 3 rotary (src/cpu/llama3_rotary.rs:44-61, 87-146): the ordinary
+//    frequency theta^(-2j/D) kept for wavelengths below original/high, divided
+//    by factor above original/low, blended linearly in original/wavelength in
+//    between, all in FP64; angle and rotation as for split-half;
 //  * LayerKv::append (src/model/cache.rs:64-85): token-major new rows into
 //    head-major cache rows, here rounded once to the cache dtype.
 // The FP64 sum runs in a different order than the reference's sequential one;
@@ -29,19 +33,34 @@ namespace tkh {
 
 namespace {
 
-__device__ __forceinline__ int rotary_pairs(int rotary, int D, int rotated_dims) {
-    return rotary == 1 ? D / 2 : (rotary == 2 ? rotated_dims / 2 : 0);
+__host__ __device__ __forceinline__ int rotary_pairs(int kind, int D, int rotated_dims) {
+    return (kind == 1 || kind == 3) ? D / 2 : (kind == 2 ? rotated_dims / 2 : 0);
 }
 
-// Rotation of pair j at absolute position pos: frequency theta^(-2j/D) (divided
-// by factor for the proportional form), angle and sine/cosine in FP64,
+// Inverse frequency of pair j in FP64: theta^(-2j/D), divided by factor for
+// the proportional form (src/cpu/proportional_rotary.rs:68-70), or scaled by
+// wavelength band for Llama 3 (Llama3Scaling::inverse_frequency,
+// src/cpu/llama3_rotary.rs:44-61; 6.283185307179586 is 2*pi rounded to FP64).
+__device__ __forceinline__ double inverse_frequency(const RotarySpec &r, int D, int j) {
+#pragma clang fp contract(off)
+    const double ordinary = pow((double)r.theta, -(2.0 * (double)j) / (double)D);
+    if (r.kind == 2) return ordinary / (double)r.factor;
+    if (r.kind != 3) return ordinary;
+    const double factor = r.factor, low = r.low, high = r.high;
+    const double wavelength = 6.283185307179586 / ordinary;
+    if (factor == 1.0 || wavelength < r.original / high) return ordinary;
+    if (wavelength > r.original / low) return ordinary / factor;
+    const double smooth = (r.original / wavelength - low) / (high - low);
+    return (1.0 - smooth) * ordinary / factor + smooth * ordinary;
+}
+
+// Rotation of pair j at absolute position pos: angle and sine/cosine in FP64,
 // rounded once to FP32 (src/cpu/attention.rs:41-46,
-// src/cpu/proportional_rotary.rs:68-74).
-__device__ __forceinline__ void rotary_cos_sin(int rotary, float theta, float factor, int D,
-                                               int64_t pos, int j, float *c, float *s) {
-    double inv = pow((double)theta, -(2.0 * (double)j) / (double)D);
-    if (rotary == 2) inv = inv / (double)factor;
-    const double angle = (double)pos * inv;
+// src/cpu/proportional_rotary.rs:68-74, src/cpu/llama3_rotary.rs:126-128).
+__device__ __forceinline__ void rotary_cos_sin(const RotarySpec &r, int D, int64_t pos, int j,
+                                               float *c, float *s) {
+#pragma clang fp contract(off)
+    const double angle = (double)pos * inverse_frequency(r, D, j);
     *s = (float)sin(angle);
     *c = (float)cos(angle);
 }
@@ -82,7 +101,7 @@ __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
     constexpr int KMAX = 8;  // elements per lane, D <= 512
     const float *w = kind == 0 ? p.q_norm : (kind == 1 ? p.k_norm : nullptr);
     const int half = D / 2;
-    const int pairs = kind == 2 ? 0 : rotary_pairs(p.rotary, D, p.rotated_dims);
+    const int pairs = kind == 2 ? 0 : rotary_pairs(p.rot.kind, D, p.rot.rotated_dims);
     float xv[KMAX], wv[KMAX], cv[KMAX / 2], sv[KMAX / 2];
     for (int k = 0; k < KMAX; ++k) {
         const int i = lane + 64 * k;
@@ -99,7 +118,7 @@ __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
                 cv[k] = cs[0];
                 sv[k] = cs[1];
             } else {
-                rotary_cos_sin(p.rotary, p.theta, p.factor, D, p.position + t, j, &cv[k], &sv[k]);
+                rotary_cos_sin(p.rot, D, p.position + t, j, &cv[k], &sv[k]);
             }
         }
     }
@@ -155,15 +174,14 @@ __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
 // (cos, sin) of every (position, pair) for rows [pos0, pos0 + rows): the
 // producer's table, filled once per session with the same FP64 formulas.
 __global__ __launch_bounds__(256) void rotary_table(float *out, int64_t pos0, int64_t rows,
-                                                    int pairs, int rotary, float theta,
-                                                    float factor, int D) {
+                                                    int pairs, RotarySpec rot, int D) {
 #pragma clang fp contract(off)
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows * pairs) return;
     const int64_t r = i / pairs;
     const int j = (int)(i % pairs);
     float c, s;
-    rotary_cos_sin(rotary, theta, factor, D, pos0 + r, j, &c, &s);
+    rotary_cos_sin(rot, D, pos0 + r, j, &c, &s);
     out[2 * i] = c;
     out[2 * i + 1] = s;
 }
@@ -171,19 +189,19 @@ __global__ __launch_bounds__(256) void rotary_table(float *out, int64_t pos0, in
 }  // namespace tkh
 
 extern "C" int tkh_rotary_pairs(int rotary, int head_dim, int rotated_dims) {
-    return rotary == 1 ? head_dim / 2 : (rotary == 2 ? rotated_dims / 2 : 0);
+    return tkh::rotary_pairs(rotary, head_dim, rotated_dims);
 }
 
-extern "C" hipError_t tkh_launch_rotary_table(float *out, int64_t pos0, int64_t rows, int rotary,
-                                              float theta, float factor, int head_dim,
-                                              int rotated_dims, hipStream_t stream) {
+extern "C" hipError_t tkh_launch_rotary_table(float *out, int64_t pos0, int64_t rows,
+                                              const tkh::RotarySpec *rot, int head_dim,
+                                              hipStream_t stream) {
     using namespace tkh;
-    const int pairs = tkh_rotary_pairs(rotary, head_dim, rotated_dims);
+    const int pairs = rotary_pairs(rot->kind, head_dim, rot->rotated_dims);
     const int64_t n = rows * pairs;
     if (n <= 0) return hipSuccess;
     dim3 grid((unsigned)((n + 255) / 256)), block(256);
-    hipLaunchKernelGGL(rotary_table, grid, block, 0, stream, out, pos0, rows, pairs, rotary, theta,
-                       factor, head_dim);
+    hipLaunchKernelGGL(rotary_table, grid, block, 0, stream, out, pos0, rows, pairs, *rot,
+                       head_dim);
     return hipGetLastError();
 }
 

@@ -20,9 +20,9 @@
 extern "C" hipError_t tkh_launch_produce(const tkh::ProduceParams *p, int dtype, hipStream_t stream);
 extern "C" hipError_t tkh_launch_fill_u64(uint64_t *p, uint64_t v, hipStream_t stream);
 extern "C" int tkh_rotary_pairs(int rotary, int head_dim, int rotated_dims);
-extern "C" hipError_t tkh_launch_rotary_table(float *out, int64_t pos0, int64_t rows, int rotary,
-                                              float theta, float factor, int head_dim,
-                                              int rotated_dims, hipStream_t stream);
+extern "C" hipError_t tkh_launch_rotary_table(float *out, int64_t pos0, int64_t rows,
+                                              const tkh::RotarySpec *rot, int head_dim,
+                                              hipStream_t stream);
 
 using namespace tkh_host;
 
@@ -39,7 +39,7 @@ uint32_t check_producer(const tkh_producer_shape *sh, tkh_error *err) {
     if (sh->head_dim % 2 != 0) return invalid("rotary head_dim must be even", err);
     if (sh->head_dim > 512) return fail(err, TKH_UNSUPPORTED, "head_dim", 0, 512, sh->head_dim,
                                         "head_dim above 512 is not supported");
-    if (sh->rotary > TKH_ROTARY_PROPORTIONAL) return invalid("rotary kind", err);
+    if (sh->rotary > TKH_ROTARY_LLAMA3) return invalid("rotary kind", err);
     if (sh->rotary != TKH_ROTARY_NONE && (!std::isfinite(sh->theta) || sh->theta <= 0.0f))
         return invalid("theta must be finite and positive", err);
     if (sh->rotary == TKH_ROTARY_PROPORTIONAL) {
@@ -48,10 +48,50 @@ uint32_t check_producer(const tkh_producer_shape *sh, tkh_error *err) {
         if (!std::isfinite(sh->factor) || sh->factor <= 0.0f)
             return invalid("proportional rotary base/factor", err);
     }
+    if (sh->rotary == TKH_ROTARY_LLAMA3) {
+        // Llama3Scaling::new (src/cpu/llama3_rotary.rs:14-37).
+        const float f = sh->factor, lo = sh->low_freq_factor, hi = sh->high_freq_factor;
+        if (!std::isfinite(f) || f < 1.0f || !std::isfinite(lo) || lo <= 0.0f ||
+            !std::isfinite(hi) || hi <= lo || sh->original_max_positions == 0 ||
+            sh->original_max_positions > (uint64_t{1} << 53))
+            return invalid("Llama3 rotary scaling", err);
+        // The scaled frequency of every pair must stay finite and positive
+        // (src/cpu/llama3_rotary.rs:57-59); the kernels evaluate the same band
+        // formula.
+        const double orig = (double)sh->original_max_positions;
+        for (uint64_t j = 0; j < sh->head_dim / 2; ++j) {
+            const double ordinary =
+                std::pow((double)sh->theta, -(2.0 * (double)j) / (double)sh->head_dim);
+            const double wavelength = 6.283185307179586 / ordinary;
+            double inv = ordinary;
+            if (f != 1.0f && !(wavelength < orig / hi)) {
+                if (wavelength > orig / lo) {
+                    inv = ordinary / f;
+                } else {
+                    const double smooth = (orig / wavelength - lo) / ((double)hi - lo);
+                    inv = (1.0 - smooth) * ordinary / f + smooth * ordinary;
+                }
+            }
+            if (!std::isfinite(ordinary) || ordinary <= 0.0 || !std::isfinite(inv) || inv <= 0.0)
+                return invalid("Llama3 scaled frequency underflow", err);
+        }
+    }
     uint64_t last;
     TRY(add(sh->position, sh->tokens - 1, &last, err));
     if (last > (uint64_t{1} << 53)) return invalid("rotary positions must be at most 2^53", err);
     return TKH_OK;
+}
+
+tkh::RotarySpec rotary_spec(const tkh_producer_shape *sh) {
+    tkh::RotarySpec r{};
+    r.kind = (int32_t)sh->rotary;
+    r.rotated_dims = (int32_t)sh->rotated_dims;
+    r.theta = sh->theta;
+    r.factor = sh->factor;
+    r.low = sh->low_freq_factor;
+    r.high = sh->high_freq_factor;
+    r.original = (double)sh->original_max_positions;
+    return r;
 }
 
 uint32_t launch_producer(tkh_context *ctx, const tkh_producer_shape *sh, tkh_dtype dtype,
@@ -76,11 +116,8 @@ uint32_t launch_producer(tkh_context *ctx, const tkh_producer_shape *sh, tkh_dty
     p.hq = (int32_t)sh->query_heads;
     p.hkv = (int32_t)sh->kv_heads;
     p.d = (int32_t)sh->head_dim;
-    p.rotary = (int32_t)sh->rotary;
-    p.rotated_dims = (int32_t)sh->rotated_dims;
+    p.rot = rotary_spec(sh);
     p.eps = sh->norm_epsilon;
-    p.theta = sh->theta;
-    p.factor = sh->factor;
     p.status = ctx->status_dev;
     HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
     HIP_TRY(tkh_launch_produce(&p, (int)dtype, ctx->stream), "producer launch");
@@ -284,6 +321,9 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
     sh.theta = o->theta;
     sh.rotated_dims = o->rotated_dims;
     sh.factor = o->factor;
+    sh.low_freq_factor = o->low_freq_factor;
+    sh.high_freq_factor = o->high_freq_factor;
+    sh.original_max_positions = o->original_max_positions;
     TRY(check_producer(&sh, err));
     uint64_t last;
     TRY(add(o->position_offset, o->capacity, &last, err));
@@ -357,10 +397,10 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
         if (e == hipSuccess && pairs > 0) {
             const size_t bytes = (size_t)o->capacity * pairs * 2 * sizeof(float);
             e = hipMalloc(&s->rope, bytes);
+            const tkh::RotarySpec rot = rotary_spec(&sh);
             if (e == hipSuccess)
-                e = tkh_launch_rotary_table(s->rope, (int64_t)o->position_offset, (int64_t)o->capacity,
-                                            (int)o->rotary, o->theta, o->factor, (int)D,
-                                            (int)o->rotated_dims, ctx->stream);
+                e = tkh_launch_rotary_table(s->rope, (int64_t)o->position_offset,
+                                            (int64_t)o->capacity, &rot, (int)D, ctx->stream);
             if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
             s->scratch_bytes += bytes;
         }
@@ -500,6 +540,9 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
     sh.theta = o.theta;
     sh.rotated_dims = o.rotated_dims;
     sh.factor = o.factor;
+    sh.low_freq_factor = o.low_freq_factor;
+    sh.high_freq_factor = o.high_freq_factor;
+    sh.original_max_positions = o.original_max_positions;
     const uint64_t checked = s->checked;
     const bool checked_valid = s->checked_valid;
     std::vector<tkh_kv *> ring_kv;

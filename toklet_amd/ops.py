@@ -321,13 +321,15 @@ def prefill_batch(ctx: Context, q, k_base, v_base, offsets, head_strides, positi
 
 # ---- producer: the step before attention (Model::run, src/model/mod.rs:611-662) ----
 
-ROTARY_NONE, ROTARY_SPLIT_HALF, ROTARY_PROPORTIONAL = 0, 1, 2
+ROTARY_NONE, ROTARY_SPLIT_HALF, ROTARY_PROPORTIONAL, ROTARY_LLAMA3 = 0, 1, 2, 3
 
 
 @dataclass
 class ProducerShape:
     """Per-layer producer geometry: norm epsilon, rotary kind and its parameters
-    (split-half theta, or proportional base / rotated_dims / factor)."""
+    (split-half theta; proportional base / rotated_dims / factor; Llama 3 theta,
+    factor, low/high frequency factors and original context length, as
+    Llama3Scaling::new takes them, src/cpu/llama3_rotary.rs:14-37)."""
     tokens: int
     query_heads: int
     kv_heads: int
@@ -338,11 +340,15 @@ class ProducerShape:
     theta: float = 1e6
     rotated_dims: int = 0
     factor: float = 1.0
+    low_freq_factor: float = 1.0
+    high_freq_factor: float = 4.0
+    original_max_positions: int = 8192
 
     def c(self):
         return _lib.ProducerShape(self.tokens, self.query_heads, self.kv_heads, self.head_dim,
                                   self.position, self.norm_epsilon, self.rotary, self.theta,
-                                  self.rotated_dims, self.factor)
+                                  self.rotated_dims, self.factor, self.low_freq_factor,
+                                  self.high_freq_factor, self.original_max_positions)
 
 
 def produce_qkv(ctx: Context, shape: ProducerShape, q_proj, k_proj, v_proj, q_norm, k_norm,

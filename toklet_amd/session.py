@@ -44,6 +44,9 @@ class Options:
     theta: float = 1e6
     rotated_dims: int = 0
     factor: float = 1.0
+    low_freq_factor: float = 1.0       # Llama 3 rotary only
+    high_freq_factor: float = 4.0
+    original_max_positions: int = 8192
     layer_windows: Optional[Sequence[int]] = None   # per layer, 0 = full
 
     def c(self):
@@ -51,7 +54,8 @@ class Options:
                                    self.vocab_size, self.layers, self.query_heads, self.kv_heads,
                                    self.head_dim, _STORAGE[self.storage], self.score_scale,
                                    self.softcap, self.norm_epsilon, self.rotary, self.theta,
-                                   self.rotated_dims, self.factor)
+                                   self.rotated_dims, self.factor, self.low_freq_factor,
+                                   self.high_freq_factor, self.original_max_positions)
 
 
 @dataclass
