@@ -283,6 +283,26 @@ def _context_with_env(ops, env):
                 os.environ[k] = v
 
 
+@pytest.mark.parametrize("groups,keys_per_lane", [(256, 4), (512, 2), (512, 4)])
+def test_in_kernel_merge_of_many_splits(torch_mod, ops, orc, groups, keys_per_lane):
+    """The last split's own merge (the second launch switched off) at 32 and 64
+    splits per KV head: its output loads run over four split groups at a time, so
+    these take two and four runs; against the oracle and bit-equal to the merge
+    launch's result (the same weights and sums in the same order)."""
+    torch = torch_mod
+    env = {"TKH_DECODE_GROUPS": groups, "TKH_DECODE_KEYS_PER_LANE": keys_per_lane}
+    inkernel = _context_with_env(ops, dict(env, TKH_DECODE_MERGE_LAUNCH=0))
+    launch = _context_with_env(ops, dict(env, TKH_DECODE_MERGE_LAUNCH=1))
+    got, ref = _cached_case(torch, inkernel, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
+                            capacity=8200, offset=8191, tokens=1, seed=groups + keys_per_lane)
+    err = max_err(got, ref)
+    log(f"in-kernel merge, {groups} groups, {keys_per_lane} keys per lane: max abs error {err:.3e}")
+    assert err <= TOL_HALF
+    again, _ = _cached_case(torch, launch, ops, orc, hq=16, hkv=8, D=128, dt="bf16",
+                            capacity=8200, offset=8191, tokens=1, seed=groups + keys_per_lane)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
 def test_stream_load_form_does_not_change_results(torch_mod, ops, orc):
     """The K/V stream's load form (nontemporal for much work, plain for latency-bound
     launches) is forced both ways in both regimes: the outputs are bit-identical and

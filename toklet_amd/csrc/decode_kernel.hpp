@@ -875,10 +875,13 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     // (g4, q4) = (lane / 16, lane % 16) reads, for splits 4 g + g4, the four
     // outputs d0 + 4 q4 .. + 3 (16-byte buffer loads, sc1) and the split's
     // (max, mass); lanes past the other splits read out of the buffer's range,
-    // which returns zeros and touches no memory, so every load of the merge is
-    // issued in one straight run with no branches and no repeated address.
-    // Then: the row maximum, per-split weights, the weighted sums over the
-    // lane's splits, and lane swaps over the four split groups.
+    // which returns zeros and touches no memory, so the loads are issued in
+    // straight runs with no branches and no repeated address: every split's
+    // (max, mass) at once, then the outputs of four split groups per run (the
+    // merge's registers stay below the stream's: one run over all sixteen
+    // groups held 64 more).  Then: the row maximum, per-split weights, the
+    // weighted sums over the lane's splits, and lane swaps over the four
+    // split groups.
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc(p.part_ml, 0, 0x7FFFFFFF, BUFFER_RSRC_WORD3);
     const uint32_t o_base = (uint32_t)(reinterpret_cast<const char *>(p.part_o) -
@@ -886,18 +889,17 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     const int g4 = lane >> 4, q4 = lane & 15;
     const int ng = (S + 3) >> 2;
     const int chunks = R * D / 64;
+    constexpr int GRUN = 4;  // split groups per run of output loads
     for (int c = wave; c < chunks && !timed_out; c += nw) {
         const int r = c * 64 / D, d = c * 64 - r * D + 4 * q4;
         if (r >= nrows) continue;  // uniform over the wave
         const uint32_t ml0 = (uint32_t)((slot0 * R + r) * 2) * 4u, ml_step = (uint32_t)R * 8u;
         const uint32_t o0 = o_base + (uint32_t)((slot0 * R + r) * D + d) * 4u, o_step = (uint32_t)(R * D) * 4u;
-        f32x4 ov[DECODE_MAX_SPLITS / 4];
         f32x2 mv[DECODE_MAX_SPLITS / 4];
         for (int g = 0; g < DECODE_MAX_SPLITS / 4; ++g) {
             if (g < ng) {
                 const int sp = 4 * g + g4;
                 const bool theirs = sp < S - 1;
-                ov[g] = __builtin_amdgcn_raw_buffer_load_b128(prs, theirs ? o0 + (uint32_t)sp * o_step : OUT_OF_RANGE, 0, CPOL_SC1_NT);
                 mv[g] = __builtin_amdgcn_raw_buffer_load_b64(prs, theirs ? ml0 + (uint32_t)sp * ml_step : OUT_OF_RANGE, 0, CPOL_SC1_NT);
             }
         }
@@ -908,7 +910,6 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
             if (g < ng) {
                 const int sp = 4 * g + g4;
                 if (sp == S - 1) {
-                    ov[g] = own_o;
                     mv[g] = own_ml;
                 } else if (sp >= S) {
                     mv[g][0] = NEG_INF;
@@ -927,10 +928,24 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
         float lsum = 0.0f;
         for (int g = 0; g < DECODE_MAX_SPLITS / 4; ++g) {
-            if (g < ng) {
-                const float wgt = __builtin_amdgcn_exp2f(mv[g][0] - base);
-                for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(wgt, ov[g][k], acc[k]);
-                lsum = __builtin_fmaf(wgt, mv[g][1], lsum);
+            if (g < ng) lsum = __builtin_fmaf(__builtin_amdgcn_exp2f(mv[g][0] - base), mv[g][1], lsum);
+        }
+        for (int g0 = 0; g0 < DECODE_MAX_SPLITS / 4; g0 += GRUN) {
+            if (g0 >= ng) break;  // uniform over the wave
+            f32x4 ov[GRUN];
+            for (int j = 0; j < GRUN; ++j) {
+                const int sp = 4 * (g0 + j) + g4;
+                const bool theirs = g0 + j < ng && sp < S - 1;
+                ov[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, theirs ? o0 + (uint32_t)sp * o_step : OUT_OF_RANGE, 0, CPOL_SC1_NT);
+            }
+            for (int j = 0; j < GRUN; ++j) {
+                const int g = g0 + j;
+                if (g < ng) {
+                    const int sp = 4 * g + g4;
+                    if (sp == S - 1) ov[j] = own_o;
+                    const float wgt = __builtin_amdgcn_exp2f(mv[g][0] - base);
+                    for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(wgt, ov[j][k], acc[k]);
+                }
             }
         }
         lane_pair<16>(lsum, pa, pb);
