@@ -51,7 +51,8 @@ extern "C" {
 #endif
 
 /* 2: tkh_producer_shape and tkh_session_options end with the Llama 3 rotary
- * parameters (low/high frequency factors, original context length). */
+ * parameters (low/high frequency factors, original context length), and
+ * tkh_session_options with shared_layers. */
 #define TKH_ABI_VERSION 2u
 
 typedef enum tkh_status {
@@ -374,7 +375,15 @@ typedef struct tkh_session tkh_session;
  * score_scale 0 selects attention_cached semantics (dot / sqrt(D), no
  * softcap) for full layers, and a nonzero softcap with it is rejected
  * (TKH_INVALID_CONFIG); otherwise every layer uses window/span semantics
- * with this scale and the optional score softcap. */
+ * with this scale and the optional score softcap.
+ * shared_layers: the last shared_layers layers own no KV cache; each attends
+ * over the current-step view of the last earlier owning layer of its kind
+ * (sliding: nonzero window, which must be equal; full: 0), as
+ * SharedKvPlan::new routes them (src/model/shared_kv.rs:50-120).  Their K/V
+ * projections and k_norm are not read (they may be NULL); only Q is
+ * normalised and rotated.  At least one layer must own a cache
+ * (TKH_INVALID_CONFIG otherwise, as for a shared layer without a producer of
+ * its kind or with a different window). */
 typedef struct tkh_session_options {
     uint64_t capacity;
     uint64_t prefill_chunk_size;
@@ -392,6 +401,7 @@ typedef struct tkh_session_options {
     float low_freq_factor;    /* Llama 3 parameters, as in tkh_producer_shape */
     float high_freq_factor;
     uint64_t original_max_positions;
+    uint64_t shared_layers;   /* trailing layers that borrow an earlier layer's KV */
 } tkh_session_options;
 
 /* Session::new (src/session.rs:205-245): validates, then allocates every
@@ -419,6 +429,9 @@ typedef struct tkh_session_state {
     uint64_t kv_bytes, scratch_bytes;
 } tkh_session_state;
 uint32_t tkh_session_state_get(const tkh_session *s, tkh_session_state *out);
+/* SharedKvPlan::producer_for (src/model/shared_kv.rs:141-146): the layer
+ * whose KV cache `layer` attends over (itself for an owning layer). */
+uint32_t tkh_session_kv_producer(const tkh_session *s, uint64_t layer, uint64_t *producer);
 /* Copies min(capacity_tokens, history_len) tokens of Session::history(). */
 uint64_t tkh_session_history(const tkh_session *s, uint32_t *tokens, uint64_t capacity_tokens);
 

@@ -20,6 +20,8 @@ Fixture sets taken (all used by the reference's own attention tests):
   qwen3-attention-inputs-v1  src/metal/compensated_attention.rs:465-561 (inputs only)
   gemma-rotary-v1            src/cpu/proportional_rotary/tests.rs:34-71
   llama3-rotary-v1           src/cpu/llama3_rotary/tests.rs:33-127 (-> llama3_rotary_v1)
+  gemma-shared-kv-v1         src/model/shared_kv/tests.rs:56-200 (-> gemma_shared_kv_v1: routing
+                             and per-step views only; the fixture carries no numerics)
   tiny-v1 rmsnorm arrays     tests/cpu_reductions.rs:16-62, 140-175 (-> tiny_v1_norms)
   tiny-v1 linear + greedy    tests/cpu_linear.rs:59-165, tests/cpu_decoder.rs:170-192
                              (-> tiny_v1_linear)
@@ -129,6 +131,36 @@ def llama3_rotary(ref: str, out: str):
     json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
 
 
+def shared_kv(ref: str, out: str):
+    """gemma-shared-kv-v1: per case the layer kinds, shared count, window, chunk
+    sizes and producer map; per step and layer the producer, the view's key range
+    [key_start, key_end) and whether K/V were produced (src/model/shared_kv/tests.rs:56-200)."""
+    path = os.path.join(ref, "tests", "fixtures", "gemma-shared-kv-v1", "expected.json")
+    raw = open(path, "rb").read()
+    data = json.loads(raw)
+    cases = []
+    for case in data["cases"]:
+        kinds = "".join("S" if t == "sliding_attention" else "F" for t in case["types"])
+        steps = []
+        for step in case["steps"]:
+            layers = []
+            for layer in step["layers"]:
+                ops = layer["ops"]
+                produced = ops["k_proj"] == 1 and ops["v_proj"] == 1 and ops["append"] == 1
+                assert produced == layer["cache_present"], (case["name"], layer["layer"])
+                assert ops["q_proj"] == ops["q_norm"] == ops["q_rope"] == 1
+                layers.append([layer["layer"], layer["producer"], layer["key_start"],
+                               layer["key_end"], int(produced)])
+            steps.append({"before": step["before"], "count": step["count"],
+                          "after": step["after"], "layers": layers})
+        cases.append({"name": case["name"], "kinds": kinds, "shared": case["shared"],
+                      "window": case["window"], "chunks": case["chunks"],
+                      "producer_map": case["producer_map"], "steps": steps})
+    meta = {"source_sha256": sha(raw), "format": data["format"], "cases": cases,
+            "layer_fields": ["layer", "producer", "key_start", "key_end", "produces_kv"]}
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=None, sort_keys=True)
+
+
 def qwen3_inputs(ref: str, out: str):
     root = os.path.join(ref, "tests", "fixtures", "qwen3-attention-inputs-v1")
     manifest = json.load(open(os.path.join(root, "manifest.json")))
@@ -229,6 +261,7 @@ def main(ref: str):
     qwen3_inputs(ref, "qwen3_attention_inputs_v1")
     math_json(ref, "gemma-rotary-v1", "gemma_rotary_v1")
     llama3_rotary(ref, "llama3_rotary_v1")
+    shared_kv(ref, "gemma_shared_kv_v1")
     tiny_norms(ref, "tiny_v1_norms")
     tiny_linear(ref, "tiny_v1_linear")
     reference_attention(ref, "gemma_reference_attention_v1")

@@ -344,6 +344,68 @@ def test_session_llama3_rotary_prefill_then_decode(torch_mod, ctx, ops, sess_mod
     s.close()
 
 
+@pytest.mark.parametrize("fused", ["1", "0"])
+def test_session_shared_kv_layers_attend_over_their_producers(torch_mod, ctx, ops, sess_mod, orc,
+                                                               fused):
+    """Six Gemma-shaped layers (8/4/256, bf16, scale 1/16, softcap 50, proportional
+    rotary), kinds sliding/full alternating with window 64, the last three shared
+    (gemma-shared-kv-v1's alternating6 routing: 3 -> 1, 4 -> 2, 5 -> 1): 150 prompt
+    tokens in 64-token chunks, then 4 decode steps.  A shared layer's context is its
+    own Q (own q_norm) over its producer's K/V (the producer's k_norm), with its own
+    window; its K/V projections are passed as None and never read."""
+    import os
+
+    torch = torch_mod
+    rng = np.random.default_rng(14)
+    L, hq, hkv, D, prompt, steps, W, shared = 6, 8, 4, 256, 150, 4, 64, 3
+    total = prompt + steps
+    qs, ks, vs, wq, wk = _session_inputs(rng, L, total, hq, hkv, D, scale=2.0)
+    windows = [W, 0, W, 0, W, 0]
+    opts = sess_mod.Options(capacity=total, prefill_chunk_size=64, vocab_size=100, layers=L,
+                            query_heads=hq, kv_heads=hkv, head_dim=D, storage="bf16",
+                            score_scale=1.0 / 16.0, softcap=50.0, rotary=2, theta=1e6,
+                            rotated_dims=128, factor=8.0, layer_windows=windows,
+                            shared_layers=shared)
+    saved = os.environ.get("TKH_FUSED_DECODE")
+    os.environ["TKH_FUSED_DECODE"] = fused
+    try:
+        s = sess_mod.Session(ctx, opts)
+    finally:
+        if saved is None:
+            os.environ.pop("TKH_FUSED_DECODE", None)
+        else:
+            os.environ["TKH_FUSED_DECODE"] = saved
+    route = [s.kv_producer(l) for l in range(L)]
+    assert route == [0, 1, 2, 1, 2, 1]
+    ctxs = [torch.full((total, hq * D), np.nan, dtype=torch.float32, device="cuda") for _ in range(L)]
+    io = []
+    for l in range(L):
+        own = l < L - shared
+        io.append(sess_mod.LayerIo(_t(torch, qs[l]), _t(torch, ks[l]) if own else None,
+                                   _t(torch, vs[l]) if own else None, ctxs[l], _t(torch, wq[l]),
+                                   _t(torch, wk[l]) if own else None))
+    s.set_tokens([1] * prompt)
+    assert s.evaluate(io) == prompt
+    s.append([2] * steps)
+    assert s.evaluate(io, chunk_limit=1) == steps
+    kw = dict(rotary="proportional", theta=1e6, rotated=128, factor=8.0)
+    for l in range(L):
+        p = route[l]
+        q = stored(_oracle_produce(orc, qs[l], wq[l], total, hq, D, 0, **kw), "bf16")
+        k = stored(_oracle_produce(orc, ks[p], wk[p], total, hkv, D, 0, **kw), "bf16")
+        v = stored(vs[p], "bf16")
+        kh = k.transpose(1, 0, 2).copy()
+        vh = v.transpose(1, 0, 2).copy()
+        window = windows[l] or None
+        ref, _, _ = orc.window_attention(q.reshape(-1), kh.reshape(-1), vh.reshape(-1), total, total,
+                                         total, hq, hkv, D, 0, 0, window, 1.0 / 16.0, softcap=50.0)
+        err = max_err(host(ctxs[l]).reshape(-1), ref)
+        log(f"fused {fused} layer {l} (KV of layer {p}, window {window}): max abs error {err:.3e}")
+        assert err <= TOL_HALF
+    assert s.memory()["kv_bytes"] > 0
+    s.close()
+
+
 def test_session_failed_chunk_commits_nothing_and_retry_succeeds(torch_mod, ctx, ops, sess_mod, orc):
     """src/session.rs:357-363: a chunk whose layer fails leaves the committed prefix
     and the pending history; fixing the input and evaluating again succeeds."""

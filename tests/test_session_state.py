@@ -208,3 +208,65 @@ def test_llama3_rotary_options_are_validated():
     with pytest.raises(TkhError) as e:
         Session(None, opts(rotary=4))
     assert e.value.code == _lib.INVALID_PARAMETER
+
+
+def _shared_fixture():
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gemma_shared_kv_v1.json")
+    return json.load(open(path))
+
+
+def test_shared_kv_routing_matches_gemma_shared_kv_fixture():
+    """Every case of gemma-shared-kv-v1 (35 layers with 20 shared, alternating, no
+    sharing, irregular kinds): each layer's KV producer is the fixture's
+    (SharedKvPlan::new / producer_for, src/model/shared_kv.rs:50-146), the KV bytes
+    count the owners only, and the chunk steps commit as the fixture's do."""
+    data = _shared_fixture()
+    assert len(data["cases"]) == 4
+    for case in data["cases"]:
+        kinds, W = case["kinds"], case["window"]
+        total = sum(case["chunks"])
+        windows = [W if k == "S" else 0 for k in kinds]
+        s = Session(None, Options(capacity=max(total, W), prefill_chunk_size=max(case["chunks"]),
+                                  vocab_size=64, layers=len(kinds), query_heads=2, kv_heads=1,
+                                  head_dim=8, score_scale=0.125, layer_windows=windows,
+                                  shared_layers=case["shared"]))
+        assert [s.kv_producer(l) for l in range(len(kinds))] == case["producer_map"], case["name"]
+        producers = len(kinds) - case["shared"]
+        for step in case["steps"]:
+            for layer, producer, key_start, key_end, produces in step["layers"]:
+                assert s.kv_producer(layer) == producer
+                assert bool(produces) == (layer < producers)
+                assert key_end == step["after"]
+                w = W if kinds[layer] == "S" else None
+                assert key_start == (max(0, step["before"] - w + 1) if w else 0)
+        for step in case["steps"]:
+            s.append([1] * step["count"])
+            assert s.next_chunk() == (step["before"], step["count"])
+            assert s.evaluate(None) == step["count"]
+            assert s.evaluated_len() == step["after"]
+        with pytest.raises(IndexError):
+            s.kv_producer(len(kinds))
+        s.close()
+
+
+def test_shared_kv_routing_rejections():
+    """SharedKvPlan::new's refusals (src/model/shared_kv.rs:57-87): no producer left,
+    no earlier owner of the shared layer's kind, a different window."""
+    def opts(windows, shared):
+        return Options(capacity=16, layers=len(windows), query_heads=2, kv_heads=1, head_dim=8,
+                       score_scale=0.125, layer_windows=windows, shared_layers=shared)
+
+    for windows, shared in [([3, 0], 2), ([3, 0], 3), ([3, 3], 1 << 40)]:
+        with pytest.raises(TkhError) as e:
+            Session(None, opts(windows, shared))
+        assert e.value.code == _lib.INVALID_CONFIG
+    for windows, shared in [([3, 0], 1), ([3, 3, 0], 1), ([3, 4], 1), ([0, 3, 0, 5], 1)]:
+        with pytest.raises(TkhError) as e:
+            Session(None, opts(windows, shared))
+        assert e.value.code == _lib.INVALID_CONFIG, (windows, shared)
+    s = Session(None, opts([3, 0, 3, 0], 2))
+    assert [s.kv_producer(l) for l in range(4)] == [0, 1, 0, 1]
+    s.close()

@@ -90,7 +90,8 @@ class SessionOptions(ctypes.Structure):
                                    "head_dim")] + [
         ("storage", ctypes.c_int), ("score_scale", f32), ("softcap", f32), ("norm_epsilon", f32),
         ("rotary", u32), ("theta", f32), ("rotated_dims", u64), ("factor", f32),
-        ("low_freq_factor", f32), ("high_freq_factor", f32), ("original_max_positions", u64)]
+        ("low_freq_factor", f32), ("high_freq_factor", f32), ("original_max_positions", u64),
+        ("shared_layers", u64)]
 
 
 class SessionState(ctypes.Structure):
@@ -149,6 +150,7 @@ SIGNATURES = {
     "tkh_session_reset": (None, [vp]),
     "tkh_session_state_get": (u32, [vp, P(SessionState)]),
     "tkh_session_history": (u64, [vp, P(u32), u64]),
+    "tkh_session_kv_producer": (u32, [vp, u64, P(u64)]),
     "tkh_session_next_chunk": (u32, [vp, P(u64), P(u64)]),
     "tkh_session_evaluate_next_chunk": (u32, [vp, P(LayerIo), P(u64), E]),
     "tkh_session_evaluate": (u32, [vp, P(LayerIo), u64, P(u64), E]),

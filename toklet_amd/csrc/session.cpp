@@ -154,7 +154,9 @@ struct tkh_session {
     int device = 0;
     tkh_session_options opt{};
     std::vector<uint64_t> windows;  // per layer, 0 = full retention
-    std::vector<tkh_kv *> kv;       // per layer owner
+    std::vector<uint64_t> route;    // per layer: the owning layer whose KV it attends over
+    uint64_t producers = 0;         // layers [0, producers) own a KV cache
+    std::vector<tkh_kv *> kv;       // per owning layer
     std::vector<uint32_t> history;
     uint64_t evaluated = 0;
     bool dist_valid = false, dist_replay = false;
@@ -355,6 +357,42 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
         return fail(err, TKH_INVALID_CONFIG, "session options", 0, 0, 0,
                     "a score softcap needs an explicit score scale (window/span semantics)");
     }
+    // SharedKvPlan::new (src/model/shared_kv.rs:50-120): the first
+    // layers - shared_layers layers own caches; a shared layer borrows the
+    // last owning layer of its kind (sliding or full), whose geometry (here:
+    // the window) must be its own.
+    if (o->shared_layers >= o->layers) {
+        free_session(s);
+        return fail(err, TKH_INVALID_CONFIG, "KV routing", 0, o->layers, o->shared_layers,
+                    "KV routing needs a producer");
+    }
+    s->producers = o->layers - o->shared_layers;
+    s->route.resize(o->layers);
+    for (uint64_t l = 0; l < o->layers; ++l) {
+        if (l < s->producers) {
+            s->route[l] = l;
+            continue;
+        }
+        const bool sliding = s->windows[l] != 0;
+        uint64_t p = s->producers;
+        for (uint64_t c = s->producers; c-- > 0;)
+            if ((s->windows[c] != 0) == sliding) {
+                p = c;
+                break;
+            }
+        if (p == s->producers) {
+            free_session(s);
+            return fail(err, TKH_INVALID_CONFIG, "KV routing", l, 0, 0,
+                        "missing shared KV producer kind for layer %llu", (unsigned long long)l);
+        }
+        if (s->windows[p] != s->windows[l]) {
+            free_session(s);
+            return fail(err, TKH_INVALID_CONFIG, "KV routing", l, s->windows[p], s->windows[l],
+                        "shared KV producer geometry differs for layer %llu",
+                        (unsigned long long)l);
+        }
+        s->route[l] = p;
+    }
     s->history.reserve(o->capacity);
     // Decode steps with the producer inside the decode kernel (one launch per
     // step and layer instead of two; TKH_FUSED_DECODE=0 turns it off): the
@@ -373,10 +411,10 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
     if (ctx) {
         const uint64_t D = o->head_dim, es = (uint64_t)esize(o->storage);
         const uint64_t chunk = s->opt.prefill_chunk_size;
-        s->kv.assign(o->layers, nullptr);
-        s->stage_k.assign(o->layers, nullptr);
-        s->stage_v.assign(o->layers, nullptr);
-        for (uint64_t l = 0; l < o->layers; ++l) {
+        s->kv.assign(s->producers, nullptr);
+        s->stage_k.assign(s->producers, nullptr);
+        s->stage_v.assign(s->producers, nullptr);
+        for (uint64_t l = 0; l < s->producers; ++l) {
             const uint64_t w = s->windows[l];
             const bool ring = w != 0 && w < o->capacity;
             uint32_t rc = tkh_kv_create(ctx, o->kv_heads, D, ring ? w : o->capacity, o->capacity,
@@ -404,7 +442,7 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
             if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
             s->scratch_bytes += bytes;
         }
-        for (uint64_t l = 0; e == hipSuccess && l < o->layers; ++l) {
+        for (uint64_t l = 0; e == hipSuccess && l < s->producers; ++l) {
             if (!s->kv[l]->has_window) continue;
             const size_t bytes = chunk * o->kv_heads * D * es;
             e = hipMalloc(&s->stage_k[l], bytes);
@@ -494,6 +532,13 @@ extern "C" uint32_t tkh_session_state_get(const tkh_session *s, tkh_session_stat
     return TKH_OK;
 }
 
+extern "C" uint32_t tkh_session_kv_producer(const tkh_session *s, uint64_t layer,
+                                            uint64_t *producer) {
+    if (!s || !producer || layer >= s->route.size()) return TKH_INVALID_PARAMETER;
+    *producer = s->route[layer];
+    return TKH_OK;
+}
+
 extern "C" uint64_t tkh_session_history(const tkh_session *s, uint32_t *tokens,
                                         uint64_t capacity_tokens) {
     if (!s) return 0;
@@ -547,19 +592,70 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
     const bool checked_valid = s->checked_valid;
     std::vector<tkh_kv *> ring_kv;
     std::vector<tkh_kv_frame> frames;
+    std::vector<tkh_kv_frame> owner_frame(s->kv.size());  // this chunk's frame of each ring owner
+    // Attention of the chunk's Q (in the Q scratch) over a linear cache's keys
+    // [0, start + count): Model::run -> LayerKv::attend -> attention_cached
+    // (src/model/mod.rs:645-662), or the window form with a score scale.
+    auto attend_linear = [&](tkh_kv *kv, uint64_t window, float *context) -> uint32_t {
+        if (o.score_scale == 0.0f) {
+            tkh_cached_shape cs{count, Hq, Hkv, D, kv->capacity, start};
+            return tkh_attention_cached(ctx, &cs, o.storage, s->q_scratch, count * Hq * D, kv->k,
+                                        Hkv * kv->capacity * D, kv->v, Hkv * kv->capacity * D,
+                                        context, count * Hq * D, nullptr, 0, nullptr, 0, err);
+        }
+        tkh_window_shape ws{};
+        ws.queries = count;
+        ws.keys = start + count;
+        ws.capacity = kv->capacity;
+        ws.query_heads = Hq;
+        ws.kv_heads = Hkv;
+        ws.head_dim = D;
+        ws.query_start = start;
+        ws.key_start = 0;
+        ws.has_window = window != 0;
+        ws.window = window;
+        ws.scale = o.score_scale;
+        ws.softcap = o.softcap;
+        return tkh_window_attention(ctx, &ws, o.storage, s->q_scratch, count * Hq * D, kv->k,
+                                    Hkv * kv->capacity * D, kv->v, Hkv * kv->capacity * D, context,
+                                    count * Hq * D, nullptr, 0, nullptr, 0, err);
+    };
     for (uint64_t l = 0; l < o.layers; ++l) {
         const tkh_layer_io &io = layers[l];
-        if (!io.q_proj || !io.k_proj || !io.v_proj || !io.context)
+        const uint64_t owner = s->route[l];
+        const bool shared = l >= s->producers;
+        if (!io.q_proj || !io.context || (!shared && (!io.k_proj || !io.v_proj)))
             return invalid("layer inputs", err);
-        if ((io.q_norm || io.k_norm) && (!std::isfinite(o.norm_epsilon) || o.norm_epsilon <= 0.0f))
+        if ((io.q_norm || (!shared && io.k_norm)) &&
+            (!std::isfinite(o.norm_epsilon) || o.norm_epsilon <= 0.0f))
             return invalid("epsilon must be finite and positive", err);
         const float *q = io.q_proj + row0 * Hq * D;
-        const float *k = io.k_proj + row0 * Hkv * D;
-        const float *v = io.v_proj + row0 * Hkv * D;
+        const float *k = shared ? nullptr : io.k_proj + row0 * Hkv * D;
+        const float *v = shared ? nullptr : io.v_proj + row0 * Hkv * D;
         float *context = io.context + row0 * Hq * D;
-        tkh_kv *kv = s->kv[l];
+        tkh_kv *kv = s->kv[owner];
         const bool ring = kv->has_window;
         const uint64_t window = s->windows[l];
+        if (shared) {
+            // A shared layer (SharedKvPlan::view, src/model/shared_kv.rs:333-343):
+            // its own Q, normalised and rotated, over the owner's current-step
+            // view; no K/V is produced or appended.
+            tkh_producer_shape qs = sh;
+            qs.kv_heads = 0;
+            TRY(launch_producer(ctx, &qs, o.storage, q, nullptr, nullptr, io.q_norm, nullptr,
+                                s->q_scratch, nullptr, nullptr, 0, err, s->rope, o.position_offset));
+            if (!ring) {
+                TRY(attend_linear(kv, window, context));
+            } else {
+                tkh_segment segs[3];
+                tkh_span_shape span{};
+                TRY(tkh_kv_view(kv, &owner_frame[owner], Hq, o.score_scale, segs, &span, err));
+                span.softcap = o.softcap;
+                TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
+                                       context, count * Hq * D, nullptr, 0, nullptr, 0, err));
+            }
+            continue;
+        }
         // A decode step folds the producer into the decode kernel: its Q/K/V
         // projections are normalised, rotated and rounded there, and the new
         // K/V row goes to the cache (linear) or the staging rows (ring).
@@ -617,30 +713,7 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
             uint8_t *kb = (uint8_t *)kv->k + start * D * es, *vb = (uint8_t *)kv->v + start * D * es;
             TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
                                 kb, vb, kv->capacity * D, err, s->rope, o.position_offset));
-            if (o.score_scale == 0.0f) {
-                // Model::run -> LayerKv::attend -> attention_cached (src/model/mod.rs:645-662).
-                tkh_cached_shape cs{count, Hq, Hkv, D, kv->capacity, start};
-                TRY(tkh_attention_cached(ctx, &cs, o.storage, s->q_scratch, count * Hq * D, kv->k,
-                                         Hkv * kv->capacity * D, kv->v, Hkv * kv->capacity * D,
-                                         context, count * Hq * D, nullptr, 0, nullptr, 0, err));
-            } else {
-                tkh_window_shape ws{};
-                ws.queries = count;
-                ws.keys = start + count;
-                ws.capacity = kv->capacity;
-                ws.query_heads = Hq;
-                ws.kv_heads = Hkv;
-                ws.head_dim = D;
-                ws.query_start = start;
-                ws.key_start = 0;
-                ws.has_window = window != 0;
-                ws.window = window;
-                ws.scale = o.score_scale;
-                ws.softcap = o.softcap;
-                TRY(tkh_window_attention(ctx, &ws, o.storage, s->q_scratch, count * Hq * D, kv->k,
-                                         Hkv * kv->capacity * D, kv->v, Hkv * kv->capacity * D,
-                                         context, count * Hq * D, nullptr, 0, nullptr, 0, err));
-            }
+            TRY(attend_linear(kv, window, context));
         } else {
             // Sliding layer: stage the chunk, attend over the ring's old spans
             // plus the staged rows (WindowKvCache::view), commit later.
@@ -651,11 +724,11 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
                             (unsigned long long)start);
             if (!fused_step)
                 TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
-                                    s->stage_k[l], s->stage_v[l], count * D, err, s->rope,
+                                    s->stage_k[owner], s->stage_v[owner], count * D, err, s->rope,
                                     o.position_offset));
             tkh_kv_frame f{};
-            f.k = s->stage_k[l];
-            f.v = s->stage_v[l];
+            f.k = s->stage_k[owner];
+            f.v = s->stage_v[owner];
             f.owner = kv->owner;
             f.generation = kv->generation;
             f.offset = kv->offset;
@@ -666,8 +739,8 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
             span.softcap = o.softcap;
             if (fused_step) {
                 // The new row is the view's last key; its K/V go to staging row 0.
-                const tkh::FusedDecode fd = fused_desc(s->stage_k[l], s->stage_v[l], (int64_t)D,
-                                                       (int64_t)(span.keys - 1), 0);
+                const tkh::FusedDecode fd = fused_desc(s->stage_k[owner], s->stage_v[owner],
+                                                       (int64_t)D, (int64_t)(span.keys - 1), 0);
                 TRY(span_attention_fused(ctx, &span, o.storage, segs, context, fd, err));
             } else {
                 TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
@@ -675,6 +748,7 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
             }
             ring_kv.push_back(kv);
             frames.push_back(f);
+            owner_frame[owner] = f;
         }
     }
     // Commit only after every layer of the chunk succeeded.

@@ -48,6 +48,7 @@ class Options:
     high_freq_factor: float = 4.0
     original_max_positions: int = 8192
     layer_windows: Optional[Sequence[int]] = None   # per layer, 0 = full
+    shared_layers: int = 0   # trailing layers attending over an earlier layer's KV
 
     def c(self):
         return _lib.SessionOptions(self.capacity, self.prefill_chunk_size, self.position_offset,
@@ -55,7 +56,8 @@ class Options:
                                    self.head_dim, _STORAGE[self.storage], self.score_scale,
                                    self.softcap, self.norm_epsilon, self.rotary, self.theta,
                                    self.rotated_dims, self.factor, self.low_freq_factor,
-                                   self.high_freq_factor, self.original_max_positions)
+                                   self.high_freq_factor, self.original_max_positions,
+                                   self.shared_layers)
 
 
 @dataclass
@@ -130,6 +132,13 @@ class Session:
     def memory(self) -> dict:
         st = self._state()
         return {"kv_bytes": int(st.kv_bytes), "scratch_bytes": int(st.scratch_bytes)}
+
+    def kv_producer(self, layer: int) -> int:
+        """SharedKvPlan::producer_for (src/model/shared_kv.rs:141-146)."""
+        out = ctypes.c_uint64()
+        if _lib.load().tkh_session_kv_producer(self.handle, layer, ctypes.byref(out)) != 0:
+            raise IndexError(f"layer {layer}")
+        return int(out.value)
 
     def next_chunk(self):
         start, count = ctypes.c_uint64(), ctypes.c_uint64()
