@@ -50,7 +50,7 @@ extern "C" hipError_t tkh_launch_decode_merge_batch(const tkh::DecodeArgs *a, in
                                                     hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 extern "C" hipError_t tkh_launch_copy_batch(const tkh::CopyBatch *b, hipStream_t stream);
 extern "C" int tkh_prefill_max_splits(void);
-extern "C" int tkh_prefill_merge_rows_per_block(int head_dim);
+extern "C" int tkh_prefill_merge_blocks_per_row_block(int head_dim, int rows);
 extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int rows,
                                                int64_t blocks, hipStream_t stream,
                                                hipEvent_t start, hipEvent_t stop);
@@ -574,7 +574,7 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
     }
     // Splits of one row block are combined by a second kernel, in merge blocks
     // of a few rows; Problem::part_base is the problem's first merge block.
-    const int64_t merge_rows = tkh_prefill_merge_rows_per_block((int)D);
+    const int64_t merge_per_rb = tkh_prefill_merge_blocks_per_row_block((int)D, (int)rows_per);
     int64_t wgs = 0, slots = 0, merge_blocks = 0;
     for (auto &p : group) {
         if (sk > INT32_MAX) return fail(err, TKH_UNSUPPORTED, "keys", 0, 0, 0, "key range too large");
@@ -587,7 +587,7 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
         wgs += g * p.splits;
         if (p.splits > 1) {
             slots += g * p.splits;
-            merge_blocks += g * (rows_per / merge_rows);
+            merge_blocks += g * merge_per_rb;
         }
     }
     const size_t need = (size_t)slots * rows_per * (D + 2) * sizeof(float);

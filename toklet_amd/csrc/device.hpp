@@ -140,7 +140,7 @@ struct Params {
     float softcap_inv;      // 1 / softcap (0 when disabled)
     int64_t total_tiles;
     // split-K partials
-    float *part_o;          // [rows, splits, D]
+    float *part_o;          // per slot: [rows, D] (generic kernel), [D, rows] (chunk kernel)
     float *part_ml;         // [rows, splits, 2] (max in log2 units, mass)
     uint32_t *status;
     // optional diagnostics (generic kernel only)

@@ -864,34 +864,38 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         return;
     }
 
-    // ---- split-K partial: slot (row block, split) holds ROWS x (D + 2)
-    // floats, merged by attn_prefill_merge after this kernel.
+    // ---- split-K partial: slot (row block, split) holds the unnormalised
+    // context feature-major, D x ROWS floats (the rows of a feature
+    // contiguous), and (max, mass) per row; attn_prefill_merge combines the
+    // slots after this kernel.  Feature-major stores are one dword per lane:
+    // the 32 rows of each lane half fill one 128-byte line, so a store writes
+    // two whole lines, where a row-major 16-byte store touched 32 lines (its
+    // stores took 3.5 instead of 1.4 us per workgroup at head_dim 256).
     raise_status(p, bad, ST_NONFINITE_INPUT);
     raise_status(p, v_range, ST_V_RANGE);
     const int64_t group = (int64_t)kvh * pv.row_blocks + rb;
     const int64_t slot = pv.slot_base + group * pv.splits + split;
-    float *po = p.part_o + (slot * ROWS + wave * 32 + j) * D;
+    float *pf = p.part_o + slot * ROWS * D + wave * 32 + j;
     for (int mb = 0; mb < MB; ++mb)
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 v = {acc[mb][4 * q] * oscale, acc[mb][4 * q + 1] * oscale,
-                             acc[mb][4 * q + 2] * oscale, acc[mb][4 * q + 3] * oscale};
-            *gstore_ptr<f32x4>(po + 32 * mb + 8 * q + 4 * h) = v;
-        }
+        for (int q = 0; q < 4; ++q)
+            for (int r = 0; r < 4; ++r)
+                *gstore_ptr<float>(pf + (int64_t)(32 * mb + 8 * q + 4 * h + r) * ROWS) =
+                    acc[mb][4 * q + r] * oscale;
     if (h == 0) {
         const f32x2 ml = {m_run, l_run};
         *gstore_ptr<f32x2>(p.part_ml + (slot * ROWS + wave * 32 + j) * 2) = ml;
     }
 }
 
-// Merge of the split-K partials of attn_prefill.  Merge block b covers
-// PF_MERGE_ROWS packed rows of one (problem, KV head, row block); each thread
-// owns four features of one row and reads the S partials of its row at once
-// (one round trip): m and l of every split, then the weighted sum of the
+// Merge of the split-K partials of attn_prefill.  Merge block b covers 64
+// packed rows and 16 features of one (problem, KV head, row block); each
+// thread owns four features of one row and reads the S partials of its row at
+// once (one round trip): m and l of every split, then the weighted sum of the
 // unnormalised contexts.  Problem::part_base is the problem's first merge block.
 template <int D, int ROWS>
 __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t blocks) {
-    constexpr int TPR = D / 4;                  // threads per row
-    constexpr int RPB = 256 / TPR;              // rows per merge block
+    constexpr int FB = D / 16;                  // 16-feature blocks per row
+    constexpr int RC = ROWS / 64;               // 64-row chunks per row block
     constexpr int MAXS = 16;
     const int64_t b = blockIdx.x;
     if (b >= blocks) return;
@@ -910,11 +914,14 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t bloc
     const int G = p.group, Hq = p.query_heads;
     const int m_kv = pr->queries * G;
     const int64_t local = b - pr->part_base;
-    const int blocks_per_rb = ROWS / RPB;
-    const int64_t group = local / blocks_per_rb;          // kvh * row_blocks + rb
+    const int64_t group = local / (RC * FB);              // kvh * row_blocks + rb
+    const int within = (int)(local % (RC * FB));
     const int kvh = (int)(group / pr->row_blocks), rb = (int)(group % pr->row_blocks);
-    const int r = (int)(local % blocks_per_rb) * RPB + (int)(threadIdx.x / TPR);
-    const int f = (int)(threadIdx.x % TPR) * 4;
+    // Thread (fq, rr) = (threadIdx.x / 64, threadIdx.x % 64): row rr of the
+    // block's 64, features 4 fq .. 4 fq + 3 of its 16, so each dword load of
+    // a wave reads 64 consecutive rows of one feature.
+    const int r = (within / FB) * 64 + (int)(threadIdx.x & 63);
+    const int f = (within % FB) * 16 + (int)(threadIdx.x >> 6) * 4;
     const int prow = rb * ROWS + r;
     if (prow >= m_kv) return;
     const int S = pr->splits;
@@ -925,9 +932,9 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t bloc
 #pragma unroll
     for (int sp = 0; sp < MAXS; ++sp) {
         if (sp < S) {
-            const int64_t srow = (slot0 + sp) * ROWS + r;
-            ml[sp] = *gload_ptr<f32x2>(p.part_ml + srow * 2);
-            po[sp] = *gload_ptr<f32x4>(p.part_o + srow * D + f);
+            ml[sp] = *gload_ptr<f32x2>(p.part_ml + ((slot0 + sp) * ROWS + r) * 2);
+            const float *col = p.part_o + ((slot0 + sp) * D + f) * ROWS + r;
+            for (int e = 0; e < 4; ++e) po[sp][e] = *gload_ptr<float>(col + (int64_t)e * ROWS);
         }
     }
     float M = NEG_INF;
@@ -966,7 +973,9 @@ extern "C" int tkh_prefill_waves(int head_dim, int wide) {
     return wide ? tkh::pf_wide_waves(head_dim) : tkh::PF_WAVES_NARROW;
 }
 extern "C" int tkh_prefill_max_splits(void) { return 16; }
-extern "C" int tkh_prefill_merge_rows_per_block(int head_dim) { return 256 / (head_dim / 4); }
+extern "C" int tkh_prefill_merge_blocks_per_row_block(int head_dim, int rows) {
+    return (rows / 64) * (head_dim / 16);
+}
 
 extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int rows,
                                                int64_t blocks, hipStream_t stream,
