@@ -465,6 +465,28 @@ uint32_t tkh_session_evaluate_next_chunk(tkh_session *s, const tkh_layer_io *lay
 uint32_t tkh_session_evaluate(tkh_session *s, const tkh_layer_io *layers, uint64_t chunk_limit,
                               uint64_t *evaluated, tkh_error *err);
 
+/* Session::evaluate_chunk (src/session.rs:364-418) for a host whose model
+ * runs between the layers: Model::run (src/model/mod.rs:530-755) computes
+ * layer l + 1's projections from layer l's context, so the layers of a chunk
+ * are evaluated one call at a time.  chunk_begin fixes the chunk: the next
+ * min(pending, chunk_limit, prefill_chunk_size) tokens from *start
+ * (*count 0: nothing pending, no chunk).  chunk_layer runs layer `layer`
+ * (0, 1, .. in order; inputs chunk-relative, as in evaluate_next_chunk): its
+ * producer and attention, ring layers staging their rows.  chunk_commit,
+ * after the last layer, checks the status word (synchronous contexts) and
+ * commits every ring and evaluated_len together, as the whole-chunk calls do
+ * (*count: the tokens committed).  Nothing is committed before it: a failing
+ * layer, a commit before the last layer (TKH_INVALID_CONFIG), chunk_abort,
+ * and every state edit, evaluate call or synchronize drop the chunk and leave
+ * the session as it was.  Layers out of order, or chunk_layer without a
+ * chunk, return TKH_INVALID_CONFIG without dropping it. */
+uint32_t tkh_session_chunk_begin(tkh_session *s, uint64_t chunk_limit, uint64_t *start,
+                                 uint64_t *count, tkh_error *err);
+uint32_t tkh_session_chunk_layer(tkh_session *s, uint64_t layer, const tkh_layer_io *io,
+                                 tkh_error *err);
+uint32_t tkh_session_chunk_commit(tkh_session *s, uint64_t *count, tkh_error *err);
+void tkh_session_chunk_abort(tkh_session *s);
+
 /* Waits for queued chunks and checks the status word.  On failure the
  * provisional chunks are dropped: the session returns to the last checked
  * prefix, or, with sliding layers, to the end of the last chunk whose ring

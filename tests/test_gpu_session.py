@@ -406,6 +406,97 @@ def test_session_shared_kv_layers_attend_over_their_producers(torch_mod, ctx, op
     s.close()
 
 
+@pytest.mark.parametrize("fused", ["1", "0"])
+def test_layer_by_layer_chunks_with_layer_dependent_inputs(torch_mod, ctx, ops, sess_mod, orc,
+                                                           fused):
+    """A host whose next layer depends on this one (Model::run, src/model/mod.rs:530-755):
+    three Qwen3-shaped layers (16/8/128, bf16, QK-norm) through tkh_session_chunk_*,
+    layer l + 1's Q/K/V made on the device from layer l's context of the same chunk.
+    150 prompt tokens in 64-token chunks, then 3 decode steps.  Every layer matches
+    full-prefix attention over the oracle-produced Q/K/V of the inputs it was given,
+    and feeding those inputs to tkh_session_evaluate gives the same contexts bit for bit."""
+    import os
+
+    torch = torch_mod
+    rng = np.random.default_rng(15)
+    L, hq, hkv, D, prompt, steps = 3, 16, 8, 128, 150, 3
+    total = prompt + steps
+    base = _session_inputs(rng, L, total, hq, hkv, D)
+    qs, ks, vs, wq, wk = base
+    opts = sess_mod.Options(capacity=total, prefill_chunk_size=64, vocab_size=100, layers=L,
+                            query_heads=hq, kv_heads=hkv, head_dim=D, storage="bf16")
+
+    def session():
+        saved = os.environ.get("TKH_FUSED_DECODE")
+        os.environ["TKH_FUSED_DECODE"] = fused
+        try:
+            return sess_mod.Session(ctx, opts)
+        finally:
+            if saved is None:
+                os.environ.pop("TKH_FUSED_DECODE", None)
+            else:
+                os.environ["TKH_FUSED_DECODE"] = saved
+
+    s = session()
+    q_all = [np.zeros((total, hq, D), np.float32) for _ in range(L)]
+    k_all = [np.zeros((total, hkv, D), np.float32) for _ in range(L)]
+    v_all = [np.zeros((total, hkv, D), np.float32) for _ in range(L)]
+    ctx_all = [np.zeros((total, hq * D), np.float32) for _ in range(L)]
+    wq_d = [_t(torch, w) for w in wq]
+    wk_d = [_t(torch, w) for w in wk]
+    s.set_tokens([5] * prompt)
+    for limit, todo in ((64, prompt), (1, steps)):
+        if limit == 1:
+            s.append([6] * steps)
+        done = 0
+        while done < todo:
+            start, n = s.chunk_begin(limit)
+            assert n > 0
+            prev = None
+            for l in range(L):
+                if l == 0:
+                    q = _t(torch, qs[0][start:start + n])
+                    k = _t(torch, ks[0][start:start + n])
+                    v = _t(torch, vs[0][start:start + n])
+                else:
+                    c = prev.view(n, hq, D)
+                    q = (0.5 * c + _t(torch, qs[l][start:start + n])).contiguous()
+                    k = (0.5 * c[:, :hkv] + _t(torch, ks[l][start:start + n])).contiguous()
+                    v = (c[:, hkv:2 * hkv] + _t(torch, vs[l][start:start + n])).contiguous()
+                out = torch.full((n, hq * D), np.nan, dtype=torch.float32, device="cuda")
+                s.chunk_layer(l, sess_mod.LayerIo(q, k, v, out, wq_d[l], wk_d[l]))
+                q_all[l][start:start + n] = host(q).reshape(n, hq, D)
+                k_all[l][start:start + n] = host(k).reshape(n, hkv, D)
+                v_all[l][start:start + n] = host(v).reshape(n, hkv, D)
+                ctx_all[l][start:start + n] = host(out).reshape(n, hq * D)
+                prev = out
+            assert s.chunk_commit() == n
+            done += n
+    assert (s.evaluated_len(), s.pending_len()) == (total, 0) and s.distribution_valid()
+    for l in range(L):
+        q = stored(_oracle_produce(orc, q_all[l], wq[l], total, hq, D, 0), "bf16")
+        k = stored(_oracle_produce(orc, k_all[l], wk[l], total, hkv, D, 0), "bf16")
+        v = stored(v_all[l], "bf16")
+        ref, _, _ = orc.attention(q.reshape(-1), k.reshape(-1), v.reshape(-1), total, hq, hkv, D)
+        err = max_err(ctx_all[l].reshape(-1), ref)
+        log(f"fused {fused} layer {l}: max abs error {err:.3e}")
+        assert err <= TOL_HALF
+    # The whole-chunk calls on the same inputs: the same kernels, the same bits.
+    s2 = session()
+    outs = [torch.full((total, hq * D), np.nan, dtype=torch.float32, device="cuda") for _ in range(L)]
+    io = [sess_mod.LayerIo(_t(torch, q_all[l]), _t(torch, k_all[l]), _t(torch, v_all[l]), outs[l],
+                           wq_d[l], wk_d[l]) for l in range(L)]
+    s2.set_tokens([5] * prompt)
+    assert s2.evaluate(io, chunk_limit=64) == prompt
+    s2.append([6] * steps)
+    assert s2.evaluate(io, chunk_limit=1) == steps
+    for l in range(L):
+        assert np.array_equal(host(outs[l]).reshape(total, -1).view(np.uint32),
+                              ctx_all[l].view(np.uint32)), l
+    s.close()
+    s2.close()
+
+
 def test_session_failed_chunk_commits_nothing_and_retry_succeeds(torch_mod, ctx, ops, sess_mod, orc):
     """src/session.rs:357-363: a chunk whose layer fails leaves the committed prefix
     and the pending history; fixing the input and evaluating again succeeds."""

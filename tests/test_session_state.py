@@ -270,3 +270,47 @@ def test_shared_kv_routing_rejections():
     s = Session(None, opts([3, 0, 3, 0], 2))
     assert [s.kv_producer(l) for l in range(4)] == [0, 1, 0, 1]
     s.close()
+
+
+def test_layer_by_layer_chunks_follow_the_whole_chunk_state_machine():
+    """tkh_session_chunk_*: layers in order, the commit after the last layer commits
+    the chunk as Session::evaluate_chunk does (src/session.rs:364-418); out-of-order
+    layers are refused without dropping the chunk; an early commit, an abort or a
+    state edit drops it and commits nothing."""
+    s = Session(None, Options(capacity=32, prefill_chunk_size=4, vocab_size=64, layers=3,
+                              query_heads=4, kv_heads=2, head_dim=8))
+    s.set_tokens(list(range(1, 11)))
+    assert s.chunk_begin() == (0, 4)
+    s.chunk_layer(0, None)
+    with pytest.raises(TkhError) as e:
+        s.chunk_layer(2, None)
+    assert e.value.code == _lib.INVALID_CONFIG
+    s.chunk_layer(1, None)
+    with pytest.raises(TkhError) as e:
+        s.chunk_commit()  # two of three layers: dropped
+    assert e.value.code == _lib.INVALID_CONFIG
+    assert s.evaluated_len() == 0
+    with pytest.raises(TkhError):
+        s.chunk_layer(2, None)  # no chunk any more
+    assert s.chunk_begin() == (0, 4)
+    for layer in range(3):
+        s.chunk_layer(layer, None)
+    assert s.chunk_commit() == 4
+    assert (s.evaluated_len(), s.pending_len()) == (4, 6)
+    assert s.chunk_begin(chunk_limit=1) == (4, 1)
+    s.chunk_layer(0, None)
+    s.chunk_abort()
+    with pytest.raises(TkhError):
+        s.chunk_commit()
+    assert s.evaluated_len() == 4
+    assert s.chunk_begin(chunk_limit=2) == (4, 2)
+    s.chunk_layer(0, None)
+    s.set_tokens(list(range(1, 9)))  # a state edit drops the chunk
+    with pytest.raises(TkhError):
+        s.chunk_layer(1, None)
+    assert s.evaluate(None) == 4 and s.evaluated_len() == 8
+    assert s.chunk_begin() == (8, 0)
+    with pytest.raises(TkhError):
+        s.chunk_commit()
+    assert s.distribution_valid() and s.pending_len() == 0
+    s.close()

@@ -151,6 +151,10 @@ SIGNATURES = {
     "tkh_session_state_get": (u32, [vp, P(SessionState)]),
     "tkh_session_history": (u64, [vp, P(u32), u64]),
     "tkh_session_kv_producer": (u32, [vp, u64, P(u64)]),
+    "tkh_session_chunk_begin": (u32, [vp, u64, P(u64), P(u64), E]),
+    "tkh_session_chunk_layer": (u32, [vp, u64, P(LayerIo), E]),
+    "tkh_session_chunk_commit": (u32, [vp, P(u64), E]),
+    "tkh_session_chunk_abort": (None, [vp]),
     "tkh_session_next_chunk": (u32, [vp, P(u64), P(u64)]),
     "tkh_session_evaluate_next_chunk": (u32, [vp, P(LayerIo), P(u64), E]),
     "tkh_session_evaluate": (u32, [vp, P(LayerIo), u64, P(u64), E]),

@@ -173,6 +173,17 @@ struct tkh_session {
     bool fused_decode = false;                 // decode steps fold the producer into attention
     std::vector<void *> stage_k, stage_v;      // sliding layers: [Hkv, chunk, D]
     uint64_t scratch_bytes = 0, kv_bytes = 0;
+    // The chunk being evaluated (layer by layer through tkh_session_chunk_*,
+    // or every layer at once), until its commit or abort.
+    struct Chunk {
+        bool active = false;
+        uint64_t start = 0, count = 0, next_layer = 0;
+        bool position_indexed = false;
+        uint64_t checked = 0;  // the checked prefix when the chunk began
+        bool checked_valid = false;
+        std::vector<tkh_kv *> ring_kv;  // ring owners staged by this chunk
+        std::vector<tkh_kv_frame> frames, owner_frame;
+    } chunk;
 };
 
 namespace {
@@ -250,6 +261,7 @@ uint32_t synchronize(tkh_session *s, tkh_error *err);
 // Queued contexts: state edits first settle the provisional chunks, so that
 // a late failure cannot land on an edited history.
 void settle(tkh_session *s) {
+    s->chunk = tkh_session::Chunk{};  // a chunk in progress is dropped
     if (s->ctx && !s->ctx->synchronous && s->checked != s->evaluated) synchronize(s, nullptr);
 }
 
@@ -565,10 +577,34 @@ void commit_state(tkh_session *s, uint64_t count) {
     s->checked_valid = true;
 }
 
-// One chunk of `count` tokens at session position `start`: every layer, then
-// the status check (when required) and the joint commit.
-uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t start,
-                        uint64_t count, bool position_indexed, tkh_error *err) {
+// A chunk of `count` tokens at session position `start`, evaluated layer by
+// layer: begin fixes it, eval_layer runs layers 0.. in order (the producer,
+// then attention; ring layers stage their rows), commit_chunk checks the
+// status (synchronous contexts) and commits every ring and evaluated_len
+// together.  Nothing is committed before commit_chunk, so dropping the chunk
+// (abort_chunk) leaves the session as it was: rows a layer wrote past
+// evaluated_len in a linear cache are not part of any prefix.
+void begin_chunk(tkh_session *s, uint64_t start, uint64_t count, bool position_indexed) {
+    tkh_session::Chunk &c = s->chunk;
+    c = tkh_session::Chunk{};
+    c.active = true;
+    c.start = start;
+    c.count = count;
+    c.position_indexed = position_indexed;
+    c.checked = s->checked;
+    c.checked_valid = s->checked_valid;
+    c.owner_frame.assign(s->kv.size(), tkh_kv_frame{});
+}
+
+void abort_chunk(tkh_session *s) { s->chunk = tkh_session::Chunk{}; }
+
+uint32_t eval_layer(tkh_session *s, uint64_t l, const tkh_layer_io &io, tkh_error *err) {
+    tkh_session::Chunk &c = s->chunk;
+    const uint64_t start = c.start, count = c.count;
+    const bool position_indexed = c.position_indexed;
+    std::vector<tkh_kv *> &ring_kv = c.ring_kv;
+    std::vector<tkh_kv_frame> &frames = c.frames;
+    std::vector<tkh_kv_frame> &owner_frame = c.owner_frame;
     tkh_context *ctx = s->ctx;
     const tkh_session_options &o = s->opt;
     const uint64_t Hq = o.query_heads, Hkv = o.kv_heads, D = o.head_dim;
@@ -588,11 +624,6 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
     sh.low_freq_factor = o.low_freq_factor;
     sh.high_freq_factor = o.high_freq_factor;
     sh.original_max_positions = o.original_max_positions;
-    const uint64_t checked = s->checked;
-    const bool checked_valid = s->checked_valid;
-    std::vector<tkh_kv *> ring_kv;
-    std::vector<tkh_kv_frame> frames;
-    std::vector<tkh_kv_frame> owner_frame(s->kv.size());  // this chunk's frame of each ring owner
     // Attention of the chunk's Q (in the Q scratch) over a linear cache's keys
     // [0, start + count): Model::run -> LayerKv::attend -> attention_cached
     // (src/model/mod.rs:645-662), or the window form with a score scale.
@@ -620,161 +651,247 @@ uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t sta
                                     Hkv * kv->capacity * D, kv->v, Hkv * kv->capacity * D, context,
                                     count * Hq * D, nullptr, 0, nullptr, 0, err);
     };
-    for (uint64_t l = 0; l < o.layers; ++l) {
-        const tkh_layer_io &io = layers[l];
-        const uint64_t owner = s->route[l];
-        const bool shared = l >= s->producers;
-        if (!io.q_proj || !io.context || (!shared && (!io.k_proj || !io.v_proj)))
-            return invalid("layer inputs", err);
-        if ((io.q_norm || (!shared && io.k_norm)) &&
-            (!std::isfinite(o.norm_epsilon) || o.norm_epsilon <= 0.0f))
-            return invalid("epsilon must be finite and positive", err);
-        const float *q = io.q_proj + row0 * Hq * D;
-        const float *k = shared ? nullptr : io.k_proj + row0 * Hkv * D;
-        const float *v = shared ? nullptr : io.v_proj + row0 * Hkv * D;
-        float *context = io.context + row0 * Hq * D;
-        tkh_kv *kv = s->kv[owner];
-        const bool ring = kv->has_window;
-        const uint64_t window = s->windows[l];
-        if (shared) {
-            // A shared layer (SharedKvPlan::view, src/model/shared_kv.rs:333-343):
-            // its own Q, normalised and rotated, over the owner's current-step
-            // view; no K/V is produced or appended.
-            tkh_producer_shape qs = sh;
-            qs.kv_heads = 0;
-            TRY(launch_producer(ctx, &qs, o.storage, q, nullptr, nullptr, io.q_norm, nullptr,
-                                s->q_scratch, nullptr, nullptr, 0, err, s->rope, o.position_offset));
-            if (!ring) {
-                TRY(attend_linear(kv, window, context));
-            } else {
-                tkh_segment segs[3];
-                tkh_span_shape span{};
-                TRY(tkh_kv_view(kv, &owner_frame[owner], Hq, o.score_scale, segs, &span, err));
-                span.softcap = o.softcap;
-                TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
-                                       context, count * Hq * D, nullptr, 0, nullptr, 0, err));
-            }
-            continue;
-        }
-        // A decode step folds the producer into the decode kernel: its Q/K/V
-        // projections are normalised, rotated and rounded there, and the new
-        // K/V row goes to the cache (linear) or the staging rows (ring).
-        auto fused_desc = [&](void *kc, void *vc, int64_t head_stride, int64_t new_key,
-                              int64_t new_row) {
-            tkh::FusedDecode f{};
-            f.q_proj = q;
-            f.k_proj = k;
-            f.v_proj = v;
-            f.q_norm = io.q_norm;
-            f.k_norm = io.k_norm;
-            f.pairs = tkh_rotary_pairs((int)o.rotary, (int)D, (int)o.rotated_dims);
-            f.rope = f.pairs > 0 ? s->rope + 2 * start * (uint64_t)f.pairs : nullptr;
-            f.eps = o.norm_epsilon;
-            f.k_cache = kc;
-            f.v_cache = vc;
-            f.head_stride = head_stride;
-            f.new_key = new_key;
-            f.new_row = new_row;
-            return f;
-        };
-        const bool fused_step = count == 1 && s->fused_decode;
-        if (!ring && fused_step && o.score_scale != 0.0f) {
-            // Window/score-scale layer with a linear cache: the span form over
-            // keys [first visible, start] of the cache.
-            tkh_span_shape span{};
-            const uint64_t first = window != 0 && start + 1 > window ? start + 1 - window : 0;
-            span.queries = 1;
-            span.keys = start + 1 - first;
-            span.query_heads = Hq;
-            span.kv_heads = Hkv;
-            span.head_dim = D;
-            span.query_start = start;
-            span.key_start = first;
-            span.has_window = window != 0;
-            span.window = window;
-            span.scale = o.score_scale;
-            span.softcap = o.softcap;
-            const uint64_t stride = kv->capacity * D;
-            tkh_segment segs[3]{};
-            segs[0] = tkh_segment{(const uint8_t *)kv->k + first * D * es, (Hkv - 1) * stride + span.keys * D,
-                                  (const uint8_t *)kv->v + first * D * es, (Hkv - 1) * stride + span.keys * D,
-                                  span.keys, stride, first};
-            segs[1].key_start = segs[2].key_start = start + 1;
-            const tkh::FusedDecode f = fused_desc(kv->k, kv->v, (int64_t)stride,
-                                                  (int64_t)(span.keys - 1), (int64_t)start);
-            TRY(span_attention_fused(ctx, &span, o.storage, segs, context, f, err));
-        } else if (!ring && fused_step) {
-            // attention_cached form: every key up to the new one.
-            const tkh::FusedDecode f = fused_desc(kv->k, kv->v, (int64_t)(kv->capacity * D),
-                                                  (int64_t)start, (int64_t)start);
-            tkh_cached_shape cs{1, Hq, Hkv, D, kv->capacity, start};
-            TRY(attention_cached_fused(ctx, &cs, o.storage, kv->k, kv->v, context, f, err));
-        } else if (!ring) {
-            uint8_t *kb = (uint8_t *)kv->k + start * D * es, *vb = (uint8_t *)kv->v + start * D * es;
-            TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
-                                kb, vb, kv->capacity * D, err, s->rope, o.position_offset));
+    const uint64_t owner = s->route[l];
+    const bool shared = l >= s->producers;
+    if (!io.q_proj || !io.context || (!shared && (!io.k_proj || !io.v_proj)))
+        return invalid("layer inputs", err);
+    if ((io.q_norm || (!shared && io.k_norm)) &&
+        (!std::isfinite(o.norm_epsilon) || o.norm_epsilon <= 0.0f))
+        return invalid("epsilon must be finite and positive", err);
+    const float *q = io.q_proj + row0 * Hq * D;
+    const float *k = shared ? nullptr : io.k_proj + row0 * Hkv * D;
+    const float *v = shared ? nullptr : io.v_proj + row0 * Hkv * D;
+    float *context = io.context + row0 * Hq * D;
+    tkh_kv *kv = s->kv[owner];
+    const bool ring = kv->has_window;
+    const uint64_t window = s->windows[l];
+    if (shared) {
+        // A shared layer (SharedKvPlan::view, src/model/shared_kv.rs:333-343):
+        // its own Q, normalised and rotated, over the owner's current-step
+        // view; no K/V is produced or appended.
+        tkh_producer_shape qs = sh;
+        qs.kv_heads = 0;
+        TRY(launch_producer(ctx, &qs, o.storage, q, nullptr, nullptr, io.q_norm, nullptr,
+                            s->q_scratch, nullptr, nullptr, 0, err, s->rope, o.position_offset));
+        if (!ring) {
             TRY(attend_linear(kv, window, context));
         } else {
-            // Sliding layer: stage the chunk, attend over the ring's old spans
-            // plus the staged rows (WindowKvCache::view), commit later.
-            if (kv->offset != start)
-                return fail(err, TKH_INVALID_CONFIG, "KV frame", l, start, kv->offset,
-                            "ring cache of layer %llu is at %llu, chunk starts at %llu",
-                            (unsigned long long)l, (unsigned long long)kv->offset,
-                            (unsigned long long)start);
-            if (!fused_step)
-                TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
-                                    s->stage_k[owner], s->stage_v[owner], count * D, err, s->rope,
-                                    o.position_offset));
-            tkh_kv_frame f{};
-            f.k = s->stage_k[owner];
-            f.v = s->stage_v[owner];
-            f.owner = kv->owner;
-            f.generation = kv->generation;
-            f.offset = kv->offset;
-            f.tokens = count;
             tkh_segment segs[3];
             tkh_span_shape span{};
-            TRY(tkh_kv_view(kv, &f, Hq, o.score_scale, segs, &span, err));
+            TRY(tkh_kv_view(kv, &owner_frame[owner], Hq, o.score_scale, segs, &span, err));
             span.softcap = o.softcap;
-            if (fused_step) {
-                // The new row is the view's last key; its K/V go to staging row 0.
-                const tkh::FusedDecode fd = fused_desc(s->stage_k[owner], s->stage_v[owner],
-                                                       (int64_t)D, (int64_t)(span.keys - 1), 0);
-                TRY(span_attention_fused(ctx, &span, o.storage, segs, context, fd, err));
-            } else {
-                TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
-                                       context, count * Hq * D, nullptr, 0, nullptr, 0, err));
-            }
-            ring_kv.push_back(kv);
-            frames.push_back(f);
-            owner_frame[owner] = f;
+            TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
+                                   context, count * Hq * D, nullptr, 0, nullptr, 0, err));
         }
+        return ok(err);
     }
-    // Commit only after every layer of the chunk succeeded.
-    if (ctx->synchronous) TRY(tkh_context_synchronize(ctx, err));
-    if (!ring_kv.empty()) {
-        // Queued: the ring copies run on the device only while the status word
-        // is clean, and record how far the rings got.
-        const bool gated = !ctx->synchronous;
-        TRY(commit_frames(ring_kv.data(), frames.data(), ring_kv.size(),
-                          gated ? ctx->status_dev : nullptr, gated ? s->committed_dev : nullptr,
-                          start + count, err));
-    }
-    commit_state(s, count);
-    if (!ctx->synchronous) {
-        // Provisional until tkh_session_synchronize confirms the status word.
-        s->checked = checked;
-        s->checked_valid = checked_valid;
+    // A decode step folds the producer into the decode kernel: its Q/K/V
+    // projections are normalised, rotated and rounded there, and the new
+    // K/V row goes to the cache (linear) or the staging rows (ring).
+    auto fused_desc = [&](void *kc, void *vc, int64_t head_stride, int64_t new_key,
+                          int64_t new_row) {
+        tkh::FusedDecode f{};
+        f.q_proj = q;
+        f.k_proj = k;
+        f.v_proj = v;
+        f.q_norm = io.q_norm;
+        f.k_norm = io.k_norm;
+        f.pairs = tkh_rotary_pairs((int)o.rotary, (int)D, (int)o.rotated_dims);
+        f.rope = f.pairs > 0 ? s->rope + 2 * start * (uint64_t)f.pairs : nullptr;
+        f.eps = o.norm_epsilon;
+        f.k_cache = kc;
+        f.v_cache = vc;
+        f.head_stride = head_stride;
+        f.new_key = new_key;
+        f.new_row = new_row;
+        return f;
+    };
+    const bool fused_step = count == 1 && s->fused_decode;
+    if (!ring && fused_step && o.score_scale != 0.0f) {
+        // Window/score-scale layer with a linear cache: the span form over
+        // keys [first visible, start] of the cache.
+        tkh_span_shape span{};
+        const uint64_t first = window != 0 && start + 1 > window ? start + 1 - window : 0;
+        span.queries = 1;
+        span.keys = start + 1 - first;
+        span.query_heads = Hq;
+        span.kv_heads = Hkv;
+        span.head_dim = D;
+        span.query_start = start;
+        span.key_start = first;
+        span.has_window = window != 0;
+        span.window = window;
+        span.scale = o.score_scale;
+        span.softcap = o.softcap;
+        const uint64_t stride = kv->capacity * D;
+        tkh_segment segs[3]{};
+        segs[0] = tkh_segment{(const uint8_t *)kv->k + first * D * es, (Hkv - 1) * stride + span.keys * D,
+                              (const uint8_t *)kv->v + first * D * es, (Hkv - 1) * stride + span.keys * D,
+                              span.keys, stride, first};
+        segs[1].key_start = segs[2].key_start = start + 1;
+        const tkh::FusedDecode f = fused_desc(kv->k, kv->v, (int64_t)stride,
+                                              (int64_t)(span.keys - 1), (int64_t)start);
+        TRY(span_attention_fused(ctx, &span, o.storage, segs, context, f, err));
+    } else if (!ring && fused_step) {
+        // attention_cached form: every key up to the new one.
+        const tkh::FusedDecode f = fused_desc(kv->k, kv->v, (int64_t)(kv->capacity * D),
+                                              (int64_t)start, (int64_t)start);
+        tkh_cached_shape cs{1, Hq, Hkv, D, kv->capacity, start};
+        TRY(attention_cached_fused(ctx, &cs, o.storage, kv->k, kv->v, context, f, err));
+    } else if (!ring) {
+        uint8_t *kb = (uint8_t *)kv->k + start * D * es, *vb = (uint8_t *)kv->v + start * D * es;
+        TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
+                            kb, vb, kv->capacity * D, err, s->rope, o.position_offset));
+        TRY(attend_linear(kv, window, context));
+    } else {
+        // Sliding layer: stage the chunk, attend over the ring's old spans
+        // plus the staged rows (WindowKvCache::view), commit later.
+        if (kv->offset != start)
+            return fail(err, TKH_INVALID_CONFIG, "KV frame", l, start, kv->offset,
+                        "ring cache of layer %llu is at %llu, chunk starts at %llu",
+                        (unsigned long long)l, (unsigned long long)kv->offset,
+                        (unsigned long long)start);
+        if (!fused_step)
+            TRY(launch_producer(ctx, &sh, o.storage, q, k, v, io.q_norm, io.k_norm, s->q_scratch,
+                                s->stage_k[owner], s->stage_v[owner], count * D, err, s->rope,
+                                o.position_offset));
+        tkh_kv_frame f{};
+        f.k = s->stage_k[owner];
+        f.v = s->stage_v[owner];
+        f.owner = kv->owner;
+        f.generation = kv->generation;
+        f.offset = kv->offset;
+        f.tokens = count;
+        tkh_segment segs[3];
+        tkh_span_shape span{};
+        TRY(tkh_kv_view(kv, &f, Hq, o.score_scale, segs, &span, err));
+        span.softcap = o.softcap;
+        if (fused_step) {
+            // The new row is the view's last key; its K/V go to staging row 0.
+            const tkh::FusedDecode fd = fused_desc(s->stage_k[owner], s->stage_v[owner],
+                                                   (int64_t)D, (int64_t)(span.keys - 1), 0);
+            TRY(span_attention_fused(ctx, &span, o.storage, segs, context, fd, err));
+        } else {
+            TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
+                                   context, count * Hq * D, nullptr, 0, nullptr, 0, err));
+        }
+        ring_kv.push_back(kv);
+        frames.push_back(f);
+        owner_frame[owner] = f;
     }
     return ok(err);
 }
 
+uint32_t commit_chunk(tkh_session *s, tkh_error *err) {
+    tkh_context *ctx = s->ctx;
+    tkh_session::Chunk c = std::move(s->chunk);
+    abort_chunk(s);
+    // Commit only after every layer of the chunk succeeded.
+    if (ctx->synchronous) TRY(tkh_context_synchronize(ctx, err));
+    if (!c.ring_kv.empty()) {
+        // Queued: the ring copies run on the device only while the status word
+        // is clean, and record how far the rings got.
+        const bool gated = !ctx->synchronous;
+        TRY(commit_frames(c.ring_kv.data(), c.frames.data(), c.ring_kv.size(),
+                          gated ? ctx->status_dev : nullptr, gated ? s->committed_dev : nullptr,
+                          c.start + c.count, err));
+    }
+    commit_state(s, c.count);
+    if (!ctx->synchronous) {
+        // Provisional until tkh_session_synchronize confirms the status word.
+        s->checked = c.checked;
+        s->checked_valid = c.checked_valid;
+    }
+    return ok(err);
+}
+
+// One chunk, every layer at once (the inputs of all layers given together).
+uint32_t evaluate_chunk(tkh_session *s, const tkh_layer_io *layers, uint64_t start,
+                        uint64_t count, bool position_indexed, tkh_error *err) {
+    begin_chunk(s, start, count, position_indexed);
+    for (uint64_t l = 0; l < s->opt.layers; ++l) {
+        const uint32_t rc = eval_layer(s, l, layers[l], err);
+        if (rc != TKH_OK) {
+            abort_chunk(s);
+            return rc;
+        }
+    }
+    return commit_chunk(s, err);
+}
+
 }  // namespace
+
+extern "C" uint32_t tkh_session_chunk_begin(tkh_session *s, uint64_t chunk_limit, uint64_t *start,
+                                            uint64_t *count, tkh_error *err) {
+    if (!s || !start || !count) return invalid("session", err);
+    abort_chunk(s);
+    *start = s->evaluated;
+    *count = 0;
+    TRY(nonzero(chunk_limit, "chunk limit", err));
+    const uint64_t n = std::min<uint64_t>(s->history.size() - s->evaluated,
+                                          std::min<uint64_t>(chunk_limit, s->opt.prefill_chunk_size));
+    if (n == 0) return ok(err);
+    begin_chunk(s, s->evaluated, n, false);
+    *count = n;
+    return ok(err);
+}
+
+extern "C" uint32_t tkh_session_chunk_layer(tkh_session *s, uint64_t layer, const tkh_layer_io *io,
+                                            tkh_error *err) {
+    if (!s) return invalid("session", err);
+    tkh_session::Chunk &c = s->chunk;
+    if (!c.active)
+        return fail(err, TKH_INVALID_CONFIG, "chunk", layer, 0, 0,
+                    "no chunk in progress (tkh_session_chunk_begin)");
+    if (layer != c.next_layer)
+        return fail(err, TKH_INVALID_CONFIG, "chunk layer", layer, c.next_layer, layer,
+                    "layers are evaluated in order: layer %llu expected, %llu given",
+                    (unsigned long long)c.next_layer, (unsigned long long)layer);
+    if (!io) return invalid("layer inputs", err);
+    if (s->ctx) {
+        const uint32_t rc = eval_layer(s, layer, *io, err);
+        if (rc != TKH_OK) {
+            abort_chunk(s);
+            return rc;
+        }
+    }
+    ++c.next_layer;
+    return ok(err);
+}
+
+extern "C" uint32_t tkh_session_chunk_commit(tkh_session *s, uint64_t *count, tkh_error *err) {
+    if (!s) return invalid("session", err);
+    if (count) *count = 0;
+    tkh_session::Chunk &c = s->chunk;
+    if (!c.active)
+        return fail(err, TKH_INVALID_CONFIG, "chunk", 0, 0, 0,
+                    "no chunk in progress (tkh_session_chunk_begin)");
+    if (c.next_layer != s->opt.layers) {
+        const uint64_t done = c.next_layer;
+        abort_chunk(s);
+        return fail(err, TKH_INVALID_CONFIG, "chunk", done, s->opt.layers, done,
+                    "chunk committed after %llu of %llu layers", (unsigned long long)done,
+                    (unsigned long long)s->opt.layers);
+    }
+    const uint64_t n = c.count;
+    if (!s->ctx) {
+        abort_chunk(s);
+        commit_state(s, n);
+    } else {
+        TRY(commit_chunk(s, err));
+    }
+    if (count) *count = n;
+    return ok(err);
+}
+
+extern "C" void tkh_session_chunk_abort(tkh_session *s) {
+    if (s) abort_chunk(s);
+}
 
 extern "C" uint32_t tkh_session_evaluate_next_chunk(tkh_session *s, const tkh_layer_io *layers,
                                                     uint64_t *count, tkh_error *err) {
     if (!s) return invalid("session", err);
+    abort_chunk(s);
     if (count) *count = 0;
     const uint64_t n = std::min<uint64_t>(s->history.size() - s->evaluated, s->opt.prefill_chunk_size);
     if (n == 0) return ok(err);
@@ -791,6 +908,7 @@ extern "C" uint32_t tkh_session_evaluate_next_chunk(tkh_session *s, const tkh_la
 extern "C" uint32_t tkh_session_evaluate(tkh_session *s, const tkh_layer_io *layers,
                                          uint64_t chunk_limit, uint64_t *evaluated, tkh_error *err) {
     if (!s) return invalid("session", err);
+    abort_chunk(s);
     if (evaluated) *evaluated = 0;
     TRY(nonzero(chunk_limit, "chunk limit", err));
     const uint64_t limit = std::min<uint64_t>(chunk_limit, s->opt.prefill_chunk_size);
@@ -811,5 +929,6 @@ extern "C" uint32_t tkh_session_evaluate(tkh_session *s, const tkh_layer_io *lay
 
 extern "C" uint32_t tkh_session_synchronize(tkh_session *s, tkh_error *err) {
     if (!s) return invalid("session", err);
+    abort_chunk(s);
     return synchronize(s, err);
 }

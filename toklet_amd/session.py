@@ -182,6 +182,32 @@ class Session:
                                                 ctypes.byref(err)), err)
         return int(done.value)
 
+    # ---- layer-by-layer chunks (the host's model runs between the layers)
+    def chunk_begin(self, chunk_limit: Optional[int] = None):
+        """Fix the next chunk: (start, count); count 0 when nothing is pending."""
+        err = _lib.Error()
+        start, count = ctypes.c_uint64(), ctypes.c_uint64()
+        limit = chunk_limit or self.options.prefill_chunk_size
+        _check(_lib.load().tkh_session_chunk_begin(self.handle, limit, ctypes.byref(start),
+                                                   ctypes.byref(count), ctypes.byref(err)), err)
+        return int(start.value), int(count.value)
+
+    def chunk_layer(self, layer: int, io: Optional[LayerIo]):
+        """Evaluate one layer of the chunk (in order); inputs chunk-relative."""
+        err = _lib.Error()
+        arr = _layers([io]) if io is not None else (_lib.LayerIo * 1)()
+        _check(_lib.load().tkh_session_chunk_layer(self.handle, layer, arr, ctypes.byref(err)), err)
+
+    def chunk_commit(self) -> int:
+        err = _lib.Error()
+        count = ctypes.c_uint64()
+        _check(_lib.load().tkh_session_chunk_commit(self.handle, ctypes.byref(count),
+                                                    ctypes.byref(err)), err)
+        return int(count.value)
+
+    def chunk_abort(self):
+        _lib.load().tkh_session_chunk_abort(self.handle)
+
     def synchronize(self):
         err = _lib.Error()
         _check(_lib.load().tkh_session_synchronize(self.handle, ctypes.byref(err)), err)
