@@ -1087,8 +1087,10 @@ uint32_t tkh_host::span_attention_fused(tkh_context *ctx, const tkh_span_shape *
     if (s.softcap != 0.0f && (!std::isfinite(s.softcap) || s.softcap < 0.0f))
         return invalid("attention score softcap", err);
     // The new key is the view's last (fused.new_key counts from the view's
-    // first key, as its segments do), at the query's position.
-    if (fused.new_key != (int64_t)(s.keys - 1) || s.query_start + 1 != s.key_start + s.keys)
+    // first key, as its segments do), at the query's position; -1: no new
+    // row to make (the view's keys are all stored; the Q rows alone are made).
+    if ((fused.new_key != -1 && fused.new_key != (int64_t)(s.keys - 1)) ||
+        s.query_start + 1 != s.key_start + s.keys)
         return invalid("fused decode: the new key must end the view", err);
     Plan plan;
     plan.dtype = dtype;

@@ -665,26 +665,6 @@ uint32_t eval_layer(tkh_session *s, uint64_t l, const tkh_layer_io &io, tkh_erro
     tkh_kv *kv = s->kv[owner];
     const bool ring = kv->has_window;
     const uint64_t window = s->windows[l];
-    if (shared) {
-        // A shared layer (SharedKvPlan::view, src/model/shared_kv.rs:333-343):
-        // its own Q, normalised and rotated, over the owner's current-step
-        // view; no K/V is produced or appended.
-        tkh_producer_shape qs = sh;
-        qs.kv_heads = 0;
-        TRY(launch_producer(ctx, &qs, o.storage, q, nullptr, nullptr, io.q_norm, nullptr,
-                            s->q_scratch, nullptr, nullptr, 0, err, s->rope, o.position_offset));
-        if (!ring) {
-            TRY(attend_linear(kv, window, context));
-        } else {
-            tkh_segment segs[3];
-            tkh_span_shape span{};
-            TRY(tkh_kv_view(kv, &owner_frame[owner], Hq, o.score_scale, segs, &span, err));
-            span.softcap = o.softcap;
-            TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
-                                   context, count * Hq * D, nullptr, 0, nullptr, 0, err));
-        }
-        return ok(err);
-    }
     // A decode step folds the producer into the decode kernel: its Q/K/V
     // projections are normalised, rotated and rounded there, and the new
     // K/V row goes to the cache (linear) or the staging rows (ring).
@@ -707,10 +687,10 @@ uint32_t eval_layer(tkh_session *s, uint64_t l, const tkh_layer_io &io, tkh_erro
         return f;
     };
     const bool fused_step = count == 1 && s->fused_decode;
-    if (!ring && fused_step && o.score_scale != 0.0f) {
-        // Window/score-scale layer with a linear cache: the span form over
-        // keys [first visible, start] of the cache.
-        tkh_span_shape span{};
+    // The span form of a decode step over a linear cache: keys [first
+    // visible, start] (window/score-scale layers).
+    auto linear_span = [&](tkh_span_shape &span, tkh_segment (&segs)[3]) {
+        span = tkh_span_shape{};
         const uint64_t first = window != 0 && start + 1 > window ? start + 1 - window : 0;
         span.queries = 1;
         span.keys = start + 1 - first;
@@ -724,12 +704,57 @@ uint32_t eval_layer(tkh_session *s, uint64_t l, const tkh_layer_io &io, tkh_erro
         span.scale = o.score_scale;
         span.softcap = o.softcap;
         const uint64_t stride = kv->capacity * D;
-        tkh_segment segs[3]{};
         segs[0] = tkh_segment{(const uint8_t *)kv->k + first * D * es, (Hkv - 1) * stride + span.keys * D,
                               (const uint8_t *)kv->v + first * D * es, (Hkv - 1) * stride + span.keys * D,
                               span.keys, stride, first};
+        segs[1] = segs[2] = tkh_segment{};
         segs[1].key_start = segs[2].key_start = start + 1;
-        const tkh::FusedDecode f = fused_desc(kv->k, kv->v, (int64_t)stride,
+    };
+    if (shared) {
+        // A shared layer (SharedKvPlan::view, src/model/shared_kv.rs:333-343):
+        // its own Q, normalised and rotated, over the owner's current-step
+        // view; no K/V is produced or appended.  A decode step makes the Q
+        // rows inside the decode kernel, with no new row to make (new_key -1:
+        // the owner's step has written it, to the cache or its staging row).
+        if (fused_step) {
+            tkh::FusedDecode f = fused_desc(nullptr, nullptr, 0, -1, 0);
+            f.k_norm = nullptr;
+            tkh_segment segs[3]{};
+            tkh_span_shape span{};
+            if (!ring && o.score_scale != 0.0f) {
+                linear_span(span, segs);
+                TRY(span_attention_fused(ctx, &span, o.storage, segs, context, f, err));
+            } else if (!ring) {
+                tkh_cached_shape cs{1, Hq, Hkv, D, kv->capacity, start};
+                TRY(attention_cached_fused(ctx, &cs, o.storage, kv->k, kv->v, context, f, err));
+            } else {
+                TRY(tkh_kv_view(kv, &owner_frame[owner], Hq, o.score_scale, segs, &span, err));
+                span.softcap = o.softcap;
+                TRY(span_attention_fused(ctx, &span, o.storage, segs, context, f, err));
+            }
+            return ok(err);
+        }
+        tkh_producer_shape qs = sh;
+        qs.kv_heads = 0;
+        TRY(launch_producer(ctx, &qs, o.storage, q, nullptr, nullptr, io.q_norm, nullptr,
+                            s->q_scratch, nullptr, nullptr, 0, err, s->rope, o.position_offset));
+        if (!ring) {
+            TRY(attend_linear(kv, window, context));
+        } else {
+            tkh_segment segs[3];
+            tkh_span_shape span{};
+            TRY(tkh_kv_view(kv, &owner_frame[owner], Hq, o.score_scale, segs, &span, err));
+            span.softcap = o.softcap;
+            TRY(tkh_span_attention(ctx, &span, o.storage, s->q_scratch, count * Hq * D, segs,
+                                   context, count * Hq * D, nullptr, 0, nullptr, 0, err));
+        }
+        return ok(err);
+    }
+    if (!ring && fused_step && o.score_scale != 0.0f) {
+        tkh_span_shape span{};
+        tkh_segment segs[3]{};
+        linear_span(span, segs);
+        const tkh::FusedDecode f = fused_desc(kv->k, kv->v, (int64_t)(kv->capacity * D),
                                               (int64_t)(span.keys - 1), (int64_t)start);
         TRY(span_attention_fused(ctx, &span, o.storage, segs, context, f, err));
     } else if (!ring && fused_step) {
