@@ -406,25 +406,40 @@ def test_session_shared_kv_layers_attend_over_their_producers(torch_mod, ctx, op
     s.close()
 
 
+@pytest.mark.parametrize("shape", ["qwen3", "gemma"])
+@pytest.mark.parametrize("queued", [False, True])
 @pytest.mark.parametrize("fused", ["1", "0"])
-def test_layer_by_layer_chunks_with_layer_dependent_inputs(torch_mod, ctx, ops, sess_mod, orc,
-                                                           fused):
+def test_layer_by_layer_chunks_with_layer_dependent_inputs(torch_mod, ops, sess_mod, orc, shape,
+                                                           queued, fused):
     """A host whose next layer depends on this one (Model::run, src/model/mod.rs:530-755):
-    three Qwen3-shaped layers (16/8/128, bf16, QK-norm) through tkh_session_chunk_*,
-    layer l + 1's Q/K/V made on the device from layer l's context of the same chunk.
-    150 prompt tokens in 64-token chunks, then 3 decode steps.  Every layer matches
-    full-prefix attention over the oracle-produced Q/K/V of the inputs it was given,
-    and feeding those inputs to tkh_session_evaluate gives the same contexts bit for bit."""
+    three layers through tkh_session_chunk_*, layer l + 1's Q/K/V made on the device
+    from layer l's context of the same chunk.  qwen3: 16/8/128 linear caches, QK-norm,
+    attention_cached semantics; gemma: 8/4/256 with a sliding (W = 64, ring) layer
+    between two global ones, scale 1/16, softcap 50, proportional rotary.  150 prompt
+    tokens in 64-token chunks, then 3 decode steps, with a synchronous or a queued
+    context.  Every layer matches attention over the oracle-produced Q/K/V of the
+    inputs it was given, and feeding those inputs to tkh_session_evaluate gives the
+    same contexts bit for bit."""
     import os
 
     torch = torch_mod
+    ctx = ops.Context(0, synchronous=not queued)
     rng = np.random.default_rng(15)
-    L, hq, hkv, D, prompt, steps = 3, 16, 8, 128, 150, 3
+    if shape == "qwen3":
+        L, hq, hkv, D = 3, 16, 8, 128
+        windows, extra = None, {}
+        kw = {}
+    else:
+        L, hq, hkv, D = 3, 8, 4, 256
+        windows = [0, 64, 0]
+        extra = dict(score_scale=1.0 / 16.0, softcap=50.0, rotary=2, theta=1e6, rotated_dims=128,
+                     factor=8.0, layer_windows=windows)
+        kw = dict(rotary="proportional", theta=1e6, rotated=128, factor=8.0)
+    prompt, steps = 150, 3
     total = prompt + steps
-    base = _session_inputs(rng, L, total, hq, hkv, D)
-    qs, ks, vs, wq, wk = base
+    qs, ks, vs, wq, wk = _session_inputs(rng, L, total, hq, hkv, D)
     opts = sess_mod.Options(capacity=total, prefill_chunk_size=64, vocab_size=100, layers=L,
-                            query_heads=hq, kv_heads=hkv, head_dim=D, storage="bf16")
+                            query_heads=hq, kv_heads=hkv, head_dim=D, storage="bf16", **extra)
 
     def session():
         saved = os.environ.get("TKH_FUSED_DECODE")
@@ -472,14 +487,22 @@ def test_layer_by_layer_chunks_with_layer_dependent_inputs(torch_mod, ctx, ops, 
                 prev = out
             assert s.chunk_commit() == n
             done += n
+    s.synchronize()
     assert (s.evaluated_len(), s.pending_len()) == (total, 0) and s.distribution_valid()
     for l in range(L):
-        q = stored(_oracle_produce(orc, q_all[l], wq[l], total, hq, D, 0), "bf16")
-        k = stored(_oracle_produce(orc, k_all[l], wk[l], total, hkv, D, 0), "bf16")
+        q = stored(_oracle_produce(orc, q_all[l], wq[l], total, hq, D, 0, **kw), "bf16")
+        k = stored(_oracle_produce(orc, k_all[l], wk[l], total, hkv, D, 0, **kw), "bf16")
         v = stored(v_all[l], "bf16")
-        ref, _, _ = orc.attention(q.reshape(-1), k.reshape(-1), v.reshape(-1), total, hq, hkv, D)
+        if shape == "qwen3":
+            ref, _, _ = orc.attention(q.reshape(-1), k.reshape(-1), v.reshape(-1), total, hq, hkv, D)
+        else:
+            kh = k.transpose(1, 0, 2).copy()
+            vh = v.transpose(1, 0, 2).copy()
+            ref, _, _ = orc.window_attention(q.reshape(-1), kh.reshape(-1), vh.reshape(-1), total,
+                                             total, total, hq, hkv, D, 0, 0, windows[l] or None,
+                                             1.0 / 16.0, softcap=50.0)
         err = max_err(ctx_all[l].reshape(-1), ref)
-        log(f"fused {fused} layer {l}: max abs error {err:.3e}")
+        log(f"{shape} queued {queued} fused {fused} layer {l}: max abs error {err:.3e}")
         assert err <= TOL_HALF
     # The whole-chunk calls on the same inputs: the same kernels, the same bits.
     s2 = session()
@@ -490,6 +513,7 @@ def test_layer_by_layer_chunks_with_layer_dependent_inputs(torch_mod, ctx, ops, 
     assert s2.evaluate(io, chunk_limit=64) == prompt
     s2.append([6] * steps)
     assert s2.evaluate(io, chunk_limit=1) == steps
+    s2.synchronize()
     for l in range(L):
         assert np.array_equal(host(outs[l]).reshape(total, -1).view(np.uint32),
                               ctx_all[l].view(np.uint32)), l
