@@ -103,7 +103,8 @@ __global__ __launch_bounds__(256) void project_logits(ProjectParams p) {
                 const int i = t + 256 * n, row = i >> 4, c = i & 15;
                 const int64_t v = v0 + row;
                 wb[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (v < p.vocab && 4 * c < dn) wb[n] = *gload_ptr<f32x4>(p.weights + v * H + d0 + 4 * c);
+                if (v < p.vocab && 4 * c < dn)
+                    wb[n] = __builtin_nontemporal_load(gload_ptr<f32x4>(p.weights + v * H + d0 + 4 * c));
             }
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
