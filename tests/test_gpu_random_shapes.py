@@ -1,0 +1,75 @@
+"""Seeded random shapes through attention_cached and window_attention against the
+CPU oracle: head sizes 64/128/256, GQA groups 1/2/4/7/8, bf16/f16/f32 storage,
+1..130 queries at offsets to 6000, windows from 1 key to none, score softcaps and
+scales.  The combinations the fixed cases leave out (a group of 7 at head_dim 256,
+a softcap at head_dim 64, an offset past every split boundary) go through the
+same planner, kernels and merge.  Bar: max abs error 2e-3 for half storage; the
+reference's gate 1e-5 + 1e-4|e| for FP32 (tests/cpu_attention.rs:6-14)."""
+
+import numpy as np
+import pytest
+
+from gpu_util import TOL_HALF, dev, host, log, stored
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from toklet_amd import ops
+
+    return ops
+
+
+def _case(rng):
+    D = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 4, 7, 8]))
+    return dict(D=D, hkv=hkv, hq=hkv * G, dt=str(rng.choice(["bf16", "f16", "f32"])),
+                Q=int(rng.choice([1, 1, 2, 5, 17, 64, 130])), start=int(rng.integers(0, 6000)),
+                kind=str(rng.choice(["cached", "window"])), pad=int(rng.integers(0, 7)),
+                W=int(rng.choice([0, 1, 7, 64, 300, 1024, 5000])),
+                softcap=float(rng.choice([0.0, 0.0, 30.0, 50.0])), scale_pick=int(rng.integers(0, 3)))
+
+
+@pytest.mark.parametrize("seed", [7, 11])
+def test_random_shapes_match_oracle(torch_mod, ops, orc, seed):
+    torch = torch_mod
+    rng = np.random.default_rng(seed)
+    ctx = ops.Context(0)
+    for n in range(30):
+        c = _case(rng)
+        D, hkv, hq, dt, Q, start = c["D"], c["hkv"], c["hq"], c["dt"], c["Q"], c["start"]
+        keys = start + Q
+        cap = keys + c["pad"]
+        k = stored(rng.standard_normal((hkv, cap, D)).astype(np.float32), dt)
+        v = stored(rng.standard_normal((hkv, cap, D)).astype(np.float32), dt)
+        q = stored(rng.standard_normal((Q, hq, D)).astype(np.float32), dt).reshape(-1)
+        out = torch.full((Q * hq * D,), np.nan, dtype=torch.float32, device="cuda")
+        log(f"seed {seed} case {n}: {c}")
+        if c["kind"] == "cached":
+            ops.attention_cached(ctx, dev(q, dt), dev(k, dt), dev(v, dt), out, None, None,
+                                 ops.CachedAttentionShape(Q, hq, hkv, D, cap, start))
+            ref, _, _ = orc.attention_cached(q, k, v, Q, hq, hkv, D, cap, start)
+        else:
+            scale = [1.0 / np.sqrt(D), 1.0 / 16.0, 0.3][c["scale_pick"]]
+            W = c["W"] or None
+            shape = ops.WindowAttentionShape(Q, keys, cap, hq, hkv, D, start, 0, W, scale, c["softcap"])
+            ops.window_attention(ctx, dev(q, dt), dev(k, dt), dev(v, dt), out, None, None, shape)
+            ref, _, _ = orc.window_attention(q, k.reshape(-1), v.reshape(-1), Q, keys, cap, hq, hkv, D,
+                                             start, 0, W, scale, softcap=c["softcap"])
+        got = host(out).astype(np.float64)
+        ref = np.asarray(ref, np.float64)
+        assert np.all(np.isfinite(got))
+        if dt == "f32":
+            assert np.all(np.abs(got - ref) <= 1e-5 + 1e-4 * np.abs(ref)), c
+        else:
+            assert np.max(np.abs(got - ref)) <= TOL_HALF, c
