@@ -73,3 +73,53 @@ def test_random_shapes_match_oracle(torch_mod, ops, orc, seed):
             assert np.all(np.abs(got - ref) <= 1e-5 + 1e-4 * np.abs(ref)), c
         else:
             assert np.max(np.abs(got - ref)) <= TOL_HALF, c
+
+
+@pytest.mark.parametrize("seed", [3, 5])
+def test_random_ring_chunks_match_window_attention(torch_mod, ops, orc, seed):
+    """A ring owner (WindowKvCache, src/model/window_cache.rs:21-350) fed random chunk
+    sizes (single tokens, chunks shorter and longer than the window): each chunk's
+    prepare -> view -> span_attention -> commit gives the contexts of window_attention
+    over the whole history, which the ring no longer holds."""
+    from toklet_amd import kv as kvmod
+
+    torch = torch_mod
+    rng = np.random.default_rng(seed)
+    ctx = ops.Context(0)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16}
+    for trial in range(3):
+        D = int(rng.choice([64, 128, 256]))
+        hkv = int(rng.choice([1, 2, 4]))
+        hq = hkv * int(rng.choice([1, 2, 4]))
+        dt = str(rng.choice(["bf16", "f16"]))
+        W = int(rng.choice([8, 33, 64, 200]))
+        T = int(rng.integers(W, 3 * W + 50))
+        scale = float(1.0 / np.sqrt(D))
+        softcap = float(rng.choice([0.0, 50.0]))
+        cache = kvmod.WindowKvCache(ctx, hkv, D, W, T, W, tdt[dt])
+        k_all = stored(rng.standard_normal((hkv, T, D)).astype(np.float32), dt)
+        v_all = stored(rng.standard_normal((hkv, T, D)).astype(np.float32), dt)
+        q_all = stored(rng.standard_normal((T, hq, D)).astype(np.float32), dt)
+        pos = 0
+        while pos < T:
+            n = int(min(T - pos, rng.choice([1, 1, 3, 17, W, W + 5])))
+            log(f"seed {seed} trial {trial}: {hq}/{hkv}/{D} {dt} W={W} softcap {softcap}, chunk {pos}+{n}")
+            kn = dev(np.ascontiguousarray(k_all[:, pos:pos + n]), dt)
+            vn = dev(np.ascontiguousarray(v_all[:, pos:pos + n]), dt)
+            prepared = cache.prepare(kn, vn, n)
+            view = cache.view(prepared)
+            s = view.attention_shape(hq, scale)
+            shape = ops.SpanAttentionShape(s.queries, s.keys, s.query_heads, s.kv_heads, s.head_dim,
+                                           s.query_start, s.key_start, s.window, s.scale, softcap)
+            q = q_all[pos:pos + n].reshape(-1)
+            out = torch.full((n * hq * D,), np.nan, dtype=torch.float32, device="cuda")
+            ops.span_attention(ctx, dev(q, dt), view.segments(), out, None, None, shape)
+            keys = pos + n
+            kh = np.ascontiguousarray(k_all[:, :keys]).reshape(-1)
+            vh = np.ascontiguousarray(v_all[:, :keys]).reshape(-1)
+            ref, _, _ = orc.window_attention(q, kh, vh, n, keys, keys, hq, hkv, D, pos, 0, W, scale,
+                                             softcap=softcap)
+            assert np.max(np.abs(host(out).astype(np.float64) - ref)) <= TOL_HALF
+            cache.commit(prepared)
+            pos += n
+        cache.close()
