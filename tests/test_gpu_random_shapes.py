@@ -123,3 +123,58 @@ def test_random_ring_chunks_match_window_attention(torch_mod, ops, orc, seed):
             cache.commit(prepared)
             pos += n
         cache.close()
+
+
+@pytest.mark.parametrize("seed", [13, 17])
+def test_random_batches_match_per_session_attention(torch_mod, ops, orc, seed):
+    """tkh_decode_batch and tkh_prefill_batch over random batches (1 to 70 sessions,
+    past the 64 that travel in the kernel arguments), lengths, head sizes, GQA
+    groups, dtypes, scales and per-session cache strides: every session's context
+    equals window attention over its own cache (no window)."""
+    torch = torch_mod
+    rng = np.random.default_rng(seed)
+    ctx = ops.Context(0)
+    for trial in range(4):
+        D = int(rng.choice([64, 128, 256]))
+        hkv = int(rng.choice([1, 2, 8]))
+        hq = hkv * int(rng.choice([1, 2, 4]))
+        dt = str(rng.choice(["bf16", "f16"]))
+        B = int(rng.choice([1, 3, 17, 64, 70]))
+        scale = float(rng.choice([1.0 / np.sqrt(D), 0.05]))
+        decode = trial % 2 == 0
+        tokens = 1 if decode else int(rng.choice([1, 16, 64, 128]))
+        if decode:
+            lengths = [int(x) for x in rng.integers(1, 3000, B)]
+            positions = [n - 1 for n in lengths]
+        else:
+            positions = [int(x) for x in rng.integers(0, 1500, B)]
+            lengths = [p + tokens for p in positions]
+        caps = [n + int(rng.integers(0, 5)) for n in lengths]
+        log(f"seed {seed} trial {trial}: {'decode' if decode else 'prefill'} B={B} tokens={tokens} "
+            f"{hq}/{hkv}/{D} {dt} scale {scale:.4f}")
+        offsets, pool_k, pool_v, total = [], [], [], 0
+        for b in range(B):
+            n = hkv * caps[b] * D
+            offsets.append(total)
+            pool_k.append(stored(rng.standard_normal(n).astype(np.float32), dt))
+            pool_v.append(stored(rng.standard_normal(n).astype(np.float32), dt))
+            total += n
+        kpool, vpool = np.concatenate(pool_k), np.concatenate(pool_v)
+        q = stored(rng.standard_normal((B, tokens, hq, D)).astype(np.float32), dt)
+        out = torch.full((B * tokens * hq * D,), np.nan, dtype=torch.float32, device="cuda")
+        strides = [c * D for c in caps]
+        if decode:
+            ops.decode_batch(ctx, dev(q, dt), dev(kpool, dt), dev(vpool, dt), offsets, strides, lengths,
+                             out, query_heads=hq, kv_heads=hkv, head_dim=D, scale=scale)
+        else:
+            ops.prefill_batch(ctx, dev(q, dt), dev(kpool, dt), dev(vpool, dt), offsets, strides,
+                              positions, out, tokens=tokens, query_heads=hq, kv_heads=hkv, head_dim=D,
+                              scale=scale)
+        got = host(out).reshape(B, -1).astype(np.float64)
+        for b in range(B):
+            kb = kpool[offsets[b]:offsets[b] + hkv * caps[b] * D]
+            vb = vpool[offsets[b]:offsets[b] + hkv * caps[b] * D]
+            ref, _, _ = orc.window_attention(q[b].reshape(-1), kb, vb, tokens, lengths[b], caps[b], hq,
+                                             hkv, D, positions[b] if not decode else lengths[b] - 1, 0,
+                                             None, scale)
+            assert np.max(np.abs(got[b] - ref)) <= TOL_HALF, (trial, b)
