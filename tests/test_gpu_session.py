@@ -704,7 +704,8 @@ def test_queued_linear_session_failure_returns_to_checked_prefix(torch_mod, ops,
 
 
 @pytest.mark.parametrize("storage,hq,hkv,D", [("bf16", 16, 8, 128), ("f32", 8, 2, 64), ("f16", 8, 1, 64),
-                                              ("bf16", 32, 8, 128)])
+                                              ("bf16", 32, 8, 128), ("f32", 14, 2, 64),
+                                              ("f32", 16, 4, 128)])
 def test_decode_steps_with_fused_producer_match_separate_producer(torch_mod, ops, sess_mod, orc,
                                                                   storage, hq, hkv, D):
     """Decode steps run the producer inside the decode kernel; the contexts match the
