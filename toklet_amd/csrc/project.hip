@@ -13,8 +13,8 @@
 // step (one row) a stream over [vocab, hidden] FP32: HBM-bound.
 //
 //  * project_logits: a workgroup owns 256 vocabulary rows (one per lane) and
-//    R context rows.  Feature tiles of 64 stage the 256 weight rows through
-//    LDS with coalesced 16-byte loads (rows padded to 68 floats, so a lane's
+//    R context rows.  Feature tiles of 32 stage the 256 weight rows through
+//    LDS with coalesced 16-byte loads (rows padded to 36 floats, so a lane's
 //    16-byte reads of its own row hit distinct bank groups within each
 //    16-lane phase) while the context tile is read by every lane at once (a
 //    broadcast); the next tile's loads are in flight while a tile is
@@ -34,8 +34,13 @@ namespace tkh {
 namespace {
 
 constexpr int PJ_V = 256;   // vocabulary rows per workgroup, one per lane
-constexpr int PJ_D = 64;    // features per staged tile
-constexpr int PJ_PAD = 68;  // staged row stride in floats
+// 32 features per tile keep a workgroup's LDS at 37 KiB, so four fit on a CU
+// and a one-row launch over a 151,936-row vocabulary (594 workgroups) runs
+// in one round; 64-feature tiles (70 KiB, two per CU) left 82 workgroups to
+// a second round on an otherwise idle device.
+constexpr int PJ_D = 32;    // features per staged tile
+constexpr int PJ_CPR = PJ_D / 4;  // 16-byte chunks per staged row
+constexpr int PJ_PAD = 36;  // staged row stride in floats
 
 __device__ __forceinline__ uint32_t order_key(float x) {
     const uint32_t b = __builtin_bit_cast(uint32_t, x);
@@ -88,19 +93,20 @@ __global__ __launch_bounds__(256) void project_logits(ProjectParams p) {
     };
 
     if constexpr (VEC) {
-        // Thread t stages chunks i = t + 256 n (n < 16) of the tile: row i / 16,
-        // features 4 (i % 16) ..+3; the context tile's R x 16 chunks likewise.
+        // Thread t stages chunks i = t + 256 n (n < PJ_CPR) of the tile: row
+        // i / PJ_CPR, features 4 (i % PJ_CPR) ..+3; the context tile's
+        // R x PJ_CPR chunks likewise.
         // A tile's loads are all issued at once, and the next tile's go out
         // before the current one is multiplied, so every thread keeps a whole
         // tile in flight instead of one load at a time.
-        constexpr int NW = PJ_V * (PJ_D / 4) / 256;            // weight chunks per thread
-        constexpr int NC = (R * (PJ_D / 4) + 255) / 256;       // context chunks per thread
+        constexpr int NW = PJ_V * PJ_CPR / 256;            // weight chunks per thread
+        constexpr int NC = (R * PJ_CPR + 255) / 256;       // context chunks per thread
         f32x4 wb[NW], cb[NC];
         auto load = [&](int64_t d0) {
             const int dn = (int)(H - d0 < PJ_D ? H - d0 : PJ_D);
 #pragma unroll
             for (int n = 0; n < NW; ++n) {
-                const int i = t + 256 * n, row = i >> 4, c = i & 15;
+                const int i = t + 256 * n, row = i / PJ_CPR, c = i % PJ_CPR;
                 const int64_t v = v0 + row;
                 wb[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 if (v < p.vocab && 4 * c < dn)
@@ -108,9 +114,9 @@ __global__ __launch_bounds__(256) void project_logits(ProjectParams p) {
             }
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
-                const int i = t + 256 * n, r = i >> 4, c = i & 15;
+                const int i = t + 256 * n, r = i / PJ_CPR, c = i % PJ_CPR;
                 cb[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (i < R * (PJ_D / 4) && r < nr && 4 * c < dn)
+                if (i < R * PJ_CPR && r < nr && 4 * c < dn)
                     cb[n] = *gload_ptr<f32x4>(p.context + (r0 + r) * H + d0 + 4 * c);
             }
         };
@@ -120,12 +126,12 @@ __global__ __launch_bounds__(256) void project_logits(ProjectParams p) {
 #pragma unroll
             for (int n = 0; n < NW; ++n) {
                 const int i = t + 256 * n;
-                *reinterpret_cast<f32x4 *>(wt + (i >> 4) * PJ_PAD + 4 * (i & 15)) = wb[n];
+                *reinterpret_cast<f32x4 *>(wt + (i / PJ_CPR) * PJ_PAD + 4 * (i % PJ_CPR)) = wb[n];
             }
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
                 const int i = t + 256 * n;
-                if (i < R * (PJ_D / 4)) *reinterpret_cast<f32x4 *>(ct + (i >> 4) * PJ_D + 4 * (i & 15)) = cb[n];
+                if (i < R * PJ_CPR) *reinterpret_cast<f32x4 *>(ct + (i / PJ_CPR) * PJ_D + 4 * (i % PJ_CPR)) = cb[n];
             }
             __syncthreads();
             if (d0 + PJ_D < H) load(d0 + PJ_D);
