@@ -81,8 +81,8 @@ def test_non_finite_inputs_are_reported(torch_mod, ops, ctx):
         assert e.value.name == "NonFinite", where
 
 
-@pytest.mark.parametrize("rows,hidden,vocab", [(1, 896, 3000), (3, 70, 1025), (17, 257, 600),
-                                               (40, 128, 513)])
+@pytest.mark.parametrize("rows,hidden,vocab", [(1, 896, 3000), (1, 80, 1500), (1, 20, 257),
+                                               (3, 70, 1025), (17, 257, 600), (40, 128, 513)])
 def test_logits_bit_exact_and_tokens_identical(torch_mod, ops, ctx, orc, rows, hidden, vocab):
     """Every build of the kernel (1, 4 and 16 rows per workgroup; 16-byte and
     scalar weight loads; vocabularies that end inside a workgroup; several row

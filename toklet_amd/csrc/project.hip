@@ -96,46 +96,66 @@ __global__ __launch_bounds__(256) void project_logits(ProjectParams p) {
         // Thread t stages chunks i = t + 256 n (n < PJ_CPR) of the tile: row
         // i / PJ_CPR, features 4 (i % PJ_CPR) ..+3; the context tile's
         // R x PJ_CPR chunks likewise.
-        // A tile's loads are all issued at once, and the next tile's go out
-        // before the current one is multiplied, so every thread keeps a whole
-        // tile in flight instead of one load at a time.
+        // A tile's loads are all issued at once, and later tiles' go out
+        // before the current one is multiplied: one tile ahead, or two for a
+        // single context row, whose launch is a bare stream of the weights
+        // (two register sets; the two sets alternate, unrolled by two, so no
+        // set is copied).
         constexpr int NW = PJ_V * PJ_CPR / 256;            // weight chunks per thread
         constexpr int NC = (R * PJ_CPR + 255) / 256;       // context chunks per thread
-        f32x4 wb[NW], cb[NC];
-        auto load = [&](int64_t d0) {
+        constexpr int AHEAD = R == 1 ? 2 : 1;              // tiles in flight
+        f32x4 wb[2][NW], cb[2][NC];
+        auto load = [&](int64_t d0, f32x4 (&w)[NW], f32x4 (&cx)[NC]) {
             const int dn = (int)(H - d0 < PJ_D ? H - d0 : PJ_D);
 #pragma unroll
             for (int n = 0; n < NW; ++n) {
                 const int i = t + 256 * n, row = i / PJ_CPR, c = i % PJ_CPR;
                 const int64_t v = v0 + row;
-                wb[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                w[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 if (v < p.vocab && 4 * c < dn)
-                    wb[n] = __builtin_nontemporal_load(gload_ptr<f32x4>(p.weights + v * H + d0 + 4 * c));
+                    w[n] = __builtin_nontemporal_load(gload_ptr<f32x4>(p.weights + v * H + d0 + 4 * c));
             }
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
                 const int i = t + 256 * n, r = i / PJ_CPR, c = i % PJ_CPR;
-                cb[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                cx[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 if (i < R * PJ_CPR && r < nr && 4 * c < dn)
-                    cb[n] = *gload_ptr<f32x4>(p.context + (r0 + r) * H + d0 + 4 * c);
+                    cx[n] = *gload_ptr<f32x4>(p.context + (r0 + r) * H + d0 + 4 * c);
             }
         };
-        load(0);
-        for (int64_t d0 = 0; d0 < H; d0 += PJ_D) {
+        auto stage = [&](const f32x4 (&w)[NW], const f32x4 (&cx)[NC]) {
             __syncthreads();  // the previous tile is no longer read
 #pragma unroll
             for (int n = 0; n < NW; ++n) {
                 const int i = t + 256 * n;
-                *reinterpret_cast<f32x4 *>(wt + (i / PJ_CPR) * PJ_PAD + 4 * (i % PJ_CPR)) = wb[n];
+                *reinterpret_cast<f32x4 *>(wt + (i / PJ_CPR) * PJ_PAD + 4 * (i % PJ_CPR)) = w[n];
             }
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
                 const int i = t + 256 * n;
-                if (i < R * PJ_CPR) *reinterpret_cast<f32x4 *>(ct + (i / PJ_CPR) * PJ_D + 4 * (i % PJ_CPR)) = cb[n];
+                if (i < R * PJ_CPR) *reinterpret_cast<f32x4 *>(ct + (i / PJ_CPR) * PJ_D + 4 * (i % PJ_CPR)) = cx[n];
             }
             __syncthreads();
-            if (d0 + PJ_D < H) load(d0 + PJ_D);
-            compute();
+        };
+        if constexpr (AHEAD == 1) {
+            load(0, wb[0], cb[0]);
+            for (int64_t d0 = 0; d0 < H; d0 += PJ_D) {
+                stage(wb[0], cb[0]);
+                if (d0 + PJ_D < H) load(d0 + PJ_D, wb[0], cb[0]);
+                compute();
+            }
+        } else {
+            load(0, wb[0], cb[0]);
+            if (PJ_D < H) load(PJ_D, wb[1], cb[1]);
+            for (int64_t d0 = 0; d0 < H; d0 += 2 * PJ_D) {
+                stage(wb[0], cb[0]);
+                if (d0 + 2 * PJ_D < H) load(d0 + 2 * PJ_D, wb[0], cb[0]);
+                compute();
+                if (d0 + PJ_D >= H) break;
+                stage(wb[1], cb[1]);
+                if (d0 + 3 * PJ_D < H) load(d0 + 3 * PJ_D, wb[1], cb[1]);
+                compute();
+            }
         }
     } else {
         for (int64_t d0 = 0; d0 < H; d0 += PJ_D) {
