@@ -23,12 +23,9 @@
  *    unspecified and must be discarded, as the reference discards partial
  *    output after an arithmetic failure (src/cpu/mod.rs:5-7).  Shape and
  *    length errors are reported before any launch and leave every output
- *    untouched.  One value-range limit is found the same way: the bf16/f16
- *    chunk kernel takes bf16 V values as f16 scaled by 2^-8, so a finite bf16
- *    V value of magnitude 2^24 or more that a chunk attends to is reported as
- *    TKH_UNSUPPORTED (tensor "attention value"), with the context
- *    unspecified; single-token decode and FP32 calls compute with any finite
- *    value.
+ *    untouched.  Every finite input is computed, at every dtype and by every
+ *    kernel (the chunk kernel forms rows whose bf16 V exceeds f16's range
+ *    again in FP32).
  *  - Tensors passed to operators are device pointers (HBM).  Q/context use
  *    [tokens, query_heads, head_dim]; K/V use the reference's head-major
  *    [kv_heads, capacity, head_dim] layout (strides [capacity*D, D, 1]).

@@ -15,7 +15,8 @@ the HIP kernels.
   * qwen3-attention-inputs-v1: real Qwen3 layer-0 rows (16/8/128) at positions
     0, 41 and 65 (src/metal/compensated_attention.rs:465-561), f16 and bf16,
     through the decode and the chunk kernel.
-  * bf16 V values at and beyond the chunk kernel's range.
+  * bf16 V values beyond f16's range (the chunk kernel's FP32 recompute) and of
+    small magnitude.
 """
 
 import contextlib
@@ -196,7 +197,7 @@ def test_qwen3_layer0_rows_decode_and_chunk_kernels(torch_mod, ops, orc, dt):
         c.close()
 
 
-# ---- bf16 V values at and beyond the chunk kernel's range ----
+# ---- bf16 V values beyond f16's range and of small magnitude ----
 
 def _chunk_case(rng, tokens, hq, hkv, D, cap, offset, v_value, where):
     q = stored(rng.standard_normal((tokens, hq, D)), "bf16").reshape(-1)
@@ -208,9 +209,11 @@ def _chunk_case(rng, tokens, hq, hkv, D, cap, offset, v_value, where):
 
 @pytest.mark.parametrize("offset", [0, 2000])  # 2000: the chunk's keys are split
 def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset):
-    """|v| < 2^24 is computed; a finite 2^24 returns the dedicated Unsupported
-    code (tensor "attention value"); inf is a non-finite input; the decode
-    kernel computes 2^24 in FP32."""
+    """Every finite bf16 V is computed, as the reference computes it
+    (src/cpu/attention.rs:247-251 rejects only non-finite values): 65280, the
+    largest value f16 holds, on the MFMA path; 65536, 2^24 - 2^16, 2^24,
+    -2^25 and 2^100 by the kernel's FP32 recompute of the rows it overflowed;
+    inf is a non-finite input.  The decode kernel computes 2^24 in FP32."""
     torch = torch_mod
     rng = np.random.default_rng(81)
     hq, hkv, D, tokens = 8, 4, 128, 64
@@ -218,15 +221,17 @@ def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset):
     ctx = ops.Context(0)
     shape = ops.CachedAttentionShape(tokens, hq, hkv, D, cap, offset)
     where = (2, offset + 5, 17)
-    for v_value, expect in ((16711680.0, None), (2.0 ** 24, "Unsupported"), (-(2.0 ** 25), "Unsupported"),
-                            (np.inf, "NonFinite")):
+    for v_value, expect in ((65280.0, None), (65536.0, None), (16711680.0, None), (2.0 ** 24, None),
+                            (-(2.0 ** 25), None), (2.0 ** 100, None), (np.inf, "NonFinite")):
         q, k, v = _chunk_case(rng, tokens, hq, hkv, D, cap, offset, v_value, where)
         out = torch.zeros(tokens * hq * D, dtype=torch.float32, device="cuda")
         if expect is None:
             ops.attention_cached(ctx, dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), out, None, None,
                                  shape)
             ref, _, _ = orc.attention_cached(q, k, v, tokens, hq, hkv, D, cap, offset)
-            rel = max_err(host(out), ref) / float(np.abs(ref).max())
+            got = host(out)
+            assert np.isfinite(got).all()
+            rel = max_err(got, ref) / float(np.abs(ref).max())
             log(f"bf16 V {v_value:g} at offset {offset}: relative error {rel:.3e}")
             assert rel <= 2e-3
             continue
@@ -235,8 +240,6 @@ def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset):
                                  shape)
         log(f"bf16 V {v_value:g} at offset {offset}: {e.value}")
         assert e.value.name == expect
-        if expect == "Unsupported":
-            assert e.value.tensor == "attention value"
     # The decode kernel widens bf16 V to FP32: 2^24 is an ordinary value there.
     q, k, v = _chunk_case(rng, 1, hq, hkv, D, cap, cap - 1, 2.0 ** 24, (1, cap - 3, 9))
     out = torch.zeros(hq * D, dtype=torch.float32, device="cuda")
@@ -244,4 +247,27 @@ def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset):
                          ops.CachedAttentionShape(1, hq, hkv, D, cap, cap - 1))
     ref, _, _ = orc.attention_cached(q, k, v, 1, hq, hkv, D, cap, cap - 1)
     assert max_err(host(out), ref) / float(np.abs(ref).max()) <= 1e-5
+    ctx.close()
+
+
+@pytest.mark.parametrize("offset", [0, 2000])
+def test_small_bf16_values_in_the_chunk_kernel(torch_mod, ops, orc, offset):
+    """V of magnitude about 1e-4 (bf16 values above f16's smallest normal are
+    carried exactly): the context's error relative to its own magnitude stays
+    at the bar of ordinary values."""
+    torch = torch_mod
+    rng = np.random.default_rng(82)
+    hq, hkv, D, tokens = 8, 4, 128, 64
+    cap = offset + tokens
+    ctx = ops.Context(0)
+    q = stored(rng.standard_normal((tokens, hq, D)), "bf16").reshape(-1)
+    k = stored(rng.standard_normal((hkv, cap, D)), "bf16")
+    v = stored(1e-4 * rng.standard_normal((hkv, cap, D)), "bf16")
+    out = torch.zeros(tokens * hq * D, dtype=torch.float32, device="cuda")
+    ops.attention_cached(ctx, dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), out, None, None,
+                         ops.CachedAttentionShape(tokens, hq, hkv, D, cap, offset))
+    ref, _, _ = orc.attention_cached(q, k, v, tokens, hq, hkv, D, cap, offset)
+    rel = max_err(host(out), ref) / float(np.abs(ref).max())
+    log(f"bf16 V of scale 1e-4 at offset {offset}: relative error {rel:.3e}")
+    assert rel <= 2e-3
     ctx.close()

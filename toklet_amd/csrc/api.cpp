@@ -77,12 +77,7 @@ uint32_t status_error(uint32_t st, tkh_error *err) {
         return fail(err, TKH_DEVICE, "decode splits", 0, 0, 0,
                     "a decode merge timed out waiting for its key splits (status 0x%x)", st);
     // A non-finite input anywhere decides first (the reference checks every
-    // input before computing); a merge of partials that held the overflowed
-    // V values also reports a non-finite context, which ST_V_RANGE explains.
-    if ((st & tkh::ST_V_RANGE) && !(st & tkh::ST_NONFINITE_INPUT))
-        return fail(err, TKH_UNSUPPORTED, "attention value", 0, 0, 0,
-                    "a bf16 value of magnitude 2^24 or more is beyond the chunk kernel's f16 "
-                    "value range (status 0x%x)", st);
+    // input before computing).
     if (st & tkh::ST_NONFINITE_INPUT)
         return fail(err, TKH_NON_FINITE, "attention inputs", 0, 0, 0,
                     "non-finite value in attention inputs or scores (status 0x%x)", st);

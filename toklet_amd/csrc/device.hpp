@@ -22,8 +22,7 @@ enum StatusBits : uint32_t {
     ST_BAD_MASS = 2u,          // softmax mass not finite or not positive
     ST_NONFINITE_OUTPUT = 4u,  // combined context not finite
     ST_SPLIT_TIMEOUT = 8u,     // a decode merge gave up waiting for the other key splits
-    ST_V_RANGE = 16u,          // a finite bf16 V value of magnitude 2^24 or more met the chunk
-                               // kernel, whose P.V products take V as f16 scaled by 2^-8
+    // 16u: unused (a value-range refusal the chunk kernel no longer makes)
     ST_NONFINITE_LOGIT = 32u,  // a projected logit is not finite (project.hip)
 };
 

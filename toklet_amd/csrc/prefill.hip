@@ -23,11 +23,16 @@
 //    rounded once to f16 for both dtypes (a single bf16 rounding of P can
 //    move the output by more than 2e-3), and the row mass is summed from the
 //    same rounded values (one v_dot2 with (1, 1) per pair).  For bf16 the
-//    transposing pass also converts V to f16 scaled by 2^-8 (exact for every bf16
-//    value from 2^-6 up; smaller ones lose at most 2^-17 absolute, and the
-//    f16 range then covers |v| < 2^24), and the context is scaled back by 2^8.
-//  * The online-softmax rescale of O is skipped for a tile unless some
-//    row's running maximum moved.
+//    transposing pass also converts V to f16 (exact for every bf16 value from
+//    2^-14 up to 65280, the largest bf16 below f16's overflow; smaller ones
+//    lose at most 2^-25 absolute).  A wave whose V tile held a larger finite
+//    value recomputes its rows on the vector unit in FP32 after the loop.
+//  * The softmax maximum is lazy: a tile's probabilities are formed against
+//    the running maximum without computing the tile's own maximum, and only
+//    a wave in which some row's tile mass exceeds 2^8 (a score more than 8
+//    log2 units above the base, a non-finite score, or a row's first tile)
+//    computes the tile maximum, rescales O and forms the tile again.  A
+//    max-of-magnitudes chain over the scores checks their finiteness.
 //  * Workgroups are mapped XCD-major (dispatch slot b runs on XCD b % 8) so
 //    the row blocks of one (problem, KV head) sit on one XCD and share its
 //    L2 for the K/V stream.
@@ -204,9 +209,10 @@ template <int D, int W> struct PrefillLds {
 // f16 form (PrefillLds::vt_at), by the whole workgroup: each thread builds
 // `per` 16-byte chunks.  A 16-lane group reads four keys x 16 features with
 // ds_read_b64_tr_b16 (lane j receives the four keys of feature fb + j), twice
-// for the chunk's two key quads; for bf16 each value is then converted to f16
-// scaled by 2^-8.  Split in a read half and a write half so a caller can put
-// MFMAs between.
+// for the chunk's two key quads; for bf16 each pair is then widened (a shift
+// and a mask) and rounded to f16 in one v_cvt_pk_f16_f32, which is exact for
+// bf16 values up to 65280 and gives inf above.  Split in a read half and a
+// write half so a caller can put MFMAs between.
 template <int D, int W, bool CONV> struct VTranspose {
     using L = PrefillLds<D, W>;
     static constexpr int threads = 64 * W;
@@ -238,8 +244,8 @@ template <int D, int W, bool CONV> struct VTranspose {
             if constexpr (CONV)
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t w = o[j];
-                    const f32x2 v = {__builtin_bit_cast(float, w << 16) * 0x1p-8f,
-                                     __builtin_bit_cast(float, w & 0xffff0000u) * 0x1p-8f};
+                    const f32x2 v = {__builtin_bit_cast(float, w << 16),
+                                     __builtin_bit_cast(float, w & 0xffff0000u)};
                     o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
                 }
             *(lds_ptr<u32x4>)(vt + dst[n]) = o;
@@ -276,12 +282,18 @@ template <int LPT, int A> __device__ __forceinline__ void ring_sync_fixed() {
     __asm__ volatile("" ::: "memory");
 }
 
-// The running maximum of a row is moved (and O and l rescaled) only when a
-// tile's maximum exceeds it by more than 2^RESCALE_SLACK in probability: until
-// then probabilities up to 2^RESCALE_SLACK are accumulated against the stale
-// maximum, which bf16/f16 P and the FP32 accumulators hold exactly.  The final
-// division by l is unchanged, so the result is the same softmax.
+// The running maximum of a row (the exp base) is moved, and O and l rescaled,
+// only when a tile's mass against it exceeds 2^RESCALE_SLACK: until then
+// probabilities up to 2^RESCALE_SLACK are accumulated against the stale base,
+// which f16 P and the FP32 accumulators hold exactly.  The base is always a
+// score the row has seen, so its mass stays at least 1.  The final division
+// by l is unchanged, so the result is the same softmax.
 constexpr float RESCALE_SLACK = 8.0f;
+constexpr float MASS_LIMIT = 256.0f;  // 2^RESCALE_SLACK
+// The exp base of a row that has seen no score: finite (a masked score of
+// -inf gives 2^-inf = 0, not NaN) and large enough that any finite visible
+// score exceeds MASS_LIMIT, which sends the row's first tile to the exact path.
+constexpr float BASE_NONE = 0x1p100f;
 
 __device__ __forceinline__ int uniform32(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
@@ -483,15 +495,16 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     f32x16 acc[MB];
     for (int mb = 0; mb < MB; ++mb)
         for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
-    float m_run = NEG_INF, l_run = 0.0f;
-    // The smallest visible score of fully visible tiles (a -inf one is a
-    // non-finite score) and the exp base -m_run * tmul, updated with m_run.
-    float lo_run = -NEG_INF, nbase_run = 0.0f;
-    bool bad = false;  // an infinite visible score (NaN reaches the mass and the context)
+    // m_run: the row's exp base in t units (a score it has seen; -inf before
+    // the first), nbase_run = -m_run * tmul (BASE_NONE before the first).
+    float m_run = NEG_INF, l_run = 0.0f, nbase_run = BASE_NONE;
+    // The largest |score| of fully visible tiles: not below +inf exactly when
+    // one of them was not finite (masked tiles check their visible scores
+    // themselves).
+    float amax_run = 0.0f;
+    bool bad = false;  // a non-finite visible score
     const float scale = p.scale, softcap = p.softcap, softcap_inv = p.softcap_inv;
     const float tmul = CAP ? 1.0f : p.scale_log2;  // t units -> log2 units
-    const float slack = RESCALE_SLACK / tmul;      // in t units
-    float m_thr = NEG_INF;                         // rescale when a tile maximum exceeds this
     // A row maximum of 2^10 or more in log2 units (natural-log logits above
     // about 700) makes the rounding of m * tmul worth a large part of an
     // exponent, so 2^(t * tmul - round(m * tmul)) would lose the mass.  A wave
@@ -610,11 +623,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         lds_ptr<uint8_t> kn = lds + L::k_at(STG_NEXT);
 
         // ---- step 1.  t = raw dot (or, with the softcap, the capped score in
-        // log2 units); p = 2^(t * tmul - m * tmul).  Both transforms are
-        // increasing, so the tile maximum follows from the raw one.
+        // log2 units); p = 2^(t * tmul + nbase) against the row's current base,
+        // with no tile maximum (the check after step 3 catches a base that is
+        // too low).
         float tv[CAP ? 16 : 1];  // softcapped scores (the raw scores serve otherwise)
-        float hi = NEG_INF, corr = 1.0f, nbase = 0.0f;
-        bool rescale = false;
+        float nbase = nbase_run;
+        float shift = 0.0f;      // subtracted from st in raw units (huge rows)
+        float lt = 0.0f;         // this lane's mass of the tile
         uint32_t nh[4];
 #pragma unroll
         for (int k = 0; k < NPV; ++k) {
@@ -626,11 +641,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             __builtin_amdgcn_sched_barrier(0);
             if (k == 0) {
                 if (bulk || (t >= tf_lo && t < tf_hi)) {
-                    hi = maxn(st[0], st[1]);
-                    float lo = minn(lo_run, st[0]);
-                    for (int i = 2; i < 16; ++i) hi = maxn(hi, st[i]);
-                    for (int i = 1; i < 16; ++i) lo = minn(lo, st[i]);
-                    lo_run = lo;
+                    float a = amax_run;
+                    for (int i = 0; i < 16; ++i) a = maxn(a, __builtin_fabsf(st[i]));
+                    amax_run = a;
                     if constexpr (CAP)
                         for (int i = 0; i < 16; ++i) tv[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
                 } else {
@@ -640,47 +653,20 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                     for (int i = 0; i < 16; ++i) {
                         const int kk = 8 * (i >> 2) + 4 * h + (i & 3);
                         const bool vis = kk >= lo_rel && kk < hi_rel;
-                        bad |= vis && st[i] == NEG_INF;
+                        bad |= vis && !(__builtin_fabsf(st[i]) < -NEG_INF);
                         if constexpr (CAP) tv[i] = vis ? softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E : NEG_INF;
                         st[i] = vis ? st[i] : NEG_INF;  // masked in place: no copy of the scores
                     }
-                    hi = maxn(st[0], st[1]);
-                    for (int i = 2; i < 16; ++i) hi = maxn(hi, st[i]);
                 }
             }
             if (k == (NPV > 1 ? 1 : 0)) {
-                // A +inf score: checked here under the softcap (which maps it
-                // to the cap); otherwise it becomes the running maximum, which
-                // is checked once after the loop.
-                if constexpr (CAP) bad |= hi == -NEG_INF;
-                float mt;
-                if constexpr (CAP) mt = hi == NEG_INF ? NEG_INF : softcap_fast(hi * scale, softcap, softcap_inv) * LOG2E;
-                else mt = hi;
-                const uint32_t u = __builtin_bit_cast(uint32_t, mt);
-                const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-                const uint32_t a0 = pr32[0], a1 = pr32[1];
-                mt = maxn(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
-                // Rare: a maximum moved past the slack.  l and the maximum change
-                // now; O, which still receives tile t - 1's P.V, after step 1.
-                if (__ballot(mt > m_thr) != 0) {
-                    const float m_new = fmaxf(m_run, mt);
-                    if (m_new != m_run) {
-                        corr = m_run == NEG_INF ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * tmul);
-                        l_run *= corr;
-                        m_run = m_new;
-                        m_thr = m_new == NEG_INF ? NEG_INF : m_new + slack;
-                        nbase_run = m_new == NEG_INF ? 0.0f : -m_new * tmul;
-                    }
-                    rescale = true;
-                    if constexpr (!CAP)
-                        huge = __ballot(m_run != NEG_INF && fabsf(m_run * tmul) >= 1024.0f) != 0;
-                }
-                nbase = nbase_run;
                 if constexpr (!CAP) {
                     if (huge) {
-                        const float mr = m_run == NEG_INF ? 0.0f : m_run;
-                        for (int i = 0; i < 16; ++i) st[i] -= mr;
-                        nbase = 0.0f;
+                        // Rows with no base yet keep BASE_NONE (their first
+                        // visible tile takes the exact path).
+                        shift = m_run == NEG_INF ? 0.0f : m_run;
+                        for (int i = 0; i < 16; ++i) st[i] -= shift;
+                        nbase = m_run == NEG_INF ? BASE_NONE : 0.0f;
                     }
                 }
             }
@@ -690,17 +676,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                     const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
                     const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
                     nh[i] = pack2<PDT>(e0, e1);
-                    l_run = add_pair(nh[i], l_run);
+                    lt = add_pair(nh[i], lt);
                     // Pin the pair here: the compiler would otherwise sink it to
                     // its use after step 1, out of the MFMA shadow.
-                    asm volatile("" : "+v"(nh[i]), "+v"(l_run));
+                    asm volatile("" : "+v"(nh[i]), "+v"(lt));
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (rescale)
-            for (int mb = 0; mb < MB; ++mb)
-                for (int i = 0; i < 16; ++i) acc[mb][i] *= corr;
         for (int i = 0; i < 4; ++i) {
             ph[i] = nh[i];
         }
@@ -759,11 +742,60 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
                 const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
                 ph[i] = pack2<PDT>(e0, e1);
-                l_run = add_pair(ph[i], l_run);
-                asm volatile("" : "+v"(ph[i]), "+v"(l_run));
+                lt = add_pair(ph[i], lt);
+                asm volatile("" : "+v"(ph[i]), "+v"(lt));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+
+        // ---- the exact path, rare: some row's tile mass exceeds MASS_LIMIT
+        // (a score more than RESCALE_SLACK log2 units above its base, the
+        // row's first visible tile, or a non-finite score).  The wave moves
+        // each such row's base to the tile maximum, rescales O (which holds
+        // tiles up to t - 1) and l, and forms tile t's probabilities again.
+        if (__ballot(!(lt <= MASS_LIMIT)) != 0) {
+            float hi = CAP ? tv[0] : st[0];
+            for (int i = 1; i < 16; ++i) hi = maxn(hi, CAP ? tv[i % (CAP ? 16 : 1)] : st[i]);
+            {
+                const uint32_t u = __builtin_bit_cast(uint32_t, hi);
+                const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+                // Copied to scalars first: a bit_cast of a vector element reads
+                // element 0 whatever the index.
+                const uint32_t a0 = pr32[0], a1 = pr32[1];
+                hi = maxn(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+            }
+            hi += shift;  // raw units (st of a huge row was shifted)
+            // A NaN maximum leaves the base (the row already reports a
+            // non-finite score).
+            const float m_new = fmaxf(m_run, hi);
+            if (m_new > m_run) {
+                const float corr = m_run == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * tmul);
+                l_run *= corr;
+                for (int mb = 0; mb < MB; ++mb)
+                    for (int i = 0; i < 16; ++i) acc[mb][i] *= corr;
+                m_run = m_new;
+            }
+            if constexpr (!CAP)
+                huge = __ballot(m_run != NEG_INF && fabsf(m_run * tmul) >= 1024.0f) != 0;
+            nbase_run = m_run == NEG_INF ? BASE_NONE : -m_run * tmul;
+            // Tile t against the new base, in the units st holds.
+            const float delta = m_run == NEG_INF ? 0.0f : m_run - shift;
+            const float nb = -delta * tmul;
+            lt = 0.0f;
+            for (int i = 0; i < 8; ++i) {
+                float y0, y1;
+                if (!CAP && huge) {
+                    y0 = (st[2 * i] - delta) * tmul;
+                    y1 = (st[2 * i + 1] - delta) * tmul;
+                } else {
+                    y0 = __builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nb);
+                    y1 = __builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nb);
+                }
+                ph[i] = pack2<PDT>(__builtin_amdgcn_exp2f(y0), __builtin_amdgcn_exp2f(y1));
+                lt = add_pair(ph[i], lt);
+            }
+        }
+        l_run += lt;
 
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -793,8 +825,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             acc[mb] = mfma32<PDT>(vop[stp][mb], bv, acc[mb]);
         }
     }
-    bad |= lo_run == NEG_INF;
-    if constexpr (!CAP) bad |= m_run == -NEG_INF;
+    bad |= !(amax_run < -NEG_INF);
     // ---- the two key halves of each row (lanes j and j + 32) share m_run; add l.
     {
         const uint32_t u = __builtin_bit_cast(uint32_t, l_run);
@@ -805,17 +836,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     bool bad_acc = false;
     for (int mb = 0; mb < MB; ++mb)
         for (int i = 0; i < 16; ++i) bad_acc |= !is_finite_f(acc[mb][i]);
-    // bf16: the P.V products took V as f16 scaled by 2^-8, which overflows for
-    // finite values of magnitude 2^24 or more.  Only a wave whose context is
-    // not finite while its scores were reads the workgroup's V rows again, to
-    // tell a non-finite input (ST_NONFINITE_INPUT) from such a value, which is
-    // reported as out of this kernel's range (ST_V_RANGE) instead.
-    bool v_range = false;
+    // bf16: the P.V products took V as f16, which overflows for finite values
+    // above 65280.  Only a wave whose context is not finite while its scores
+    // were reads the workgroup's V rows again, to tell a non-finite input
+    // (ST_NONFINITE_INPUT) from such a value.  For the latter the wave forms
+    // its rows again on the vector unit in FP32 (scores, probabilities against
+    // the same base, context and mass), which is slow and exact for every
+    // finite value.
     if constexpr (VCONV) {
         if (__ballot(bad_acc && !bad) != 0) {
             constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
             constexpr int RPI = 64 / CPR;    // rows per wave iteration
             const uint8_t *vrows = reinterpret_cast<const uint8_t *>(pv.sg.v) + first * 2;
+            const uint8_t *krows = reinterpret_cast<const uint8_t *>(pv.sg.k) + first * 2;
             bool nonfinite = false, big = false;
             for (int r0 = 0; r0 < nkeys; r0 += RPI) {
                 const int r = r0 + lane / CPR;
@@ -825,13 +858,56 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                         const uint32_t x = w[e];
                         const uint32_t lo = x & 0x7fffu, hi = (x >> 16) & 0x7fffu;
                         nonfinite |= lo >= 0x7f80u || hi >= 0x7f80u;  // bf16 inf / NaN
-                        big |= lo >= 0x4b80u || hi >= 0x4b80u;        // |v| >= 2^24
+                        big |= lo >= 0x4780u || hi >= 0x4780u;        // |v| >= 65536
                     }
                 }
             }
             if (__ballot(nonfinite) == 0 && __ballot(big) != 0) {
-                v_range = true;
+                // Lane (j, h) holds Q features 16 ks + 8 h .. + 7 and context
+                // features 32 mb + 8 q + 4 h .. + 3 of row j; a score is the
+                // lane pair's two partial dots added.
+                for (int mb = 0; mb < MB; ++mb)
+                    for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
+                float l = 0.0f;
+                const bool any = m_run != NEG_INF;
+                for (int kk = 0; kk < nkeys; ++kk) {
+                    const uint8_t *kr = krows + (int64_t)kk * prow;
+                    float d = 0.0f;
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const u32x4 kw = *gload_ptr<u32x4>(kr + 32 * ks + 16 * h);
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t qw = qb[ks][e], kx = kw[e];
+                            d = __builtin_fmaf(lo_f<BF16>(qw), lo_f<BF16>(kx), d);
+                            d = __builtin_fmaf(hi_f<BF16>(qw), hi_f<BF16>(kx), d);
+                        }
+                    }
+                    {
+                        const uint32_t u = __builtin_bit_cast(uint32_t, d);
+                        const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+                        const uint32_t a0 = pr32[0], a1 = pr32[1];
+                        d = __builtin_bit_cast(float, a0) + __builtin_bit_cast(float, a1);
+                    }
+                    float y;
+                    if constexpr (CAP) y = softcap_fast(d * scale, softcap, softcap_inv) * LOG2E - m_run;
+                    else y = (d - m_run) * tmul;
+                    const bool vis = any && kk >= rlo0 && kk < rhi0;
+                    const float pk = vis ? __builtin_amdgcn_exp2f(y) : 0.0f;
+                    l += pk;
+                    const uint8_t *vr = vrows + (int64_t)kk * prow;
+                    for (int mb = 0; mb < MB; ++mb)
+                        for (int q = 0; q < 4; ++q) {
+                            const u32x2 vw = *gload_ptr<u32x2>(vr + (32 * mb + 8 * q + 4 * h) * 2);
+                            const uint32_t v0 = vw[0], v1 = vw[1];
+                            acc[mb][4 * q + 0] = __builtin_fmaf(pk, lo_f<BF16>(v0), acc[mb][4 * q + 0]);
+                            acc[mb][4 * q + 1] = __builtin_fmaf(pk, hi_f<BF16>(v0), acc[mb][4 * q + 1]);
+                            acc[mb][4 * q + 2] = __builtin_fmaf(pk, lo_f<BF16>(v1), acc[mb][4 * q + 2]);
+                            acc[mb][4 * q + 3] = __builtin_fmaf(pk, hi_f<BF16>(v1), acc[mb][4 * q + 3]);
+                        }
+                }
+                l_run = l;  // both lanes of the pair summed every key
                 bad_acc = false;
+                for (int mb = 0; mb < MB; ++mb)
+                    for (int i = 0; i < 16; ++i) bad_acc |= !is_finite_f(acc[mb][i]);
             }
         }
     }
@@ -840,11 +916,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // O^T lane layout: row j, features 32 mb + 8 q + 4 h + r (register 4 q + r).
     const bool single = pv.splits == 1;
     bool bad_mass = false, bad_out = false;
-    // bf16: the P.V products used V scaled by 2^-8.
-    constexpr float oscale = VCONV ? 256.0f : 1.0f;
     if (single) {
         if (rvalid) {
-            const float inv = oscale / l_run;
+            const float inv = 1.0f / l_run;
             bad_mass |= !(l_run > 0.0f) || !is_finite_f(l_run);
             float *orow = pv.out + ((int64_t)t_row * Hq + h_row) * D;
             for (int mb = 0; mb < MB; ++mb)
@@ -859,8 +933,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
         raise_status(p, bad, ST_NONFINITE_INPUT);
         raise_status(p, bad_mass, ST_BAD_MASS);
-        raise_status(p, bad_out && !v_range, ST_NONFINITE_OUTPUT);
-        raise_status(p, v_range, ST_V_RANGE);
+        raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
         return;
     }
 
@@ -872,7 +945,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // two whole lines, where a row-major 16-byte store touched 32 lines (its
     // stores took 3.5 instead of 1.4 us per workgroup at head_dim 256).
     raise_status(p, bad, ST_NONFINITE_INPUT);
-    raise_status(p, v_range, ST_V_RANGE);
     const int64_t group = (int64_t)kvh * pv.row_blocks + rb;
     const int64_t slot = pv.slot_base + group * pv.splits + split;
     float *pf = p.part_o + slot * ROWS * D + wave * 32 + j;
@@ -880,7 +952,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int q = 0; q < 4; ++q)
             for (int r = 0; r < 4; ++r)
                 *gstore_ptr<float>(pf + (int64_t)(32 * mb + 8 * q + 4 * h + r) * ROWS) =
-                    acc[mb][4 * q + r] * oscale;
+                    acc[mb][4 * q + r];
     if (h == 0) {
         const f32x2 ml = {m_run, l_run};
         *gstore_ptr<f32x2>(p.part_ml + (slot * ROWS + wave * 32 + j) * 2) = ml;
