@@ -10,8 +10,9 @@ attention GB/s over the timed steps (algorithmic bytes: visible keys x
 its stream, with HBM traffic from the committed rocprofv3 counter passes.
 
 Also on the line: `prefill_roofline` on configs[4] (32 sessions x (4096 cached
-+ 128 new), the MFMA-bound prefill), the CPU baselines of both on BASELINE.md's
-subsets (the oracle on one host core), configs[0] (FP32 session, GPU and CPU
++ 128 new) with Q/K rotated at theta 500000, the MFMA-bound prefill), the CPU
+baselines of both on BASELINE.md's subsets (the oracle on one host core),
+configs[0] (FP32 session, GPU and CPU
 tokens/s, and the device o-projection + greedy pick), configs[1] (Qwen3
 session job), configs[3] (Gemma local/global session), decode at 8192 keys for
 one and 16 sessions, and the host CPU model.
@@ -267,17 +268,35 @@ def bench_decode_batch(torch, ops, ctx, steps, warmup, *, batch, lmin, lmax, dty
 
 def bench_prefill_batch(torch, ops, ctx, steps, warmup, *, batch=32, cached=4096, tokens=128,
                         seed=11, dtype=None):
-    """32 sessions x (4096 cached + 128 new causal), Llama-3-8B heads, bf16."""
-    hq, hkv, d = 32, 8, 128
+    """32 sessions x (4096 cached + 128 new causal), Llama-3-8B heads, bf16.
+    Inputs (untimed): per session N(0, 1) FP32 Q/K/V projections, 5% of K rows x8,
+    through the library's producer with split-half rotary theta 500000 (the cached
+    positions into the session's cache, then the new ones: Q for the batch, K/V
+    appended)."""
+    hq, hkv, d, theta = 32, 8, 128, 5e5
     gd = torch.Generator(device="cuda").manual_seed(seed)
     cap = cached + tokens
     per = hkv * cap * d
-    k = torch.randn(batch, hkv, cap, d, generator=gd, device="cuda")
-    mask = torch.rand(batch, hkv, cap, 1, generator=gd, device="cuda") < 0.05
     dtype = dtype or torch.bfloat16
-    k = torch.where(mask, k * 8.0, k).to(dtype).reshape(-1)
-    v = torch.randn(batch * per, generator=gd, device="cuda").to(dtype)
-    q = torch.randn(batch, tokens, hq, d, generator=gd, device="cuda").to(dtype)
+    k = torch.empty(batch * per, dtype=dtype, device="cuda")
+    v = torch.empty_like(k)
+    q = torch.empty(batch, tokens, hq, d, dtype=dtype, device="cuda")
+    q_prefix = torch.zeros(cached, hq, d, device="cuda")  # the cached positions' Q is not used
+    q_scratch = torch.empty(cached, hq, d, dtype=dtype, device="cuda")
+    for b in range(batch):
+        kp = torch.randn(cap, hkv, d, generator=gd, device="cuda")
+        mask = torch.rand(cap, hkv, 1, generator=gd, device="cuda") < 0.05
+        kp = torch.where(mask, kp * 8.0, kp)
+        vp = torch.randn(cap, hkv, d, generator=gd, device="cuda")
+        qp = torch.randn(tokens, hq, d, generator=gd, device="cuda")
+        kb, vb = k[b * per:(b + 1) * per], v[b * per:(b + 1) * per]
+        ops.produce_qkv(ctx, ops.ProducerShape(cached, hq, hkv, d, 0, theta=theta), q_prefix,
+                        kp[:cached], vp[:cached], None, None, q_scratch, kb, vb, cap * d)
+        ops.produce_qkv(ctx, ops.ProducerShape(tokens, hq, hkv, d, cached, theta=theta), qp,
+                        kp[cached:], vp[cached:], None, None, q[b], kb[cached * d:], vb[cached * d:],
+                        cap * d)
+    ctx.synchronize()
+    del q_prefix, q_scratch
     out = torch.zeros(batch * tokens * hq * d, dtype=torch.float32, device="cuda")
     offsets = [b * per for b in range(batch)]
     strides = [cap * d] * batch
@@ -750,7 +769,7 @@ def main():
         line["prefill_roofline"] = {
             "bound": "mfma",
             "kernel": "attn_prefill<bf16, D=128, 8 waves> (configs[4]: 32 sessions x (4096 cached "
-                      "+ 128 new), 32q/8kv/d128)",
+                      "+ 128 new), 32q/8kv/d128, Q/K rotary theta 5e5)",
             "achieved": round(c5["kernel_tflops"], 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",

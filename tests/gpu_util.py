@@ -82,3 +82,12 @@ def assert_tokens_agree(got: np.ndarray, ref: np.ndarray, weight: np.ndarray, ma
         ties += 1
     assert ties <= max(1, int(max_ties * len(ta))), f"{ties} of {len(ta)} rows changed token"
     return ties
+
+
+def assert_tokens_identical(got: np.ndarray, ref: np.ndarray, weight: np.ndarray):
+    """Greedy tokens of the GPU context equal the oracle's on every row (the
+    north star's "argmax-identical next tokens"), with no allowance for ties."""
+    ta, tb = greedy_tokens(ref, weight), greedy_tokens(got, weight)
+    rows = np.nonzero(ta != tb)[0]
+    assert rows.size == 0, (f"{rows.size} of {len(ta)} rows changed token "
+                            f"(first rows {rows[:8].tolist()})")

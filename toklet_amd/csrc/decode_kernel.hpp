@@ -867,6 +867,10 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
             if (__builtin_amdgcn_s_memrealtime() - t_start > p.split_wait_ticks) break;
             __builtin_amdgcn_s_sleep(1);
         }
+        // Every flag was seen: clear them, so no later launch that carries
+        // the same epoch (a replayed graph of this launch) can take them for
+        // its own.  The next launch starts after this one has ended.
+        if (arrived && lane < S - 1) flag_store(p.flags + slot0 + lane, 0u);
         if (lane == 0) lds_own[R * D + 2 * R] = arrived ? 1.0f : 0.0f;
     }
     __syncthreads();
