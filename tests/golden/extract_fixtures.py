@@ -30,6 +30,15 @@ Fixture sets taken (all used by the reference's own attention tests):
                              frozen outputs of both contracts; the inputs are rebuilt from the
                              fixture's published rational recipe and checked against the
                              manifest's SHA-256 (tests/goldens.py: reference_attention_inputs)
+  staged-gqa-half-v1         src/metal/staged_gqa_fixture.rs:6-40, src/metal/staged_attention/
+                             gqa_tests.rs (-> staged_gqa_half_v1)
+  gemma3-staged-attention-v1 src/metal/staged_attention/tests.rs:9-60 (-> gemma3_staged_attention_v1)
+                             Both: the `main` profile's scores, probabilities and Half
+                             contexts of every case, each case's gates, views and copy runs,
+                             and the SHA-256 of every physical input and after-commit array;
+                             the physical arrays themselves are rebuilt from the fixtures'
+                             published seeded recipe and checked against those hashes
+                             (tests/goldens.py: staged_physical)
 """
 
 from __future__ import annotations
@@ -250,6 +259,41 @@ def reference_attention(ref: str, out: str):
     json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
 
 
+def staged(ref: str, name: str, out: str):
+    """A staged old-ring/new-chunk Half fixture: per case the main profile's
+    numerical arrays (checked against their SHA-256) and the metadata a device
+    replay needs; physical inputs are kept as hashes only."""
+    root = os.path.join(ref, "tests", "fixtures", name)
+    raw_meta = open(os.path.join(root, "manifest.json"), "rb").read()
+    manifest = json.loads(raw_meta)
+    raw = open(os.path.join(root, "arrays.bin"), "rb").read()
+    assert sha(raw) == manifest["files"]["arrays.bin"]["sha256"]
+
+    def take(item):
+        body = raw[item["offset"]:item["offset"] + item["bytes"]]
+        assert sha(body) == item["sha256"]
+        dtype = {"u16le": "<u2", "f32le": "<f4"}[item["dtype"]]
+        return np.frombuffer(body, dtype=dtype).reshape(item["shape"]).copy()
+
+    arrays, cases = {}, []
+    for c in manifest["cases"]:
+        meta = {k: v for k, v in c.items() if k not in ("arrays", "inputs", "intervals",
+                                                         "source_input_immutability")}
+        meta["gates"] = {}
+        for stage in ("scores", "probabilities", "context"):
+            d = c["arrays"][stage]
+            arrays[f"{c['name']}.{stage}"] = take(d["main"])
+            meta["gates"][stage] = d["gate"]
+        meta["input_sha256"] = {k: {"sha256": v["sha256"], "words": v["shape"][0]}
+                                for k, v in c["inputs"].items()}
+        cases.append(meta)
+    meta = {"source_manifest_sha256": sha(raw_meta), "format": manifest["format"],
+            "guard": manifest["guard"], "pad": manifest["input_padding_half_word"],
+            "policy": manifest["policy"], "cases": cases}
+    np.savez_compressed(os.path.join(HERE, out + ".npz"), **arrays)
+    json.dump(meta, open(os.path.join(HERE, out + ".json"), "w"), indent=1, sort_keys=True)
+
+
 def main(ref: str):
     attn = ["q_projection", "k_projection", "q_rotary", "k_rotary", "v_projection",
             "attention_scores", "attention_probabilities", "attention_context"]
@@ -265,6 +309,8 @@ def main(ref: str):
     tiny_norms(ref, "tiny_v1_norms")
     tiny_linear(ref, "tiny_v1_linear")
     reference_attention(ref, "gemma_reference_attention_v1")
+    staged(ref, "staged-gqa-half-v1", "staged_gqa_half_v1")
+    staged(ref, "gemma3-staged-attention-v1", "gemma3_staged_attention_v1")
 
 
 if __name__ == "__main__":

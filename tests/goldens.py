@@ -79,3 +79,95 @@ def reference_attention_inputs(golden: "Golden", case: dict, contract: str):
         assert digest == item["sha256"], f"rebuilt {case['name']}/{contract}/{name} differs"
         out.append(values)
     return out
+
+
+# ---- staged-gqa-half-v1 and gemma3-staged-attention-v1 physical inputs ----
+
+# The fixtures' published seeded recipe (tools/reference/staged_gqa_half.py:75-110 and
+# tools/reference/gemma3_staged_attention.py:93-133): Half rows of small dyadic
+# rationals from modular walks over (position, head, feature), laid out as the
+# staged kernels' physical buffers -- old rows [kv, retention, D] at their ring or
+# linear slots, staged rows [kv, 32, D] (head stride 32 whatever the chunk), Q
+# [32, Hq, D] -- with every unwritten word, and a 7-word guard, holding the pad
+# word.  Rebuilt here and checked word for word against the SHA-256 each
+# manifest records for the arrays.
+
+STAGED_CHUNK = 32
+
+
+def _half_words(values) -> np.ndarray:
+    return np.asarray(values, dtype=np.float64).astype(np.float16).view(np.uint16)
+
+
+def _staged_row(fixture: str, case: dict, position: int, head: int, kind: str) -> np.ndarray:
+    d = case["dim"]
+    f = np.arange(d)
+    if fixture == "staged_gqa_half_v1":
+        if kind == "k":
+            values = ((position * 5 + head * 7 + f * 3 + 1) % 17 - 8) / 32
+        else:
+            values = ((position * 11 + head * 13 + f * 5 + 7) % 31 - 15) / 16
+        words = _half_words(values)
+        if case["name"] == "tiny_single" and kind == "v" and position == 0:
+            words[0] = 0x0001 if head == 0 else 0x8001
+        return words
+    if kind == "v" and case["pattern"] == "uniform":
+        values = np.zeros(d)
+        for feature, key in enumerate((0, 1, 512, 513)):
+            if position == key:
+                values[feature] = 512.0
+        return _half_words(values)
+    modulus, divisor, shift = (17, 32, 1) if kind == "k" else (19, 16, 7)
+    return _half_words(((position * 5 + f * 3 + shift) % modulus - modulus // 2) / divisor)
+
+
+def staged_physical(golden: "Golden", fixture: str, case: dict) -> dict:
+    """The physical u16 arrays of one case: q, old_k/old_v, new_k/new_v and the
+    expected after-commit expected_after_k/_v, each with its guard, each checked
+    against the manifest's SHA-256."""
+    guard, pad = golden.meta["guard"], golden.meta["pad"]
+    d, n, committed = case["dim"], case["tokens"], case["committed"]
+    window = case["window"]
+    retention = window or case["capacity"]
+    qh, kv = case["query_heads"], case["kv_heads"]
+    out = {}
+    old = {}
+    for kind in ("k", "v"):
+        words = np.full(kv * retention * d + guard, pad, np.uint16)
+        first = max(0, committed - retention) if window else 0
+        for head in range(kv):
+            for position in range(first, committed):
+                slot = position % retention if window else position
+                words[(head * retention + slot) * d:(head * retention + slot + 1) * d] = \
+                    _staged_row(fixture, case, position, head, kind)
+        old[kind] = words
+        staged = np.full(kv * STAGED_CHUNK * d + guard, pad, np.uint16)
+        for head in range(kv):
+            for token in range(n):
+                off = (head * STAGED_CHUNK + token) * d
+                staged[off:off + d] = _staged_row(fixture, case, committed + token, head, kind)
+        out["old_" + kind] = words
+        out["new_" + kind] = staged
+        after = words.copy()
+        for head in range(kv):
+            for run in case["copy_runs"]:
+                src = (head * STAGED_CHUNK + run["source_row"]) * d
+                dst = (head * retention + run["destination_row"]) * d
+                after[dst:dst + run["rows"] * d] = staged[src:src + run["rows"] * d]
+        out["expected_after_" + kind] = after
+    q = np.full(STAGED_CHUNK * qh * d + guard, pad, np.uint16)
+    f = np.arange(d)
+    for token in range(n):
+        for head in range(qh):
+            if case.get("pattern") == "uniform":
+                values = np.zeros(d)
+            else:
+                values = ((7 * (committed + token) + 5 * head + 3 * f) % 13 - 6) / 32
+            q[(token * qh + head) * d:(token * qh + head + 1) * d] = _half_words(values)
+    out["q"] = q
+    for name, words in out.items():
+        want = case["input_sha256"][name]
+        assert words.size == want["words"], (case["name"], name)
+        digest = hashlib.sha256(words.astype("<u2").tobytes()).hexdigest()
+        assert digest == want["sha256"], f"rebuilt {case['name']}/{name} differs"
+    return out
