@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <new>
 #include <vector>
 
 #include "../../include/tokhip.h"
@@ -112,8 +113,18 @@ uint32_t after_launch(tkh_context *ctx, tkh_error *err) {
 }
 
 // A launch plan: problems sharing head geometry, dtype and mask parameters.
+// Its problems live in fixed storage, so planning a call allocates nothing:
+// one inline problem for the single-problem entry points, or the context's
+// batch store (kSlotProblems problems, allocated with the context) for the
+// batched ones, which plan and launch their sessions a store at a time.
 struct Plan {
-    std::vector<tkh::Problem> problems;
+    tkh::Problem one{};
+    tkh::Problem *store = &one;
+    size_t capacity = 1, count = 0;
+    Plan() = default;
+    Plan(const Plan &) = delete;
+    Plan &operator=(const Plan &) = delete;
+    void add(const tkh::Problem &p) { store[count++] = p; }  // count < capacity by construction
     tkh_dtype dtype = TKH_BF16;
     int64_t query_heads = 0, kv_heads = 0, head_dim = 0;
     bool has_window = false;
@@ -713,7 +724,7 @@ uint32_t launch_all(tkh_context *ctx, const Plan &plan, tkh::Problem *probs, siz
 }
 
 uint32_t run(tkh_context *ctx, Plan &plan, tkh_error *err) {
-    TRY(launch_all(ctx, plan, plan.problems.data(), plan.problems.size(), err));
+    TRY(launch_all(ctx, plan, plan.store, plan.count, err));
     return after_launch(ctx, err);
 }
 
@@ -809,6 +820,8 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
     // Decode tags start at 0, which no launch epoch equals.
     if ((e = hipMemset(decode_region(ctx), 0, decode_region_bytes(ctx))) != hipSuccess)
         return cleanup(e, "workspace");
+    ctx->batch_store = new (std::nothrow) tkh::Problem[kSlotProblems];
+    if (!ctx->batch_store) return cleanup(hipErrorOutOfMemory, "batch plan store");
     size_t ring = sizeof(tkh::Problem) * kSlots * kSlotProblems;
     if ((e = hipMalloc(&ctx->ring_dev, ring)) != hipSuccess) return cleanup(e, "problem ring");
     if ((e = hipHostMalloc(&ctx->ring_host, ring, hipHostMallocDefault)) != hipSuccess)
@@ -822,6 +835,7 @@ uint32_t tkh_context_create(int device, void *stream, size_t workspace_bytes, in
 
 void tkh_context_destroy(tkh_context *ctx) {
     if (!ctx) return;
+    delete[] ctx->batch_store;
     hipSetDevice(ctx->device);
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
     for (int i = 0; i < kSlots; ++i)
@@ -929,7 +943,7 @@ uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, t
     plan.probs = probabilities;
     tkh::Problem p = make_problem(q, context, d.q_stride, s.offset, 0, d.end, s.tokens);
     add_segment(p, k, v, d.head_stride, s.head_dim, d.end, 0);
-    plan.problems.push_back(p);
+    plan.add(p);
     return run(ctx, plan, err);
 }
 
@@ -1060,7 +1074,7 @@ uint32_t tkh_host::attention_cached_fused(tkh_context *ctx, const tkh_cached_sha
     plan.fused = &fused;
     tkh::Problem p = make_problem(nullptr, context, s.query_heads * s.head_dim, s.offset, 0, end, 1);
     add_segment(p, k, v, s.capacity * s.head_dim, s.head_dim, end, 0);
-    plan.problems.push_back(p);
+    plan.add(p);
     return run(ctx, plan, err);
 }
 
@@ -1107,7 +1121,7 @@ uint32_t tkh_host::span_attention_fused(tkh_context *ctx, const tkh_span_shape *
         logical += seg.keys;
     }
     if (logical != s.keys) return invalid("attention segment keys", err);
-    plan.problems.push_back(p);
+    plan.add(p);
     return run(ctx, plan, err);
 }
 
@@ -1153,7 +1167,7 @@ uint32_t tkh_attention(tkh_context *ctx, const tkh_attention_shape *shape, tkh_d
     plan.probs = probabilities;
     tkh::Problem p = make_problem(q, context, q_stride, 0, 0, s.tokens, s.tokens);
     add_segment(p, k, v, s.head_dim, kv_stride, s.tokens, 0);
-    plan.problems.push_back(p);
+    plan.add(p);
     return run(ctx, plan, err);
 }
 
@@ -1218,7 +1232,7 @@ uint32_t tkh_window_attention(tkh_context *ctx, const tkh_window_shape *shape, t
     tkh::Problem p = make_problem(q, context, query_stride, s.query_start, s.key_start, s.keys,
                                   s.queries);
     add_segment(p, k, v, kv_stride, s.head_dim, s.keys, 0);
-    plan.problems.push_back(p);
+    plan.add(p);
     return run(ctx, plan, err);
 }
 
@@ -1303,7 +1317,7 @@ uint32_t tkh_span_attention(tkh_context *ctx, const tkh_span_shape *shape, tkh_d
         add_segment(p, seg.k, seg.v, seg.head_stride, s.head_dim, seg.keys, logical);
         logical += seg.keys;
     }
-    plan.problems.push_back(p);
+    plan.add(p);
     return run(ctx, plan, err);
 }
 
@@ -1399,18 +1413,25 @@ uint32_t tkh_decode_batch(tkh_context *ctx, uint64_t batch, uint64_t query_heads
     plan.scale = scale;
     const int64_t es = esize(dtype);
     const int64_t row = (int64_t)(query_heads * head_dim);
-    plan.problems.reserve(batch);
     for (uint64_t b = 0; b < batch; ++b) {
         if (lengths[b] == 0) return fail(err, TKH_ZERO_DIMENSION, "lengths", b, 0, 0, "session %llu has no keys", (unsigned long long)b);
         if (head_strides[b] < lengths[b] * head_dim) return invalid("attention segment heads overlap", err);
-        tkh::Problem p = make_problem((const uint8_t *)q + b * row * es, context + b * row, row,
-                                      (int64_t)lengths[b] - 1, 0, (int64_t)lengths[b], 1);
-        add_segment(p, (const uint8_t *)k_base + offsets[b] * es,
-                    (const uint8_t *)v_base + offsets[b] * es, (int64_t)head_strides[b],
-                    (int64_t)head_dim, (int64_t)lengths[b], 0);
-        plan.problems.push_back(p);
     }
-    return run(ctx, plan, err);
+    plan.store = ctx->batch_store;
+    plan.capacity = kSlotProblems;
+    for (uint64_t b0 = 0; b0 < batch; b0 += kSlotProblems) {
+        plan.count = 0;
+        for (uint64_t b = b0; b < std::min<uint64_t>(batch, b0 + kSlotProblems); ++b) {
+            tkh::Problem p = make_problem((const uint8_t *)q + b * row * es, context + b * row, row,
+                                          (int64_t)lengths[b] - 1, 0, (int64_t)lengths[b], 1);
+            add_segment(p, (const uint8_t *)k_base + offsets[b] * es,
+                        (const uint8_t *)v_base + offsets[b] * es, (int64_t)head_strides[b],
+                        (int64_t)head_dim, (int64_t)lengths[b], 0);
+            plan.add(p);
+        }
+        TRY(launch_all(ctx, plan, plan.store, plan.count, err));
+    }
+    return after_launch(ctx, err);
 }
 
 uint32_t tkh_prefill_batch(tkh_context *ctx, uint64_t batch, uint64_t tokens,
@@ -1429,19 +1450,27 @@ uint32_t tkh_prefill_batch(tkh_context *ctx, uint64_t batch, uint64_t tokens,
     plan.scale = scale;
     const int64_t es = esize(dtype);
     const int64_t row = (int64_t)(query_heads * head_dim);
-    plan.problems.reserve(batch);
     for (uint64_t b = 0; b < batch; ++b) {
-        int64_t keys = (int64_t)(positions[b] + tokens);
-        if (head_strides[b] < (uint64_t)keys * head_dim) return invalid("attention segment heads overlap", err);
-        tkh::Problem p = make_problem((const uint8_t *)q + b * tokens * row * es,
-                                      context + b * tokens * row, row, (int64_t)positions[b], 0,
-                                      keys, (int64_t)tokens);
-        add_segment(p, (const uint8_t *)k_base + offsets[b] * es,
-                    (const uint8_t *)v_base + offsets[b] * es, (int64_t)head_strides[b],
-                    (int64_t)head_dim, keys, 0);
-        plan.problems.push_back(p);
+        const uint64_t keys = positions[b] + tokens;
+        if (head_strides[b] < keys * head_dim) return invalid("attention segment heads overlap", err);
     }
-    return run(ctx, plan, err);
+    plan.store = ctx->batch_store;
+    plan.capacity = kSlotProblems;
+    for (uint64_t b0 = 0; b0 < batch; b0 += kSlotProblems) {
+        plan.count = 0;
+        for (uint64_t b = b0; b < std::min<uint64_t>(batch, b0 + kSlotProblems); ++b) {
+            const int64_t keys = (int64_t)(positions[b] + tokens);
+            tkh::Problem p = make_problem((const uint8_t *)q + b * tokens * row * es,
+                                          context + b * tokens * row, row, (int64_t)positions[b], 0,
+                                          keys, (int64_t)tokens);
+            add_segment(p, (const uint8_t *)k_base + offsets[b] * es,
+                        (const uint8_t *)v_base + offsets[b] * es, (int64_t)head_strides[b],
+                        (int64_t)head_dim, keys, 0);
+            plan.add(p);
+        }
+        TRY(launch_all(ctx, plan, plan.store, plan.count, err));
+    }
+    return after_launch(ctx, err);
 }
 
 }  // extern "C"

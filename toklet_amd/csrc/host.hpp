@@ -105,6 +105,7 @@ struct tkh_context {
     size_t workspace_bytes = 0;
     tkh::Problem *ring_dev = nullptr;
     tkh::Problem *ring_host = nullptr;
+    tkh::Problem *batch_store = nullptr;  // kSlotProblems: the batched entry points' plans
     hipEvent_t ring_events[kSlots] = {};
     bool ring_used[kSlots] = {};
     int ring_next = 0;

@@ -181,9 +181,23 @@ struct tkh_session {
         bool position_indexed = false;
         uint64_t checked = 0;  // the checked prefix when the chunk began
         bool checked_valid = false;
+        // Sized at tkh_session_create (one entry per owning layer) and only
+        // cleared afterwards, so evaluating allocates nothing.
         std::vector<tkh_kv *> ring_kv;  // ring owners staged by this chunk
         std::vector<tkh_kv_frame> frames, owner_frame;
+        // Drops the chunk, keeping the vectors' storage.
+        void clear() {
+            active = false;
+            start = count = next_layer = 0;
+            position_indexed = false;
+            checked = 0;
+            checked_valid = false;
+            ring_kv.clear();
+            frames.clear();
+            owner_frame.clear();
+        }
     } chunk;
+    std::vector<tkh_kv *> ring_owners;  // the ring caches, for reset_batch
 };
 
 namespace {
@@ -261,7 +275,7 @@ uint32_t synchronize(tkh_session *s, tkh_error *err);
 // Queued contexts: state edits first settle the provisional chunks, so that
 // a late failure cannot land on an edited history.
 void settle(tkh_session *s) {
-    s->chunk = tkh_session::Chunk{};  // a chunk in progress is dropped
+    s->chunk.clear();  // a chunk in progress is dropped
     if (s->ctx && !s->ctx->synchronous && s->checked != s->evaluated) synchronize(s, nullptr);
 }
 
@@ -437,7 +451,11 @@ extern "C" uint32_t tkh_session_create(tkh_context *ctx, const tkh_session_optio
             }
             s->kv_bytes += s->kv[l]->allocated_bytes;
             s->rings |= ring;
+            if (ring) s->ring_owners.push_back(s->kv[l]);
         }
+        s->chunk.ring_kv.reserve(s->producers);
+        s->chunk.frames.reserve(s->producers);
+        s->chunk.owner_frame.reserve(s->producers);
         s->scratch_bytes = chunk * o->query_heads * D * es;
         hipError_t e = hipMalloc(&s->q_scratch, chunk * o->query_heads * D * es);
         if (e == hipSuccess) e = hipMalloc(&s->committed_dev, sizeof(uint64_t));
@@ -525,10 +543,8 @@ extern "C" void tkh_session_reset(tkh_session *s) {
     s->checked_valid = false;
     s->dist_valid = false;
     s->dist_replay = false;
-    std::vector<tkh_kv *> rings;
-    for (auto *kv : s->kv)
-        if (kv->has_window) rings.push_back(kv);
-    if (!rings.empty()) tkh_kv_reset_batch(rings.data(), rings.size(), nullptr);
+    if (!s->ring_owners.empty())
+        tkh_kv_reset_batch(s->ring_owners.data(), s->ring_owners.size(), nullptr);
     if (s->committed_dev) tkh_launch_fill_u64(s->committed_dev, 0, s->ctx->stream);
 }
 
@@ -586,7 +602,7 @@ void commit_state(tkh_session *s, uint64_t count) {
 // evaluated_len in a linear cache are not part of any prefix.
 void begin_chunk(tkh_session *s, uint64_t start, uint64_t count, bool position_indexed) {
     tkh_session::Chunk &c = s->chunk;
-    c = tkh_session::Chunk{};
+    c.clear();
     c.active = true;
     c.start = start;
     c.count = count;
@@ -596,7 +612,7 @@ void begin_chunk(tkh_session *s, uint64_t start, uint64_t count, bool position_i
     c.owner_frame.assign(s->kv.size(), tkh_kv_frame{});
 }
 
-void abort_chunk(tkh_session *s) { s->chunk = tkh_session::Chunk{}; }
+void abort_chunk(tkh_session *s) { s->chunk.clear(); }
 
 uint32_t eval_layer(tkh_session *s, uint64_t l, const tkh_layer_io &io, tkh_error *err) {
     tkh_session::Chunk &c = s->chunk;
@@ -809,8 +825,12 @@ uint32_t eval_layer(tkh_session *s, uint64_t l, const tkh_layer_io &io, tkh_erro
 
 uint32_t commit_chunk(tkh_session *s, tkh_error *err) {
     tkh_context *ctx = s->ctx;
-    tkh_session::Chunk c = std::move(s->chunk);
-    abort_chunk(s);
+    tkh_session::Chunk &c = s->chunk;
+    // The chunk is dropped on every way out (its vectors keep their storage).
+    struct Drop {
+        tkh_session *s;
+        ~Drop() { abort_chunk(s); }
+    } drop{s};
     // Commit only after every layer of the chunk succeeded.
     if (ctx->synchronous) TRY(tkh_context_synchronize(ctx, err));
     if (!c.ring_kv.empty()) {
