@@ -476,7 +476,12 @@ uint32_t tkh_session_evaluate(tkh_session *s, const tkh_layer_io *layers, uint64
  * layer, a commit before the last layer (TKH_INVALID_CONFIG), chunk_abort,
  * and every state edit, evaluate call or synchronize drop the chunk and leave
  * the session as it was.  Layers out of order, or chunk_layer without a
- * chunk, return TKH_INVALID_CONFIG without dropping it. */
+ * chunk, return TKH_INVALID_CONFIG without dropping it.  With a queued
+ * context, the kernels of a dropped chunk's layers still run: a non-finite
+ * value they meet is reported by the next synchronize, which then also
+ * returns the session to its last checked prefix, dropping chunks committed
+ * since; a caller that may drop a chunk keeps earlier chunks by calling
+ * tkh_session_synchronize before beginning it. */
 uint32_t tkh_session_chunk_begin(tkh_session *s, uint64_t chunk_limit, uint64_t *start,
                                  uint64_t *count, tkh_error *err);
 uint32_t tkh_session_chunk_layer(tkh_session *s, uint64_t layer, const tkh_layer_io *io,

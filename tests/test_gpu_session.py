@@ -703,6 +703,50 @@ def test_queued_linear_session_failure_returns_to_checked_prefix(torch_mod, ops,
     c.close()
 
 
+def test_queued_abort_after_a_failing_layer_keeps_the_checked_chunks(torch_mod, ops, sess_mod):
+    """A queued context, layer by layer: chunk A committed and synchronized, chunk
+    B begun, a non-finite value in its layer 0, B aborted.  The next synchronize
+    reports B's non-finite value and the session keeps A (its checked prefix),
+    as tkh_session_chunk_abort documents; a retry of B with clean inputs then
+    commits."""
+    torch = torch_mod
+    rng = np.random.default_rng(9)
+    hq, hkv, D, total = 4, 2, 64, 64
+    qs, ks, vs, wq, wk = _session_inputs(rng, 1, total, hq, hkv, D)
+    c = ops.Context(0, synchronous=False)
+    s = sess_mod.Session(c, sess_mod.Options(capacity=total, prefill_chunk_size=16, vocab_size=10,
+                                             layers=2, query_heads=hq, kv_heads=hkv, head_dim=D,
+                                             storage="bf16"))
+    out = torch.zeros((16, hq * D), dtype=torch.float32, device="cuda")
+    good = [sess_mod.LayerIo(_t(torch, qs[0][p:p + 16]), _t(torch, ks[0][p:p + 16]),
+                             _t(torch, vs[0][p:p + 16]), out, None, None) for p in (0, 16)]
+    vbad = vs[0][16:32].copy()
+    vbad[3, 1, 0] = np.nan
+    bad = sess_mod.LayerIo(_t(torch, qs[0][16:32]), _t(torch, ks[0][16:32]), _t(torch, vbad), out,
+                           None, None)
+    s.set_tokens([1] * 32)
+    assert s.chunk_begin(16) == (0, 16)
+    s.chunk_layer(0, good[0])
+    s.chunk_layer(1, good[0])
+    assert s.chunk_commit() == 16
+    s.synchronize()                          # chunk A checked
+    assert s.chunk_begin(16) == (16, 16)
+    s.chunk_layer(0, bad)                    # queued: nothing is checked yet
+    s.chunk_abort()
+    with pytest.raises(ops.TkhError) as e:
+        s.synchronize()
+    assert e.value.name == "NonFinite"
+    assert (s.evaluated_len(), s.pending_len()) == (16, 16)
+    assert s.chunk_begin(16) == (16, 16)
+    s.chunk_layer(0, good[1])
+    s.chunk_layer(1, good[1])
+    assert s.chunk_commit() == 16
+    s.synchronize()
+    assert (s.evaluated_len(), s.pending_len()) == (32, 0)
+    s.close()
+    c.close()
+
+
 @pytest.mark.parametrize("storage,hq,hkv,D", [("bf16", 16, 8, 128), ("f32", 8, 2, 64), ("f16", 8, 1, 64),
                                               ("bf16", 32, 8, 128), ("f32", 14, 2, 64),
                                               ("f32", 16, 4, 128)])
