@@ -28,9 +28,9 @@
 //    lose at most 2^-25 absolute).  A wave whose V tile held a larger finite
 //    value recomputes its rows on the vector unit in FP32 after the loop.
 //  * The softmax maximum is lazy: a tile's probabilities are formed against
-//    the running maximum without computing the tile's own maximum, and only
-//    a wave in which some row's tile mass exceeds 2^8 (a score more than 8
-//    log2 units above the base, a non-finite score, or a row's first tile)
+//    the row's base without computing the tile's own maximum, and only a
+//    wave in which some row's tile mass exceeds 2^15 (a score about 15 log2
+//    units above the base, a non-finite score, or a row's first tile)
 //    computes the tile maximum, rescales O and forms the tile again.  A
 //    max-of-magnitudes chain over the scores checks their finiteness.
 //  * Workgroups are mapped XCD-major (dispatch slot b runs on XCD b % 8) so
@@ -282,14 +282,16 @@ template <int LPT, int A> __device__ __forceinline__ void ring_sync_fixed() {
     __asm__ volatile("" ::: "memory");
 }
 
-// The running maximum of a row (the exp base) is moved, and O and l rescaled,
-// only when a tile's mass against it exceeds 2^RESCALE_SLACK: until then
-// probabilities up to 2^RESCALE_SLACK are accumulated against the stale base,
-// which f16 P and the FP32 accumulators hold exactly.  The base is always a
-// score the row has seen, so its mass stays at least 1.  The final division
-// by l is unchanged, so the result is the same softmax.
-constexpr float RESCALE_SLACK = 8.0f;
-constexpr float MASS_LIMIT = 256.0f;  // 2^RESCALE_SLACK
+// The running maximum of a row (the exp base) is moved, and O and l
+// rescaled, only when a tile's mass against it exceeds MASS_LIMIT = 2^15:
+// until then probabilities up to 2^15 are accumulated against the stale
+// base, which f16 P (largest finite 65504) and the FP32 accumulators hold.
+// The base is always a score the row has seen, so its mass stays at least 1,
+// and every key within 14 log2 units of the row's maximum is a normal f16.
+// (Moving the base above the maximum would send fewer tiles here but leaves
+// keys a few units below a dominant one subnormal in f16.)  The final
+// division by l is unchanged, so the result is the same softmax.
+constexpr float MASS_LIMIT = 0x1p15f;
 // The exp base of a row that has seen no score: finite (a masked score of
 // -inf gives 2^-inf = 0, not NaN) and large enough that any finite visible
 // score exceeds MASS_LIMIT, which sends the row's first tile to the exact path.
@@ -749,8 +751,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
 
         // ---- the exact path, rare: some row's tile mass exceeds MASS_LIMIT
-        // (a score more than RESCALE_SLACK log2 units above its base, the
-        // row's first visible tile, or a non-finite score).  The wave moves
+        // (a score about 15 log2 units above its base, the row's first
+        // visible tile, or a non-finite score).  The wave moves
         // each such row's base to the tile maximum, rescales O (which holds
         // tiles up to t - 1) and l, and forms tile t's probabilities again.
         if (__ballot(!(lt <= MASS_LIMIT)) != 0) {
