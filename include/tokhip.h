@@ -140,9 +140,8 @@ uint32_t tkh_attention_cached(tkh_context *ctx, const tkh_cached_shape *shape, t
  *  - status != NULL: a device word owned by the caller; the kernels OR their
  *    status bits into it and the call returns once the work is queued.  The
  *    word is never cleared here.  Nonzero means the results are invalid:
- *    bit 3 (8) a decode merge timed out (TKH_DEVICE), bit 4 (16) without
- *    bit 0 a bf16 V value beyond the chunk kernel's range (TKH_UNSUPPORTED),
- *    any other bit a non-finite input or result (TKH_NON_FINITE).
+ *    bit 3 (8) a decode merge timed out (TKH_DEVICE), any other bit a
+ *    non-finite input or result (TKH_NON_FINITE).
  *  - status == NULL: the call waits for the stream and reports as a
  *    synchronous context does.
  * Every call on one GPU shares that GPU's array and keeps its last contents:
