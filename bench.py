@@ -32,6 +32,10 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
+# Idle seconds before each workload after the first: the chip's clock depends on
+# the heat the previous workload left (configs[4]'s kernel measured 375 us right
+# after configs[2] and 349-352 us on its own), so each workload starts cool.
+SETTLE_S = 3.0
 
 
 def log(msg):
@@ -691,33 +695,48 @@ def main():
     run = lambda name: args.only in (None, name) and (args.only == name or not args.no_north_star
                                                       or name in ("c3", "c5"))
     result, states = {}, {}
+    started = [False]
+
+    def settle():
+        if started[0]:
+            torch.cuda.synchronize()
+            time.sleep(SETTLE_S)
+        started[0] = True
+
     if run("c3"):
+        settle()
         c3, states["c3"] = bench_decode_batch(torch, ops, ctx, args.steps, args.warmup, batch=64,
                                               lmin=512, lmax=8192, dtype=torch.float16)
         log("c3 (configs[2] batched decode): " + json.dumps(c3))
         result["c3"] = c3
     if run("c5"):
+        settle()
         c5, states["c5"] = bench_prefill_batch(torch, ops, ctx, 10, 2)
         log("c5 (configs[4] batched prefill): " + json.dumps(c5))
         result["c5"] = c5
     if run("c1"):
+        settle()
         c1 = bench_c1(torch, ops, sessmod, ctx, 10, 2)
         log("c1 (configs[0] FP32 session): " + json.dumps(c1))
         result["c1"] = c1
     if run("c2"):
+        settle()
         c2, _ = bench_c2(torch, ops, sessmod, ctx, 5, 1)
         log("c2 (configs[1] session job): " + json.dumps(c2))
         result["c2"] = c2
     if run("c4"):
+        settle()
         c4 = bench_c4(torch, ops, sessmod, ctx, 2, 1)
         log("c4 (configs[3] Gemma session): " + json.dumps(c4))
         result["c4"] = c4
     if run("d8k"):
+        settle()
         d8k, _ = bench_decode_batch(torch, ops, ctx, 50, 5, batch=1, lmin=8192, lmax=8192,
                                     dtype=torch.bfloat16)
         log("single-session decode at 8192: " + json.dumps(d8k))
         result["decode_8k"] = d8k
     if run("d8kb"):
+        settle()
         d8kb, _ = bench_decode_batch(torch, ops, ctx, 20, 3, batch=16, lmin=8192, lmax=8192,
                                      dtype=torch.bfloat16)
         log("sustained decode at 8192, 16 sessions: " + json.dumps(d8kb))
