@@ -583,6 +583,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // tile) that is never used.
     constexpr int NPV = 2 * MB;  // P.V MFMAs per tile
     static_assert(NPV == KS, "one V^T operand read per Q.K k-step");
+    // head_dim 256: the V^T operands of a tile are read just before its P.V
+    // MFMAs, VPF ahead, instead of a whole Q.K chain ahead: 16 operands held
+    // across an iteration (64 registers) made the compiler spill in the loop.
+    constexpr bool VLATE = D >= 256;
+    constexpr int VPF = 4;
+    auto vt_buf = [&](int tile_stage) { return lds + L::vt_base + (tile_stage % L::vt_bufs) * L::vt_bytes; };
+    auto vt_operand = [&](lds_ptr<uint8_t> buf, int k) {
+        return *(lds_ptr<u32x4>)(buf + vt_off[k / MB] + (k % MB) * 32 * L::vt_row);
+    };
     static_for<NS - 1>([&](auto stg) {
         if (decltype(stg)::value < ntiles) issue(stg, std::false_type{});
     });
@@ -590,6 +599,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     for (int i = 0; i < 16; ++i) st[i] = 0.0f;
     VTranspose<D, W, VCONV> vtr(threadIdx.x);
     if (ntiles > 0) {
+        if constexpr (VLATE) {
+            // Iteration 0's P.V reads the buffer of "tile -1" (stage NS - 1):
+            // zeros, which the zero probabilities of iteration 0 multiply.
+            lds_ptr<uint8_t> z = vt_buf(NS - 1);
+            for (int i = threadIdx.x; i < L::vt_bytes / 16; i += 64 * W)
+                *(lds_ptr<u32x4>)(z + 16 * i) = u32x4{0, 0, 0, 0};
+        }
         wait_tile(0);
         for (int ks = 0; ks < KS; ++ks)
             st = mfma32<DT>(*(lds_ptr<u32x4>)(lds + L::k_at(0) + k_off[ks]), qb[ks], st);
@@ -599,10 +615,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         // its step 2, which a single tile does not have.
         if (ntiles == 1) __syncthreads();
     }
-    u32x4 vop[2][MB];                  // V^T operands of the tile whose P.V is pending
+    // V^T operands of the tile whose P.V is pending (read ahead unless VLATE).
+    u32x4 vop[VLATE ? 1 : 2][VLATE ? 1 : MB];
     uint32_t ph[8];                    // its probabilities (f16 pairs)
-    for (int stp = 0; stp < 2; ++stp)
-        for (int mb = 0; mb < MB; ++mb) vop[stp][mb] = u32x4{0, 0, 0, 0};
+    for (int stp = 0; stp < (VLATE ? 1 : 2); ++stp)
+        for (int mb = 0; mb < (VLATE ? 1 : MB); ++mb) vop[stp][mb] = u32x4{0, 0, 0, 0};
     for (int i = 0; i < 8; ++i) {
         ph[i] = 0u;
     }
@@ -628,17 +645,26 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         // log2 units); p = 2^(t * tmul + nbase) against the row's current base,
         // with no tile maximum (the check after step 3 catches a base that is
         // too low).
-        float tv[CAP ? 16 : 1];  // softcapped scores (the raw scores serve otherwise)
         float nbase = nbase_run;
         float shift = 0.0f;      // subtracted from st in raw units (huge rows)
         float lt = 0.0f;         // this lane's mass of the tile
         uint32_t nh[4];
+        u32x4 vq[VLATE ? VPF : 1];
+        lds_ptr<uint8_t> vtp = vt_buf((STG + NS - 1) % NS);  // tile t - 1's V^T
+        if constexpr (VLATE)
+            for (int i = 0; i < VPF; ++i) vq[i] = vt_operand(vtp, i);
 #pragma unroll
         for (int k = 0; k < NPV; ++k) {
             {
                 const int stp = k / MB, mb = k % MB;
                 const u32x4 bv = u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
-                acc[mb] = mfma32<PDT>(vop[stp][mb], bv, acc[mb]);
+                if constexpr (VLATE) {
+                    const u32x4 a = vq[k % VPF];
+                    if (k + VPF < NPV) vq[k % VPF] = vt_operand(vtp, k + VPF);
+                    acc[mb] = mfma32<PDT>(a, bv, acc[mb]);
+                } else {
+                    acc[mb] = mfma32<PDT>(vop[stp][mb], bv, acc[mb]);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
             if (k == 0) {
@@ -646,8 +672,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                     float a = amax_run;
                     for (int i = 0; i < 16; ++i) a = maxn(a, __builtin_fabsf(st[i]));
                     amax_run = a;
+                    // With the softcap the capped scores (log2 units) replace
+                    // the raw ones in place, which keeps 16 registers free.
                     if constexpr (CAP)
-                        for (int i = 0; i < 16; ++i) tv[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
+                        for (int i = 0; i < 16; ++i) st[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
                 } else {
                     // Visible keys of this row inside the tile: [lo_rel, hi_rel).
                     const int lo_rel = min(max(rlo0 - t * PF_KT, 0), PF_KT);
@@ -656,8 +684,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                         const int kk = 8 * (i >> 2) + 4 * h + (i & 3);
                         const bool vis = kk >= lo_rel && kk < hi_rel;
                         bad |= vis && !(__builtin_fabsf(st[i]) < -NEG_INF);
-                        if constexpr (CAP) tv[i] = vis ? softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E : NEG_INF;
-                        st[i] = vis ? st[i] : NEG_INF;  // masked in place: no copy of the scores
+                        // masked (and capped) in place: no copy of the scores
+                        if constexpr (CAP) st[i] = vis ? softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E : NEG_INF;
+                        else st[i] = vis ? st[i] : NEG_INF;
                     }
                 }
             }
@@ -675,8 +704,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             // First half of tile t's probabilities (tile t - 1's are still being read).
             for (int i = 0; i < 4; ++i) {
                 if (k == (NPV > 2 ? 2 + (i * (NPV - 2)) / 4 : NPV - 1)) {
-                    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
-                    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
+                    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i], tmul, nbase));
+                    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i + 1], tmul, nbase));
                     nh[i] = pack2<PDT>(e0, e1);
                     lt = add_pair(nh[i], lt);
                     // Pin the pair here: the compiler would otherwise sink it to
@@ -726,7 +755,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             // chain ahead of their use.  B slots 8h..8h+7 of step stp are keys
             // {16 stp + 4h + 0..3, 16 stp + 8 + 4h + 0..3}, the order in which
             // the transposed tile stores them.  (2 MB == KS.)
-            vop[ks / MB][ks % MB] = *(lds_ptr<u32x4>)(vt + vt_off[ks / MB] + (ks % MB) * 32 * L::vt_row);
+            if constexpr (!VLATE) vop[ks / MB][ks % MB] = vt_operand(vt, ks);
             // The two waves of a SIMD leave the step-2 barrier together and
             // would contend for the matrix core and the vector unit in
             // lockstep.  A raised priority over the first half of the Q.K
@@ -741,8 +770,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             if (ks == 0 && conv_next) vtr.read(vn);
             if (ks == KS / 2 && conv_next) vtr.write(vtn);
             for (int i = 4 + 4 * ks / KS; i < 4 + 4 * (ks + 1) / KS; ++i) {
-                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nbase));
-                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nbase));
+                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i], tmul, nbase));
+                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i + 1], tmul, nbase));
                 ph[i] = pack2<PDT>(e0, e1);
                 lt = add_pair(ph[i], lt);
                 asm volatile("" : "+v"(ph[i]), "+v"(lt));
@@ -756,8 +785,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         // each such row's base to the tile maximum, rescales O (which holds
         // tiles up to t - 1) and l, and forms tile t's probabilities again.
         if (__ballot(!(lt <= MASS_LIMIT)) != 0) {
-            float hi = CAP ? tv[0] : st[0];
-            for (int i = 1; i < 16; ++i) hi = maxn(hi, CAP ? tv[i % (CAP ? 16 : 1)] : st[i]);
+            float hi = st[0];
+            for (int i = 1; i < 16; ++i) hi = maxn(hi, st[i]);
             {
                 const uint32_t u = __builtin_bit_cast(uint32_t, hi);
                 const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
@@ -790,8 +819,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                     y0 = (st[2 * i] - delta) * tmul;
                     y1 = (st[2 * i + 1] - delta) * tmul;
                 } else {
-                    y0 = __builtin_fmaf(CAP ? tv[(2 * i) % (CAP ? 16 : 1)] : st[2 * i], tmul, nb);
-                    y1 = __builtin_fmaf(CAP ? tv[(2 * i + 1) % (CAP ? 16 : 1)] : st[2 * i + 1], tmul, nb);
+                    y0 = __builtin_fmaf(st[2 * i], tmul, nb);
+                    y1 = __builtin_fmaf(st[2 * i + 1], tmul, nb);
                 }
                 ph[i] = pack2<PDT>(__builtin_amdgcn_exp2f(y0), __builtin_amdgcn_exp2f(y1));
                 lt = add_pair(ph[i], lt);
@@ -820,11 +849,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
     // P.V of the last tile.
     if (ntiles > 0) {
+        lds_ptr<uint8_t> vtl = vt_buf((ntiles - 1) % NS);
 #pragma unroll
         for (int k = 0; k < NPV; ++k) {
             const int stp = k / MB, mb = k % MB;
             const u32x4 bv = u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
-            acc[mb] = mfma32<PDT>(vop[stp][mb], bv, acc[mb]);
+            if constexpr (VLATE) acc[mb] = mfma32<PDT>(vt_operand(vtl, k), bv, acc[mb]);
+            else acc[mb] = mfma32<PDT>(vop[stp][mb], bv, acc[mb]);
         }
     }
     bad |= !(amax_run < -NEG_INF);
