@@ -79,7 +79,12 @@ template <> __device__ __forceinline__ void store_out<BF16>(void *base, int64_t 
 
 }  // namespace
 
-template <int DT>
+// TABLE: (cos, sin) come from p.rope.  Without it the kernel carries the FP64
+// pow/sin/cos of rotary_cos_sin, which takes its register count to 129: three
+// waves per SIMD instead of four, so a session chunk's 4096 waves
+// needed a second round (launch span 6.7 us, the last waves starting 3.9 us
+// late).  Sessions always pass the table.
+template <int DT, bool TABLE>
 __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
 #pragma clang fp contract(off)
     __shared__ float row[512];
@@ -113,7 +118,7 @@ __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
         cv[k] = 1.0f;
         sv[k] = 0.0f;
         if (j < half && j < pairs) {
-            if (p.rope) {
+            if constexpr (TABLE) {
                 const float *cs = p.rope + 2 * ((p.position + t - p.rope_pos0) * pairs + j);
                 cv[k] = cs[0];
                 sv[k] = cs[1];
@@ -210,9 +215,18 @@ extern "C" hipError_t tkh_launch_produce(const tkh::ProduceParams *p, int dtype,
     const int64_t blocks = p->tokens * (p->hq + 2 * p->hkv);
     if (blocks <= 0 || p->d > 512 || p->d % 2) return hipErrorInvalidValue;
     dim3 grid((unsigned)blocks), block(64);
-    if (dtype == F32) hipLaunchKernelGGL((produce_qkv<F32>), grid, block, 0, stream, *p);
-    else if (dtype == F16) hipLaunchKernelGGL((produce_qkv<F16>), grid, block, 0, stream, *p);
-    else if (dtype == BF16) hipLaunchKernelGGL((produce_qkv<BF16>), grid, block, 0, stream, *p);
-    else return hipErrorInvalidValue;
+    const bool table = p->rope != nullptr;
+    if (dtype == F32) {
+        if (table) hipLaunchKernelGGL((produce_qkv<F32, true>), grid, block, 0, stream, *p);
+        else hipLaunchKernelGGL((produce_qkv<F32, false>), grid, block, 0, stream, *p);
+    } else if (dtype == F16) {
+        if (table) hipLaunchKernelGGL((produce_qkv<F16, true>), grid, block, 0, stream, *p);
+        else hipLaunchKernelGGL((produce_qkv<F16, false>), grid, block, 0, stream, *p);
+    } else if (dtype == BF16) {
+        if (table) hipLaunchKernelGGL((produce_qkv<BF16, true>), grid, block, 0, stream, *p);
+        else hipLaunchKernelGGL((produce_qkv<BF16, false>), grid, block, 0, stream, *p);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
