@@ -31,12 +31,6 @@ extern "C" hipError_t tkh_launch_kv_append(int src, int dst, const void *k, cons
                                            void *kc, void *vc, int64_t tokens, int heads,
                                            int dims, int64_t capacity, int64_t offset,
                                            uint32_t *status, hipStream_t stream);
-extern "C" hipError_t tkh_launch_copy_runs(const void *src_k, const void *src_v, void *dst_k,
-                                           void *dst_v, int64_t tokens, int heads,
-                                           int64_t row_bytes, int64_t capacity,
-                                           const int64_t runs[6], const uint32_t *gate,
-                                           uint64_t *committed, uint64_t committed_value,
-                                           hipStream_t stream);
 extern "C" hipError_t tkh_launch_check_finite(int dtype, const void *a, const void *b, int64_t n,
                                               uint32_t *status, hipStream_t stream);
 extern "C" hipError_t tkh_launch_softcap(float *x, int64_t n, float cap, uint32_t *status,

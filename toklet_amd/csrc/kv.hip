@@ -4,9 +4,10 @@
 //    head-major cache rows [offset, offset+tokens) in the storage dtype,
 //    rounding to nearest even and flagging non-finite input
 //    (LayerKv::append, src/model/cache.rs:64-85).
-//  * kv_copy_runs: the ring commit of WindowKvCache::commit_validated
-//    (src/model/window_cache.rs:298-321): up to two contiguous row runs per
-//    head from the staged chunk [heads, tokens, D] into ring slots.
+//  * kv_copy_batch: the ring commits of WindowKvCache::commit_validated
+//    (src/model/window_cache.rs:298-321), every sliding layer of a chunk in
+//    one launch: up to two contiguous row runs per head from the staged
+//    chunk [heads, tokens, D] into ring slots.
 //  * check_finite: finiteness scan of a staged chunk (the device half of
 //    WindowKvCache::prepare's finite() checks, src/model/window_cache.rs:193-212).
 //  * logit_softcap: cap * tanh(x / cap) in FP64, rounded once to FP32
@@ -55,61 +56,61 @@ __global__ __launch_bounds__(256) void kv_append(const void *k, const void *v, v
     flag(status, bad, ST_NONFINITE_INPUT);
 }
 
-// Element-size generic row copy: runs[r] = {source_row, slot, rows}.
-__global__ __launch_bounds__(256) void kv_copy_runs(const uint8_t *src_k, const uint8_t *src_v,
-                                                    uint8_t *dst_k, uint8_t *dst_v,
-                                                    int64_t tokens, int32_t heads,
-                                                    int64_t row_bytes, int64_t capacity,
-                                                    int64_t r0_src, int64_t r0_slot,
-                                                    int64_t r0_rows, int64_t r1_src,
-                                                    int64_t r1_slot, int64_t r1_rows,
-                                                    const uint32_t *gate, uint64_t *committed,
-                                                    uint64_t committed_value) {
-    // Gated commit (queued sessions): nothing is copied once the status word
-    // reports a failure in this or an earlier chunk; otherwise the session's
-    // device-side committed length moves to the end of this chunk.
-    if (gate && *(volatile const uint32_t *)gate != 0) return;
-    if (committed && blockIdx.x == 0 && threadIdx.x == 0) *committed = committed_value;
-    const int64_t words = row_bytes / 2;  // rows are whole 2-byte units
-    const int64_t rows = r0_rows + r1_rows;
-    const int64_t total = (int64_t)heads * rows * words;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        int64_t w = i % words;
-        int64_t r = (i / words) % rows;
-        int64_t h = i / (words * rows);
-        int64_t srow = r < r0_rows ? r0_src + r : r1_src + (r - r0_rows);
-        int64_t slot = r < r0_rows ? r0_slot + r : r1_slot + (r - r0_rows);
-        int64_t s = ((h * tokens + srow) * row_bytes) / 2 + w;
-        int64_t d = ((h * capacity + slot) * row_bytes) / 2 + w;
-        reinterpret_cast<uint16_t *>(dst_k)[d] = reinterpret_cast<const uint16_t *>(src_k)[s];
-        reinterpret_cast<uint16_t *>(dst_v)[d] = reinterpret_cast<const uint16_t *>(src_v)[s];
-    }
-}
+// The ring commits of one chunk in one launch, WindowKvCache::commit_validated
+// (src/model/window_cache.rs:298-321) for every sliding layer: blockIdx.y is
+// the entry, whose staged rows [heads, tokens, row] go to up to two runs of
+// ring slots, runs {source row, slot, rows}.  A thread copies one UNIT-byte
+// piece of a row (16 when every row is whole 16-byte pieces, else 2), with
+// 32-bit index arithmetic when the pieces fit.  Gated commit (queued
+// sessions): the status word is read together with the rows, and nothing is
+// stored when it reports a failure in this or an earlier chunk, so either
+// every entry is copied or none is; otherwise the session's device-side
+// committed length moves to the end of this chunk.  (The first form copied
+// 2-byte elements with 64-bit divisions per element and read the gate before
+// the rows: 4.1 us per commit at configs[3].)
+template <int UNIT> struct Piece;
+template <> struct Piece<16> { using T = u32x4; };
+template <> struct Piece<2> { using T = uint16_t; };
 
-// kv_copy_runs for several rings at once: blockIdx.y is the entry.  The gate
-// is read once per workgroup before any copy, so either every entry is
-// copied or none is, as with one launch per ring in a row.
+template <int UNIT>
 __global__ __launch_bounds__(256) void kv_copy_batch(CopyBatch b) {
-    if (b.gate && *(volatile const uint32_t *)b.gate != 0) return;
-    if (b.committed && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
-        *b.committed = b.committed_value;
-    const CopyRunsEntry &e = b.e[blockIdx.y];
-    const int64_t words = e.row_bytes / 2;
+    using T = typename Piece<UNIT>::T;
+    // Written by earlier launches on the stream (visible at this launch's
+    // start): a plain load, which the compiler waits for only at the stores.
+    const uint32_t g = b.gate ? *b.gate : 0u;
+    const CopyRunsEntry e = b.e[blockIdx.y];  // by value: its fields in one batch of scalar loads
+    const int64_t per_row = e.row_bytes / UNIT;
     const int64_t r0_rows = e.runs[2], rows = e.runs[2] + e.runs[5];
-    const int64_t total = (int64_t)e.heads * rows * words;
+    const int64_t total = (int64_t)e.heads * rows * per_row;
+    const bool narrow = total <= 0x7fffffff;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t w = i % words;
-        const int64_t r = (i / words) % rows;
-        const int64_t h = i / (words * rows);
+        int64_t c, r, h;
+        if (narrow) {
+            const uint32_t i32 = (uint32_t)i, pr = (uint32_t)per_row, rs = (uint32_t)rows;
+            const uint32_t row = i32 / pr;
+            c = i32 - row * pr;
+            h = row / rs;
+            r = row - (uint32_t)h * rs;
+        } else {
+            const int64_t row = i / per_row;
+            c = i - row * per_row;
+            h = row / rows;
+            r = row - h * rows;
+        }
         const int64_t srow = r < r0_rows ? e.runs[0] + r : e.runs[3] + (r - r0_rows);
         const int64_t slot = r < r0_rows ? e.runs[1] + r : e.runs[4] + (r - r0_rows);
-        const int64_t sidx = ((h * e.tokens + srow) * e.row_bytes) / 2 + w;
-        const int64_t didx = ((h * e.capacity + slot) * e.row_bytes) / 2 + w;
-        reinterpret_cast<uint16_t *>(e.dst_k)[didx] = reinterpret_cast<const uint16_t *>(e.src_k)[sidx];
-        reinterpret_cast<uint16_t *>(e.dst_v)[didx] = reinterpret_cast<const uint16_t *>(e.src_v)[sidx];
+        const int64_t s = (h * e.tokens + srow) * per_row + c;
+        const int64_t d = (h * e.capacity + slot) * per_row + c;
+        const T kx = reinterpret_cast<const T *>(e.src_k)[s];
+        const T vx = reinterpret_cast<const T *>(e.src_v)[s];
+        if (g == 0) {
+            reinterpret_cast<T *>(e.dst_k)[d] = kx;
+            reinterpret_cast<T *>(e.dst_v)[d] = vx;
+        }
     }
+    if (b.committed && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && g == 0)
+        *b.committed = b.committed_value;
 }
 
 template <int DT>
@@ -181,32 +182,26 @@ extern "C" hipError_t tkh_launch_kv_append(int src, int dst, const void *k, cons
     return hipErrorInvalidValue;
 }
 
-extern "C" hipError_t tkh_launch_copy_runs(const void *src_k, const void *src_v, void *dst_k,
-                                           void *dst_v, int64_t tokens, int heads,
-                                           int64_t row_bytes, int64_t capacity,
-                                           const int64_t runs[6], const uint32_t *gate,
-                                           uint64_t *committed, uint64_t committed_value,
-                                           hipStream_t stream) {
-    const int64_t rows = runs[2] + runs[5];
-    if (rows == 0 && !committed) return hipSuccess;
-    dim3 grid(rows ? grid_for(heads * rows * (row_bytes / 2)) : 1), block(256);
-    hipLaunchKernelGGL(kv_copy_runs, grid, block, 0, stream, (const uint8_t *)src_k,
-                       (const uint8_t *)src_v, (uint8_t *)dst_k, (uint8_t *)dst_v, tokens, heads,
-                       row_bytes, capacity, runs[0], runs[1], runs[2], runs[3], runs[4], runs[5],
-                       gate, committed, committed_value);
-    return hipGetLastError();
-}
-
 extern "C" hipError_t tkh_launch_copy_batch(const tkh::CopyBatch *b, hipStream_t stream) {
     using namespace tkh;
     if (b->count < 1 || b->count > COPY_BATCH_MAX) return hipErrorInvalidValue;
+    // 16-byte pieces when every row and base allows them.
+    bool vec = true;
+    for (int i = 0; i < b->count; ++i) {
+        const auto &e = b->e[i];
+        const uintptr_t bases = (uintptr_t)e.src_k | (uintptr_t)e.src_v | (uintptr_t)e.dst_k |
+                                (uintptr_t)e.dst_v;
+        vec = vec && e.row_bytes % 16 == 0 && bases % 16 == 0;
+    }
+    const int64_t unit = vec ? 16 : 2;
     int64_t most = 1;
     for (int i = 0; i < b->count; ++i) {
         const auto &e = b->e[i];
-        most = std::max<int64_t>(most, (int64_t)e.heads * (e.runs[2] + e.runs[5]) * (e.row_bytes / 2));
+        most = std::max<int64_t>(most, (int64_t)e.heads * (e.runs[2] + e.runs[5]) * (e.row_bytes / unit));
     }
     dim3 grid(grid_for(most), (unsigned)b->count), block(256);
-    hipLaunchKernelGGL(kv_copy_batch, grid, block, 0, stream, *b);
+    if (vec) hipLaunchKernelGGL(kv_copy_batch<16>, grid, block, 0, stream, *b);
+    else hipLaunchKernelGGL(kv_copy_batch<2>, grid, block, 0, stream, *b);
     return hipGetLastError();
 }
 
