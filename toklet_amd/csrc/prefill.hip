@@ -830,16 +830,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 
         __builtin_amdgcn_sched_barrier(0);
     };
-    for (bool go = true; go;) {
+    while (t < ntiles) {
         // A round of NS steady-state iterations when all of them qualify
-        // (t is a multiple of NS here, so stage K is tile t + K's).
+        // (t is a multiple of NS here, so stage K is tile t + K's).  Once t
+        // reaches ntiles the remaining iterations of the round do nothing.
         bulk = t >= tf_lo && t + NS <= tf_hi && t + 2 * NS - 1 < ntiles && t_next == t + NS - 1;
         static_for<NS>([&](auto k) {
             constexpr int K = decltype(k)::value;
-            if (!go || t >= ntiles) {
-                go = false;
-                return;
-            }
+            if (t >= ntiles) return;
             if constexpr (K % 2 == 0) body(std::integral_constant<int, K>{}, st, st_b);
             else body(std::integral_constant<int, K>{}, st_b, st);
             ++t;
