@@ -471,6 +471,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         tf_lo = uniform32((int)(lo_t < ntiles ? lo_t : ntiles));
         tf_hi = uniform32((int)hi_t);
     }
+    // Fully visible tiles as a width, for one unsigned test per tile (none
+    // when hi < lo, which happens for waves that see no whole tile).
+    const unsigned tf_n = tf_hi > tf_lo ? (unsigned)(tf_hi - tf_lo) : 0u;
     // This row's visible keys relative to k_lo.
     int rlo0, rhi0;
     {
@@ -668,7 +671,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             }
             __builtin_amdgcn_sched_barrier(0);
             if (k == 0) {
-                if (bulk || (t >= tf_lo && t < tf_hi)) {
+                if (bulk || (unsigned)(t - tf_lo) < tf_n) {  // t in [tf_lo, tf_hi)
                     float a = amax_run;
                     for (int i = 0; i < 16; ++i) a = maxn(a, __builtin_fabsf(st[i]));
                     amax_run = a;
@@ -741,9 +744,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int i = 0; i < 16; ++i) st_next[i] = 0.0f;
         u32x4 kq[KPRE];
         for (int i = 0; i < KPRE && i < KS; ++i) kq[i] = *(lds_ptr<u32x4>)(kn + k_off[i]);
-        // bf16: tile t + 1's V, resident since step 2, converted between these
-        // MFMAs; the barrier of the next step 2 precedes its V^T reads.
-        const bool conv_next = bulk || t + 1 < ntiles;
+        // Tile t + 1's V, resident since step 2, transposed (bf16: converted)
+        // between these MFMAs; the barrier of the next step 2 precedes its V^T
+        // reads.  After the last tile this transposes a stale stage into a
+        // buffer nobody reads again (the buffers of tiles t and t - 1 differ
+        // from it, and every read of its previous tile preceded this
+        // iteration's step-2 barrier), which costs less than the branch.
         lds_ptr<uint8_t> vn = lds + L::v_at(STG_NEXT);
         lds_ptr<uint8_t> vtn = lds + L::vt_base + (STG_NEXT % L::vt_bufs) * L::vt_bytes;
 #pragma unroll
@@ -767,8 +773,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             if (ks == 0) __builtin_amdgcn_s_setprio(1);
             if (ks == KS / 2) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
-            if (ks == 0 && conv_next) vtr.read(vn);
-            if (ks == KS / 2 && conv_next) vtr.write(vtn);
+            if (ks == 0) vtr.read(vn);
+            if (ks == KS / 2) vtr.write(vtn);
             for (int i = 4 + 4 * ks / KS; i < 4 + 4 * (ks + 1) / KS; ++i) {
                 const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i], tmul, nbase));
                 const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i + 1], tmul, nbase));
