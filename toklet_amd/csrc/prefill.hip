@@ -327,7 +327,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     constexpr int KS = D / 16;        // QK k-steps (16 features each)
     constexpr int MB = D / 32;        // PV M-blocks (32 features each)
     constexpr int PDT = F16;          // P and V^T operand type of the P.V MFMAs
-    constexpr bool VCONV = DT == BF16;  // V tiles converted to scaled f16 in LDS
+    constexpr bool VCONV = DT == BF16;  // V tiles converted to f16 in LDS
     static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
     using L = PrefillLds<D, W>;
     constexpr int NS = L::stages;
