@@ -100,6 +100,17 @@ __device__ __forceinline__ float add_pair(uint32_t w, float l) {
 // which fmaxf/fminf chains need, and no hazard padding, which the same chains
 // written as inline assembly get.
 __device__ __forceinline__ float maxn(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// tanh(y) = sign(y) (1 - 2 / (e^(2|y|) + 1)) in six vector instructions.  Its
+// absolute error stays below about 2e-7 (for small |y| the subtraction
+// cancels, but only absolute error reaches the softmax: the capped score is
+// t * cap in natural units, an exponent).  NaN propagates; |y| large gives
+// e = inf and exactly +-1.
+__device__ __forceinline__ float tanh_fast(float y) {
+    const float e = __builtin_amdgcn_exp2f(2.0f * LOG2E * __builtin_fabsf(y));
+    const float t = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+    return __builtin_copysignf(t, y);
+}
 __device__ __forceinline__ float minn(float a, float b) { return __builtin_elementwise_minimum(a, b); }
 
 __device__ __forceinline__ u32x2 read_tr(lds_ptr<uint8_t> p) {
@@ -508,8 +519,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // themselves).
     float amax_run = 0.0f;
     bool bad = false;  // a non-finite visible score
-    const float scale = p.scale, softcap = p.softcap, softcap_inv = p.softcap_inv;
-    const float tmul = CAP ? 1.0f : p.scale_log2;  // t units -> log2 units
+    // With the softcap a score is kept as t = tanh(raw * scale / cap), whose
+    // log2-unit value is t * cap * log2(e): the cap's factor rides on the
+    // exp's multiplier instead of a multiply per score.
+    const float ycap = p.scale * p.softcap_inv;
+    const float tmul = CAP ? p.softcap * LOG2E : p.scale_log2;  // t units -> log2 units
     // A row maximum of 2^10 or more in log2 units (natural-log logits above
     // about 700) makes the rounding of m * tmul worth a large part of an
     // exponent, so 2^(t * tmul - round(m * tmul)) would lose the mass.  A wave
@@ -644,8 +658,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         lds_ptr<uint8_t> vt = lds + L::vt_base + (STG % L::vt_bufs) * L::vt_bytes;
         lds_ptr<uint8_t> kn = lds + L::k_at(STG_NEXT);
 
-        // ---- step 1.  t = raw dot (or, with the softcap, the capped score in
-        // log2 units); p = 2^(t * tmul + nbase) against the row's current base,
+        // ---- step 1.  t = raw dot (or, with the softcap, tanh(raw * scale /
+        // cap)); p = 2^(t * tmul + nbase) against the row's current base,
         // with no tile maximum (the check after step 3 catches a base that is
         // too low).
         float nbase = nbase_run;
@@ -675,10 +689,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                     float a = amax_run;
                     for (int i = 0; i < 16; ++i) a = maxn(a, __builtin_fabsf(st[i]));
                     amax_run = a;
-                    // With the softcap the capped scores (log2 units) replace
-                    // the raw ones in place, which keeps 16 registers free.
+                    // With the softcap the tanh values replace the raw scores
+                    // in place, which keeps 16 registers free.
                     if constexpr (CAP)
-                        for (int i = 0; i < 16; ++i) st[i] = softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E;
+                        for (int i = 0; i < 16; ++i) st[i] = tanh_fast(st[i] * ycap);
                 } else {
                     // Visible keys of this row inside the tile: [lo_rel, hi_rel).
                     const int lo_rel = min(max(rlo0 - t * PF_KT, 0), PF_KT);
@@ -688,7 +702,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                         const bool vis = kk >= lo_rel && kk < hi_rel;
                         bad |= vis && !(__builtin_fabsf(st[i]) < -NEG_INF);
                         // masked (and capped) in place: no copy of the scores
-                        if constexpr (CAP) st[i] = vis ? softcap_fast(st[i] * scale, softcap, softcap_inv) * LOG2E : NEG_INF;
+                        if constexpr (CAP) st[i] = vis ? tanh_fast(st[i] * ycap) : NEG_INF;
                         else st[i] = vis ? st[i] : NEG_INF;
                     }
                 }
@@ -925,7 +939,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
                         d = __builtin_bit_cast(float, a0) + __builtin_bit_cast(float, a1);
                     }
                     float y;
-                    if constexpr (CAP) y = softcap_fast(d * scale, softcap, softcap_inv) * LOG2E - m_run;
+                    if constexpr (CAP) y = (tanh_fast(d * ycap) - m_run) * tmul;
                     else y = (d - m_run) * tmul;
                     const bool vis = any && kk >= rlo0 && kk < rhi0;
                     const float pk = vis ? __builtin_amdgcn_exp2f(y) : 0.0f;
@@ -1051,7 +1065,7 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t bloc
     for (int sp = 0; sp < MAXS; ++sp)
         if (sp < S) M = fmaxf(M, ml[sp][0]);
     const float mbase = M == NEG_INF ? 0.0f : M;
-    const float tmul = p.softcap != 0.0f ? 1.0f : p.scale_log2;
+    const float tmul = p.softcap != 0.0f ? p.softcap * LOG2E : p.scale_log2;  // the chunk kernel's units
     float L = 0.0f;
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
