@@ -241,6 +241,8 @@ tkh::Params base_params(tkh_context *ctx, const Plan &plan) {
     prm.scale_log2 = plan.scale * 1.4426950408889634f;
     prm.softcap = plan.softcap;
     prm.softcap_inv = plan.softcap != 0.0f ? 1.0f / plan.softcap : 0.0f;
+    prm.softcap_y = prm.scale * prm.softcap_inv;
+    prm.softcap_log2 = plan.softcap * 1.4426950408889634f;
     prm.status = ctx->status_dev;
     return prm;
 }
@@ -686,6 +688,8 @@ uint32_t launch_group(tkh_context *ctx, const Plan &plan, Problems group,
     prm.scale_log2 = plan.scale * 1.4426950408889634f;
     prm.softcap = plan.softcap;
     prm.softcap_inv = plan.softcap != 0.0f ? 1.0f / plan.softcap : 0.0f;
+    prm.softcap_y = prm.scale * prm.softcap_inv;
+    prm.softcap_log2 = plan.softcap * 1.4426950408889634f;
     prm.total_tiles = tiles;
     prm.part_ml = reinterpret_cast<float *>(ctx->workspace);
     prm.part_o = reinterpret_cast<float *>(ctx->workspace) + 2 * part_rows;

@@ -394,8 +394,9 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     int bcount = batch->count;
     int G = args->group, Hq = args->query_heads, has_window = args->has_window;
     int64_t window = args->window;
-    float scale_log2 = args->scale_log2, scale = args->scale;
-    float softcap = args->softcap, softcap_inv = args->softcap_inv;
+    float scale_log2 = args->scale_log2;
+    // Capped score in log2 units: tanh(raw * scale / cap) * cap * log2(e).
+    float ycap = args->softcap_y, caplog2 = args->softcap_log2;
     int stream_nt = args->stream_nt;
     FusedDecode fz{};
     if constexpr (FUSED) {
@@ -424,9 +425,8 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
     pin_scalar(has_window);
     pin_scalar(window);
     pin_scalar(scale_log2);
-    pin_scalar(scale);
-    pin_scalar(softcap);
-    pin_scalar(softcap_inv);
+    pin_scalar(ycap);
+    pin_scalar(caplog2);
     pin_scalar(stream_nt);
     if constexpr (FUSED) {
         pin_scalar(fz.q_proj);
@@ -618,7 +618,7 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
                 for (int c = 0; c < CPL; ++c) dot = chunk_dot<DT>(kb[u][c], q[r][c], dot);
                 dot = dpp_sum8(dot);
                 float x;
-                if constexpr (CAP) x = softcap_fast(dot * scale, softcap, softcap_inv) * LOG2E;
+                if constexpr (CAP) x = tanh_fast(dot * ycap) * caplog2;
                 else x = dot * scale_log2;
                 const bool vis = rel >= rlo[r] && rel < rhi[r];
                 bad |= vis && !is_finite_f(x);

@@ -137,6 +137,8 @@ struct Params {
     float scale;
     float softcap;          // 0 disables cap*tanh(score/cap)
     float softcap_inv;      // 1 / softcap (0 when disabled)
+    float softcap_y;        // scale / softcap: raw dot -> tanh argument (0 when disabled)
+    float softcap_log2;     // softcap * log2(e): tanh units -> log2 units
     int64_t total_tiles;
     // split-K partials
     float *part_o;          // per slot: [rows, D] (generic kernel), [D, rows] (chunk kernel)
@@ -438,17 +440,15 @@ __device__ __forceinline__ float softcap_f(float x, float cap) {
     return cap * t;
 }
 
-// The same without divisions or branches, for the kernels' inner loops:
-// y = x * (1 / cap), tanh by the odd series below |y| = 1/16 and by
-// 1 - 2 / (e^{2|y|} + 1) (hardware reciprocal) above.
-__device__ __forceinline__ float softcap_fast(float x, float cap, float inv_cap) {
-    const float y = x * inv_cap;
-    const float a = fabsf(y);
-    const float y2 = y * y;
-    const float series = y * (1.0f + y2 * (-1.0f / 3.0f + y2 * (2.0f / 15.0f + y2 * (-17.0f / 315.0f))));
-    const float e = __builtin_amdgcn_exp2f(fminf(2.0f * LOG2E * a, 126.0f));
-    const float t = copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f), y);
-    return cap * (a < 0.0625f ? series : t);
+// tanh(y) = sign(y) (1 - 2 / (e^(2|y|) + 1)) in six vector instructions, for
+// the kernels' inner loops (no division, no branch).  Its absolute error stays
+// below about 2e-7 (for small |y| the subtraction cancels, but only absolute
+// error reaches the softmax: the capped score is t * cap in natural units, an
+// exponent).  NaN propagates; |y| large gives e = inf and exactly +-1.
+__device__ __forceinline__ float tanh_fast(float y) {
+    const float e = __builtin_amdgcn_exp2f(2.0f * LOG2E * __builtin_fabsf(y));
+    const float t = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+    return __builtin_copysignf(t, y);
 }
 
 // Visible key range [lo, hi) (logical indices) of a query at absolute `pos`.

@@ -100,17 +100,6 @@ __device__ __forceinline__ float add_pair(uint32_t w, float l) {
 // which fmaxf/fminf chains need, and no hazard padding, which the same chains
 // written as inline assembly get.
 __device__ __forceinline__ float maxn(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-
-// tanh(y) = sign(y) (1 - 2 / (e^(2|y|) + 1)) in six vector instructions.  Its
-// absolute error stays below about 2e-7 (for small |y| the subtraction
-// cancels, but only absolute error reaches the softmax: the capped score is
-// t * cap in natural units, an exponent).  NaN propagates; |y| large gives
-// e = inf and exactly +-1.
-__device__ __forceinline__ float tanh_fast(float y) {
-    const float e = __builtin_amdgcn_exp2f(2.0f * LOG2E * __builtin_fabsf(y));
-    const float t = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
-    return __builtin_copysignf(t, y);
-}
 __device__ __forceinline__ float minn(float a, float b) { return __builtin_elementwise_minimum(a, b); }
 
 __device__ __forceinline__ u32x2 read_tr(lds_ptr<uint8_t> p) {
@@ -522,8 +511,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // With the softcap a score is kept as t = tanh(raw * scale / cap), whose
     // log2-unit value is t * cap * log2(e): the cap's factor rides on the
     // exp's multiplier instead of a multiply per score.
-    const float ycap = p.scale * p.softcap_inv;
-    const float tmul = CAP ? p.softcap * LOG2E : p.scale_log2;  // t units -> log2 units
+    const float ycap = p.softcap_y;
+    const float tmul = CAP ? p.softcap_log2 : p.scale_log2;  // t units -> log2 units
     // A row maximum of 2^10 or more in log2 units (natural-log logits above
     // about 700) makes the rounding of m * tmul worth a large part of an
     // exponent, so 2^(t * tmul - round(m * tmul)) would lose the mass.  A wave
@@ -1065,7 +1054,7 @@ __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t bloc
     for (int sp = 0; sp < MAXS; ++sp)
         if (sp < S) M = fmaxf(M, ml[sp][0]);
     const float mbase = M == NEG_INF ? 0.0f : M;
-    const float tmul = p.softcap != 0.0f ? p.softcap * LOG2E : p.scale_log2;  // the chunk kernel's units
+    const float tmul = p.softcap != 0.0f ? p.softcap_log2 : p.scale_log2;  // the chunk kernel's units
     float L = 0.0f;
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
