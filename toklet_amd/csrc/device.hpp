@@ -285,6 +285,41 @@ __device__ __forceinline__ int find_problem_wave(const Problem *problems, int n,
 // the copy inside the kernel arguments (Params must be the kernel's first
 // argument) or an entry of the uploaded descriptor array.  Its fields are
 // uniform and load through the scalar cache.  Call with the whole wave active.
+// Bring the first NL 64-byte lines of the kernel arguments, and the line at
+// byte EXTRA (the hidden arguments after them: the grid size), into the
+// scalar cache at once: one scalar load per line, all in flight together,
+// then one wait.  A kernel's descriptor fields are read by chains of
+// dependent scalar loads (a count decides which fields come next, a field
+// indexes the next one), each of which would otherwise miss the cache on its
+// own line in turn; after this they hit.  The loaded words are discarded.
+template <int NL, int EXTRA> __device__ __forceinline__ void warm_kernarg() {
+    static_assert(NL >= 1 && NL <= 11, "kernel-argument lines");
+    static_assert(EXTRA >= 0 && EXTRA % 4 == 0, "a dword offset");
+    const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+    constexpr int L = 64;
+    uint32_t d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11;
+    asm volatile(
+        "s_load_dword %0, %12, %13\n\t"
+        "s_load_dword %1, %12, %14\n\t"
+        "s_load_dword %2, %12, %15\n\t"
+        "s_load_dword %3, %12, %16\n\t"
+        "s_load_dword %4, %12, %17\n\t"
+        "s_load_dword %5, %12, %18\n\t"
+        "s_load_dword %6, %12, %19\n\t"
+        "s_load_dword %7, %12, %20\n\t"
+        "s_load_dword %8, %12, %21\n\t"
+        "s_load_dword %9, %12, %22\n\t"
+        "s_load_dword %10, %12, %23\n\t"
+        "s_load_dword %11, %12, %24\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=s"(d0), "=s"(d1), "=s"(d2), "=s"(d3), "=s"(d4), "=s"(d5), "=s"(d6), "=s"(d7),
+          "=s"(d8), "=s"(d9), "=s"(d10), "=s"(d11)
+        : "s"(kp), "i"(0), "i"(NL > 1 ? L : 0), "i"(NL > 2 ? 2 * L : 0), "i"(NL > 3 ? 3 * L : 0),
+          "i"(NL > 4 ? 4 * L : 0), "i"(NL > 5 ? 5 * L : 0), "i"(NL > 6 ? 6 * L : 0),
+          "i"(NL > 7 ? 7 * L : 0), "i"(NL > 8 ? 8 * L : 0), "i"(NL > 9 ? 9 * L : 0),
+          "i"(NL > 10 ? 10 * L : 0), "i"(EXTRA));
+}
+
 __device__ __forceinline__ const_ptr<Problem> problem_ptr(const Params &p, int64_t tile) {
     if (p.nproblems == 1) {
         const_ptr<Params> args = (const_ptr<Params>)__builtin_amdgcn_kernarg_segment_ptr();

@@ -39,6 +39,7 @@
 //  * Split-K partials (max, mass, unnormalised context) go to the workspace
 //    and a second, fully parallel kernel (attn_prefill_merge) combines them,
 //    so no single workgroup reads a whole row block's partials.
+#include <cstddef>
 #include <type_traits>
 #include <utility>
 
@@ -322,6 +323,11 @@ __device__ __forceinline__ int find_prefill_entry(const_ptr<PrefillBatch> b, int
 
 template <int DT, int D, bool CAP, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(PrefillArgs a) {
+    // The problem's fields are read by dependent scalar loads (the batch
+    // count, then the problem, then its segment); with their lines already in
+    // the scalar cache the chain costs one memory round trip, not one per
+    // line (chunk launches: about 0.7 us less before the first tile).
+    warm_kernarg<(offsetof(PrefillArgs, b) + offsetof(PrefillBatch, e) + 63) / 64, sizeof(PrefillArgs)>();
     const Params &p = a.p;
     constexpr int ROWS = 32 * W;  // packed rows per workgroup
     constexpr int KS = D / 16;        // QK k-steps (16 features each)
@@ -346,11 +352,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // a contiguous range of logical tiles.
     int64_t tile;
     {
-        const int64_t nb = gridDim.x;
-        const int64_t per = (nb + 7) / 8;
-        const int64_t x = blockIdx.x % 8, k = blockIdx.x / 8;
-        const int64_t full = nb % 8 == 0 ? 8 : nb % 8;  // XCDs that receive `per` blocks
-        tile = x < full ? x * per + k : full * per + (x - full) * (per - 1) + k;
+        const uint32_t nb = gridDim.x;
+        const uint32_t per = (nb + 7) / 8;
+        const uint32_t x = blockIdx.x % 8, k = blockIdx.x / 8;
+        const uint32_t full = nb % 8 == 0 ? 8 : nb % 8;  // XCDs that receive `per` blocks
+        tile = (int64_t)(x < full ? x * per + k : full * per + (x - full) * (per - 1) + k);
     }
     const int G = p.group;
     const int Hq = p.query_heads;
@@ -383,9 +389,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             pv.sg = Segment{reinterpret_cast<const uint8_t *>(batch->k) + e.kv_offset * 2,
                             reinterpret_cast<const uint8_t *>(batch->v) + e.kv_offset * 2,
                             e.head_stride, D, position + tokens, 0};
-            int64_t local = tile - pv.tile_base;
-            rb = (int)(local % pv.row_blocks);
-            kvh = (int)(local / pv.row_blocks);
+            // 32-bit: a launch has fewer than 2^31 workgroups.
+            const uint32_t local = (uint32_t)(tile - pv.tile_base), nrb = (uint32_t)pv.row_blocks;
+            rb = (int)(local % nrb);
+            kvh = (int)(local / nrb);
             split = 0;
             sidx = 0;
         } else {
@@ -404,11 +411,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             pv.row_blocks = pr->row_blocks;
             pv.splits = pr->splits;
             pv.split_keys = pr->split_keys;
-            int64_t local = tile - pv.tile_base;
-            rb = (int)(local % pv.row_blocks);
-            local /= pv.row_blocks;
-            split = (int)(local % pv.splits);
-            kvh = (int)(local / pv.splits);
+            uint32_t local = (uint32_t)(tile - pv.tile_base);
+            const uint32_t nrb = (uint32_t)pv.row_blocks, ns = (uint32_t)pv.splits;
+            rb = (int)(local % nrb);
+            local /= nrb;
+            split = (int)(local % ns);
+            kvh = (int)(local / ns);
             // This split's segment: splits are laid out segment by segment over
             // the visible range and never straddle a boundary, so one base
             // pointer and row stride serve every tile of the workgroup.
