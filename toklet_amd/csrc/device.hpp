@@ -291,7 +291,9 @@ __device__ __forceinline__ int find_problem_wave(const Problem *problems, int n,
 // then one wait.  A kernel's descriptor fields are read by chains of
 // dependent scalar loads (a count decides which fields come next, a field
 // indexes the next one), each of which would otherwise miss the cache on its
-// own line in turn; after this they hit.  The loaded words are discarded.
+// own line in turn; after this they hit.  The loaded words are discarded;
+// the destinations are early-clobber, so none of them shares a register with
+// the base address that a later load of the same block still reads.
 template <int NL, int EXTRA> __device__ __forceinline__ void warm_kernarg() {
     static_assert(NL >= 1 && NL <= 11, "kernel-argument lines");
     static_assert(EXTRA >= 0 && EXTRA % 4 == 0, "a dword offset");
@@ -312,8 +314,8 @@ template <int NL, int EXTRA> __device__ __forceinline__ void warm_kernarg() {
         "s_load_dword %10, %12, %23\n\t"
         "s_load_dword %11, %12, %24\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=s"(d0), "=s"(d1), "=s"(d2), "=s"(d3), "=s"(d4), "=s"(d5), "=s"(d6), "=s"(d7),
-          "=s"(d8), "=s"(d9), "=s"(d10), "=s"(d11)
+        : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7),
+          "=&s"(d8), "=&s"(d9), "=&s"(d10), "=&s"(d11)
         : "s"(kp), "i"(0), "i"(NL > 1 ? L : 0), "i"(NL > 2 ? 2 * L : 0), "i"(NL > 3 ? 3 * L : 0),
           "i"(NL > 4 ? 4 * L : 0), "i"(NL > 5 ? 5 * L : 0), "i"(NL > 6 ? 6 * L : 0),
           "i"(NL > 7 ? 7 * L : 0), "i"(NL > 8 ? 8 * L : 0), "i"(NL > 9 ? 9 * L : 0),

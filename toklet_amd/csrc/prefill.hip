@@ -1014,6 +1014,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 // unnormalised contexts.  Problem::part_base is the problem's first merge block.
 template <int D, int ROWS>
 __global__ __launch_bounds__(256) void attn_prefill_merge(Params p, int64_t blocks) {
+    // The fields below arrive through dependent scalar loads (the block
+    // count, the problem count, the problem): their lines are brought in
+    // together first (Params, `blocks` and the hidden arguments after them).
+    warm_kernarg<(sizeof(Params) + sizeof(int64_t) + 63) / 64, 0>();
     constexpr int FB = D / 16;                  // 16-feature blocks per row
     constexpr int RC = ROWS / 64;               // 64-row chunks per row block
     constexpr int MAXS = 16;

@@ -87,6 +87,9 @@ template <> __device__ __forceinline__ void store_out<BF16>(void *base, int64_t 
 template <int DT, bool TABLE>
 __global__ __launch_bounds__(64) void produce_qkv(ProduceParams p) {
 #pragma clang fp contract(off)
+    // Its fields arrive through dependent scalar loads: their lines (and the
+    // hidden arguments' start) first, in one round trip.
+    warm_kernarg<(sizeof(ProduceParams) + 63) / 64, 0>();
     __shared__ float row[512];
     const int lane = threadIdx.x;
     const int D = p.d;
