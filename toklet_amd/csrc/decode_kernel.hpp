@@ -517,7 +517,8 @@ __global__ __launch_bounds__(64 * decode_waves_for(D * Elem<DT>::size, R)) void 
         rhi[r] = 0;
         for (int c = 0; c < CPL; ++c) q[r][c] = u32x4{0, 0, 0, 0};
         if (r < nrows) {
-            const int t = r / G, h = kvh * G + r % G;
+            // r and the group are non-negative: unsigned divisions.
+            const int t = (int)((uint32_t)r / (uint32_t)G), h = kvh * G + (int)((uint32_t)r % (uint32_t)G);
             int64_t lo, hi;
             visible_range(has_window != 0, window, pv.k_pos0, pv.keys, pv.q_pos0 + t, &lo, &hi);
             lo -= a;

@@ -446,7 +446,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     const int row = rb * ROWS + wave * 32 + j;
     const bool rvalid = row < m_kv;
     const int rrow = rvalid ? row : m_kv - 1;
-    const int t_row = rrow / G, h_row = kvh * G + rrow % G;
+    // Rows and the group are non-negative: unsigned divisions (shorter sequences).
+    const uint32_t ug = (uint32_t)G;
+    const int t_row = (int)((uint32_t)rrow / ug), h_row = kvh * G + (int)((uint32_t)rrow % ug);
     int64_t r_lo, r_hi;
     visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + t_row, &r_lo, &r_hi);
     if (!rvalid) r_hi = r_lo;  // no visible keys: never contributes, never stored
@@ -455,8 +457,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     const int wg_row_first = rb * ROWS;
     const int wg_row_last = min(wg_row_first + ROWS, m_kv) - 1;
     int64_t k_lo, k_hi, tmp;
-    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + wg_row_first / G, &k_lo, &tmp);
-    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + wg_row_last / G, &tmp, &k_hi);
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_first / ug, &k_lo, &tmp);
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_last / ug, &tmp, &k_hi);
     if (k_lo < s_lo) k_lo = s_lo;
     if (k_hi > s_hi) k_hi = s_hi;
     if (k_hi < k_lo) k_hi = k_lo;
@@ -469,8 +471,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         const int w_first = min(wg_row_first + wave * 32, m_kv - 1);
         const int w_last = min(wg_row_first + wave * 32 + 31, m_kv - 1);
         int64_t a, b, full_lo, full_hi;
-        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + w_first / G, &a, &full_hi);
-        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + w_last / G, &full_lo, &b);
+        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_first / ug, &a, &full_hi);
+        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_last / ug, &full_lo, &b);
         int64_t lo_t = full_lo - k_lo;
         lo_t = lo_t <= 0 ? 0 : (lo_t + PF_KT - 1) / PF_KT;
         int64_t hi_t = full_hi - k_lo;
