@@ -604,6 +604,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // across an iteration (64 registers) made the compiler spill in the loop.
     constexpr bool VLATE = D >= 256;
     constexpr int VPF = 4;
+    // head_dim 256 (one wave per SIMD): steps 1 and 3 run as one phase after
+    // the ring wait, P.V and Q.K MFMAs alternating (the merged body below).
+    constexpr bool MERGED = D >= 256;
+    static_assert(!MERGED || (VLATE && L::vt_bufs == NS && NS >= 3),
+                  "the merged phase writes tile t + 1's V^T while it reads tile t - 1's");
     auto vt_buf = [&](int tile_stage) { return lds + L::vt_base + (tile_stage % L::vt_bufs) * L::vt_bytes; };
     auto vt_operand = [&](lds_ptr<uint8_t> buf, int k) {
         return *(lds_ptr<u32x4>)(buf + vt_off[k / MB] + (k % MB) * 32 * L::vt_row);
@@ -628,8 +633,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         vtr.read(lds + L::v_at(0));
         vtr.write(lds + L::vt_base);
         // Tile 0's V^T is read at the end of iteration 0, after the barrier of
-        // its step 2, which a single tile does not have.
-        if (ntiles == 1) __syncthreads();
+        // its step 2, which a single tile does not have (the merged form opens
+        // every iteration with a barrier and needs none here).
+        if (!MERGED && ntiles == 1) __syncthreads();
     }
     // V^T operands of the tile whose P.V is pending (read ahead unless VLATE).
     u32x4 vop[VLATE ? 1 : 2][VLATE ? 1 : MB];
@@ -650,6 +656,60 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // skips the visibility test, takes a fixed ring wait and issues and
     // converts unconditionally.
     bool bulk = false;
+    // Close tile t's softmax step: st holds its scores (masked, capped, shifted
+    // by `shift` in raw units), ph its probabilities against the row's base
+    // and lt their mass in this lane.
+    auto close_tile = [&](f32x16 &st, float shift, float &lt) {
+        // ---- the exact path, rare: some row's tile mass exceeds MASS_LIMIT
+        // (a score about 15 log2 units above its base, the row's first
+        // visible tile, or a non-finite score).  The wave moves
+        // each such row's base to the tile maximum, rescales O (which holds
+        // tiles up to t - 1) and l, and forms tile t's probabilities again.
+        if (__ballot(!(lt <= MASS_LIMIT)) != 0) {
+            float hi = st[0];
+            for (int i = 1; i < 16; ++i) hi = maxn(hi, st[i]);
+            {
+                const uint32_t u = __builtin_bit_cast(uint32_t, hi);
+                const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+                // Copied to scalars first: a bit_cast of a vector element reads
+                // element 0 whatever the index.
+                const uint32_t a0 = pr32[0], a1 = pr32[1];
+                hi = maxn(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+            }
+            hi += shift;  // raw units (st of a huge row was shifted)
+            // A NaN maximum leaves the base (the row already reports a
+            // non-finite score).
+            const float m_new = fmaxf(m_run, hi);
+            if (m_new > m_run) {
+                const float corr = m_run == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * tmul);
+                l_run *= corr;
+                for (int mb = 0; mb < MB; ++mb)
+                    for (int i = 0; i < 16; ++i) acc[mb][i] *= corr;
+                m_run = m_new;
+            }
+            if constexpr (!CAP)
+                huge = __ballot(m_run != NEG_INF && fabsf(m_run * tmul) >= 1024.0f) != 0;
+            nbase_run = m_run == NEG_INF ? BASE_NONE : -m_run * tmul;
+            // Tile t against the new base, in the units st holds.
+            const float delta = m_run == NEG_INF ? 0.0f : m_run - shift;
+            const float nb = -delta * tmul;
+            lt = 0.0f;
+            for (int i = 0; i < 8; ++i) {
+                float y0, y1;
+                if (!CAP && huge) {
+                    y0 = (st[2 * i] - delta) * tmul;
+                    y1 = (st[2 * i + 1] - delta) * tmul;
+                } else {
+                    y0 = __builtin_fmaf(st[2 * i], tmul, nb);
+                    y1 = __builtin_fmaf(st[2 * i + 1], tmul, nb);
+                }
+                ph[i] = pack2<PDT>(__builtin_amdgcn_exp2f(y0), __builtin_amdgcn_exp2f(y1));
+                lt = add_pair(ph[i], lt);
+            }
+        }
+        l_run += lt;
+    };
+
     auto body = [&](auto stg_tag, f32x16 &st, f32x16 &st_next) {
         constexpr int STG = decltype(stg_tag)::value;
         constexpr int STG_NEXT = (STG + 1) % NS;
@@ -798,54 +858,123 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        // ---- the exact path, rare: some row's tile mass exceeds MASS_LIMIT
-        // (a score about 15 log2 units above its base, the row's first
-        // visible tile, or a non-finite score).  The wave moves
-        // each such row's base to the tile maximum, rescales O (which holds
-        // tiles up to t - 1) and l, and forms tile t's probabilities again.
-        if (__ballot(!(lt <= MASS_LIMIT)) != 0) {
-            float hi = st[0];
-            for (int i = 1; i < 16; ++i) hi = maxn(hi, st[i]);
-            {
-                const uint32_t u = __builtin_bit_cast(uint32_t, hi);
-                const auto pr32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-                // Copied to scalars first: a bit_cast of a vector element reads
-                // element 0 whatever the index.
-                const uint32_t a0 = pr32[0], a1 = pr32[1];
-                hi = maxn(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
-            }
-            hi += shift;  // raw units (st of a huge row was shifted)
-            // A NaN maximum leaves the base (the row already reports a
-            // non-finite score).
-            const float m_new = fmaxf(m_run, hi);
-            if (m_new > m_run) {
-                const float corr = m_run == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * tmul);
-                l_run *= corr;
-                for (int mb = 0; mb < MB; ++mb)
-                    for (int i = 0; i < 16; ++i) acc[mb][i] *= corr;
-                m_run = m_new;
-            }
-            if constexpr (!CAP)
-                huge = __ballot(m_run != NEG_INF && fabsf(m_run * tmul) >= 1024.0f) != 0;
-            nbase_run = m_run == NEG_INF ? BASE_NONE : -m_run * tmul;
-            // Tile t against the new base, in the units st holds.
-            const float delta = m_run == NEG_INF ? 0.0f : m_run - shift;
-            const float nb = -delta * tmul;
-            lt = 0.0f;
-            for (int i = 0; i < 8; ++i) {
-                float y0, y1;
-                if (!CAP && huge) {
-                    y0 = (st[2 * i] - delta) * tmul;
-                    y1 = (st[2 * i + 1] - delta) * tmul;
-                } else {
-                    y0 = __builtin_fmaf(st[2 * i], tmul, nb);
-                    y1 = __builtin_fmaf(st[2 * i + 1], tmul, nb);
-                }
-                ph[i] = pack2<PDT>(__builtin_amdgcn_exp2f(y0), __builtin_amdgcn_exp2f(y1));
-                lt = add_pair(ph[i], lt);
-            }
+        close_tile(st, shift, lt);
+
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // The merged form of iteration t (head_dim 256, where each SIMD runs one
+    // wave and nothing hides a phase's LDS reads or vector work but the same
+    // wave's MFMAs):
+    //   1. wait for tile t + 1 and hand the stage of tile t - 1 to a new load;
+    //   2. one phase of 2 KS MFMA slots: P.V of tile t - 1 in the even slots,
+    //      the scores of tile t + 1 in the odd ones, with the statistics and
+    //      the probabilities of tile t, tile t + 1's V transposition and both
+    //      chains' LDS operand reads between them.
+    // Tile t - 1's V^T (read here), tile t's (written in iteration t - 1, read
+    // in t + 1) and tile t + 1's (written here) need three buffers, one per
+    // ring stage; the buffer written in iteration t last held tile
+    // t + 1 - NS, read in iteration t + 2 - NS <= t - 1, before this
+    // iteration's barrier.  In iteration 0 the phase multiplies the zeroed
+    // buffer of "tile -1"; after the last tile it scores and transposes a
+    // stale stage into a buffer nobody reads again.
+    auto body_mg = [&](auto stg_tag, f32x16 &st, f32x16 &st_next) {
+        constexpr int STG = decltype(stg_tag)::value;
+        constexpr int STG_NEXT = (STG + 1) % NS;
+        __builtin_amdgcn_sched_barrier(0);
+        if (bulk) {
+            ring_sync_fixed<LPT, NS - 3>();
+            issue(std::integral_constant<int, (STG + NS - 1) % NS>{}, std::true_type{});
+        } else if (t + 1 < ntiles) {
+            wait_tile(t + 1);
+            if (t_next < ntiles) issue(std::integral_constant<int, (STG + NS - 1) % NS>{}, std::false_type{});
+        } else {
+            // The last tile: the V^T buffer its phase writes held tile
+            // t + 1 - NS, which a slower wave may still be reading.
+            __syncthreads();
         }
-        l_run += lt;
+        __builtin_amdgcn_sched_barrier(0);
+
+        lds_ptr<uint8_t> vtp = vt_buf((STG + NS - 1) % NS);  // tile t - 1's V^T
+        lds_ptr<uint8_t> kn = lds + L::k_at(STG_NEXT);
+        lds_ptr<uint8_t> vn = lds + L::v_at(STG_NEXT);
+        lds_ptr<uint8_t> vtn = vt_buf(STG_NEXT);
+        float nbase = nbase_run;
+        float shift = 0.0f;  // subtracted from st in raw units (huge rows)
+        float lt = 0.0f;     // this lane's mass of the tile
+        uint32_t pn[8];      // tile t's probabilities (ph holds tile t - 1's until the phase ends)
+        constexpr int KPRE = CAP ? 2 : 3;
+        constexpr int SLOTS = NPV + KS;
+        u32x4 vq[VPF];
+        for (int i = 0; i < VPF; ++i) vq[i] = vt_operand(vtp, i);
+        u32x4 kq[KPRE];
+        for (int i = 0; i < KPRE; ++i) kq[i] = *(lds_ptr<u32x4>)(kn + k_off[i]);
+        for (int i = 0; i < 16; ++i) st_next[i] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < SLOTS; ++k) {
+            const int m = k / 2;
+            if (k % 2 == 0) {
+                const int stp = m / MB, mb = m % MB;
+                const u32x4 bv = u32x4{ph[4 * stp], ph[4 * stp + 1], ph[4 * stp + 2], ph[4 * stp + 3]};
+                const u32x4 a = vq[m % VPF];
+                if (m + VPF < NPV) vq[m % VPF] = vt_operand(vtp, m + VPF);
+                acc[mb] = mfma32<PDT>(a, bv, acc[mb]);
+            } else {
+                const u32x4 kcur = kq[m % KPRE];
+                if (m + KPRE < KS) kq[m % KPRE] = *(lds_ptr<u32x4>)(kn + k_off[m + KPRE]);
+                st_next = mfma32<DT>(kcur, qb[m], st_next);
+            }
+            // Raised priority over the first half of the phase, as in the
+            // two-wave form; without these two instructions the compiler
+            // stops unrolling the softcapped phase (dynamic register indexing
+            // and scratch, 3.6x slower on the configs[3] session).
+            if (k == 1) __builtin_amdgcn_s_setprio(1);
+            if (k == SLOTS / 2) __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k == 0) {
+                if (bulk || (unsigned)(t - tf_lo) < tf_n) {  // t in [tf_lo, tf_hi)
+                    float a = amax_run;
+                    for (int i = 0; i < 16; ++i) a = maxn(a, __builtin_fabsf(st[i]));
+                    amax_run = a;
+                    if constexpr (CAP)
+                        for (int i = 0; i < 16; ++i) st[i] = tanh_fast(st[i] * ycap);
+                } else {
+                    const int lo_rel = min(max(rlo0 - t * PF_KT, 0), PF_KT);
+                    const int hi_rel = min(max(rhi0 - t * PF_KT, 0), PF_KT);
+                    for (int i = 0; i < 16; ++i) {
+                        const int kk = 8 * (i >> 2) + 4 * h + (i & 3);
+                        const bool vis = kk >= lo_rel && kk < hi_rel;
+                        bad |= vis && !(__builtin_fabsf(st[i]) < -NEG_INF);
+                        if constexpr (CAP) st[i] = vis ? tanh_fast(st[i] * ycap) : NEG_INF;
+                        else st[i] = vis ? st[i] : NEG_INF;
+                    }
+                }
+            }
+            if constexpr (!CAP) {
+                if (k == 1 && huge) {
+                    shift = m_run == NEG_INF ? 0.0f : m_run;
+                    for (int i = 0; i < 16; ++i) st[i] -= shift;
+                    nbase = m_run == NEG_INF ? BASE_NONE : 0.0f;
+                }
+            }
+            // Tile t + 1's V, resident since the ring wait, transposed
+            // (bf16: converted) for the phase of iteration t + 2.
+            if (k == 1) vtr.read(vn);
+            if (k == SLOTS / 2) vtr.write(vtn);
+            for (int i = 0; i < 8; ++i) {
+                if (k == 2 + (i * (SLOTS - 2)) / 8) {
+                    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i], tmul, nbase));
+                    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i + 1], tmul, nbase));
+                    pn[i] = pack2<PDT>(e0, e1);
+                    lt = add_pair(pn[i], lt);
+                    // Pin the pair here: the compiler would otherwise sink it
+                    // to its use after the phase, out of the MFMA shadow.
+                    asm volatile("" : "+v"(pn[i]), "+v"(lt));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int i = 0; i < 8; ++i) ph[i] = pn[i];
+        close_tile(st, shift, lt);
 
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -857,8 +986,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         static_for<NS>([&](auto k) {
             constexpr int K = decltype(k)::value;
             if (t >= ntiles) return;
-            if constexpr (K % 2 == 0) body(std::integral_constant<int, K>{}, st, st_b);
-            else body(std::integral_constant<int, K>{}, st_b, st);
+            if constexpr (MERGED) {
+                if constexpr (K % 2 == 0) body_mg(std::integral_constant<int, K>{}, st, st_b);
+                else body_mg(std::integral_constant<int, K>{}, st_b, st);
+            } else {
+                if constexpr (K % 2 == 0) body(std::integral_constant<int, K>{}, st, st_b);
+                else body(std::integral_constant<int, K>{}, st_b, st);
+            }
             ++t;
         });
         // An odd ring leaves the next scores in st_b.
