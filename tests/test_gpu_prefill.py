@@ -102,11 +102,13 @@ def test_gqa7_d64_chunk_rows_straddle_blocks(torch_mod, ctx, ops, orc):
     assert err <= TOL_HALF
 
 
+@pytest.mark.parametrize("form", ["-1", "0", "1"])  # TKH_PREFILL16: default, 32-row, 16-row kernel
 @pytest.mark.parametrize("softcap", [0.0, 50.0])
-def test_window_d256_chunk_with_split_keys(torch_mod, ctx, ops, orc, softcap):
+def test_window_d256_chunk_with_split_keys(torch_mod, ops, orc, softcap, form):
     """configs[3] sliding layer: 8/4/256, W=1024, chunk of 128 at position 3000.  The
     visible range spans 1151 keys, so splits at its ends hold keys only some rows see."""
     torch = torch_mod
+    ctx = _tuned_context(ops, TKH_PREFILL16=form)
     rng = np.random.default_rng(17)
     hq, hkv, D, W = 8, 4, 256, 1024
     queries, keys = 128, 3128
@@ -121,8 +123,9 @@ def test_window_d256_chunk_with_split_keys(torch_mod, ctx, ops, orc, softcap):
         ref, _, _ = orc.window_attention(q, k.reshape(-1), v.reshape(-1), queries, keys, keys, hq, hkv,
                                          D, keys - queries, 0, W, 1.0 / 16.0, softcap=softcap)
         err = max_err(host(out), ref)
-        log(f"gemma window chunk {dt} softcap {softcap}: max abs error {err:.3e}")
+        log(f"gemma window chunk {dt} softcap {softcap} form {form}: max abs error {err:.3e}")
         assert err <= TOL_HALF
+    ctx.close()
 
 
 def test_split_results_do_not_depend_on_split_count(torch_mod, ctx, ops, orc):

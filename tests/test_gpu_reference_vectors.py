@@ -64,14 +64,19 @@ def _env(**values):
 
 def _contexts(ops):
     """name -> context: the default planner (decode kernel for few rows), the
-    MFMA chunk kernel for every bf16/f16 call, and both with 32-key splits."""
+    MFMA chunk kernel for every bf16/f16 call in its 32-row and 16-row forms
+    (TKH_PREFILL16), and each with 32-key splits."""
     out = {"decode": ops.Context(0)}
-    with _env(TKH_DECODE_DISABLE=1):
-        out["chunk"] = ops.Context(0)
+    with _env(TKH_DECODE_DISABLE=1, TKH_PREFILL16=0):
+        out["chunk32"] = ops.Context(0)
+    with _env(TKH_DECODE_DISABLE=1, TKH_PREFILL16=1):
+        out["chunk16"] = ops.Context(0)
     with _env(TKH_SPLIT_KEYS=32):
         out["decode/split32"] = ops.Context(0)
-    with _env(TKH_DECODE_DISABLE=1, TKH_SPLIT_KEYS=32):
-        out["chunk/split32"] = ops.Context(0)
+    with _env(TKH_DECODE_DISABLE=1, TKH_SPLIT_KEYS=32, TKH_PREFILL16=0):
+        out["chunk32/split32"] = ops.Context(0)
+    with _env(TKH_DECODE_DISABLE=1, TKH_SPLIT_KEYS=32, TKH_PREFILL16=1):
+        out["chunk16/split32"] = ops.Context(0)
     return out
 
 
@@ -130,7 +135,7 @@ def _witness_keys(pattern, depth, hkv, cap, D):
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 def test_adversarial_witnesses_every_kernel(torch_mod, ops, orc, dt, D):
     torch = torch_mod
     hq, hkv, cap = 4, 2, 96
@@ -207,8 +212,10 @@ def _chunk_case(rng, tokens, hq, hkv, D, cap, offset, v_value, where):
     return q, k, v
 
 
+@pytest.mark.parametrize("form", ["0", "1"])  # TKH_PREFILL16: 32-row and 16-row kernel
+@pytest.mark.parametrize("D", [128, 256])
 @pytest.mark.parametrize("offset", [0, 2000])  # 2000: the chunk's keys are split
-def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset):
+def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset, D, form):
     """Every finite bf16 V is computed, as the reference computes it
     (src/cpu/attention.rs:247-251 rejects only non-finite values): 65280, the
     largest value f16 holds, on the MFMA path; 65536, 2^24 - 2^16, 2^24,
@@ -216,9 +223,10 @@ def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset):
     inf is a non-finite input.  The decode kernel computes 2^24 in FP32."""
     torch = torch_mod
     rng = np.random.default_rng(81)
-    hq, hkv, D, tokens = 8, 4, 128, 64
+    hq, hkv, tokens = 8, 4, 64
     cap = offset + tokens
-    ctx = ops.Context(0)
+    with _env(TKH_PREFILL16=form):
+        ctx = ops.Context(0)
     shape = ops.CachedAttentionShape(tokens, hq, hkv, D, cap, offset)
     where = (2, offset + 5, 17)
     for v_value, expect in ((65280.0, None), (65536.0, None), (16711680.0, None), (2.0 ** 24, None),
@@ -232,7 +240,7 @@ def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset):
             got = host(out)
             assert np.isfinite(got).all()
             rel = max_err(got, ref) / float(np.abs(ref).max())
-            log(f"bf16 V {v_value:g} at offset {offset}: relative error {rel:.3e}")
+            log(f"bf16 V {v_value:g} at offset {offset}, D={D}, form {form}: relative error {rel:.3e}")
             assert rel <= 2e-3
             continue
         with pytest.raises(ops.TkhError) as e:

@@ -49,6 +49,9 @@ extern "C" int tkh_prefill_merge_blocks_per_row_block(int head_dim, int rows);
 extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int rows,
                                                int64_t blocks, hipStream_t stream,
                                                hipEvent_t start, hipEvent_t stop);
+extern "C" hipError_t tkh_launch_prefill16(const tkh::PrefillArgs *p, int dtype, int head_dim,
+                                           int64_t groups, hipStream_t stream, hipEvent_t start,
+                                           hipEvent_t stop);
 extern "C" hipError_t tkh_launch_prefill(const tkh::PrefillArgs *p, int dtype, int head_dim, int waves,
                                          int64_t groups, hipStream_t stream, hipEvent_t start,
                                          hipEvent_t stop);
@@ -613,8 +616,15 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
 
     hipEvent_t *ev = nullptr;
     if (ctx->profiling) TRY(profile_slot(ctx, &ev, merge_blocks > 0, err));
-    hipError_t e = tkh_launch_prefill(&args, (int)plan.dtype, (int)D, waves, wgs, ctx->stream,
-                                      ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
+    // 16-row kernel: by default for head_dim 256 (configs[3] session chunks
+    // 5.97-6.09 -> 5.57-5.78 ms); at head_dim 128 it measured the same as the
+    // 32-row one on chunks and slower on full batches.
+    const bool rows16 = waves == 4 && (ctx->prefill16 > 0 ? (D == 128 || D == 256)
+                                       : ctx->prefill16 < 0 && D == 256);
+    hipError_t e = rows16 ? tkh_launch_prefill16(&args, (int)plan.dtype, (int)D, wgs, ctx->stream,
+                                                 ev ? ev[0] : nullptr, ev ? ev[1] : nullptr)
+                          : tkh_launch_prefill(&args, (int)plan.dtype, (int)D, waves, wgs, ctx->stream,
+                                               ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
     if (e != hipSuccess) return device_error(e, "prefill launch", err);
     if (merge_blocks > 0) {
         e = tkh_launch_prefill_merge(&prm, (int)D, (int)rows_per, merge_blocks, ctx->stream,
@@ -772,6 +782,7 @@ void init_tuning(tkh_context *ctx, int device) {
     ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 64));
     ctx->prefill_waves = env_int("TKH_PREFILL_WAVES", 0);
     ctx->prefill_compact = env_int("TKH_PREFILL_COMPACT", 1) != 0;
+    ctx->prefill16 = env_int("TKH_PREFILL16", -1);
 }
 
 // First visible key (absolute) of a query at `position` (window_attention.rs:105-107).

@@ -213,8 +213,10 @@ template <int D, int W> struct PrefillLds {
 // for the chunk's two key quads; for bf16 each pair is then widened (a shift
 // and a mask) and rounded to f16 in one v_cvt_pk_f16_f32, which is exact for
 // bf16 values up to 65280 and gives inf above.  Split in a read half and a
-// write half so a caller can put MFMAs between.
-template <int D, int W, bool CONV> struct VTranspose {
+// write half so a caller can put MFMAs between.  K16: the key order of
+// attn_prefill16's P.V operands (chunk c holds keys 4c .. 4c + 3 and
+// 16 + 4c .. 16 + 4c + 3) instead of attn_prefill's.
+template <int D, int W, bool CONV, bool K16 = false> struct VTranspose {
     using L = PrefillLds<D, W>;
     static constexpr int threads = 64 * W;
     static constexpr int per = D * 4 / threads;  // chunks per thread
@@ -226,10 +228,10 @@ template <int D, int W, bool CONV> struct VTranspose {
             const int q = n * threads + tid;
             const int g = q >> 4, jj = q & 15;  // 16-lane group, lane in it
             const int c = g & 3, fb = 16 * (g >> 2);
-            const int row = 16 * (c >> 1) + 4 * (c & 1) + (jj >> 2);
+            const int row = K16 ? 4 * c + (jj >> 2) : 16 * (c >> 1) + 4 * (c & 1) + (jj >> 2);
             const int fbyte = (fb + 4 * (jj & 3)) * 2;
             src1[n] = L::at(row, fbyte >> 4) + (fbyte & 15);
-            src2[n] = L::at(row + 8, fbyte >> 4) + (fbyte & 15);
+            src2[n] = L::at(row + (K16 ? 16 : 8), fbyte >> 4) + (fbyte & 15);
             dst[n] = L::vt_at(fb + jj, c);
         }
     }
@@ -321,33 +323,11 @@ __device__ __forceinline__ int find_prefill_entry(const_ptr<PrefillBatch> b, int
     return __builtin_amdgcn_readfirstlane(63 - __builtin_clzll(m));
 }
 
-template <int DT, int D, bool CAP, int W>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(PrefillArgs a) {
-    // The problem's fields are read by dependent scalar loads (the batch
-    // count, then the problem, then its segment); with their lines already in
-    // the scalar cache the chain costs one memory round trip, not one per
-    // line (chunk launches: about 0.7 us less before the first tile).
-    warm_kernarg<(offsetof(PrefillArgs, b) + offsetof(PrefillBatch, e) + 63) / 64, sizeof(PrefillArgs)>();
-    const Params &p = a.p;
-    constexpr int ROWS = 32 * W;  // packed rows per workgroup
-    constexpr int KS = D / 16;        // QK k-steps (16 features each)
-    constexpr int MB = D / 32;        // PV M-blocks (32 features each)
-    constexpr int PDT = F16;          // P and V^T operand type of the P.V MFMAs
-    constexpr bool VCONV = DT == BF16;  // V tiles converted to f16 in LDS
-    static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
-    using L = PrefillLds<D, W>;
-    constexpr int NS = L::stages;
-    constexpr int RPW = L::runs_per_wave;
-    constexpr int LPT = 2 * RPW;      // direct loads per wave per tile (K + V)
-
-    __shared__ __attribute__((aligned(16))) uint8_t lds_raw[L::bytes];
-    lds_ptr<uint8_t> lds = (lds_ptr<uint8_t>)lds_raw;
-
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int j = lane & 31;   // query row of this lane inside the wave
-    const int h = lane >> 5;   // which half of the k-slots / key quads
-
+// The workgroup's logical tile and what it covers: its problem (from the
+// descriptors, or built from a compact batch entry), row block, key split,
+// KV head and the split's index inside its segment.
+template <int D>
+__device__ __forceinline__ void pf_locate(const Params &p, PfView &pv, int &rb, int &split, int &kvh, int &sidx) {
     // XCD-major tile order: dispatch slot b runs on XCD b % 8; give each XCD
     // a contiguous range of logical tiles.
     int64_t tile;
@@ -358,10 +338,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         const uint32_t full = nb % 8 == 0 ? 8 : nb % 8;  // XCDs that receive `per` blocks
         tile = (int64_t)(x < full ? x * per + k : full * per + (x - full) * (per - 1) + k);
     }
-    const int G = p.group;
     const int Hq = p.query_heads;
-    PfView pv;
-    int rb, split, kvh, sidx;
     {
         const_ptr<PrefillArgs> args = (const_ptr<PrefillArgs>)__builtin_amdgcn_kernarg_segment_ptr();
         const_ptr<PrefillBatch> batch = &args->b;
@@ -434,6 +411,40 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             pv.sg = Segment{sgp.k, sgp.v, sgp.head_stride, sgp.row_stride, sgp.keys, sgp.start};
         }
     }
+}
+
+template <int DT, int D, bool CAP, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(PrefillArgs a) {
+    // The problem's fields are read by dependent scalar loads (the batch
+    // count, then the problem, then its segment); with their lines already in
+    // the scalar cache the chain costs one memory round trip, not one per
+    // line (chunk launches: about 0.7 us less before the first tile).
+    warm_kernarg<(offsetof(PrefillArgs, b) + offsetof(PrefillBatch, e) + 63) / 64, sizeof(PrefillArgs)>();
+    const Params &p = a.p;
+    constexpr int ROWS = 32 * W;  // packed rows per workgroup
+    constexpr int KS = D / 16;        // QK k-steps (16 features each)
+    constexpr int MB = D / 32;        // PV M-blocks (32 features each)
+    constexpr int PDT = F16;          // P and V^T operand type of the P.V MFMAs
+    constexpr bool VCONV = DT == BF16;  // V tiles converted to f16 in LDS
+    static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
+    using L = PrefillLds<D, W>;
+    constexpr int NS = L::stages;
+    constexpr int RPW = L::runs_per_wave;
+    constexpr int LPT = 2 * RPW;      // direct loads per wave per tile (K + V)
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds_raw[L::bytes];
+    lds_ptr<uint8_t> lds = (lds_ptr<uint8_t>)lds_raw;
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int j = lane & 31;   // query row of this lane inside the wave
+    const int h = lane >> 5;   // which half of the k-slots / key quads
+
+    const int G = p.group;
+    const int Hq = p.query_heads;
+    PfView pv;
+    int rb, split, kvh, sidx;
+    pf_locate<D>(p, pv, rb, split, kvh, sidx);
     const int m_kv = pv.queries * G;
     const int64_t seg_start = pv.sg.start;
     const int64_t seg_end = seg_start + pv.sg.keys;
@@ -1143,6 +1154,513 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
 }
 
+// ---------------------------------------------------------------------------
+// attn_prefill16: the same flash loop with sixteen packed rows per wave, on
+// v_mfma_f32_16x16x32, for launches of few row blocks (session chunks).  At
+// head_dim 256 a 32-row wave fills a SIMD's registers, and one wave per SIMD
+// leaves its LDS reads, vector work and MFMAs to hide one another alone; a
+// 16-row wave needs half the context registers, so eight waves (the same
+// 128-row block, grid, workspace slots and merge as attn_prefill<..., 4>) run
+// two per SIMD, each with half the MFMAs and half the softmax work of a tile.
+//
+// Lane (j, g) = (lane % 16, lane / 16):
+//  * S^T = K Q^T per 16-key block kb: A = K (lane: key 16 kb + j, features
+//    32 ks + 8 g .. + 7), B = Q^T (lane: row j, the same features), D: row j,
+//    keys 16 kb + 4 g + r (register r).
+//  * O^T = V^T P^T: B = P^T in the MFMA's k order k = 8 g + 4 kb + r for key
+//    16 kb + 4 g + r, which is where the scores already sit; A = V^T row
+//    16 fb + j, chunk g (keys 4 g .. + 3 and 16 + 4 g .. + 3); D: row j,
+//    features 16 fb + 4 g + r.
+// A row's 32 keys of a tile are spread over the four lanes j, j + 16, j + 32,
+// j + 48 (8 each); its statistics are reduced across them where the 32-row
+// kernel reduces across a lane pair.
+template <int DT> __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mfma16<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma16<F16>(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+// Sum and maximum over the four lanes of a row (j, j + 16, j + 32, j + 48);
+// every lane of the row gets the same bits.
+__device__ __forceinline__ float row4_sum(float x) {
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
+}
+__device__ __forceinline__ float row4_max(float x) {
+    x = maxn(x, __shfl_xor(x, 16));
+    return maxn(x, __shfl_xor(x, 32));
+}
+
+constexpr int PF16_WAVES = 8;  // 16-row waves per workgroup: a 128-row block
+
+template <int DT, int D, bool CAP>
+__global__ __launch_bounds__(64 * PF16_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill16(PrefillArgs a) {
+    warm_kernarg<(offsetof(PrefillArgs, b) + offsetof(PrefillBatch, e) + 63) / 64, sizeof(PrefillArgs)>();
+    const Params &p = a.p;
+    constexpr int W = PF16_WAVES;
+    constexpr int RW = 16;            // packed rows per wave
+    constexpr int ROWS = RW * W;      // packed rows per workgroup
+    constexpr int KS = D / 32;        // Q.K k-steps (32 features each) per 16-key block
+    constexpr int NQK = 2 * KS;       // Q.K MFMAs per tile (two 16-key blocks)
+    constexpr int FB = D / 16;        // P.V MFMAs per tile (16-feature blocks)
+    constexpr int PDT = F16;
+    constexpr bool VCONV = DT == BF16;
+    static_assert(D == 128 || D == 256, "16-row form: head_dim 128 or 256");
+    using L = PrefillLds<D, W>;
+    constexpr int NS = L::stages;
+    constexpr int RPW = L::runs_per_wave;
+    constexpr int LPT = 2 * RPW;
+    // The last iteration's Q.K pass transposes a stale stage into the buffer
+    // after tile t's; with two buffers that is tile t - 1's, which step 1 of
+    // the same iteration reads, so the last iteration always takes the step-2
+    // barrier below.
+    static_assert(L::vt_bufs >= 2, "V^T buffers");
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds_raw[L::bytes];
+    lds_ptr<uint8_t> lds = (lds_ptr<uint8_t>)lds_raw;
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int j = lane & 15;   // query row of this lane inside the wave
+    const int g = lane >> 4;   // its key quad (scores) and feature quad (context)
+
+    const int G = p.group;
+    const int Hq = p.query_heads;
+    PfView pv;
+    int rb, split, kvh, sidx;
+    pf_locate<D>(p, pv, rb, split, kvh, sidx);
+    const int m_kv = pv.queries * G;
+    const int64_t seg_start = pv.sg.start;
+    const int64_t seg_end = seg_start + pv.sg.keys;
+    const int64_t seg_lo = seg_start > pv.vis_lo ? seg_start : pv.vis_lo;
+    const int64_t seg_hi = seg_end < pv.vis_hi ? seg_end : pv.vis_hi;
+    const int64_t s_lo = seg_lo + (int64_t)sidx * pv.split_keys;
+    const int64_t s_hi = s_lo + pv.split_keys < seg_hi ? s_lo + pv.split_keys : seg_hi;
+
+    const int row = rb * ROWS + wave * RW + j;
+    const bool rvalid = row < m_kv;
+    const int rrow = rvalid ? row : m_kv - 1;
+    const uint32_t ug = (uint32_t)G;
+    const int t_row = (int)((uint32_t)rrow / ug), h_row = kvh * G + (int)((uint32_t)rrow % ug);
+    int64_t r_lo, r_hi;
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + t_row, &r_lo, &r_hi);
+    if (!rvalid) r_hi = r_lo;
+
+    const int wg_row_first = rb * ROWS;
+    const int wg_row_last = min(wg_row_first + ROWS, m_kv) - 1;
+    int64_t k_lo, k_hi, tmp;
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_first / ug, &k_lo, &tmp);
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_last / ug, &tmp, &k_hi);
+    if (k_lo < s_lo) k_lo = s_lo;
+    if (k_hi > s_hi) k_hi = s_hi;
+    if (k_hi < k_lo) k_hi = k_lo;
+    const int nkeys = uniform32((int)(k_hi - k_lo));
+    const int ntiles = (nkeys + PF_KT - 1) / PF_KT;
+    const int nlast = nkeys - (ntiles - 1) * PF_KT;
+    int tf_lo, tf_hi;
+    {
+        const int w_first = min(wg_row_first + wave * RW, m_kv - 1);
+        const int w_last = min(wg_row_first + wave * RW + RW - 1, m_kv - 1);
+        int64_t a0, b0, full_lo, full_hi;
+        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_first / ug, &a0, &full_hi);
+        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_last / ug, &full_lo, &b0);
+        int64_t lo_t = full_lo - k_lo;
+        lo_t = lo_t <= 0 ? 0 : (lo_t + PF_KT - 1) / PF_KT;
+        int64_t hi_t = full_hi - k_lo;
+        hi_t = hi_t <= 0 ? 0 : hi_t / PF_KT;
+        if (hi_t > ntiles - (nlast < PF_KT ? 1 : 0)) hi_t = ntiles - (nlast < PF_KT ? 1 : 0);
+        tf_lo = uniform32((int)(lo_t < ntiles ? lo_t : ntiles));
+        tf_hi = uniform32((int)hi_t);
+    }
+    const unsigned tf_n = tf_hi > tf_lo ? (unsigned)(tf_hi - tf_lo) : 0u;
+    int rlo0, rhi0;
+    {
+        int64_t x = r_lo - k_lo, y = r_hi - k_lo;
+        rlo0 = (int)(x < 0 ? 0 : (x > nkeys ? nkeys : x));
+        rhi0 = (int)(y < 0 ? 0 : (y > nkeys ? nkeys : y));
+    }
+
+    // Q^T B operands: lane holds row j, features 32 ks + 8 g .. + 7.
+    u32x4 qb[KS];
+    {
+        const uint8_t *qrow = reinterpret_cast<const uint8_t *>(pv.q) +
+                              ((int64_t)t_row * pv.q_row_stride + (int64_t)h_row * D) * 2;
+        for (int ks = 0; ks < KS; ++ks)
+            qb[ks] = *gload_ptr<u32x4>(qrow + 64 * ks + 16 * g);
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0), as in attn_prefill
+    }
+
+    f32x4 acc[FB];
+    for (int fb = 0; fb < FB; ++fb)
+        for (int i = 0; i < 4; ++i) acc[fb][i] = 0.0f;
+    float m_run = NEG_INF, l_run = 0.0f, nbase_run = BASE_NONE;
+    float amax_run = 0.0f;
+    bool bad = false;
+    const float ycap = p.softcap_y;
+    const float tmul = CAP ? p.softcap_log2 : p.scale_log2;
+    bool huge = false;
+
+    const int prow = uniform32((int)(pv.sg.row_stride * 2));
+    const int64_t first = (int64_t)kvh * pv.sg.head_stride + (k_lo - seg_start) * pv.sg.row_stride;
+    const uint8_t *k_next = reinterpret_cast<const uint8_t *>(pv.sg.k) + uniform64(first * 2);
+    const uint8_t *v_next = reinterpret_cast<const uint8_t *>(pv.sg.v) + uniform64(first * 2);
+    int off_full[RPW], off_last[RPW];
+    for (int i = 0; i < RPW; ++i) {
+        const int pos = (wave * RPW + i) * 1024 + lane * 16;
+        const int rr = pos / L::row;
+        const int cc = (((pos % L::row) >> 4) ^ L::swz(rr)) * 16;
+        off_full[i] = rr * prow + cc;
+        off_last[i] = (rr < nlast ? rr : nlast - 1) * prow + cc;
+    }
+    int t_next = 0;
+    const uint32_t run0 = (uint32_t)uniform32(wave) * (RPW * 1024);
+    auto issue = [&](auto stg_tag, auto full_tag) {
+        constexpr int STG = decltype(stg_tag)::value;
+        constexpr bool FULL = decltype(full_tag)::value;
+        const uint32_t mk = (uint32_t)(uintptr_t)(lds + L::k_at(STG)) + run0;
+        const uint32_t mv = (uint32_t)(uintptr_t)(lds + L::v_at(STG)) + run0;
+        if (!FULL && t_next == ntiles - 1) {
+            for (int i = 0; i < RPW; ++i) {
+                dma16(k_next, (uint32_t)off_last[i], mk + i * 1024);
+                dma16(v_next, (uint32_t)off_last[i], mv + i * 1024);
+            }
+        } else {
+            for (int i = 0; i < RPW; ++i) {
+                dma16(k_next, (uint32_t)off_full[i], mk + i * 1024);
+                dma16(v_next, (uint32_t)off_full[i], mv + i * 1024);
+            }
+        }
+        k_next += PF_KT * prow;
+        v_next += PF_KT * prow;
+        ++t_next;
+    };
+    auto wait_tile = [&](int t) {
+        const int ahead = t_next - 1 - t;
+        ring_sync<LPT, NS - 2>(ahead);
+    };
+
+    // K operand of k-step ks: key row j of a 16-key block (the swizzle of row
+    // 16 kb + j equals row j's at these row sizes), chunk 4 ks + g.
+    static_assert(L::swz(16) == L::swz(0) && L::swz(17) == L::swz(1), "16-key blocks share the swizzle");
+    int k_off[KS];
+    for (int ks = 0; ks < KS; ++ks) k_off[ks] = L::at(j, 4 * ks + g);
+    constexpr int KB_BYTES = 16 * L::row;  // second 16-key block
+    // V^T operand of feature block fb: row 16 fb + j, chunk g (the swizzle
+    // depends on (row / 4) % 4 = (j / 4) % 4 only).
+    const int vt_off = L::vt_at(j, g);
+    constexpr int VPF = 4;
+    auto vt_buf = [&](int tile_stage) { return lds + L::vt_base + (tile_stage % L::vt_bufs) * L::vt_bytes; };
+    auto vt_operand = [&](lds_ptr<uint8_t> buf, int fb) {
+        return *(lds_ptr<u32x4>)(buf + vt_off + fb * 16 * L::vt_row);
+    };
+    auto k_operand = [&](lds_ptr<uint8_t> kt, int m) {  // MFMA m: block m % 2, k-step m / 2
+        return *(lds_ptr<u32x4>)(kt + (m % 2) * KB_BYTES + k_off[m / 2]);
+    };
+    static_for<NS - 1>([&](auto stg) {
+        if (decltype(stg)::value < ntiles) issue(stg, std::false_type{});
+    });
+    f32x4 st[2];
+    for (int kb = 0; kb < 2; ++kb)
+        for (int i = 0; i < 4; ++i) st[kb][i] = 0.0f;
+    VTranspose<D, W, VCONV, true> vtr(threadIdx.x);
+    if (ntiles > 0) {
+        // Iteration 0's P.V reads the buffer of "tile -1": zeros, which the
+        // zero probabilities of iteration 0 multiply.
+        lds_ptr<uint8_t> z = vt_buf(NS - 1);
+        for (int i = threadIdx.x; i < L::vt_bytes / 16; i += 64 * W)
+            *(lds_ptr<u32x4>)(z + 16 * i) = u32x4{0, 0, 0, 0};
+        wait_tile(0);
+        for (int m = 0; m < NQK; ++m)
+            st[m % 2] = mfma16<DT>(k_operand(lds + L::k_at(0), m), qb[m / 2], st[m % 2]);
+        vtr.read(lds + L::v_at(0));
+        vtr.write(lds + L::vt_base);
+    }
+    uint32_t ph[4];  // the probabilities of the tile whose P.V is pending (f16 pairs)
+    for (int i = 0; i < 4; ++i) ph[i] = 0u;
+    int t = 0;
+    f32x4 st_b[2];
+    bool bulk = false;
+    // The exact path, rare (as in attn_prefill): some lane's tile mass exceeds
+    // MASS_LIMIT.  The wave moves each such row's base to the tile maximum,
+    // rescales O (tiles up to t - 1) and l, and forms tile t's probabilities
+    // again.
+    auto close_tile = [&](f32x4 (&st)[2], float shift, float &lt) {
+        if (__ballot(!(lt <= MASS_LIMIT)) != 0) {
+            float hi = st[0][0];
+            for (int kb = 0; kb < 2; ++kb)
+                for (int i = 0; i < 4; ++i) hi = maxn(hi, st[kb][i]);
+            hi = row4_max(hi) + shift;
+            const float m_new = fmaxf(m_run, hi);
+            if (m_new > m_run) {
+                const float corr = m_run == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * tmul);
+                l_run *= corr;
+                for (int fb = 0; fb < FB; ++fb)
+                    for (int i = 0; i < 4; ++i) acc[fb][i] *= corr;
+                m_run = m_new;
+            }
+            if constexpr (!CAP)
+                huge = __ballot(m_run != NEG_INF && fabsf(m_run * tmul) >= 1024.0f) != 0;
+            nbase_run = m_run == NEG_INF ? BASE_NONE : -m_run * tmul;
+            const float delta = m_run == NEG_INF ? 0.0f : m_run - shift;
+            const float nb = -delta * tmul;
+            lt = 0.0f;
+            for (int i = 0; i < 4; ++i) {
+                const int kb = i >> 1, r = 2 * (i & 1);
+                float y0, y1;
+                if (!CAP && huge) {
+                    y0 = (st[kb][r] - delta) * tmul;
+                    y1 = (st[kb][r + 1] - delta) * tmul;
+                } else {
+                    y0 = __builtin_fmaf(st[kb][r], tmul, nb);
+                    y1 = __builtin_fmaf(st[kb][r + 1], tmul, nb);
+                }
+                ph[i] = pack2<PDT>(__builtin_amdgcn_exp2f(y0), __builtin_amdgcn_exp2f(y1));
+                lt = add_pair(ph[i], lt);
+            }
+        }
+        l_run += lt;
+    };
+    // Iteration t: (1) P.V of tile t - 1 with tile t's statistics and first
+    // two probability pairs between the MFMAs; (2) wait for tile t + 1 and hand
+    // the stage of tile t - 1 to a new load; (3) the scores of tile t + 1 with
+    // tile t's last two pairs and tile t + 1's V transposition between them.
+    auto body = [&](auto stg_tag, f32x4 (&st)[2], f32x4 (&st_next)[2]) {
+        constexpr int STG = decltype(stg_tag)::value;
+        constexpr int STG_NEXT = (STG + 1) % NS;
+        __builtin_amdgcn_sched_barrier(0);
+        lds_ptr<uint8_t> vtp = vt_buf((STG + NS - 1) % NS);  // tile t - 1's V^T
+        lds_ptr<uint8_t> kn = lds + L::k_at(STG_NEXT);
+        float nbase = nbase_run;
+        float shift = 0.0f;
+        float lt = 0.0f;
+        uint32_t nh[2];
+        u32x4 vq[VPF];
+        for (int i = 0; i < VPF; ++i) vq[i] = vt_operand(vtp, i);
+        const u32x4 bv = u32x4{ph[0], ph[1], ph[2], ph[3]};
+#pragma unroll
+        for (int k = 0; k < FB; ++k) {
+            const u32x4 a = vq[k % VPF];
+            if (k + VPF < FB) vq[k % VPF] = vt_operand(vtp, k + VPF);
+            acc[k] = mfma16<PDT>(a, bv, acc[k]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k == 0) {
+                if (bulk || (unsigned)(t - tf_lo) < tf_n) {  // t in [tf_lo, tf_hi)
+                    float am = amax_run;
+                    for (int kb = 0; kb < 2; ++kb)
+                        for (int i = 0; i < 4; ++i) am = maxn(am, __builtin_fabsf(st[kb][i]));
+                    amax_run = am;
+                    if constexpr (CAP)
+                        for (int kb = 0; kb < 2; ++kb)
+                            for (int i = 0; i < 4; ++i) st[kb][i] = tanh_fast(st[kb][i] * ycap);
+                } else {
+                    const int lo_rel = min(max(rlo0 - t * PF_KT, 0), PF_KT);
+                    const int hi_rel = min(max(rhi0 - t * PF_KT, 0), PF_KT);
+                    for (int kb = 0; kb < 2; ++kb)
+                        for (int i = 0; i < 4; ++i) {
+                            const int kk = 16 * kb + 4 * g + i;
+                            const bool vis = kk >= lo_rel && kk < hi_rel;
+                            bad |= vis && !(__builtin_fabsf(st[kb][i]) < -NEG_INF);
+                            if constexpr (CAP) st[kb][i] = vis ? tanh_fast(st[kb][i] * ycap) : NEG_INF;
+                            else st[kb][i] = vis ? st[kb][i] : NEG_INF;
+                        }
+                }
+            }
+            if constexpr (!CAP) {
+                if (k == 1 && huge) {
+                    shift = m_run == NEG_INF ? 0.0f : m_run;
+                    for (int kb = 0; kb < 2; ++kb)
+                        for (int i = 0; i < 4; ++i) st[kb][i] -= shift;
+                    nbase = m_run == NEG_INF ? BASE_NONE : 0.0f;
+                }
+            }
+            // Tile t's first two pairs (tile t - 1's are still being read).
+            for (int i = 0; i < 2; ++i) {
+                if (k == 2 + (i * (FB - 2)) / 2) {
+                    const int kb = i >> 1, r = 2 * (i & 1);
+                    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][r], tmul, nbase));
+                    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][r + 1], tmul, nbase));
+                    nh[i] = pack2<PDT>(e0, e1);
+                    lt = add_pair(nh[i], lt);
+                    asm volatile("" : "+v"(nh[i]), "+v"(lt));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        ph[0] = nh[0];
+        ph[1] = nh[1];
+
+        if (bulk) {
+            ring_sync_fixed<LPT, NS - 3>();
+            issue(std::integral_constant<int, (STG + NS - 1) % NS>{}, std::true_type{});
+        } else if (t + 1 < ntiles) {
+            wait_tile(t + 1);
+            if (t_next < ntiles) issue(std::integral_constant<int, (STG + NS - 1) % NS>{}, std::false_type{});
+        } else {
+            __syncthreads();
+        }
+
+        constexpr int KPRE = 3;
+        for (int kb = 0; kb < 2; ++kb)
+            for (int i = 0; i < 4; ++i) st_next[kb][i] = 0.0f;
+        u32x4 kq[KPRE];
+        for (int i = 0; i < KPRE; ++i) kq[i] = k_operand(kn, i);
+        lds_ptr<uint8_t> vn = lds + L::v_at(STG_NEXT);
+        lds_ptr<uint8_t> vtn = vt_buf(STG_NEXT);
+#pragma unroll
+        for (int m = 0; m < NQK; ++m) {
+            const u32x4 kcur = kq[m % KPRE];
+            if (m + KPRE < NQK) kq[m % KPRE] = k_operand(kn, m + KPRE);
+            st_next[m % 2] = mfma16<DT>(kcur, qb[m / 2], st_next[m % 2]);
+            if (m == 0) __builtin_amdgcn_s_setprio(1);
+            if (m == NQK / 2) __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (m == 0) vtr.read(vn);
+            if (m == NQK / 2) vtr.write(vtn);
+            for (int i = 2; i < 4; ++i) {
+                if (m == 1 + ((i - 2) * (NQK - 2)) / 2) {
+                    const int kb = i >> 1, r = 2 * (i & 1);
+                    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][r], tmul, nbase));
+                    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][r + 1], tmul, nbase));
+                    ph[i] = pack2<PDT>(e0, e1);
+                    lt = add_pair(ph[i], lt);
+                    asm volatile("" : "+v"(ph[i]), "+v"(lt));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        close_tile(st, shift, lt);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    while (t < ntiles) {
+        bulk = t >= tf_lo && t + NS <= tf_hi && t + 2 * NS - 1 < ntiles && t_next == t + NS - 1;
+        static_for<NS>([&](auto k) {
+            constexpr int K = decltype(k)::value;
+            if (t >= ntiles) return;
+            if constexpr (K % 2 == 0) body(std::integral_constant<int, K>{}, st, st_b);
+            else body(std::integral_constant<int, K>{}, st_b, st);
+            ++t;
+        });
+        if constexpr (NS % 2 == 1) {
+            st[0] = st_b[0];
+            st[1] = st_b[1];
+        }
+    }
+    // P.V of the last tile.
+    if (ntiles > 0) {
+        lds_ptr<uint8_t> vtl = vt_buf((ntiles - 1) % NS);
+        const u32x4 bv = u32x4{ph[0], ph[1], ph[2], ph[3]};
+#pragma unroll
+        for (int fb = 0; fb < FB; ++fb) acc[fb] = mfma16<PDT>(vt_operand(vtl, fb), bv, acc[fb]);
+    }
+    bad |= !(amax_run < -NEG_INF);
+    l_run = row4_sum(l_run);
+    bool bad_acc = false;
+    for (int fb = 0; fb < FB; ++fb)
+        for (int i = 0; i < 4; ++i) bad_acc |= !is_finite_f(acc[fb][i]);
+    // bf16 V above f16's range: the rows again on the vector unit in FP32, as
+    // in attn_prefill (lane (j, g) holds Q features 32 ks + 8 g .. + 7 and
+    // context features 16 fb + 4 g .. + 3 of row j; a score is the four lanes'
+    // partial dots added).
+    if constexpr (VCONV) {
+        if (__ballot(bad_acc && !bad) != 0) {
+            constexpr int CPR = D * 2 / 16;
+            constexpr int RPI = 64 / CPR;
+            const uint8_t *vrows = reinterpret_cast<const uint8_t *>(pv.sg.v) + first * 2;
+            const uint8_t *krows = reinterpret_cast<const uint8_t *>(pv.sg.k) + first * 2;
+            bool nonfinite = false, big = false;
+            for (int r0 = 0; r0 < nkeys; r0 += RPI) {
+                const int r = r0 + lane / CPR;
+                if (r < nkeys) {
+                    const u32x4 w = *gload_ptr<u32x4>(vrows + (int64_t)r * prow + 16 * (lane % CPR));
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t x = w[e];
+                        const uint32_t lo = x & 0x7fffu, hi = (x >> 16) & 0x7fffu;
+                        nonfinite |= lo >= 0x7f80u || hi >= 0x7f80u;
+                        big |= lo >= 0x4780u || hi >= 0x4780u;
+                    }
+                }
+            }
+            if (__ballot(nonfinite) == 0 && __ballot(big) != 0) {
+                for (int fb = 0; fb < FB; ++fb)
+                    for (int i = 0; i < 4; ++i) acc[fb][i] = 0.0f;
+                float l = 0.0f;
+                const bool any = m_run != NEG_INF;
+                for (int kk = 0; kk < nkeys; ++kk) {
+                    const uint8_t *kr = krows + (int64_t)kk * prow;
+                    float d = 0.0f;
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const u32x4 kw = *gload_ptr<u32x4>(kr + 64 * ks + 16 * g);
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t qw = qb[ks][e], kx = kw[e];
+                            d = __builtin_fmaf(lo_f<BF16>(qw), lo_f<BF16>(kx), d);
+                            d = __builtin_fmaf(hi_f<BF16>(qw), hi_f<BF16>(kx), d);
+                        }
+                    }
+                    d = row4_sum(d);
+                    float y;
+                    if constexpr (CAP) y = (tanh_fast(d * ycap) - m_run) * tmul;
+                    else y = (d - m_run) * tmul;
+                    const bool vis = any && kk >= rlo0 && kk < rhi0;
+                    const float pk = vis ? __builtin_amdgcn_exp2f(y) : 0.0f;
+                    l += pk;
+                    const uint8_t *vr = vrows + (int64_t)kk * prow;
+                    for (int fb = 0; fb < FB; ++fb) {
+                        const u32x2 vw = *gload_ptr<u32x2>(vr + (16 * fb + 4 * g) * 2);
+                        const uint32_t v0 = vw[0], v1 = vw[1];
+                        acc[fb][0] = __builtin_fmaf(pk, lo_f<BF16>(v0), acc[fb][0]);
+                        acc[fb][1] = __builtin_fmaf(pk, hi_f<BF16>(v0), acc[fb][1]);
+                        acc[fb][2] = __builtin_fmaf(pk, lo_f<BF16>(v1), acc[fb][2]);
+                        acc[fb][3] = __builtin_fmaf(pk, hi_f<BF16>(v1), acc[fb][3]);
+                    }
+                }
+                l_run = l;  // every lane of the row summed every key
+                bad_acc = false;
+                for (int fb = 0; fb < FB; ++fb)
+                    for (int i = 0; i < 4; ++i) bad_acc |= !is_finite_f(acc[fb][i]);
+            }
+        }
+    }
+    bad |= bad_acc;
+
+    const bool single = pv.splits == 1;
+    bool bad_mass = false, bad_out = false;
+    if (single) {
+        if (rvalid) {
+            const float inv = 1.0f / l_run;
+            bad_mass |= !(l_run > 0.0f) || !is_finite_f(l_run);
+            float *orow = pv.out + ((int64_t)t_row * Hq + h_row) * D;
+            for (int fb = 0; fb < FB; ++fb) {
+                f32x4 v;
+                for (int r = 0; r < 4; ++r) {
+                    v[r] = acc[fb][r] * inv;
+                    bad_out |= !is_finite_f(v[r]);
+                }
+                *gstore_ptr<f32x4>(orow + 16 * fb + 4 * g) = v;
+            }
+        }
+        raise_status(p, bad, ST_NONFINITE_INPUT);
+        raise_status(p, bad_mass, ST_BAD_MASS);
+        raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
+        return;
+    }
+    // Split-K partial in attn_prefill's slot format (feature-major context,
+    // (max, mass) per row): lanes j of a feature store 16 consecutive rows.
+    raise_status(p, bad, ST_NONFINITE_INPUT);
+    const int64_t group = (int64_t)kvh * pv.row_blocks + rb;
+    const int64_t slot = pv.slot_base + group * pv.splits + split;
+    float *pf = p.part_o + slot * ROWS * D + wave * RW + j;
+    for (int fb = 0; fb < FB; ++fb)
+        for (int r = 0; r < 4; ++r)
+            *gstore_ptr<float>(pf + (int64_t)(16 * fb + 4 * g + r) * ROWS) = acc[fb][r];
+    if (g == 0) {
+        const f32x2 ml = {m_run, l_run};
+        *gstore_ptr<f32x2>(p.part_ml + (slot * ROWS + wave * RW + j) * 2) = ml;
+    }
+}
+
 // Merge of the split-K partials of attn_prefill.  Merge block b covers 64
 // packed rows and 16 features of one (problem, KV head, row block); each
 // thread owns four features of one row and reads the S partials of its row at
@@ -1269,5 +1787,24 @@ extern "C" hipError_t tkh_launch_prefill(const tkh::PrefillArgs *p, int dtype, i
     TKH_PF(BF16, 64, 4) TKH_PF(BF16, 128, 4) TKH_PF(BF16, 128, 8) TKH_PF(BF16, 256, 4)
     TKH_PF(F16, 64, 4) TKH_PF(F16, 128, 4) TKH_PF(F16, 128, 8) TKH_PF(F16, 256, 4)
 #undef TKH_PF
+    return hipErrorInvalidValue;
+}
+
+// The 16-row form of a four-wave (128-row) launch: same grid and workspace.
+extern "C" hipError_t tkh_launch_prefill16(const tkh::PrefillArgs *p, int dtype, int head_dim,
+                                           int64_t groups, hipStream_t stream, hipEvent_t start,
+                                           hipEvent_t stop) {
+    using namespace tkh;
+    dim3 grid((unsigned)groups), block(64 * PF16_WAVES);
+#define TKH_PF16(DT, DD)                                                                \
+    if (dtype == DT && head_dim == DD) {                                                \
+        if (p->p.softcap != 0.0f)                                                       \
+            hipExtLaunchKernelGGL((attn_prefill16<DT, DD, true>), grid, block, 0, stream, start, stop, 0, *p);  \
+        else                                                                            \
+            hipExtLaunchKernelGGL((attn_prefill16<DT, DD, false>), grid, block, 0, stream, start, stop, 0, *p); \
+        return hipGetLastError();                                                       \
+    }
+    TKH_PF16(BF16, 128) TKH_PF16(BF16, 256) TKH_PF16(F16, 128) TKH_PF16(F16, 256)
+#undef TKH_PF16
     return hipErrorInvalidValue;
 }
