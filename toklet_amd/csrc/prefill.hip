@@ -39,6 +39,12 @@
 //  * Split-K partials (max, mass, unnormalised context) go to the workspace
 //    and a second, fully parallel kernel (attn_prefill_merge) combines them,
 //    so no single workgroup reads a whole row block's partials.
+//
+// attn_prefill16<DT, D> is the same algorithm with 16 packed rows per wave on
+// v_mfma_f32_16x16x32: eight waves cover the four-wave kernel's 128-row block
+// (same grid, workspace slots and merge).  The host takes it for head_dim 256,
+// where a 32-row wave needs a whole SIMD's registers and a 16-row wave half of
+// them, so two waves share each SIMD.
 #include <cstddef>
 #include <type_traits>
 #include <utility>
