@@ -419,6 +419,161 @@ __device__ __forceinline__ void pf_locate(const Params &p, PfView &pv, int &rb, 
     }
 }
 
+// One lane's query row and its workgroup's key range inside the split.
+struct PfRows {
+    int m_kv;              // packed rows of the (problem, KV head)
+    int t_row, h_row;      // this lane's token and query head (a valid row's)
+    bool rvalid;           // the lane's row exists
+    int64_t k_lo;          // first key of the workgroup's range (absolute)
+    int nkeys, ntiles, nlast;  // keys, tiles and keys of the last tile
+    int tf_lo, tf_hi;      // tiles [tf_lo, tf_hi) are visible to every row of the wave
+    int rlo0, rhi0;        // this row's visible keys relative to k_lo
+};
+
+// The rows of workgroup row block `rb` (ROWS rows, RW per wave): lane row j of
+// `wave`, the union of the rows' visible keys clipped to split `sidx`, and
+// the tiles no row of the wave masks.
+template <int ROWS, int RW>
+__device__ __forceinline__ PfRows pf_rows(const Params &p, const PfView &pv, int rb, int kvh, int sidx,
+                                          int wave, int j) {
+    PfRows r;
+    const int G = p.group;
+    r.m_kv = pv.queries * G;
+    const int m_kv = r.m_kv;
+    const int64_t seg_start = pv.sg.start;
+    const int64_t seg_end = seg_start + pv.sg.keys;
+    const int64_t seg_lo = seg_start > pv.vis_lo ? seg_start : pv.vis_lo;
+    const int64_t seg_hi = seg_end < pv.vis_hi ? seg_end : pv.vis_hi;
+    const int64_t s_lo = seg_lo + (int64_t)sidx * pv.split_keys;
+    const int64_t s_hi = s_lo + pv.split_keys < seg_hi ? s_lo + pv.split_keys : seg_hi;
+
+    // This lane's query row.
+    const int row = rb * ROWS + wave * RW + j;
+    r.rvalid = row < m_kv;
+    const int rrow = r.rvalid ? row : m_kv - 1;
+    // Rows and the group are non-negative: unsigned divisions (shorter sequences).
+    const uint32_t ug = (uint32_t)G;
+    r.t_row = (int)((uint32_t)rrow / ug);
+    r.h_row = kvh * G + (int)((uint32_t)rrow % ug);
+    int64_t r_lo, r_hi;
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + r.t_row, &r_lo, &r_hi);
+    if (!r.rvalid) r_hi = r_lo;  // no visible keys: never contributes, never stored
+
+    // Key range of the workgroup: the union over its rows, clipped to the split.
+    const int wg_row_first = rb * ROWS;
+    const int wg_row_last = min(wg_row_first + ROWS, m_kv) - 1;
+    int64_t k_lo, k_hi, tmp;
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_first / ug, &k_lo, &tmp);
+    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_last / ug, &tmp, &k_hi);
+    if (k_lo < s_lo) k_lo = s_lo;
+    if (k_hi > s_hi) k_hi = s_hi;
+    if (k_hi < k_lo) k_hi = k_lo;
+    r.k_lo = k_lo;
+    const int nkeys = uniform32((int)(k_hi - k_lo));
+    const int ntiles = (nkeys + PF_KT - 1) / PF_KT;
+    const int nlast = nkeys - (ntiles - 1) * PF_KT;
+    r.nkeys = nkeys;
+    r.ntiles = ntiles;
+    r.nlast = nlast;
+    {
+        const int w_first = min(wg_row_first + wave * RW, m_kv - 1);
+        const int w_last = min(wg_row_first + wave * RW + RW - 1, m_kv - 1);
+        int64_t a, b, full_lo, full_hi;
+        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_first / ug, &a, &full_hi);
+        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_last / ug, &full_lo, &b);
+        int64_t lo_t = full_lo - k_lo;
+        lo_t = lo_t <= 0 ? 0 : (lo_t + PF_KT - 1) / PF_KT;
+        int64_t hi_t = full_hi - k_lo;
+        hi_t = hi_t <= 0 ? 0 : hi_t / PF_KT;
+        if (hi_t > ntiles - (nlast < PF_KT ? 1 : 0)) hi_t = ntiles - (nlast < PF_KT ? 1 : 0);
+        r.tf_lo = uniform32((int)(lo_t < ntiles ? lo_t : ntiles));
+        r.tf_hi = uniform32((int)hi_t);
+    }
+    {
+        int64_t x = r_lo - k_lo, y = r_hi - k_lo;
+        r.rlo0 = (int)(x < 0 ? 0 : (x > nkeys ? nkeys : x));
+        r.rhi0 = (int)(y < 0 ? 0 : (y > nkeys ? nkeys : y));
+    }
+    return r;
+}
+
+// The ring's direct loads: K/V tiles of PF_KT keys into stages of LDS layout
+// L, RPW 1 KiB runs per wave and tile.  Rows past the last tile's keys repeat
+// a valid row.
+template <class L> struct PfRing {
+    static constexpr int RPW = L::runs_per_wave;
+    const uint8_t *k_next, *v_next;  // the next tile's first rows
+    int64_t first;                   // element offset of the range's first row
+    int prow;                        // bytes between keys
+    int ntiles, t_next;
+    uint32_t run0;                   // this wave's first run inside a tile (scalar)
+    int off_full[RPW], off_last[RPW];
+    __device__ __forceinline__ PfRing(const PfView &pv, int kvh, const PfRows &r, int wave, int lane) {
+        prow = uniform32((int)(pv.sg.row_stride * 2));
+        first = (int64_t)kvh * pv.sg.head_stride + (r.k_lo - pv.sg.start) * pv.sg.row_stride;
+        k_next = reinterpret_cast<const uint8_t *>(pv.sg.k) + uniform64(first * 2);
+        v_next = reinterpret_cast<const uint8_t *>(pv.sg.v) + uniform64(first * 2);
+        for (int i = 0; i < RPW; ++i) {
+            const int pos = (wave * RPW + i) * 1024 + lane * 16;
+            const int rr = pos / L::row;
+            const int cc = (((pos % L::row) >> 4) ^ L::swz(rr)) * 16;
+            off_full[i] = rr * prow + cc;
+            off_last[i] = (rr < r.nlast ? rr : r.nlast - 1) * prow + cc;
+        }
+        ntiles = r.ntiles;
+        t_next = 0;
+        run0 = (uint32_t)uniform32(wave) * (RPW * 1024);
+    }
+    // Issue the next tile into stage STG (a compile-time stage: the LDS
+    // destinations are scalar constants plus run0).  FULL: the caller knows
+    // this is not the last tile.
+    template <int STG, bool FULL> __device__ __forceinline__ void issue(lds_ptr<uint8_t> lds) {
+        const uint32_t mk = (uint32_t)(uintptr_t)(lds + L::k_at(STG)) + run0;
+        const uint32_t mv = (uint32_t)(uintptr_t)(lds + L::v_at(STG)) + run0;
+        if (!FULL && t_next == ntiles - 1) {
+            for (int i = 0; i < RPW; ++i) {
+                dma16(k_next, (uint32_t)off_last[i], mk + i * 1024);
+                dma16(v_next, (uint32_t)off_last[i], mv + i * 1024);
+            }
+        } else {
+            for (int i = 0; i < RPW; ++i) {
+                dma16(k_next, (uint32_t)off_full[i], mk + i * 1024);
+                dma16(v_next, (uint32_t)off_full[i], mv + i * 1024);
+            }
+        }
+        k_next += PF_KT * prow;
+        v_next += PF_KT * prow;
+        ++t_next;
+    }
+    // Wait for tile `t` (issued earlier) and synchronise the workgroup.
+    __device__ __forceinline__ void wait(int t) {
+        const int ahead = t_next - 1 - t;  // later tiles still allowed in flight
+        ring_sync<2 * RPW, L::stages - 2>(ahead);
+    }
+};
+
+// bf16 V rows [0, nkeys) of the range: any non-finite value, any of magnitude
+// 2^16 or more (beyond what the f16 P.V operands hold), by the whole wave.
+__device__ __forceinline__ void pf_scan_v(const uint8_t *vrows, int nkeys, int prow, int D, int lane,
+                                          bool &nonfinite, bool &big) {
+    const int cpr = D * 2 / 16;  // 16-byte chunks per row
+    const int rpi = 64 / cpr;    // rows per wave iteration
+    nonfinite = false;
+    big = false;
+    for (int r0 = 0; r0 < nkeys; r0 += rpi) {
+        const int r = r0 + lane / cpr;
+        if (r < nkeys) {
+            const u32x4 w = *gload_ptr<u32x4>(vrows + (int64_t)r * prow + 16 * (lane % cpr));
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t x = w[e];
+                const uint32_t lo = x & 0x7fffu, hi = (x >> 16) & 0x7fffu;
+                nonfinite |= lo >= 0x7f80u || hi >= 0x7f80u;  // bf16 inf / NaN
+                big |= lo >= 0x4780u || hi >= 0x4780u;        // |v| >= 65536
+            }
+        }
+    }
+}
+
 template <int DT, int D, bool CAP, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill(PrefillArgs a) {
     // The problem's fields are read by dependent scalar loads (the batch
@@ -451,63 +606,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     PfView pv;
     int rb, split, kvh, sidx;
     pf_locate<D>(p, pv, rb, split, kvh, sidx);
-    const int m_kv = pv.queries * G;
-    const int64_t seg_start = pv.sg.start;
-    const int64_t seg_end = seg_start + pv.sg.keys;
-    const int64_t seg_lo = seg_start > pv.vis_lo ? seg_start : pv.vis_lo;
-    const int64_t seg_hi = seg_end < pv.vis_hi ? seg_end : pv.vis_hi;
-    const int64_t s_lo = seg_lo + (int64_t)sidx * pv.split_keys;
-    const int64_t s_hi = s_lo + pv.split_keys < seg_hi ? s_lo + pv.split_keys : seg_hi;
-
-    // This lane's query row.
-    const int row = rb * ROWS + wave * 32 + j;
-    const bool rvalid = row < m_kv;
-    const int rrow = rvalid ? row : m_kv - 1;
-    // Rows and the group are non-negative: unsigned divisions (shorter sequences).
-    const uint32_t ug = (uint32_t)G;
-    const int t_row = (int)((uint32_t)rrow / ug), h_row = kvh * G + (int)((uint32_t)rrow % ug);
-    int64_t r_lo, r_hi;
-    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + t_row, &r_lo, &r_hi);
-    if (!rvalid) r_hi = r_lo;  // no visible keys: never contributes, never stored
-
-    // Key range of the workgroup: the union over its rows, clipped to the split.
-    const int wg_row_first = rb * ROWS;
-    const int wg_row_last = min(wg_row_first + ROWS, m_kv) - 1;
-    int64_t k_lo, k_hi, tmp;
-    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_first / ug, &k_lo, &tmp);
-    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_last / ug, &tmp, &k_hi);
-    if (k_lo < s_lo) k_lo = s_lo;
-    if (k_hi > s_hi) k_hi = s_hi;
-    if (k_hi < k_lo) k_hi = k_lo;
-    const int nkeys = uniform32((int)(k_hi - k_lo));
-    const int ntiles = (nkeys + PF_KT - 1) / PF_KT;
-    const int nlast = nkeys - (ntiles - 1) * PF_KT;  // keys of the last tile
-    // Tiles [tf_lo, tf_hi) are visible to every row of this wave (no mask).
-    int tf_lo, tf_hi;
-    {
-        const int w_first = min(wg_row_first + wave * 32, m_kv - 1);
-        const int w_last = min(wg_row_first + wave * 32 + 31, m_kv - 1);
-        int64_t a, b, full_lo, full_hi;
-        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_first / ug, &a, &full_hi);
-        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_last / ug, &full_lo, &b);
-        int64_t lo_t = full_lo - k_lo;
-        lo_t = lo_t <= 0 ? 0 : (lo_t + PF_KT - 1) / PF_KT;
-        int64_t hi_t = full_hi - k_lo;
-        hi_t = hi_t <= 0 ? 0 : hi_t / PF_KT;
-        if (hi_t > ntiles - (nlast < PF_KT ? 1 : 0)) hi_t = ntiles - (nlast < PF_KT ? 1 : 0);
-        tf_lo = uniform32((int)(lo_t < ntiles ? lo_t : ntiles));
-        tf_hi = uniform32((int)hi_t);
-    }
+    const PfRows rows = pf_rows<ROWS, 32>(p, pv, rb, kvh, sidx, wave, j);
+    const int t_row = rows.t_row, h_row = rows.h_row;
+    const bool rvalid = rows.rvalid;
+    const int nkeys = rows.nkeys, ntiles = rows.ntiles;
+    const int tf_lo = rows.tf_lo, tf_hi = rows.tf_hi, rlo0 = rows.rlo0, rhi0 = rows.rhi0;
     // Fully visible tiles as a width, for one unsigned test per tile (none
     // when hi < lo, which happens for waves that see no whole tile).
     const unsigned tf_n = tf_hi > tf_lo ? (unsigned)(tf_hi - tf_lo) : 0u;
-    // This row's visible keys relative to k_lo.
-    int rlo0, rhi0;
-    {
-        int64_t x = r_lo - k_lo, y = r_hi - k_lo;
-        rlo0 = (int)(x < 0 ? 0 : (x > nkeys ? nkeys : x));
-        rhi0 = (int)(y < 0 ? 0 : (y > nkeys ? nkeys : y));
-    }
 
     // Q^T B operands: lane holds row j, features 16 ks + 8 h .. + 7.
     u32x4 qb[KS];
@@ -548,51 +654,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     bool huge = false;
 
     // ---- K/V tiles: PF_KT keys each, issued into an NS-stage LDS ring.
-    const int prow = uniform32((int)(pv.sg.row_stride * 2));  // bytes between keys
-    const int64_t first = (int64_t)kvh * pv.sg.head_stride + (k_lo - seg_start) * pv.sg.row_stride;
-    const uint8_t *k_next = reinterpret_cast<const uint8_t *>(pv.sg.k) + uniform64(first * 2);
-    const uint8_t *v_next = reinterpret_cast<const uint8_t *>(pv.sg.v) + uniform64(first * 2);
-    // Per-lane offsets of the direct loads (row in the tile, swizzled chunk);
-    // rows past the last tile's keys repeat a valid row.
-    int off_full[RPW], off_last[RPW];
-    for (int i = 0; i < RPW; ++i) {
-        const int pos = (wave * RPW + i) * 1024 + lane * 16;
-        const int rr = pos / L::row;
-        const int cc = (((pos % L::row) >> 4) ^ L::swz(rr)) * 16;
-        off_full[i] = rr * prow + cc;
-        off_last[i] = (rr < nlast ? rr : nlast - 1) * prow + cc;
-    }
-    int t_next = 0;
-    // This wave's first 1 KiB run inside a tile, as a scalar.
-    const uint32_t run0 = (uint32_t)uniform32(wave) * (RPW * 1024);
-    // Issue the next tile into stage STG (a compile-time stage: the LDS
-    // destinations are scalar constants plus run0).
-    // FULL: the caller knows this is not the last tile.
+    PfRing<L> ring(pv, kvh, rows, wave, lane);
+    const int prow = ring.prow;
+    const int64_t first = ring.first;
+    int &t_next = ring.t_next;
     auto issue = [&](auto stg_tag, auto full_tag) {
-        constexpr int STG = decltype(stg_tag)::value;
-        constexpr bool FULL = decltype(full_tag)::value;
-        const uint32_t mk = (uint32_t)(uintptr_t)(lds + L::k_at(STG)) + run0;
-        const uint32_t mv = (uint32_t)(uintptr_t)(lds + L::v_at(STG)) + run0;
-        if (!FULL && t_next == ntiles - 1) {
-            for (int i = 0; i < RPW; ++i) {
-                dma16(k_next, (uint32_t)off_last[i], mk + i * 1024);
-                dma16(v_next, (uint32_t)off_last[i], mv + i * 1024);
-            }
-        } else {
-            for (int i = 0; i < RPW; ++i) {
-                dma16(k_next, (uint32_t)off_full[i], mk + i * 1024);
-                dma16(v_next, (uint32_t)off_full[i], mv + i * 1024);
-            }
-        }
-        k_next += PF_KT * prow;
-        v_next += PF_KT * prow;
-        ++t_next;
+        ring.template issue<decltype(stg_tag)::value, decltype(full_tag)::value>(lds);
     };
-    // Wait for tile `t` (issued earlier) and synchronise the workgroup.
-    auto wait_tile = [&](int t) {
-        const int ahead = t_next - 1 - t;  // later tiles still allowed in flight
-        ring_sync<LPT, NS - 2>(ahead);
-    };
+    auto wait_tile = [&](int t) { ring.wait(t); };
 
     // LDS offsets of this lane's operand reads (tile-relative).
     int k_off[KS];
@@ -1046,23 +1115,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     // finite value.
     if constexpr (VCONV) {
         if (__ballot(bad_acc && !bad) != 0) {
-            constexpr int CPR = D * 2 / 16;  // 16-byte chunks per row
-            constexpr int RPI = 64 / CPR;    // rows per wave iteration
             const uint8_t *vrows = reinterpret_cast<const uint8_t *>(pv.sg.v) + first * 2;
             const uint8_t *krows = reinterpret_cast<const uint8_t *>(pv.sg.k) + first * 2;
-            bool nonfinite = false, big = false;
-            for (int r0 = 0; r0 < nkeys; r0 += RPI) {
-                const int r = r0 + lane / CPR;
-                if (r < nkeys) {
-                    const u32x4 w = *gload_ptr<u32x4>(vrows + (int64_t)r * prow + 16 * (lane % CPR));
-                    for (int e = 0; e < 4; ++e) {
-                        const uint32_t x = w[e];
-                        const uint32_t lo = x & 0x7fffu, hi = (x >> 16) & 0x7fffu;
-                        nonfinite |= lo >= 0x7f80u || hi >= 0x7f80u;  // bf16 inf / NaN
-                        big |= lo >= 0x4780u || hi >= 0x4780u;        // |v| >= 65536
-                    }
-                }
-            }
+            bool nonfinite, big;
+            pf_scan_v(vrows, nkeys, prow, D, lane, nonfinite, big);
             if (__ballot(nonfinite) == 0 && __ballot(big) != 0) {
                 // Lane (j, h) holds Q features 16 ks + 8 h .. + 7 and context
                 // features 32 mb + 8 q + 4 h .. + 3 of row j; a score is the
@@ -1238,56 +1294,12 @@ __global__ __launch_bounds__(64 * PF16_WAVES) __attribute__((amdgpu_waves_per_eu
     PfView pv;
     int rb, split, kvh, sidx;
     pf_locate<D>(p, pv, rb, split, kvh, sidx);
-    const int m_kv = pv.queries * G;
-    const int64_t seg_start = pv.sg.start;
-    const int64_t seg_end = seg_start + pv.sg.keys;
-    const int64_t seg_lo = seg_start > pv.vis_lo ? seg_start : pv.vis_lo;
-    const int64_t seg_hi = seg_end < pv.vis_hi ? seg_end : pv.vis_hi;
-    const int64_t s_lo = seg_lo + (int64_t)sidx * pv.split_keys;
-    const int64_t s_hi = s_lo + pv.split_keys < seg_hi ? s_lo + pv.split_keys : seg_hi;
-
-    const int row = rb * ROWS + wave * RW + j;
-    const bool rvalid = row < m_kv;
-    const int rrow = rvalid ? row : m_kv - 1;
-    const uint32_t ug = (uint32_t)G;
-    const int t_row = (int)((uint32_t)rrow / ug), h_row = kvh * G + (int)((uint32_t)rrow % ug);
-    int64_t r_lo, r_hi;
-    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + t_row, &r_lo, &r_hi);
-    if (!rvalid) r_hi = r_lo;
-
-    const int wg_row_first = rb * ROWS;
-    const int wg_row_last = min(wg_row_first + ROWS, m_kv) - 1;
-    int64_t k_lo, k_hi, tmp;
-    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_first / ug, &k_lo, &tmp);
-    visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)wg_row_last / ug, &tmp, &k_hi);
-    if (k_lo < s_lo) k_lo = s_lo;
-    if (k_hi > s_hi) k_hi = s_hi;
-    if (k_hi < k_lo) k_hi = k_lo;
-    const int nkeys = uniform32((int)(k_hi - k_lo));
-    const int ntiles = (nkeys + PF_KT - 1) / PF_KT;
-    const int nlast = nkeys - (ntiles - 1) * PF_KT;
-    int tf_lo, tf_hi;
-    {
-        const int w_first = min(wg_row_first + wave * RW, m_kv - 1);
-        const int w_last = min(wg_row_first + wave * RW + RW - 1, m_kv - 1);
-        int64_t a0, b0, full_lo, full_hi;
-        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_first / ug, &a0, &full_hi);
-        visible_range(p, pv.k_pos0, pv.keys, pv.q_pos0 + (uint32_t)w_last / ug, &full_lo, &b0);
-        int64_t lo_t = full_lo - k_lo;
-        lo_t = lo_t <= 0 ? 0 : (lo_t + PF_KT - 1) / PF_KT;
-        int64_t hi_t = full_hi - k_lo;
-        hi_t = hi_t <= 0 ? 0 : hi_t / PF_KT;
-        if (hi_t > ntiles - (nlast < PF_KT ? 1 : 0)) hi_t = ntiles - (nlast < PF_KT ? 1 : 0);
-        tf_lo = uniform32((int)(lo_t < ntiles ? lo_t : ntiles));
-        tf_hi = uniform32((int)hi_t);
-    }
+    const PfRows rows = pf_rows<ROWS, RW>(p, pv, rb, kvh, sidx, wave, j);
+    const int t_row = rows.t_row, h_row = rows.h_row;
+    const bool rvalid = rows.rvalid;
+    const int nkeys = rows.nkeys, ntiles = rows.ntiles;
+    const int tf_lo = rows.tf_lo, tf_hi = rows.tf_hi, rlo0 = rows.rlo0, rhi0 = rows.rhi0;
     const unsigned tf_n = tf_hi > tf_lo ? (unsigned)(tf_hi - tf_lo) : 0u;
-    int rlo0, rhi0;
-    {
-        int64_t x = r_lo - k_lo, y = r_hi - k_lo;
-        rlo0 = (int)(x < 0 ? 0 : (x > nkeys ? nkeys : x));
-        rhi0 = (int)(y < 0 ? 0 : (y > nkeys ? nkeys : y));
-    }
 
     // Q^T B operands: lane holds row j, features 32 ks + 8 g .. + 7.
     u32x4 qb[KS];
@@ -1309,44 +1321,14 @@ __global__ __launch_bounds__(64 * PF16_WAVES) __attribute__((amdgpu_waves_per_eu
     const float tmul = CAP ? p.softcap_log2 : p.scale_log2;
     bool huge = false;
 
-    const int prow = uniform32((int)(pv.sg.row_stride * 2));
-    const int64_t first = (int64_t)kvh * pv.sg.head_stride + (k_lo - seg_start) * pv.sg.row_stride;
-    const uint8_t *k_next = reinterpret_cast<const uint8_t *>(pv.sg.k) + uniform64(first * 2);
-    const uint8_t *v_next = reinterpret_cast<const uint8_t *>(pv.sg.v) + uniform64(first * 2);
-    int off_full[RPW], off_last[RPW];
-    for (int i = 0; i < RPW; ++i) {
-        const int pos = (wave * RPW + i) * 1024 + lane * 16;
-        const int rr = pos / L::row;
-        const int cc = (((pos % L::row) >> 4) ^ L::swz(rr)) * 16;
-        off_full[i] = rr * prow + cc;
-        off_last[i] = (rr < nlast ? rr : nlast - 1) * prow + cc;
-    }
-    int t_next = 0;
-    const uint32_t run0 = (uint32_t)uniform32(wave) * (RPW * 1024);
+    PfRing<L> ring(pv, kvh, rows, wave, lane);
+    const int prow = ring.prow;
+    const int64_t first = ring.first;
+    int &t_next = ring.t_next;
     auto issue = [&](auto stg_tag, auto full_tag) {
-        constexpr int STG = decltype(stg_tag)::value;
-        constexpr bool FULL = decltype(full_tag)::value;
-        const uint32_t mk = (uint32_t)(uintptr_t)(lds + L::k_at(STG)) + run0;
-        const uint32_t mv = (uint32_t)(uintptr_t)(lds + L::v_at(STG)) + run0;
-        if (!FULL && t_next == ntiles - 1) {
-            for (int i = 0; i < RPW; ++i) {
-                dma16(k_next, (uint32_t)off_last[i], mk + i * 1024);
-                dma16(v_next, (uint32_t)off_last[i], mv + i * 1024);
-            }
-        } else {
-            for (int i = 0; i < RPW; ++i) {
-                dma16(k_next, (uint32_t)off_full[i], mk + i * 1024);
-                dma16(v_next, (uint32_t)off_full[i], mv + i * 1024);
-            }
-        }
-        k_next += PF_KT * prow;
-        v_next += PF_KT * prow;
-        ++t_next;
+        ring.template issue<decltype(stg_tag)::value, decltype(full_tag)::value>(lds);
     };
-    auto wait_tile = [&](int t) {
-        const int ahead = t_next - 1 - t;
-        ring_sync<LPT, NS - 2>(ahead);
-    };
+    auto wait_tile = [&](int t) { ring.wait(t); };
 
     // K operand of k-step ks: key row j of a 16-key block (the swizzle of row
     // 16 kb + j equals row j's at these row sizes), chunk 4 ks + g.
@@ -1572,23 +1554,10 @@ __global__ __launch_bounds__(64 * PF16_WAVES) __attribute__((amdgpu_waves_per_eu
     // partial dots added).
     if constexpr (VCONV) {
         if (__ballot(bad_acc && !bad) != 0) {
-            constexpr int CPR = D * 2 / 16;
-            constexpr int RPI = 64 / CPR;
             const uint8_t *vrows = reinterpret_cast<const uint8_t *>(pv.sg.v) + first * 2;
             const uint8_t *krows = reinterpret_cast<const uint8_t *>(pv.sg.k) + first * 2;
-            bool nonfinite = false, big = false;
-            for (int r0 = 0; r0 < nkeys; r0 += RPI) {
-                const int r = r0 + lane / CPR;
-                if (r < nkeys) {
-                    const u32x4 w = *gload_ptr<u32x4>(vrows + (int64_t)r * prow + 16 * (lane % CPR));
-                    for (int e = 0; e < 4; ++e) {
-                        const uint32_t x = w[e];
-                        const uint32_t lo = x & 0x7fffu, hi = (x >> 16) & 0x7fffu;
-                        nonfinite |= lo >= 0x7f80u || hi >= 0x7f80u;
-                        big |= lo >= 0x4780u || hi >= 0x4780u;
-                    }
-                }
-            }
+            bool nonfinite, big;
+            pf_scan_v(vrows, nkeys, prow, D, lane, nonfinite, big);
             if (__ballot(nonfinite) == 0 && __ballot(big) != 0) {
                 for (int fb = 0; fb < FB; ++fb)
                     for (int i = 0; i < 4; ++i) acc[fb][i] = 0.0f;
