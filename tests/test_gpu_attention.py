@@ -477,7 +477,8 @@ def test_prefill_batch_compact_arguments(torch_mod, ops, orc, D, hq, hkv):
         log(f"compact prefill batch D={D} B={B} T={T} positions {pos.tolist()}")
         outs = {}
         for compact in ("1", "0"):
-            ctx = _context_with_env(ops, {"TKH_PREFILL_COMPACT": compact, "TKH_PREFILL_GROUPS": "1"})
+            ctx = _context_with_env(ops, {"TKH_PREFILL_COMPACT": compact, "TKH_PREFILL_GROUPS": "1",
+                                          "TKH_PREFILL16_GROUPS": "1"})
             out = _zeros(torch, B * T * hq * D)
             ops.prefill_batch(ctx, dev(q, "bf16"), dev(kpool, "bf16"), dev(vpool, "bf16"), offsets,
                               caps * D, pos, out, tokens=T, query_heads=hq, kv_heads=hkv, head_dim=D,

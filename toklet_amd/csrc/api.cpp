@@ -518,6 +518,11 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
         if (ctx->prefill_waves == 4 || ctx->prefill_waves == wide) waves = ctx->prefill_waves;
     }
     const int64_t rows_per = 32 * waves;
+    // 16-row kernel: by default for head_dim 256 (configs[3] session chunks
+    // 5.97-6.09 -> 5.57-5.78 ms); at head_dim 128 it measured the same as the
+    // 32-row one on chunks and slower on full batches.
+    const bool rows16 = waves == 4 && (ctx->prefill16 > 0 ? (D == 128 || D == 256)
+                                       : ctx->prefill16 < 0 && D == 256);
     int64_t base_groups = 0;
     int64_t max_span = 0;
     for (auto &p : group) {
@@ -528,7 +533,11 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
     }
     // Too few row-block workgroups to fill the device: split the keys.  The
     // target is set in 128-row workgroups and scaled to this head_dim's size.
-    const int64_t target = std::max<int64_t>(1, ctx->prefill_groups * 128 / rows_per);
+    // The 16-row kernel takes its own target: 64 gave configs[3] the time of
+    // 128 (5.57-5.75 against 5.59-5.75 ms) with half the split partials; 32
+    // was slower (6.31-6.51 ms).
+    const int64_t target =
+        std::max<int64_t>(1, (rows16 ? ctx->prefill16_groups : ctx->prefill_groups) * 128 / rows_per);
     int64_t splits = 1;
     if (base_groups < target) {
         splits = (target + base_groups - 1) / base_groups;
@@ -616,11 +625,6 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
 
     hipEvent_t *ev = nullptr;
     if (ctx->profiling) TRY(profile_slot(ctx, &ev, merge_blocks > 0, err));
-    // 16-row kernel: by default for head_dim 256 (configs[3] session chunks
-    // 5.97-6.09 -> 5.57-5.78 ms); at head_dim 128 it measured the same as the
-    // 32-row one on chunks and slower on full batches.
-    const bool rows16 = waves == 4 && (ctx->prefill16 > 0 ? (D == 128 || D == 256)
-                                       : ctx->prefill16 < 0 && D == 256);
     hipError_t e = rows16 ? tkh_launch_prefill16(&args, (int)plan.dtype, (int)D, wgs, ctx->stream,
                                                  ev ? ev[0] : nullptr, ev ? ev[1] : nullptr)
                           : tkh_launch_prefill(&args, (int)plan.dtype, (int)D, waves, wgs, ctx->stream,
@@ -783,6 +787,7 @@ void init_tuning(tkh_context *ctx, int device) {
     ctx->prefill_waves = env_int("TKH_PREFILL_WAVES", 0);
     ctx->prefill_compact = env_int("TKH_PREFILL_COMPACT", 1) != 0;
     ctx->prefill16 = env_int("TKH_PREFILL16", -1);
+    ctx->prefill16_groups = std::max(1, env_int("TKH_PREFILL16_GROUPS", 64));
 }
 
 // First visible key (absolute) of a query at `position` (window_attention.rs:105-107).

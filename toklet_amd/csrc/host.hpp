@@ -136,6 +136,7 @@ struct tkh_context {
     int prefill_waves = 0;       // waves per prefill workgroup: 0 = chosen per launch, 4 or 8
     bool prefill_compact = true; // chunks of one shape carried in the kernel arguments (no upload)
     int prefill16 = -1;          // four-wave launches on the 16-row kernel: -1 at head_dim 256, 0 never, 1 at 128 and 256
+    int prefill16_groups = 64;   // split target of the 16-row kernel's launches (in 128-row workgroups)
     // profiling: per launch, start/stop of the attention kernel and of the combine kernel
     bool profiling = false;
     std::vector<hipEvent_t> prof_events;
