@@ -66,17 +66,24 @@ namespace tkh {
 // in the kernel's log2 units; the context is divided by the mass.
 // One wave's share of the combine: 64 outputs of row r of KV head kvh of a
 // problem with S splits whose partials start at slot_base.
+// The launch fields the combine reads (from Params, passed on so that a
+// kernel can load and pin them all before the first use).
+struct MergeFields {
+    int G, Hq;
+    float *part_ml, *part_o;
+    uint32_t *status;
+};
 template <int D>
-__device__ __forceinline__ void merge_chunk(const Params &p, int rows, int S, int64_t slot_base,
+__device__ __forceinline__ void merge_chunk(const MergeFields &mf, int rows, int S, int64_t slot_base,
                                             float *out, int kvh, int r, int c) {
-    const int G = p.group, Hq = p.query_heads;
+    const int G = mf.G, Hq = mf.Hq;
     const int lane = threadIdx.x, g4 = lane >> 4, q4 = lane & 15;
     const int d = 64 * c + 4 * q4;
     const int64_t slot0 = slot_base + (int64_t)kvh * S;
     const __amdgpu_buffer_rsrc_t prs =
-        __builtin_amdgcn_make_buffer_rsrc(p.part_ml, 0, 0x7FFFFFFF, BUFFER_RSRC_WORD3);
-    const uint32_t o_base = (uint32_t)(reinterpret_cast<const char *>(p.part_o) -
-                                       reinterpret_cast<const char *>(p.part_ml));
+        __builtin_amdgcn_make_buffer_rsrc(mf.part_ml, 0, 0x7FFFFFFF, BUFFER_RSRC_WORD3);
+    const uint32_t o_base = (uint32_t)(reinterpret_cast<const char *>(mf.part_o) -
+                                       reinterpret_cast<const char *>(mf.part_ml));
     const uint32_t ml0 = (uint32_t)((slot0 * rows + r) * 2) * 4u, ml_step = (uint32_t)rows * 8u;
     const uint32_t o0 = o_base + (uint32_t)((slot0 * rows + r) * D + d) * 4u,
                    o_step = (uint32_t)(rows * D) * 4u;
@@ -90,6 +97,10 @@ __device__ __forceinline__ void merge_chunk(const Params &p, int rows, int S, in
         ov[g] = __builtin_amdgcn_raw_buffer_load_b128(prs, in ? o0 + (uint32_t)sp * o_step : OUT_OF_RANGE, 0, 0);
         mv[g] = __builtin_amdgcn_raw_buffer_load_b64(prs, in ? ml0 + (uint32_t)sp * ml_step : OUT_OF_RANGE, 0, 0);
     }
+    // Every load is issued before the first use: left to itself the scheduler
+    // interleaves the maximum's chain with the loads, and the waits for the
+    // early loads then hold back the later ones (more than one memory trip).
+    __builtin_amdgcn_sched_barrier(0);
     float mmax = NEG_INF;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -129,8 +140,8 @@ __device__ __forceinline__ void merge_chunk(const Params &p, int rows, int S, in
         const int t = r / G, h = kvh * G + r % G;
         *gstore_ptr<f32x4>(out + ((int64_t)t * Hq + h) * D + d) = v;
     }
-    raise_status(p, bad_mass, ST_BAD_MASS);
-    raise_status(p, bad_out, ST_NONFINITE_OUTPUT);
+    raise_status(mf.status, bad_mass, ST_BAD_MASS);
+    raise_status(mf.status, bad_out, ST_NONFINITE_OUTPUT);
 }
 
 // Split-K combine of a single-problem decode launch, as a second kernel: one
@@ -144,11 +155,20 @@ __device__ __forceinline__ void merge_chunk(const Params &p, int rows, int S, in
 template <int D>
 __global__ __launch_bounds__(64) void attn_decode_merge(Params p, int rows) {
     constexpr int CH = D / 64;  // 64-output chunks per row
-    const Problem &pr = p.single;
-    const int nrows = pr.queries * p.group;
-    const int b = blockIdx.x;
-    const int c = b % CH, r = (b / CH) % nrows, kvh = b / (CH * nrows);
-    merge_chunk<D>(p, rows, pr.splits, pr.slot_base, pr.out, kvh, r, c);
+    // The argument fields span several lines, which the compiler read in two
+    // dependent batches (the second missing on a line of its own): every line
+    // is brought in at once, and the fields are read after that, as hits.
+    const_ptr<Params> args = warm_kernarg_ptr<Params, (sizeof(Params) + sizeof(int) + 63) / 64, 0>();
+    (void)p;
+    rows = *(const_ptr<int>)((const_ptr<char>)args + sizeof(Params));
+    const MergeFields mf{args->group, args->query_heads, args->part_ml, args->part_o, args->status};
+    const int queries = args->single.queries, splits = args->single.splits;
+    const int64_t slot_base = args->single.slot_base;
+    float *out = args->single.out;
+    const uint32_t nrows = (uint32_t)(queries * mf.G);
+    const uint32_t b = blockIdx.x;  // non-negative: unsigned divisions
+    const int c = (int)(b % CH), r = (int)((b / CH) % nrows), kvh = (int)(b / (CH * nrows));
+    merge_chunk<D>(mf, rows, splits, slot_base, out, kvh, r, c);
 }
 
 // The same for a compact batch (one query token per session): the sessions
@@ -164,7 +184,8 @@ __global__ __launch_bounds__(64) void attn_decode_merge_batch(Params p, DecodeBa
     const int S = (int)e.splits;
     if (S <= 1) return;
     const int c = b % CH, r = (b / CH) % G, kvh = b / (CH * G);
-    merge_chunk<D>(p, rows, S, (int64_t)e.tile_base, bt.out + (int64_t)i * p.query_heads * D, kvh, r, c);
+    const MergeFields mf{p.group, p.query_heads, p.part_ml, p.part_o, p.status};
+    merge_chunk<D>(mf, rows, S, (int64_t)e.tile_base, bt.out + (int64_t)i * p.query_heads * D, kvh, r, c);
 }
 }  // namespace tkh
 

@@ -321,6 +321,17 @@ template <int NL, int EXTRA> __device__ __forceinline__ void warm_kernarg() {
           "i"(NL > 7 ? 7 * L : 0), "i"(NL > 8 ? 8 * L : 0), "i"(NL > 9 ? 9 * L : 0),
           "i"(NL > 10 ? 10 * L : 0), "i"(EXTRA));
 }
+// warm_kernarg, then the kernel-argument pointer offset by a zero the
+// compiler cannot see through.  Argument fields are invariant loads, which
+// the compiler may move above the warm-up (and wait for them there, a miss of
+// their own); read through this pointer they depend on it, so they issue
+// after its one wait and hit the scalar cache.
+template <class T, int NL, int EXTRA> __device__ __forceinline__ const_ptr<T> warm_kernarg_ptr() {
+    warm_kernarg<NL, EXTRA>();
+    uint32_t z;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+    return (const_ptr<T>)((const_ptr<char>)__builtin_amdgcn_kernarg_segment_ptr() + z);
+}
 
 __device__ __forceinline__ const_ptr<Problem> problem_ptr(const Params &p, int64_t tile) {
     if (p.nproblems == 1) {
