@@ -102,13 +102,18 @@ def test_gqa7_d64_chunk_rows_straddle_blocks(torch_mod, ctx, ops, orc):
     assert err <= TOL_HALF
 
 
-@pytest.mark.parametrize("form", ["-1", "0", "1"])  # TKH_PREFILL16: default, 32-row, 16-row kernel
+# The chunk kernel's forms: 32 rows per wave, and 16 rows per wave in four-wave
+# (64-row, the default) and eight-wave (128-row) workgroups.
+FORMS = {"32": {"TKH_PREFILL16": 0}, "16x4": {"TKH_PREFILL16_WAVES": 4}, "16x8": {"TKH_PREFILL16_WAVES": 8}}
+
+
+@pytest.mark.parametrize("form", list(FORMS))
 @pytest.mark.parametrize("softcap", [0.0, 50.0])
 def test_window_d256_chunk_with_split_keys(torch_mod, ops, orc, softcap, form):
     """configs[3] sliding layer: 8/4/256, W=1024, chunk of 128 at position 3000.  The
     visible range spans 1151 keys, so splits at its ends hold keys only some rows see."""
     torch = torch_mod
-    ctx = _tuned_context(ops, TKH_PREFILL16=form)
+    ctx = _tuned_context(ops, **FORMS[form])
     rng = np.random.default_rng(17)
     hq, hkv, D, W = 8, 4, 256, 1024
     queries, keys = 128, 3128

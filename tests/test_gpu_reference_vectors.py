@@ -65,7 +65,8 @@ def _env(**values):
 def _contexts(ops):
     """name -> context: the default planner (decode kernel for few rows), the
     MFMA chunk kernel for every bf16/f16 call in its 32-row and 16-row forms
-    (TKH_PREFILL16), and each with 32-key splits."""
+    (TKH_PREFILL16; the 16-row one in its default 64-row workgroups), and each
+    with 32-key splits."""
     out = {"decode": ops.Context(0)}
     with _env(TKH_DECODE_DISABLE=1, TKH_PREFILL16=0):
         out["chunk32"] = ops.Context(0)
@@ -212,7 +213,12 @@ def _chunk_case(rng, tokens, hq, hkv, D, cap, offset, v_value, where):
     return q, k, v
 
 
-@pytest.mark.parametrize("form", ["0", "1"])  # TKH_PREFILL16: 32-row and 16-row kernel
+# The chunk kernel's forms: 32 rows per wave, and 16 rows per wave in four-wave
+# (64-row, the default) and eight-wave (128-row) workgroups.
+FORMS = {"32": {"TKH_PREFILL16": 0}, "16x4": {"TKH_PREFILL16_WAVES": 4}, "16x8": {"TKH_PREFILL16_WAVES": 8}}
+
+
+@pytest.mark.parametrize("form", list(FORMS))
 @pytest.mark.parametrize("D", [128, 256])
 @pytest.mark.parametrize("offset", [0, 2000])  # 2000: the chunk's keys are split
 def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset, D, form):
@@ -225,7 +231,7 @@ def test_bf16_value_range_of_the_chunk_kernel(torch_mod, ops, orc, offset, D, fo
     rng = np.random.default_rng(81)
     hq, hkv, tokens = 8, 4, 64
     cap = offset + tokens
-    with _env(TKH_PREFILL16=form):
+    with _env(**FORMS[form]):
         ctx = ops.Context(0)
     shape = ops.CachedAttentionShape(tokens, hq, hkv, D, cap, offset)
     where = (2, offset + 5, 17)

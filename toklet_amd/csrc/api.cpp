@@ -49,7 +49,7 @@ extern "C" int tkh_prefill_merge_blocks_per_row_block(int head_dim, int rows);
 extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_dim, int rows,
                                                int64_t blocks, hipStream_t stream,
                                                hipEvent_t start, hipEvent_t stop);
-extern "C" hipError_t tkh_launch_prefill16(const tkh::PrefillArgs *p, int dtype, int head_dim,
+extern "C" hipError_t tkh_launch_prefill16(const tkh::PrefillArgs *p, int dtype, int head_dim, int waves,
                                            int64_t groups, hipStream_t stream, hipEvent_t start,
                                            hipEvent_t stop);
 extern "C" hipError_t tkh_launch_prefill(const tkh::PrefillArgs *p, int dtype, int head_dim, int waves,
@@ -517,12 +517,16 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
         if (wide != waves && wide_groups >= ctx->prefill_fill_groups * 128 / (32 * wide)) waves = wide;
         if (ctx->prefill_waves == 4 || ctx->prefill_waves == wide) waves = ctx->prefill_waves;
     }
-    const int64_t rows_per = 32 * waves;
-    // 16-row kernel: by default for head_dim 256 (configs[3] session chunks
-    // 5.97-6.09 -> 5.57-5.78 ms); at head_dim 128 it measured the same as the
-    // 32-row one on chunks and slower on full batches.
-    const bool rows16 = waves == 4 && (ctx->prefill16 > 0 ? (D == 128 || D == 256)
-                                       : ctx->prefill16 < 0 && D == 256);
+    // Four-wave launches at head_dim 128 and 256 take the 16-row kernel, by
+    // default with four waves (64-row blocks), which doubles a chunk's
+    // workgroups at the same partial volume: configs[3] session chunks 5.76-5.79
+    // -> 5.32-5.39 ms, configs[1] chunk kernels 14.3-14.7 -> 13.1-13.5 us
+    // (alternating runs).  Eight-wave launches (row blocks that fill the
+    // device, configs[4]) keep the 32-row kernel: the 16-row one reads each
+    // K/V operand for half as many rows and measured slower there.
+    const bool rows16 = ctx->prefill16 != 0 && waves == 4 && (D == 128 || D == 256);
+    const int waves16 = ctx->prefill16_waves;
+    const int64_t rows_per = rows16 ? 16 * waves16 : 32 * waves;
     int64_t base_groups = 0;
     int64_t max_span = 0;
     for (auto &p : group) {
@@ -533,9 +537,9 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
     }
     // Too few row-block workgroups to fill the device: split the keys.  The
     // target is set in 128-row workgroups and scaled to this head_dim's size.
-    // The 16-row kernel takes its own target: 64 gave configs[3] the time of
-    // 128 (5.57-5.75 against 5.59-5.75 ms) with half the split partials; 32
-    // was slower (6.31-6.51 ms).
+    // The 16-row kernel takes its own target: 64 gave configs[3] and configs[1]
+    // their best times with 64-row blocks (5.32-5.39 against 5.39-5.46 ms at
+    // 128; configs[1] session prefill 0.60-0.62 against 0.60-0.65 ms).
     const int64_t target =
         std::max<int64_t>(1, (rows16 ? ctx->prefill16_groups : ctx->prefill_groups) * 128 / rows_per);
     int64_t splits = 1;
@@ -625,7 +629,7 @@ uint32_t launch_prefill(tkh_context *ctx, const Plan &plan, Problems group,
 
     hipEvent_t *ev = nullptr;
     if (ctx->profiling) TRY(profile_slot(ctx, &ev, merge_blocks > 0, err));
-    hipError_t e = rows16 ? tkh_launch_prefill16(&args, (int)plan.dtype, (int)D, wgs, ctx->stream,
+    hipError_t e = rows16 ? tkh_launch_prefill16(&args, (int)plan.dtype, (int)D, waves16, wgs, ctx->stream,
                                                  ev ? ev[0] : nullptr, ev ? ev[1] : nullptr)
                           : tkh_launch_prefill(&args, (int)plan.dtype, (int)D, waves, wgs, ctx->stream,
                                                ev ? ev[0] : nullptr, ev ? ev[1] : nullptr);
@@ -786,8 +790,9 @@ void init_tuning(tkh_context *ctx, int device) {
     ctx->prefill_min_keys = std::max(32, env_int("TKH_PREFILL_MIN_KEYS", 64));
     ctx->prefill_waves = env_int("TKH_PREFILL_WAVES", 0);
     ctx->prefill_compact = env_int("TKH_PREFILL_COMPACT", 1) != 0;
-    ctx->prefill16 = env_int("TKH_PREFILL16", -1);
+    ctx->prefill16 = env_int("TKH_PREFILL16", 1);
     ctx->prefill16_groups = std::max(1, env_int("TKH_PREFILL16_GROUPS", 64));
+    ctx->prefill16_waves = env_int("TKH_PREFILL16_WAVES", 4) == 8 ? 8 : 4;
 }
 
 // First visible key (absolute) of a query at `position` (window_attention.rs:105-107).

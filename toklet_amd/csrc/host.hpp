@@ -135,8 +135,9 @@ struct tkh_context {
     int prefill_min_keys = 64;   // keys per split at least
     int prefill_waves = 0;       // waves per prefill workgroup: 0 = chosen per launch, 4 or 8
     bool prefill_compact = true; // chunks of one shape carried in the kernel arguments (no upload)
-    int prefill16 = -1;          // four-wave launches on the 16-row kernel: -1 at head_dim 256, 0 never, 1 at 128 and 256
+    int prefill16 = 1;           // four-wave launches at head_dim 128/256 on the 16-row kernel (0: never)
     int prefill16_groups = 64;   // split target of the 16-row kernel's launches (in 128-row workgroups)
+    int prefill16_waves = 4;     // 16-row waves per workgroup: 4 (64-row blocks) or 8 (128-row blocks)
     // profiling: per launch, start/stop of the attention kernel and of the combine kernel
     bool profiling = false;
     std::vector<hipEvent_t> prof_events;

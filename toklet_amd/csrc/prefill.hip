@@ -40,11 +40,12 @@
 //    and a second, fully parallel kernel (attn_prefill_merge) combines them,
 //    so no single workgroup reads a whole row block's partials.
 //
-// attn_prefill16<DT, D> is the same algorithm with 16 packed rows per wave on
-// v_mfma_f32_16x16x32: eight waves cover the four-wave kernel's 128-row block
-// (same grid, workspace slots and merge).  The host takes it for head_dim 256,
-// where a 32-row wave needs a whole SIMD's registers and a 16-row wave half of
-// them, so two waves share each SIMD.
+// attn_prefill16<DT, D, CAP, W> is the same algorithm with 16 packed rows per
+// wave on v_mfma_f32_16x16x32, for launches whose row blocks do not fill the
+// device (session chunks, small batches) at head_dim 128 and 256.  Four waves
+// make 64-row blocks (the default: twice a chunk's workgroups at the same
+// partial volume), eight the 32-row kernel's 128-row block.  At head_dim 256
+// a 32-row wave needs a whole SIMD's registers and a 16-row wave about half.
 #include <cstddef>
 #include <type_traits>
 #include <utility>
@@ -1218,12 +1219,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 
 // ---------------------------------------------------------------------------
 // attn_prefill16: the same flash loop with sixteen packed rows per wave, on
-// v_mfma_f32_16x16x32, for launches of few row blocks (session chunks).  At
-// head_dim 256 a 32-row wave fills a SIMD's registers, and one wave per SIMD
-// leaves its LDS reads, vector work and MFMAs to hide one another alone; a
-// 16-row wave needs half the context registers, so eight waves (the same
-// 128-row block, grid, workspace slots and merge as attn_prefill<..., 4>) run
-// two per SIMD, each with half the MFMAs and half the softmax work of a tile.
+// v_mfma_f32_16x16x32, for launches of few row blocks (session chunks).  A
+// wave does half the MFMAs and half the softmax work of a 32-row wave per
+// tile, and at head_dim 256 needs about half its registers.  Four-wave
+// workgroups (64-row blocks) give a chunk twice the workgroups of 128-row
+// blocks with the same split partials; eight-wave ones cover a 128-row block
+// (attn_prefill<..., 4>'s grid and workspace slots).
 //
 // Lane (j, g) = (lane % 16, lane / 16):
 //  * S^T = K Q^T per 16-key block kb: A = K (lane: key 16 kb + j, features
@@ -1256,13 +1257,12 @@ __device__ __forceinline__ float row4_max(float x) {
     return maxn(x, __shfl_xor(x, 32));
 }
 
-constexpr int PF16_WAVES = 8;  // 16-row waves per workgroup: a 128-row block
-
-template <int DT, int D, bool CAP>
-__global__ __launch_bounds__(64 * PF16_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill16(PrefillArgs a) {
+// W 16-row waves per workgroup: eight make the four-wave 32-row kernel's
+// 128-row block; four make 64-row blocks.
+template <int DT, int D, bool CAP, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill16(PrefillArgs a) {
     warm_kernarg<(offsetof(PrefillArgs, b) + offsetof(PrefillBatch, e) + 63) / 64, sizeof(PrefillArgs)>();
     const Params &p = a.p;
-    constexpr int W = PF16_WAVES;
     constexpr int RW = 16;            // packed rows per wave
     constexpr int ROWS = RW * W;      // packed rows per workgroup
     constexpr int KS = D / 32;        // Q.K k-steps (32 features each) per 16-key block
@@ -1741,7 +1741,7 @@ extern "C" hipError_t tkh_launch_prefill_merge(const tkh::Params *p, int head_di
                               *p, blocks);                                                       \
         return hipGetLastError();                                                                \
     }
-    TKH_PM(64, 128) TKH_PM(128, 128) TKH_PM(128, 256) TKH_PM(256, 128)
+    TKH_PM(64, 128) TKH_PM(128, 128) TKH_PM(128, 256) TKH_PM(256, 128) TKH_PM(128, 64) TKH_PM(256, 64)
 #undef TKH_PM
     return hipErrorInvalidValue;
 }
@@ -1765,21 +1765,23 @@ extern "C" hipError_t tkh_launch_prefill(const tkh::PrefillArgs *p, int dtype, i
     return hipErrorInvalidValue;
 }
 
-// The 16-row form of a four-wave (128-row) launch: same grid and workspace.
-extern "C" hipError_t tkh_launch_prefill16(const tkh::PrefillArgs *p, int dtype, int head_dim,
+// The 16-row kernel: `waves` 16-row waves per workgroup (8: the four-wave
+// 32-row kernel's 128-row blocks, grid and workspace; 4: 64-row blocks).
+extern "C" hipError_t tkh_launch_prefill16(const tkh::PrefillArgs *p, int dtype, int head_dim, int waves,
                                            int64_t groups, hipStream_t stream, hipEvent_t start,
                                            hipEvent_t stop) {
     using namespace tkh;
-    dim3 grid((unsigned)groups), block(64 * PF16_WAVES);
-#define TKH_PF16(DT, DD)                                                                \
-    if (dtype == DT && head_dim == DD) {                                                \
+    dim3 grid((unsigned)groups), block(64 * waves);
+#define TKH_PF16(DT, DD, WW)                                                            \
+    if (dtype == DT && head_dim == DD && waves == WW) {                                 \
         if (p->p.softcap != 0.0f)                                                       \
-            hipExtLaunchKernelGGL((attn_prefill16<DT, DD, true>), grid, block, 0, stream, start, stop, 0, *p);  \
+            hipExtLaunchKernelGGL((attn_prefill16<DT, DD, true, WW>), grid, block, 0, stream, start, stop, 0, *p);  \
         else                                                                            \
-            hipExtLaunchKernelGGL((attn_prefill16<DT, DD, false>), grid, block, 0, stream, start, stop, 0, *p); \
+            hipExtLaunchKernelGGL((attn_prefill16<DT, DD, false, WW>), grid, block, 0, stream, start, stop, 0, *p); \
         return hipGetLastError();                                                       \
     }
-    TKH_PF16(BF16, 128) TKH_PF16(BF16, 256) TKH_PF16(F16, 128) TKH_PF16(F16, 256)
+    TKH_PF16(BF16, 128, 8) TKH_PF16(BF16, 256, 8) TKH_PF16(F16, 128, 8) TKH_PF16(F16, 256, 8)
+    TKH_PF16(BF16, 128, 4) TKH_PF16(BF16, 256, 4) TKH_PF16(F16, 128, 4) TKH_PF16(F16, 256, 4)
 #undef TKH_PF16
     return hipErrorInvalidValue;
 }
