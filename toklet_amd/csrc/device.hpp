@@ -321,6 +321,11 @@ template <int NL, int EXTRA> __device__ __forceinline__ void warm_kernarg() {
           "i"(NL > 7 ? 7 * L : 0), "i"(NL > 8 ? 8 * L : 0), "i"(NL > 9 ? 9 * L : 0),
           "i"(NL > 10 ? 10 * L : 0), "i"(EXTRA));
 }
+// Hold wave-uniform values (kernel-argument fields) in scalar registers from
+// here on: each needs its load complete, so loads read before a call are all
+// issued before its first wait.
+template <class T> __device__ __forceinline__ void pin_arg(T &x) { asm volatile("" : "+s"(x)); }
+template <class... T> __device__ __forceinline__ void pin_args(T &...x) { (pin_arg(x), ...); }
 // warm_kernarg, then the kernel-argument pointer offset by a zero the
 // compiler cannot see through.  Argument fields are invariant loads, which
 // the compiler may move above the warm-up (and wait for them there, a miss of

@@ -72,19 +72,35 @@ template <int UNIT> struct Piece;
 template <> struct Piece<16> { using T = u32x4; };
 template <> struct Piece<2> { using T = uint16_t; };
 
+// The gate of ungated commits: a zero word, so that the gate is always read
+// through a valid pointer and waited for only at the stores.
+__device__ const uint32_t kv_open_gate = 0u;
+
+constexpr int COPY_THREADS = 256;  // kv_copy_batch's workgroup size
+
 template <int UNIT>
-__global__ __launch_bounds__(256) void kv_copy_batch(CopyBatch b) {
+__global__ __launch_bounds__(COPY_THREADS) void kv_copy_batch(CopyBatch b) {
     using T = typename Piece<UNIT>::T;
+    // Every argument field the copy needs, read before the first use of any:
+    // left to itself the compiler read them in several dependent batches
+    // (gate pointer, entry, run bounds), each a wait on a kernel-argument line.
+    // The grid size (a hidden argument on a line of its own) joins the batch.
+    CopyRunsEntry e = b.e[blockIdx.y];
+    const uint32_t *gate = b.gate ? b.gate : &kv_open_gate;
+    uint64_t *committed = b.committed;
+    uint64_t committed_value = b.committed_value;
+    uint32_t nblocks = gridDim.x;
+    pin_args(e.src_k, e.src_v, e.dst_k, e.dst_v, e.tokens, e.row_bytes, e.capacity, e.runs[0], e.runs[1],
+             e.runs[2], e.runs[3], e.runs[4], e.runs[5], e.heads, gate, committed, committed_value, nblocks);
     // Written by earlier launches on the stream (visible at this launch's
-    // start): a plain load, which the compiler waits for only at the stores.
-    const uint32_t g = b.gate ? *b.gate : 0u;
-    const CopyRunsEntry e = b.e[blockIdx.y];  // by value: its fields in one batch of scalar loads
+    // start).  The compiler tests it once, before the copy loop.
+    const uint32_t g = *gate;
     const int64_t per_row = e.row_bytes / UNIT;
     const int64_t r0_rows = e.runs[2], rows = e.runs[2] + e.runs[5];
     const int64_t total = (int64_t)e.heads * rows * per_row;
     const bool narrow = total <= 0x7fffffff;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
+    for (int64_t i = (int64_t)blockIdx.x * COPY_THREADS + threadIdx.x; i < total;
+         i += (int64_t)nblocks * COPY_THREADS) {
         int64_t c, r, h;
         if (narrow) {
             const uint32_t i32 = (uint32_t)i, pr = (uint32_t)per_row, rs = (uint32_t)rows;
@@ -109,8 +125,8 @@ __global__ __launch_bounds__(256) void kv_copy_batch(CopyBatch b) {
             reinterpret_cast<T *>(e.dst_v)[d] = vx;
         }
     }
-    if (b.committed && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && g == 0)
-        *b.committed = b.committed_value;
+    if (committed && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && g == 0)
+        *committed = committed_value;
 }
 
 template <int DT>
@@ -199,7 +215,7 @@ extern "C" hipError_t tkh_launch_copy_batch(const tkh::CopyBatch *b, hipStream_t
         const auto &e = b->e[i];
         most = std::max<int64_t>(most, (int64_t)e.heads * (e.runs[2] + e.runs[5]) * (e.row_bytes / unit));
     }
-    dim3 grid(grid_for(most), (unsigned)b->count), block(256);
+    dim3 grid(grid_for(most), (unsigned)b->count), block(COPY_THREADS);
     if (vec) hipLaunchKernelGGL(kv_copy_batch<16>, grid, block, 0, stream, *b);
     else hipLaunchKernelGGL(kv_copy_batch<2>, grid, block, 0, stream, *b);
     return hipGetLastError();
